@@ -1,0 +1,60 @@
+"""ctypes binding of libexl3_amd.so (the C ABI declared in include/exl3_amd.h).
+
+The library is built in-tree by ampstein_amd.build (or __graft_entry__.build()).  There is
+no fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libexl3_amd.so")
+HEADER = os.path.join(os.path.dirname(PKG), "include", "exl3_amd.h")
+
+OK, EINVAL, EUNSUPPORTED, EHIP, ENOMEM = 0, -1, -2, -3, -4
+TAG_GEMV, TAG_GEMM = 90, 91
+
+_lib = None
+
+_vp, _i32, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "exl3_amd_last_error": (ctypes.c_char_p, []),
+    "exl3_amd_version": (_i32, []),
+    "exl3_amd_init": (_i32, [_i32]),
+    "exl3_amd_reconstruct": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_reconstruct_had": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_had_r_128": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _f32, _vp]),
+    "exl3_amd_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
+}
+
+
+class Exl3Error(RuntimeError):
+    """Raised when a C-ABI call returns a negative code (the reference raises c10::Error)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def lib():
+    """Load libexl3_amd.so (torch first, so the process shares torch's HIP runtime)."""
+    global _lib
+    if _lib is None:
+        import torch  # noqa: F401
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m ampstein_amd.build` "
+                               "(or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise Exl3Error(rc, lib().exl3_amd_last_error().decode())
+    return rc

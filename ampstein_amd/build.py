@@ -1,0 +1,87 @@
+"""Build libexl3_amd.so (HIP, gfx950) in-tree: ampstein_amd/lib/libexl3_amd.so.
+
+    python -m ampstein_amd.build [-j N]
+
+Each kernel unit is compiled separately with hipcc (the GEMV once per bitrate K) and the
+objects are linked into one shared library exporting the C ABI of include/exl3_amd.h.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+import time
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+OBJ = os.path.join(PKG, "_build")
+LIB_DIR = os.path.join(PKG, "lib")
+LIB = os.path.join(LIB_DIR, "libexl3_amd.so")
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    # packed fp32 ops stay off on this pool; every fp32 / fp16 operation rounds once
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-ffp-contract=off", "-fno-fast-math",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-result",
+    f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
+]
+
+
+def units():
+    u = [
+        ("exl3_capi.cpp", "exl3_capi.o", []),
+        ("exl3_reconstruct.hip", "exl3_reconstruct.o", []),
+        ("exl3_hadamard.hip", "exl3_hadamard.o", []),
+    ]
+    for k in range(1, 9):
+        u.append(("exl3_gemv.hip", f"exl3_gemv_k{k}.o", [f"-DEXL3_INST_K={k}"]))
+    return u
+
+
+def _compile(src, obj, extra):
+    cmd = [HIPCC] + COMMON + extra + ["-x", "hip", "-c", os.path.join(CSRC, src), "-o", os.path.join(OBJ, obj)]
+    t0 = time.time()
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src} {extra}:\n{p.stderr[-6000:]}")
+    return obj, time.time() - t0
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        futs = [ex.submit(_compile, *u) for u in units()]
+        for f in cf.as_completed(futs):
+            obj, dt = f.result()
+            if verbose:
+                print(f"  {obj}: {dt:.1f}s", flush=True)
+    objs = [os.path.join(OBJ, o) for _, o, _ in units()]
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"link failed:\n{p.stderr[-6000:]}")
+    shutil.move(tmp, LIB)
+    return LIB
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("-j", type=int, default=None)
+    args = ap.parse_args(argv)
+    t0 = time.time()
+    path = build(args.j, verbose=True)
+    print(f"built {path} in {time.time() - t0:.1f}s")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,39 @@
+// Internal launcher interface between the C-ABI layer (exl3_capi.cpp) and the kernel units.
+// Launchers validate nothing: the C-ABI checks every shape, pointer and bitrate first.
+// They return 0 or a hipError_t / -1 (no instance for the requested K / codebook).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct GemvArgs
+{
+    const uint16_t* A;          // (m, k) fp16
+    const uint16_t* trellis;    // (k/16, n/16, 16K) uint16
+    void* C;                    // (m, n) fp16 or fp32
+    const uint16_t* suh;        // (k) fp16 or null
+    const uint16_t* svh;        // (n) fp16 or null
+    int m, k, n;
+    int c_fp32;
+    int splits;                 // requested k-splits (>= 1)
+    float* partials;            // workspace: splits * m * n fp32
+    int* counters;              // workspace: n / 128 ints, zero between calls
+};
+
+int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
+                      int nt_off, int K, int cb, hipStream_t s);
+int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
+                          const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                          int K, int cb, hipStream_t s);
+
+int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
+                 const uint16_t* pre, const uint16_t* post, float scale, hipStream_t s);
+
+int exl3k_gemv_k1(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k2(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k3(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k4(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k5(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k6(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k7(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k8(const GemvArgs& g, int cb, hipStream_t s);

@@ -1,0 +1,267 @@
+// Trellis -> fp16 weight reconstruction for gfx950.
+//
+//   reconstruct      W_hat (k, n) in the Hadamard basis        (quant/reconstruct.cu:14-98)
+//   reconstruct_had  W = diag(suh) H W_hat H diag(svh) per 128x128 block, original basis,
+//                    with the reference's fp16 rounding points  (quant/reconstruct.cu:212-364)
+//
+// Both are bit-exact restatements: the decode is the codebook arithmetic of exl3_common.cuh,
+// and every fp16 operation of the fused form is issued in the reference's order (the column
+// pass rounds after each add / sub and after the 1/sqrt(128) multiply; the row pass runs its
+// first two butterfly stages in fp32, then fp16).
+#include "exl3_common.cuh"
+#include "exl3_kernels.h"
+
+using namespace exl3;
+
+namespace {
+
+// Load this lane's K words of the 8-tile chunk; ring_prev supplies the word before them.
+template <int K>
+__device__ __forceinline__ void load_lane_words(const uint32_t* __restrict__ p, uint32_t* w)
+{
+    if constexpr (K % 4 == 0)
+    {
+        #pragma unroll
+        for (int i = 0; i < K / 4; ++i)
+        {
+            u32x4 v = __builtin_nontemporal_load((const u32x4*) p + i);
+            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        }
+    }
+    else if constexpr (K % 2 == 0)
+    {
+        #pragma unroll
+        for (int i = 0; i < K / 2; ++i)
+        {
+            u32x2 v = __builtin_nontemporal_load((const u32x2*) p + i);
+            w[2 * i] = v.x; w[2 * i + 1] = v.y;
+        }
+    }
+    else
+    {
+        #pragma unroll
+        for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(p + i);
+    }
+}
+
+// Decode one k-slice x 128-column chunk per wave: returns the 16 packed pairs of this lane.
+template <int K, int CB>
+__device__ __forceinline__ void decode_slice(const uint16_t* __restrict__ trellis, int tiles_n,
+                                             int kt, int nt0, int lane, uint32_t* pairs,
+                                             const DecodeRegs& r)
+{
+    const uint32_t* base = (const uint32_t*) trellis
+                         + ((size_t) kt * tiles_n + nt0) * (8 * K) + (size_t) lane * K;
+    uint32_t wv[K + 1];
+    load_lane_words<K>(base, wv + 1);
+    wv[0] = ring_prev(wv[K], lane);
+    decode_lane32<K, CB>(wv, pairs, r);
+}
+
+// ------------------------------------------------------------------------------ reconstruct
+// Grid (n / 128, ceil(k / 64)), 256 threads: wave w decodes k-slice 4*blockIdx.y + w of the
+// 128-column chunk, transposes through LDS and writes 16 coalesced 256-byte rows.
+template <int K, int CB>
+__global__ __launch_bounds__(256)
+void reconstruct_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ trellis,
+                        int k, int n, int tiles_n, int nt_off)
+{
+    __shared__ uint32_t sh[4][16][64 + 4];     // per wave: 16 rows x 128 halves (+pad)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kt = blockIdx.y * 4 + wave;
+    const int chunk = blockIdx.x;
+    if (kt >= k / 16) return;
+    const DecodeRegs r = make_decode_regs<CB>();
+
+    uint32_t pairs[16];
+    decode_slice<K, CB>(trellis, tiles_n, kt, nt_off + chunk * 8, lane, pairs, r);
+
+    uint16_t* s16 = (uint16_t*) &sh[wave][0][0];
+    const int j = lane & 7, tcol = (lane >> 3) * 16;
+    #pragma unroll
+    for (int q = 0; q < 16; ++q)
+    {
+        const int c = tcol + pair_col(j, q), row = pair_row(q);
+        s16[row * 136 + c] = (uint16_t) pairs[q];
+        s16[(row + 1) * 136 + c] = (uint16_t)(pairs[q] >> 16);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // 4 stores of 64 lanes x 16 bytes: lane -> row (4i + lane/16), 8 halves at (lane%16)*8
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int row = 4 * i + (lane >> 4), c8 = (lane & 15) * 8;
+        u32x4 v = *(const u32x4*) (s16 + row * 136 + c8);
+        *(u32x4*) (W + (size_t) (kt * 16 + row) * n + chunk * 128 + c8) = v;
+    }
+}
+
+// -------------------------------------------------------------------------- reconstruct_had
+// One 128x128 block per workgroup.  LDS holds the block as 128 rows x 64 dwords with the
+// dword index of (row R, column pair cp) swizzled to cp ^ (2 * ((R >> 2) & 31)): conflict-free
+// for the column pass (32 lanes, 4 rows each, one column pair) and 8-byte aligned for the row
+// pass (32 lanes, 4 columns each).
+__device__ __forceinline__ int rh_dw(int R, int cp) { return R * 64 + (cp ^ (((R >> 2) & 31) << 1)); }
+
+__device__ __forceinline__ f16x2 shfl_h2(f16x2 v, int src_lane)
+{
+    return as_h2(__builtin_amdgcn_ds_bpermute(src_lane << 2, as_u32(v)));
+}
+
+// fp16 lane stages xor 1..16 within a 32-lane half: lower lane a + b, upper (-b) + a
+// (shuffle_had_h2x32, hadamard_inner.cuh:83-93).
+__device__ __forceinline__ f16x2 had_h2x32(f16x2 v, int lane)
+{
+    #pragma unroll
+    for (int m = 1; m < 32; m <<= 1)
+    {
+        f16x2 p = shfl_h2(v, lane ^ m);
+        v = (lane & m) ? (p + (-v)) : (v + p);
+    }
+    return v;
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(256)
+void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ trellis,
+                            const uint16_t* __restrict__ suh, const uint16_t* __restrict__ svh,
+                            int n, int tiles_n, int nt_off)
+{
+    __shared__ uint32_t blk[128 * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = blockIdx.x, kb = blockIdx.y;
+    const DecodeRegs r = make_decode_regs<CB>();
+    uint16_t* b16 = (uint16_t*) blk;
+
+    // 1. decode 8 k-slices x 8 tiles (wave w: slices w, w + 4)
+    #pragma unroll
+    for (int it = 0; it < 2; ++it)
+    {
+        const int js = wave + 4 * it;
+        uint32_t pairs[16];
+        decode_slice<K, CB>(trellis, tiles_n, kb * 8 + js, nt_off + nb * 8, lane, pairs, r);
+        const int j = lane & 7, tcol = (lane >> 3) * 16;
+        #pragma unroll
+        for (int q = 0; q < 16; ++q)
+        {
+            const int c = tcol + pair_col(j, q), R = js * 16 + pair_row(q);
+            b16[rh_dw(R, c >> 1) * 2 + (c & 1)] = (uint16_t) pairs[q];
+            b16[rh_dw(R + 1, c >> 1) * 2 + (c & 1)] = (uint16_t)(pairs[q] >> 16);
+        }
+    }
+    __syncthreads();
+
+    const f16x2 rs2 = { (f16) 0.08838834764831845f, (f16) 0.08838834764831845f };
+    const int t = lane & 31, half = lane >> 5;
+
+    // 2. column pass (reconstruct.cu:290-325): per column pair, rows 4t..4t+3 in lane t;
+    //    fp16 4-point stage, times rs, fp16 lane stages
+    for (int it = 0; it < 8; ++it)
+    {
+        const int cp = (wave * 8 + it) * 2 + half;
+        f16x2 v[4];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = as_h2(blk[rh_dw(4 * t + i, cp)]);
+        f16x2 s0 = v[0] + v[1], d0 = v[0] - v[1];
+        f16x2 s1 = v[2] + v[3], d1 = v[2] - v[3];
+        v[0] = (s0 + s1) * rs2;
+        v[1] = (d0 + d1) * rs2;
+        v[2] = (s0 - s1) * rs2;
+        v[3] = (d0 - d1) * rs2;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = had_h2x32(v[i], lane);
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) blk[rh_dw(4 * t + i, cp)] = as_u32(v[i]);
+    }
+    __syncthreads();
+
+    // 3. row pass fused with the store (reconstruct.cu:331-357): row R, columns 4t..4t+3 in
+    //    lane t; fp32 4-point stage, round, times rs in fp16, fp16 lane stages, * suh * svh
+    const uint32_t sv01 = ((const uint32_t*) svh)[nb * 64 + 2 * t];
+    const uint32_t sv23 = ((const uint32_t*) svh)[nb * 64 + 2 * t + 1];
+    for (int it = 0; it < 16; ++it)
+    {
+        const int R = (wave * 16 + it) * 2 + half;
+        const int d = rh_dw(R, 2 * t);
+        f16x2 a = as_h2(blk[d]), b = as_h2(blk[d + 1]);
+        float v0 = (float) a.x, v1 = (float) a.y, v2 = (float) b.x, v3 = (float) b.y;
+        float s0 = v0 + v1, d0 = v0 - v1, s1 = v2 + v3, d1 = v2 - v3;
+        f16x2 h01 = { (f16) (s0 + s1), (f16) (d0 + d1) };
+        f16x2 h23 = { (f16) (s0 - s1), (f16) (d0 - d1) };
+        h01 = h01 * rs2;
+        h23 = h23 * rs2;
+        h01 = had_h2x32(h01, lane);
+        h23 = had_h2x32(h23, lane);
+        const f16 su = as_h(suh[kb * 128 + R]);
+        const f16x2 su2 = { su, su };
+        h01 = (h01 * su2) * as_h2(sv01);
+        h23 = (h23 * su2) * as_h2(sv23);
+        u32x2 o = { as_u32(h01), as_u32(h23) };
+        *(u32x2*) (W + (size_t) (kb * 128 + R) * n + nb * 128 + 4 * t) = o;
+    }
+}
+
+template <int K, int CB>
+int launch_reconstruct_t(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
+                         int nt_off, hipStream_t s)
+{
+    dim3 grid(n / 128, (k / 16 + 3) / 4);
+    hipLaunchKernelGGL((reconstruct_kernel<K, CB>), grid, dim3(256), 0, s, W, trellis, k, n, tiles_n, nt_off);
+    return (int) hipGetLastError();
+}
+
+template <int K, int CB>
+int launch_reconstruct_had_t(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
+                             const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                             hipStream_t s)
+{
+    dim3 grid(n / 128, k / 128);
+    hipLaunchKernelGGL((reconstruct_had_kernel<K, CB>), grid, dim3(256), 0, s, W, trellis, suh, svh, n, tiles_n, nt_off);
+    return (int) hipGetLastError();
+}
+
+}  // namespace
+
+#define EXL3_DISPATCH_K_CB(K, CB, FN, ...)                                        \
+    switch (CB * 16 + K)                                                          \
+    {                                                                             \
+        case 0 * 16 + 1: return FN<1, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 2: return FN<2, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 3: return FN<3, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 4: return FN<4, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 5: return FN<5, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 6: return FN<6, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 7: return FN<7, 0>(__VA_ARGS__);                            \
+        case 0 * 16 + 8: return FN<8, 0>(__VA_ARGS__);                            \
+        case 1 * 16 + 1: return FN<1, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 2: return FN<2, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 3: return FN<3, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 4: return FN<4, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 5: return FN<5, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 6: return FN<6, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 7: return FN<7, 1>(__VA_ARGS__);                            \
+        case 1 * 16 + 8: return FN<8, 1>(__VA_ARGS__);                            \
+        case 2 * 16 + 1: return FN<1, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 2: return FN<2, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 3: return FN<3, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 4: return FN<4, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 5: return FN<5, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 6: return FN<6, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 7: return FN<7, 2>(__VA_ARGS__);                            \
+        case 2 * 16 + 8: return FN<8, 2>(__VA_ARGS__);                            \
+    }                                                                             \
+    return -1;
+
+int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
+                      int nt_off, int K, int cb, hipStream_t s)
+{
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_t, W, trellis, k, n, tiles_n, nt_off, s)
+}
+
+int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
+                          const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                          int K, int cb, hipStream_t s)
+{
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_had_t, W, trellis, suh, svh, k, n, tiles_n, nt_off, s)
+}

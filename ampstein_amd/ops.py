@@ -1,0 +1,215 @@
+"""The reference's EXL3 operator interface over torch tensors, backed by libexl3_amd.so.
+
+Names, argument order, argument meaning and error behaviour follow the vendored
+exllamav3 functions that ampstein's torch.so binds (argument checks raise, as TORCH_CHECK
+does; nothing falls back to a CPU path):
+
+  reconstruct            vendor/exl3/exllamav3_ext/quant/reconstruct.cu:492-501
+  reconstruct_slice      vendor/exl3/exllamav3_ext/quant/reconstruct.cu:141-194
+  reconstruct_had_slice  vendor/exl3/exllamav3_ext/quant/reconstruct.cu:431-490
+  had_r_128              vendor/exl3/exllamav3_ext/quant/hadamard.cu:125-210
+  exl3_gemm              vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:114-350
+  exl3_gemm_recon        src/torch/amp_torch.cpp:11149-11230 (prefill policy)
+
+Tensors stay on the caller's device; work is enqueued on torch's current stream.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import check
+
+Tensor = torch.Tensor
+
+RECON_FUSED_ROWS = 2048      # amp_torch.cpp:11203-11209 (AMP_RECON_FUSED_ROWS default)
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(cond: bool, msg: str):
+    if not cond:
+        raise _lib.Exl3Error(_lib.EINVAL, msg)
+
+
+def _dtype(t: Tensor, dt, name: str):
+    _need(t.dtype == dt, f"{name} is incorrect datatype, must be {dt}")
+
+
+def _cuda(*ts):
+    for t in ts:
+        if t is not None:
+            _need(t.is_cuda, "tensors must be on a GPU device")
+            _need(t.is_contiguous(), "tensors must be contiguous")
+
+
+def _trellis_dtype(t: Tensor, name: str):
+    _need(t.dtype in (torch.int16, torch.uint16), f"{name} is incorrect datatype, must be int16")
+
+
+def _codebook_flags(mcg: bool, mul1: bool):
+    _need(not (mcg and mul1), "Specified both mcg and mul1")
+    return int(bool(mcg)), int(bool(mul1))
+
+
+def bits_from_K(K: float):
+    """quant/bits_k.cuh:178-185: integer 1..8, or 1.5 / 2.5 / 3.5."""
+    bits = int(K)
+    f = float(K) - bits
+    _need(1 <= bits <= 8 and (f == 0.0 or (f == 0.5 and bits <= 3)),
+          f"Unsupported EXL3 bitrate {K} (integer 1..8, or 1.5 / 2.5 / 3.5)")
+    return bits, f == 0.5
+
+
+def reconstruct_slice(unpacked: Tensor, packed: Tensor, K: float, mcg: bool, mul1: bool,
+                      n_offset: int) -> None:
+    """Decode trellis columns [n_offset, n_offset + unpacked.size(1)) into `unpacked`
+    (fp16, rotated basis), bit-exact with the reference."""
+    bits, half = bits_from_K(K)
+    _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
+    _need(packed.dim() == 3 and unpacked.dim() == 2, "reconstruct: bad tensor ranks")
+    _need(unpacked.size(0) == packed.size(0) * 16, "unpacked and packed shapes are incompatible")
+    _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
+    _dtype(unpacked, torch.half, "unpacked")
+    _trellis_dtype(packed, "packed")
+    if unpacked.numel() == 0:
+        return
+    _cuda(unpacked, packed)
+    mcg_i, mul1_i = int(bool(mcg)), int(bool(mul1))     # mcg wins when both are set
+    with torch.cuda.device(unpacked.device):
+        check(_lib.lib().exl3_amd_reconstruct(
+            unpacked.data_ptr(), packed.data_ptr(), unpacked.size(0), packed.size(1) * 16,
+            unpacked.size(1), int(n_offset), float(K), mcg_i, mul1_i, _stream(unpacked)))
+
+
+def reconstruct(unpacked: Tensor, packed: Tensor, K: float, mcg: bool = False,
+                mul1: bool = False) -> None:
+    _need(unpacked.dim() == 2 and packed.dim() == 3 and unpacked.size(1) == packed.size(1) * 16,
+          "unpacked and packed shapes are incompatible")
+    reconstruct_slice(unpacked, packed, K, mcg, mul1, 0)
+
+
+def reconstruct_had_slice(unpacked: Tensor, packed: Tensor, suh: Tensor, svh: Tensor,
+                          K: float, mcg: bool, mul1: bool, n_offset: int) -> None:
+    """Original-basis weights diag(suh) H W_hat H diag(svh) per 128x128 block."""
+    bits, half = bits_from_K(K)
+    _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
+    _need(packed.dim() == 3 and unpacked.dim() == 2, "reconstruct_had: bad tensor ranks")
+    _need(unpacked.size(0) == packed.size(0) * 16, "unpacked and packed shapes are incompatible")
+    _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
+    _dtype(unpacked, torch.half, "unpacked")
+    _dtype(suh, torch.half, "suh")
+    _dtype(svh, torch.half, "svh")
+    _trellis_dtype(packed, "packed")
+    if unpacked.numel() == 0:
+        return
+    _need(suh.numel() >= unpacked.size(0), "reconstruct_had: suh size")
+    _need(svh.numel() >= unpacked.size(1), "reconstruct_had: svh size")
+    _cuda(unpacked, packed, suh, svh)
+    mcg_i, mul1_i = int(bool(mcg)), int(bool(mul1))     # mcg wins when both are set
+    with torch.cuda.device(unpacked.device):
+        check(_lib.lib().exl3_amd_reconstruct_had(
+            unpacked.data_ptr(), packed.data_ptr(), suh.data_ptr(), svh.data_ptr(),
+            unpacked.size(0), packed.size(1) * 16, unpacked.size(1), int(n_offset), float(K),
+            mcg_i, mul1_i, _stream(unpacked)))
+
+
+def had_r_128(input: Tensor, output: Tensor, pre_scale: Optional[Tensor] = None,
+              post_scale: Optional[Tensor] = None, scale: float = 1.0) -> None:
+    """y = (x.view(-1, 128) @ H128 / sqrt(128)).view(x.shape) with an optional fp16 pre- or
+    post-scale; works in place.  As in the reference, a given pre_scale takes precedence and
+    post_scale is then ignored (hadamard.cu:170-186)."""
+    _need(input.shape == output.shape, "input and output shapes differ")
+    _need(input.dim() == 2, "input must be 2-dimensional")
+    _need(input.size(1) % 128 == 0, "input columns must be divisible by 128")
+    if input.dtype == torch.half:
+        _dtype(output, torch.half, "output")
+        fp32 = 0
+    elif input.dtype == torch.float:
+        _dtype(output, torch.float, "output")
+        fp32 = 1
+    else:
+        raise _lib.Exl3Error(_lib.EINVAL, "unsupported datatype")
+    if post_scale is not None and pre_scale is not None:
+        post_scale = None
+    for s in (pre_scale, post_scale):
+        if s is not None:
+            _dtype(s, torch.half, "scale")
+            _need(s.numel() >= input.size(1), "scale vector too short")
+    if input.numel() == 0:
+        return
+    _cuda(input, output, pre_scale, post_scale)
+    with torch.cuda.device(input.device):
+        check(_lib.lib().exl3_amd_had_r_128(
+            input.data_ptr(), output.data_ptr(), input.size(0), input.size(1), fp32,
+            _ptr(pre_scale), _ptr(post_scale), float(scale), _stream(input)))
+
+
+def exl3_gemm(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], A_had: Optional[Tensor],
+              svh: Optional[Tensor], force_shape_idx: int = 0, mcg: bool = False,
+              mul1: bool = False, force_num_sms: int = 0) -> int:
+    """C = A @ dequant(B), with the input / output rotations when suh / svh are given.
+    A (..., k) fp16, B trellis (k/16, n/16, 16K) int16, C (..., n) fp16 or fp32.
+    Returns the kernel tag (90 = GEMV, 91 = MFMA GEMM).  force_num_sms is accepted for
+    interface parity (the reference's cooperative-grid override) and has no effect."""
+    _need(B.dim() == 3, "B must be 3-dimensional")
+    _need(A.size(-1) == B.size(0) * 16, "A and B shapes are incompatible")
+    _need(C.size(-1) == B.size(1) * 16, "C and B shapes are incompatible")
+    _dtype(A, torch.half, "A")
+    _trellis_dtype(B, "B")
+    _need(C.dtype in (torch.half, torch.float), "C is incorrect datatype, must be half or float")
+    tile = B.size(2)
+    half_k = tile % 16 != 0
+    _need(not half_k or (tile % 16 == 8 and mul1),
+          "exl3_gemm: half-integer bitrates require the mul1 codebook")
+    K = tile // 16 + (0.5 if half_k else 0.0)
+    mcg_i, mul1_i = _codebook_flags(mcg, mul1)
+    m = A.numel() // max(A.size(-1), 1) if A.size(-1) else 0
+    _need(C.numel() == m * C.size(-1), "A and C row counts differ")
+    _cuda(A, B, C, suh, svh)
+    for s, n, name in ((suh, A.size(-1), "suh"), (svh, C.size(-1), "svh")):
+        if s is not None:
+            _dtype(s, torch.half, name)
+            _need(s.numel() >= n, f"{name} too short")
+    with torch.cuda.device(A.device):
+        return check(_lib.lib().exl3_amd_gemm(
+            A.data_ptr(), B.data_ptr(), C.data_ptr(), int(C.dtype == torch.float), _ptr(suh),
+            _ptr(A_had), _ptr(svh), m, A.size(-1), C.size(-1), float(K), mcg_i, mul1_i,
+            int(force_shape_idx), _stream(A)))
+
+
+def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
+                    mul1: bool = False, mcg: bool = False) -> Tensor:
+    """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to
+    fp16 once, then one dense GEMM.  rows >= 2048: original-basis W and y = x @ W; otherwise
+    y = had(had(x o suh) @ W_hat) o svh.  The dense GEMM is torch.mm (hipBLASLt)."""
+    _need(trellis.dim() == 3, "exl3_gemm_recon: trellis must be 3-D")
+    k, n = trellis.size(0) * 16, trellis.size(1) * 16
+    _need(x.dim() == 2 and x.size(1) == k and suh.numel() == k and svh.numel() == n and n <= 32768,
+          f"exl3_gemm_recon: incompatible shapes (x {tuple(x.shape)}, weight {k} x {n})")
+    rows = x.size(0)
+    y = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    w = torch.empty((k, n), dtype=x.dtype, device=x.device)
+    if rows >= RECON_FUSED_ROWS:
+        reconstruct_had_slice(w, trellis, suh, svh, K, mcg, mul1, 0)
+        torch.mm(x, w, out=y)
+    else:
+        xh = torch.empty_like(x)
+        had_r_128(x, xh, suh, None, 1.0)
+        reconstruct(w, trellis, K, mcg, mul1)
+        torch.mm(xh, w, out=y)
+        had_r_128(y, y, None, svh, 1.0)
+    return y
+
+
+def init(device: int = 0) -> None:
+    """Allocate the per-device workspace now (before graph capture)."""
+    check(_lib.lib().exl3_amd_init(int(device)))

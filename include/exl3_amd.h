@@ -1,0 +1,91 @@
+/*
+ * exl3_amd.h -- C ABI of the MI355X (gfx950) EXL3 quantized-linear library (libexl3_amd.so).
+ *
+ * Plain pointers and sizes only; no torch or C++ types cross this boundary.  Every entry
+ * point validates its arguments before launching anything, returns 0 (or a non-negative
+ * kernel tag) on success and a negative EXL3_AMD_E* code on failure, never throws, and
+ * enqueues its work on `stream` (a hipStream_t; NULL = the default stream) without host
+ * synchronisation, so the calls are graph-capturable once the device is initialised.
+ * exl3_amd_last_error() returns the message of the calling thread's last failure.
+ *
+ * Data layout (the reference's, unchanged):
+ *   trellis  uint16 (k/16, n/16, 16*K) row-major, K = bits per weight (1..8)
+ *   suh      fp16 (k) input sign/scale vector;  svh fp16 (n) output vector
+ *   A / x    fp16 (m, k) row-major;  C / y fp16 or fp32 (m, n) row-major
+ *   W        fp16 (k, n) row-major, y = x @ W (no transpose)
+ * Codebook: mcg = 1 selects MCG, mul1 = 1 selects MUL1, neither = 3INST (not both).
+ *
+ * Each entry point names the reference interface it replaces (file:line, paths relative to
+ * the jow-/ampstein tree; vendor/exl3 = exllamav3 v1.5.3 @ d3739fd).
+ */
+#ifndef EXL3_AMD_H
+#define EXL3_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_AMD_OK            0
+#define EXL3_AMD_EINVAL       -1   /* bad argument: shape, bitrate, null pointer, codebook  */
+#define EXL3_AMD_EUNSUPPORTED -2   /* valid reference input this build does not implement  */
+#define EXL3_AMD_EHIP         -3   /* HIP runtime error                                     */
+#define EXL3_AMD_ENOMEM       -4   /* workspace allocation failed                           */
+
+/* Kernel tags returned by exl3_amd_gemm (the reference returns a shape index, 90 = GEMV). */
+#define EXL3_AMD_TAG_GEMV     90
+#define EXL3_AMD_TAG_GEMM     91
+
+/* Thread-local message of the last failing call ("" if none). */
+const char* exl3_amd_last_error(void);
+
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int exl3_amd_version(void);
+
+/* Allocate the per-device workspace (split-k partials and completion counters) of `device`.
+ * Optional: the first call on a device does it lazily.  Call it before capturing a graph.
+ * Replaces DevCtx::get_locks (vendor/exl3/exllamav3_ext/quant/exl3_devctx.cu:81-93). */
+int exl3_amd_init(int device);
+
+/* W_hat (k, n) fp16 = decoded trellis columns [n_offset, n_offset + n) of a packed tensor
+ * whose full width is n_packed, in the Hadamard basis.  k % 16 == 0, n % 128 == 0,
+ * n_offset % 128 == 0.  Bit-exact with the reference.
+ * Replaces reconstruct / reconstruct_slice (vendor/exl3/exllamav3_ext/quant/reconstruct.cu:141-208,
+ * :492-501), bound at src/torch/amp_torch.cpp:11016-11057 (torch.exl3_reconstruct). */
+int exl3_amd_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n_packed, int n,
+                         int n_offset, float K, int mcg, int mul1, void* stream);
+
+/* W (k, n) fp16 = diag(suh) . H128 . W_hat . H128 . diag(svh) per 128x128 block (original
+ * basis), bit-exact with the reference's fp16 rounding.  k, n, n_offset multiples of 128;
+ * suh has k entries, svh has n entries (pre-offset by the caller for a slice).
+ * Replaces reconstruct_had_slice (vendor/exl3/exllamav3_ext/quant/reconstruct.cu:431-490),
+ * declared at src/torch/amp_torch.cpp:11068-11078. */
+int exl3_amd_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
+                             const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                             float K, int mcg, int mul1, void* stream);
+
+/* y = H128(x (o pre)) * scale / sqrt(128) (o post) over each 128-column chunk of each row.
+ * fp32 = 0: x, y fp16; fp32 = 1: x, y fp32.  pre / post fp16 (cols) or NULL; at most one
+ * of them may be given.  In place (x == y) allowed.  cols % 128 == 0.
+ * Replaces had_r_128 (vendor/exl3/exllamav3_ext/quant/hadamard.cu:125-210), declared at
+ * src/torch/amp_torch.cpp:11060-11066. */
+int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
+                       const uint16_t* pre, const uint16_t* post, float scale, void* stream);
+
+/* C (m, n) = had(had(A o suh) @ W_hat) o svh, C fp16 (c_fp32 = 0) or fp32.  suh / svh may be
+ * NULL (that rotation is skipped).  A_had: caller scratch of A's shape, accepted for interface
+ * parity and not written (the rotation is recomputed per workgroup).  k % 128 == 0 and
+ * n % 128 == 0 when a rotation is requested, else k % 16 and n % 128.  Returns a kernel tag.
+ * force_shape_idx > 0 forces a kernel (1 = GEMV, 2 = MFMA GEMM); 0 = by shape.
+ * Replaces exl3_gemm (vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:321-350, dispatcher
+ * :114-319), bound at src/torch/amp_torch.cpp:11251-11294 (torch.exl3_gemm). */
+int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+                  const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                  int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,110 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point include/exl3_amd.h
+declares, and rejects bad arguments before touching a GPU (tests/bindings_errors.uc of the
+reference requires every binding to raise on bad arguments)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from ampstein_amd import _lib
+
+
+def header_symbols():
+    text = open(_lib.HEADER).read()
+    return sorted(set(re.findall(r"\b(exl3_amd_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    assert set(header_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in header_symbols():
+        assert hasattr(L, name), name
+    assert L.exl3_amd_version() >= 100
+
+
+def call_err(fn, *args):
+    rc = fn(*args)
+    return rc, _lib.lib().exl3_amd_last_error().decode()
+
+
+def test_reconstruct_rejects_bad_arguments():
+    L = _lib.lib()
+    f = ctypes.c_float
+    rc, msg = call_err(L.exl3_amd_reconstruct, 1, 1, 16, 128, 128, 0, f(9.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "bitrate" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct, 1, 1, 16, 128, 128, 0, f(2.5), 0, 0, None)
+    assert rc == _lib.EINVAL and "mul1" in msg
+    rc, msg = call_err(L.exl3_amd_gemm, 1, 1, 1, 0, 1, None, 1, 1, 256, 256, f(4.0), 1, 1, 0, None)
+    assert rc == _lib.EINVAL and "both" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct, 1, 1, 16, 256, 64, 0, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "128" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct, 1, 1, 16, 256, 128, 64, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "n_offset" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct, 1, 1, 16, 256, 256, 128, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "bounds" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct, None, 1, 16, 128, 128, 0, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "null" in msg
+    # empty output is a successful no-op (reconstruct.cu:169-170)
+    assert L.exl3_amd_reconstruct(None, None, 0, 128, 128, 0, f(4.0), 0, 0, None) == 0
+
+
+def test_reconstruct_had_rejects_bad_arguments():
+    L = _lib.lib()
+    f = ctypes.c_float
+    rc, msg = call_err(L.exl3_amd_reconstruct_had, 1, 1, 1, 1, 144, 128, 128, 0, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "K dimension" in msg
+    rc, msg = call_err(L.exl3_amd_reconstruct_had, 1, 1, None, 1, 128, 128, 128, 0, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "null" in msg
+
+
+def test_had_rejects_bad_arguments():
+    L = _lib.lib()
+    rc, msg = call_err(L.exl3_amd_had_r_128, 1, 1, 4, 100, 0, None, None, ctypes.c_float(1.0), None)
+    assert rc == _lib.EINVAL and "128" in msg
+    rc, msg = call_err(L.exl3_amd_had_r_128, 1, 1, 4, 128, 0, 1, 1, ctypes.c_float(1.0), None)
+    assert rc == _lib.EINVAL
+
+
+def test_gemm_rejects_bad_arguments():
+    L = _lib.lib()
+    f = ctypes.c_float
+    args = lambda **kw: [kw.get(x, d) for x, d in (
+        ("A", 1), ("B", 1), ("C", 1), ("fp32", 0), ("suh", 1), ("ahad", None), ("svh", 1),
+        ("m", 1), ("k", 256), ("n", 256), ("K", f(4.0)), ("mcg", 0), ("mul1", 0), ("force", 0),
+        ("stream", None))]
+    rc, msg = call_err(L.exl3_amd_gemm, *args(n=100))
+    assert rc == _lib.EINVAL and "n must" in msg
+    rc, msg = call_err(L.exl3_amd_gemm, *args(k=24))
+    assert rc == _lib.EINVAL and "k must" in msg
+    rc, msg = call_err(L.exl3_amd_gemm, *args(K=f(0.5)))
+    assert rc == _lib.EINVAL
+    rc, msg = call_err(L.exl3_amd_gemm, *args(A=None))
+    assert rc == _lib.EINVAL and "null" in msg
+    rc, msg = call_err(L.exl3_amd_gemm, *args(force=7))
+    assert rc == _lib.EINVAL and "force_shape_idx" in msg
+    # m == 0 is an empty product: nothing to launch
+    assert L.exl3_amd_gemm(*args(m=0)) == _lib.TAG_GEMV
+
+
+def test_python_ops_raise_like_torch_check():
+    import torch
+    from ampstein_amd import ops
+    W = torch.empty((32, 128), dtype=torch.half)
+    T = torch.zeros((2, 8, 64), dtype=torch.int16)
+    with pytest.raises(_lib.Exl3Error, match="bitrate"):
+        ops.reconstruct(W, T, 9.0)
+    with pytest.raises(_lib.Exl3Error, match="both"):
+        ops.exl3_gemm(torch.empty((1, 32), dtype=torch.half), T, torch.empty((1, 128), dtype=torch.half),
+                      None, None, None, mcg=True, mul1=True)
+    with pytest.raises(_lib.Exl3Error, match="tile size"):
+        ops.reconstruct(W, T, 3.0)
+    with pytest.raises(_lib.Exl3Error, match="datatype"):
+        ops.reconstruct(W.float(), T, 4.0)
+    with pytest.raises(_lib.Exl3Error, match="incompatible"):
+        ops.exl3_gemm(torch.empty((1, 64), dtype=torch.half), T, torch.empty((1, 128), dtype=torch.half), None, None, None)
+    with pytest.raises(_lib.Exl3Error, match="128"):
+        ops.had_r_128(torch.empty((2, 100), dtype=torch.half), torch.empty((2, 100), dtype=torch.half))
