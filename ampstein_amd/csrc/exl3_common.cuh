@@ -52,7 +52,6 @@ struct DecodeRegs
     uint32_t b;           // VGPR: additive constant
     uint32_t mask;        // SGPR: 0x8fff8fff
     uint32_t xorv;        // VGPR: 0x3b603b60
-    uint32_t ones;        // SGPR: 0x01010101 (mul1 byte sum)
     uint32_t acc;         // VGPR: 0x6400     (mul1 byte-sum bias -> fp16 1024.0)
     uint32_t kinv2;       // SGPR: fp16x2 0x1eee (mul1 scale)
     uint32_t bias2;       // VGPR: fp16x2 0xc931 (mul1 bias)
@@ -68,7 +67,6 @@ __device__ __forceinline__ DecodeRegs make_decode_regs()
     r.b = vconst(cb_consts<CB>::B);
     r.mask = sconst(0x8fff8fffu);
     r.xorv = vconst(0x3b603b60u);
-    r.ones = sconst(0x01010101u);
     r.acc = vconst(0x6400u);
     r.kinv2 = sconst(0x1eee1eeeu);
     r.bias2 = vconst(0xc931c931u);
@@ -84,6 +82,8 @@ __device__ __forceinline__ DecodeRegs make_decode_regs()
 //   3INST / MCG: (x & 0x8fff8fff) ^ 0x3b603b60 (lop3 0x6a of codebook.cuh:47 = v_bitop3 0x6a),
 //   then the fp16 sum of its halves, rounded once (written as fma(lo, 1.0, hi)).
 //   MUL1: byte sum + 0x6400 read as fp16 (1024 + sum), then one fp16 fma with 0x1eee, 0xc931.
+//   The byte sum is v_sad_u8(x, 0, 0x6400) (sum of |byte - 0|, the vabsdiff4 form noted at
+//   codebook.cuh:31-34): a plain VALU op, unlike v_dot4 whose result needs 3 wait states.
 // One asm block per group: the four chains are interleaved so that no instruction reads a
 // register written by the instruction just before it (gfx950 needs one wait state after a
 // write to the high half only), and the compiler adds a single wait after the block.
@@ -128,10 +128,10 @@ template <> struct Quad<2, H0, H1, H2, H3> {                                    
     {                                                                                          \
         uint32_t t0, t1, t2, t3;                                                               \
         asm(EXL3_MUL_BLOCK(H0, H1, H2, H3, "0")                                                \
-            "v_dot4_u32_u8 %[t0], %[t0], %[ones], %[acc]\n\t"                                  \
-            "v_dot4_u32_u8 %[t1], %[t1], %[ones], %[acc]\n\t"                                  \
-            "v_dot4_u32_u8 %[t2], %[t2], %[ones], %[acc]\n\t"                                  \
-            "v_dot4_u32_u8 %[t3], %[t3], %[ones], %[acc]\n\t"                                  \
+            "v_sad_u8 %[t0], %[t0], 0, %[acc]\n\t"                                  \
+            "v_sad_u8 %[t1], %[t1], 0, %[acc]\n\t"                                  \
+            "v_sad_u8 %[t2], %[t2], 0, %[acc]\n\t"                                  \
+            "v_sad_u8 %[t3], %[t3], 0, %[acc]\n\t"                                  \
             "v_perm_b32 %[o0], %[t1], %[t0], %[sel]\n\t"                                       \
             "v_perm_b32 %[o1], %[t3], %[t2], %[sel]\n\t"                                       \
             "v_pk_fma_f16 %[o0], %[o0], %[kinv], %[bias]\n\t"                                  \
@@ -139,7 +139,7 @@ template <> struct Quad<2, H0, H1, H2, H3> {                                    
             : [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3),                  \
               [o0] "=&v"(o0), [o1] "=&v"(o1)                                                   \
             : [s0] "v"(s0), [s1] "v"(s1), [s2] "v"(s2), [s3] "v"(s3), [a0] "s"(r.a0),          \
-              [a1] "s"(r.a1), [ones] "s"(r.ones), [acc] "v"(r.acc), [sel] "s"(r.sel),          \
+              [a1] "s"(r.a1), [acc] "v"(r.acc), [sel] "s"(r.sel),          \
               [kinv] "s"(r.kinv2), [bias] "v"(r.bias2));                                       \
     }                                                                                          \
 };

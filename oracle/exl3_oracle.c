@@ -532,25 +532,27 @@ struct mm_ctx { const h16* A; const h16* W; double* P; int m, k, n; };
 
 static void mm_cols(void* vctx, int c0, int c1)
 {
-    /* P[:, c0*64 .. c1*64) = A @ W in double, W row-major (k, n) */
+    /* P[:, 64-column blocks c0 .. c1) = A @ W in double, W row-major (k, n) */
     struct mm_ctx* c = (struct mm_ctx*) vctx;
-    int j0 = c0 * 64, j1 = c1 * 64;
-    if (j1 > c->n) j1 = c->n;
-    float* wrow = (float*) malloc(sizeof(float) * 64);
-    for (int r = 0; r < c->m; ++r)
+    double wrow[64];
+    for (int blk = c0; blk < c1; ++blk)
     {
-        double* pr = c->P + (size_t) r * c->n;
-        for (int j = j0; j < j1; ++j) pr[j] = 0.0;
-        for (int i = 0; i < c->k; ++i)
+        int j0 = blk * 64, j1 = j0 + 64;
+        if (j1 > c->n) j1 = c->n;
+        for (int r = 0; r < c->m; ++r)
         {
-            double a = half_to_float_bits(c->A[(size_t) r * c->k + i]);
-            if (a == 0.0) continue;
-            const h16* wr = c->W + (size_t) i * c->n;
-            for (int j = j0; j < j1; ++j) wrow[j - j0] = half_to_float_bits(wr[j]);
-            for (int j = j0; j < j1; ++j) pr[j] += a * (double) wrow[j - j0];
+            double* pr = c->P + (size_t) r * c->n;
+            for (int j = j0; j < j1; ++j) pr[j] = 0.0;
+            for (int i = 0; i < c->k; ++i)
+            {
+                double a = half_to_float_bits(c->A[(size_t) r * c->k + i]);
+                if (a == 0.0) continue;
+                const h16* wr = c->W + (size_t) i * c->n;
+                for (int j = j0; j < j1; ++j) wrow[j - j0] = half_to_float_bits(wr[j]);
+                for (int j = j0; j < j1; ++j) pr[j] += a * wrow[j - j0];
+            }
         }
     }
-    free(wrow);
 }
 
 static void matmul_d(const h16* A, const h16* W, double* P, int m, int k, int n, int nthreads)
