@@ -8,6 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -115,21 +116,33 @@ int current_device(DeviceState** out)
     return init_device(dev, out);
 }
 
-// GEMV k-split: aim for ~2 workgroups per CU, within the LDS budget (rotated input of the
-// split's k range + the cross-wave reduction) and the partial-sum workspace.
-int gemv_splits(int m, int k, int n, int num_cus)
+// GEMV work split (exl3_gemv.hip): SB slices per workgroup, a divisor of k/16 (so no
+// workgroup straddles two column chunks), sized for ~TARGET workgroups per CU within the LDS
+// budget (rotated input + reduction buffer) and the split-partial workspace.
+int gemv_plan(int m, int k, int n, int num_cus, GemvArgs& g)
 {
     const int mt = m == 1 ? 1 : (m <= 4 ? 4 : 8);
-    const int kchunks = k / 128, cols = n / 128;
+    const int KS = k / 16, chunks = n / 128;
+    int per_cu = 2;
+    if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
+    const long target = (long) per_cu * num_cus;
     const int lds_budget = 64 * 1024 - 4 * mt * 128 * 4;
-    const int max_kcps = lds_budget / (mt * 256);
-    int splits = (2 * num_cus + cols - 1) / cols;
-    if (splits > kchunks) splits = kchunks;
-    const int min_splits = (kchunks + max_kcps - 1) / max_kcps;
-    if (splits < min_splits) splits = min_splits;
-    if (splits < 1) splits = 1;
-    while (splits > min_splits && splits > 1 && (size_t) splits * m * n * 4 > WS_PARTIAL_BYTES) --splits;
-    return splits;
+    const int max_chunks = lds_budget / (mt * 512);           // rotated 128-row chunks in LDS
+    int best = -1;
+    for (int d = 1; d <= KS; ++d)
+    {
+        if (KS % d) continue;
+        if (d / 8 + 2 > max_chunks) break;
+        if ((size_t) (KS / d) * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
+        if (best < 0 || (long) chunks * (KS / best) > target) best = d;   // fewest blocks >= target
+        if ((long) chunks * (KS / d) <= target) break;
+    }
+    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && KS % v == 0) best = v; }
+    if (best < 0) return -1;
+    g.slices_per_block = best;
+    g.slots = KS / best;
+    g.xs_chunks = best / 8 + 2;
+    return 0;
 }
 
 int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s)
@@ -241,7 +254,7 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
         GemvArgs g;
         g.A = A; g.trellis = trellis; g.C = C; g.suh = suh; g.svh = svh;
         g.m = m; g.k = k; g.n = n; g.c_fp32 = c_fp32 ? 1 : 0;
-        g.splits = gemv_splits(m, k, n, d->num_cus);
+        if (gemv_plan(m, k, n, d->num_cus, g)) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: shape exceeds the GEMV workspace");
         g.partials = d->partials;
         g.counters = d->counters;
         if ((size_t) n / 128 > WS_COUNTERS) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: n too large for the counter workspace");

@@ -1,18 +1,32 @@
 // Decode-shaped EXL3 GEMV for gfx950: C = had(had(A o suh) @ W_hat) o svh, m = 1..8.
 //
 // Semantics of exl3_gemv_kernel / exl3_gemm (quant/exl3_gemv_kernel.cuh:186-482), built
-// differently for CDNA4:
-//   * no cooperative launch: each workgroup owns one 128-column output chunk and a range of
-//     128-row input chunks; it recomputes the input rotation had(x o suh) for its own k range
-//     from x (2 bytes per input element, negligible next to the weights) into LDS;
-//   * split-k across workgroups writes fp32 partials; the last workgroup to arrive on a column
-//     chunk (device-scope counter) sums them in split order -- deterministic -- and applies
-//     the output rotation and svh, then re-arms the counter, so no memset is needed per call;
-//   * trellis words are streamed with 64-lane coalesced non-temporal loads: one k-slice of a
-//     128-column chunk (8 tiles, 256*K bytes) per wave instruction group, K words per lane;
-//   * decode in registers (exl3_common.cuh), dot products with v_dot2_f32_f16 into fp32
-//     accumulators: lane j of tile t owns output columns 16t+j and 16t+j+8, so no cross-lane
-//     reduction is needed inside a wave.
+// for CDNA4 from rocprof measurements:
+//
+// Work split.  The weight is a sequence of "slices" (one 16-row k-slice of one 128-column
+// output chunk: 8 tiles, 256*K contiguous bytes), ordered column-chunk-major.  Workgroup b
+// streams the SB slices [b*SB, (b+1)*SB) of one chunk; its 4 waves take every 4th slice, so
+// they read adjacent rows, and every wave runs one software-pipelined stream.  SB divides
+// k/16, so a workgroup never straddles two chunks; it is chosen on the host for several
+// resident waves per SIMD (one wave per SIMD issues VALU at half rate on gfx950).
+//
+// Reduction.  The 4 waves reduce through LDS.  A chunk owned by one workgroup (SB = k/16)
+// finishes in place; otherwise each workgroup stores an fp32 partial to its slot and a second
+// small kernel (gemv_finish) sums the slots in slot order -- deterministic -- and applies the
+// output rotation and svh.  No atomics: on MI355X a device-scope atomic per workgroup costs
+// 2.5-11 us per launch (measured), more than the kernel boundary.
+//
+// Input rotation.  Each workgroup computes had(x o suh) (fp32 butterfly, rounded to fp16 as
+// the reference's A_had) only for the 128-row chunks its slices touch, into LDS, stored as
+// duplicated pairs (x, x) so one v_dot2 consumes a decoded weight's two fp16 halves.
+//
+// Decode (per weight: extract the 16-bit window, x = s*A (+B), mask/xor, one v_dot2):
+//   3INST / MCG: the weight is lo + hi of the masked word; v_dot2((x, x), (lo, hi)) adds
+//   x*lo + x*hi in fp32 instead of first rounding lo + hi to fp16 (the reference's weight
+//   differs from this by at most half an fp16 ulp; outputs stay far inside 2e-3).
+//   MUL1: w = h * k_inv + bias with h = 1024 + bytesum (an exact small integer): the kernel
+//   accumulates x*h and applies k_inv and bias * sum(x) per segment, in fp32.
+// All ops are full-rate gfx950 VALU (no high-half-only writes, which issue at half rate).
 //
 // Compiled once per K (EXL3_INST_K) to keep build units small.
 #include "exl3_common.cuh"
@@ -21,6 +35,10 @@
 #ifndef EXL3_INST_K
 #define EXL3_INST_K 4
 #endif
+// Prefetch ring depth (k-slices in flight per wave); HBM needs many bytes in flight
+#ifndef EXL3_GEMV_PF
+#define EXL3_GEMV_PF (EXL3_INST_K <= 2 ? 16 : (EXL3_INST_K <= 4 ? 8 : 4))
+#endif
 
 using namespace exl3;
 
@@ -28,6 +46,12 @@ namespace {
 
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
+
+// Load this lane's K words of a slice into w[1..K] and the word before them (the last word of
+// the previous lane of the same tile, cyclically: the window start of the lane's first
+// position) into w[0], all from global memory: no cross-lane traffic in the loop.
+template <int K>
+__device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int prev_off, uint32_t* w);
 
 template <int K>
 __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint32_t* w)
@@ -57,11 +81,43 @@ __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint3
     }
 }
 
-// Input rotation of rows [0, m) over chunks [kc0, kc0 + nkc) into LDS (fp16 pairs):
-// had_hf_r_128_inner<true,false> (hadamard_inner.cuh:93-150): fp16 pre-scale, fp32
-// butterfly, * 1/sqrt(128), round to fp16.
-__device__ __forceinline__ void rotate_input(const uint16_t* __restrict__ A, const uint16_t* __restrict__ suh,
-                                             uint32_t* xs, int m, int k, int kc0, int nkc, int xs_stride)
+template <int K>
+__device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int prev_off, uint32_t* w)
+{
+    load_words<K>(p, w + 1);
+    w[0] = __builtin_nontemporal_load(p + prev_off);
+}
+
+// Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe when the window sits in a
+// single word, else alignbit + mask.
+template <int K, int I>
+__device__ __forceinline__ uint32_t state16(const uint32_t* wv)
+{
+    constexpr int hi = Win<K>::hi(I), s = Win<K>::s(I);
+    if constexpr (s + 16 <= 32) return __builtin_amdgcn_ubfe(wv[hi], s, 16);
+    else return __builtin_amdgcn_alignbit(wv[hi - 1], wv[hi], s) & 0xffffu;
+}
+
+// Codebook word consumed by v_dot2 against (x, x): 3INST/MCG masked halves, MUL1 (h, 0).
+template <int CB>
+__device__ __forceinline__ uint32_t raw_weight(uint32_t s)
+{
+    if constexpr (CB == 0)
+        return ((s * 89226354u + 64248484u) & 0x8fff8fffu) ^ 0x3b603b60u;   // codebook.cuh:61-63
+    else if constexpr (CB == 1)
+        return ((s * 0xCBAC1FEDu) & 0x8fff8fffu) ^ 0x3b603b60u;             // codebook.cuh:69-72
+    else
+        return __builtin_amdgcn_sad_u8(s * 0x83DCD12Du, 0u, 0x6400u);       // codebook.cuh:78-84
+}
+
+template <int K, int CB, int I>
+__device__ __forceinline__ uint32_t raw_at(const uint32_t* wv) { return raw_weight<CB>(state16<K, I>(wv)); }
+
+// Input rotation of chunks [kc0, kc0 + nkc) of rows [0, m) into xs (u32 units: 128
+// duplicated pairs per chunk).  had_hf_r_128_inner<true,false> (hadamard_inner.cuh:93-150):
+// fp16 pre-scale, fp32 butterfly, * 1/sqrt(128), round to fp16.
+__device__ __forceinline__ void rotate_chunks(const uint16_t* __restrict__ A, const uint16_t* __restrict__ suh,
+                                              uint32_t* xs, int xs_stride, int m, int k, int kc0, int nkc)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int job = wave; job < m * nkc; job += GEMV_WAVES)
@@ -69,17 +125,19 @@ __device__ __forceinline__ void rotate_input(const uint16_t* __restrict__ A, con
         const int row = job / nkc, c = job % nkc;
         const int col = (kc0 + c) * 128 + 2 * lane;
         f16x2 v = as_h2(*(const uint32_t*) (A + (size_t) row * k + col));
-        uint32_t out;
+        f16x2 o;
         if (suh)
         {
             v = v * as_h2(*(const uint32_t*) (suh + col));
             float v0 = (float) v.x, v1 = (float) v.y;
             fwht128_wave(v0, v1, lane);
-            f16x2 o = { (f16) (v0 * EXL3_HAD_RSCALE), (f16) (v1 * EXL3_HAD_RSCALE) };
-            out = as_u32(o);
+            o.x = (f16) (v0 * EXL3_HAD_RSCALE);
+            o.y = (f16) (v1 * EXL3_HAD_RSCALE);
         }
-        else out = as_u32(v);
-        xs[row * xs_stride + c * 64 + lane] = out;
+        else o = v;
+        f16x2 d0 = { o.x, o.x }, d1 = { o.y, o.y };
+        u32x2 pr = { as_u32(d0), as_u32(d1) };
+        *(u32x2*) (xs + row * xs_stride + c * 128 + 2 * lane) = pr;
     }
 }
 
@@ -94,18 +152,15 @@ __device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_
         v0 *= EXL3_HAD_RSCALE;
         v1 *= EXL3_HAD_RSCALE;
         f16x2 s = as_h2(*(const uint32_t*) (svh + col));
-        if (c_fp32)
-        {
-            v0 *= (float) s.x;
-            v1 *= (float) s.y;
-        }
-        else
+        if (!c_fp32)
         {
             f16x2 h = { (f16) v0, (f16) v1 };
             h = h * s;
             *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
             return;
         }
+        v0 *= (float) s.x;
+        v1 *= (float) s.y;
     }
     if (c_fp32)
     {
@@ -119,45 +174,56 @@ __device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_
     }
 }
 
+__device__ __forceinline__ float wave_sum(float v, int lane)
+{
+    #pragma unroll
+    for (int msk = 1; msk < 64; msk <<= 1) v += xor_shfl(v, msk, lane);
+    return v;
+}
+
 template <int K, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ trellis,
                  void* __restrict__ C, const uint16_t* __restrict__ suh,
                  const uint16_t* __restrict__ svh, int m, int k, int n, int c_fp32,
-                 int kc_per_split, float* __restrict__ partials, int* __restrict__ counters)
+                 int SB, int xs_chunks, float* __restrict__ partials)
 {
     extern __shared__ uint32_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
-    const int kchunks = k / 128;
-    const int kc0 = split * kc_per_split;
-    const int nkc = min(kc_per_split, kchunks - kc0);
-    const int xs_stride = kc_per_split * 64;            // u32 (fp16 pairs) per row
-    uint32_t* xs = smem;                                 // [MT][kc_per_split * 64]
-    float* red = (float*) (smem + MT * xs_stride);       // [GEMV_WAVES][MT][128]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KS = k / 16;                                // slices per column chunk
+    const int splits = KS / SB;
+    const int chunk = blockIdx.x / splits;
+    const int slot = blockIdx.x - chunk * splits;
+    const int ks0 = slot * SB;
+    const int kc0 = ks0 / 8;
+    const int nkc = (ks0 + SB - 1) / 8 - kc0 + 1;
+    const int xs_stride = xs_chunks * 128;                // u32 per row
+    uint32_t* xs = smem;                                  // [MT][xs_chunks][128] dup pairs
+    float* red = (float*) (smem + MT * xs_stride);        // [GEMV_WAVES][MT][128]
 
-    rotate_input(A, suh, xs, m, k, kc0, nkc, xs_stride);
-    __syncthreads();
-
-    const DecodeRegs r = make_decode_regs<CB>();
+    // this wave's slices: ks0 + wave + 4 i, i < myn
+    const int myn = SB > wave ? (SB - wave + GEMV_WAVES - 1) / GEMV_WAVES : 0;
     const int tiles_n = n / 16;
-    const int nslices = nkc * 8;
-    const int kt0 = kc0 * 8;
-    // wave w handles local slices w, w + 4, ... : the 4 waves stream 4 adjacent 256K-byte rows
-    const int myn = nslices > wave ? (nslices - wave + GEMV_WAVES - 1) / GEMV_WAVES : 0;
-    const uint32_t* bp = (const uint32_t*) trellis
-                       + ((size_t) (kt0 + wave) * tiles_n + chunk * 8) * (8 * K) + (size_t) lane * K;
-    const size_t wstride = (size_t) GEMV_WAVES * tiles_n * 8 * K;   // u32 between my slices
+    const size_t kstride = (size_t) GEMV_WAVES * tiles_n * 8 * K;         // u32 between my slices
+    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
+                         + ((size_t) (ks0 + min(wave, SB - 1)) * tiles_n + chunk * 8) * (8 * K);
+
+    // prefetch ring (unconditional, clamped loads keep the wait counts static)
+    constexpr int PF = EXL3_GEMV_PF;
+    const int last_i = myn > 0 ? myn - 1 : 0;
+    const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;   // ring predecessor of my first word
+    uint32_t ring[PF][K + 1];
+    #pragma unroll
+    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+
+    // input rotation of the chunks this workgroup touches (overlaps the first loads)
+    rotate_chunks(A, suh, xs, xs_stride, m, k, kc0, nkc);
+    __syncthreads();
 
     float acc[MT][2];
     #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = 0.0f;
-
-    constexpr int PF = K <= 4 ? 4 : 2;
-    uint32_t ring[PF][K];
-    #pragma unroll
-    for (int d = 0; d < PF; ++d)
-        if (d < myn) load_words<K>(bp + d * wstride, ring[d]);
+    for (int r = 0; r < MT; ++r) acc[r][0] = acc[r][1] = 0.0f;
 
     for (int i0 = 0; i0 < myn; i0 += PF)
     {
@@ -165,108 +231,157 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
         for (int d = 0; d < PF; ++d)
         {
             const int i = i0 + d;
-            if (i >= myn) break;
+            const bool live = i < myn;
+            const int ks = ks0 + wave + min(i, last_i) * GEMV_WAVES;
+            const int xo = (ks / 8 - kc0) * 128 + (ks & 7) * 16;
             uint32_t wv[K + 1];
             #pragma unroll
-            for (int w = 0; w < K; ++w) wv[w + 1] = ring[d][w];
-            if (i + PF < myn) load_words<K>(bp + (size_t) (i + PF) * wstride, ring[d]);
-            wv[0] = ring_prev(wv[K], lane);
-            uint32_t pairs[16];
-            decode_lane32<K, CB>(wv, pairs, r);
+            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            uint32_t raw[32];
+            raw[0] = raw_at<K, CB, 0>(wv);   raw[1] = raw_at<K, CB, 1>(wv);
+            raw[2] = raw_at<K, CB, 2>(wv);   raw[3] = raw_at<K, CB, 3>(wv);
+            raw[4] = raw_at<K, CB, 4>(wv);   raw[5] = raw_at<K, CB, 5>(wv);
+            raw[6] = raw_at<K, CB, 6>(wv);   raw[7] = raw_at<K, CB, 7>(wv);
+            raw[8] = raw_at<K, CB, 8>(wv);   raw[9] = raw_at<K, CB, 9>(wv);
+            raw[10] = raw_at<K, CB, 10>(wv); raw[11] = raw_at<K, CB, 11>(wv);
+            raw[12] = raw_at<K, CB, 12>(wv); raw[13] = raw_at<K, CB, 13>(wv);
+            raw[14] = raw_at<K, CB, 14>(wv); raw[15] = raw_at<K, CB, 15>(wv);
+            raw[16] = raw_at<K, CB, 16>(wv); raw[17] = raw_at<K, CB, 17>(wv);
+            raw[18] = raw_at<K, CB, 18>(wv); raw[19] = raw_at<K, CB, 19>(wv);
+            raw[20] = raw_at<K, CB, 20>(wv); raw[21] = raw_at<K, CB, 21>(wv);
+            raw[22] = raw_at<K, CB, 22>(wv); raw[23] = raw_at<K, CB, 23>(wv);
+            raw[24] = raw_at<K, CB, 24>(wv); raw[25] = raw_at<K, CB, 25>(wv);
+            raw[26] = raw_at<K, CB, 26>(wv); raw[27] = raw_at<K, CB, 27>(wv);
+            raw[28] = raw_at<K, CB, 28>(wv); raw[29] = raw_at<K, CB, 29>(wv);
+            raw[30] = raw_at<K, CB, 30>(wv); raw[31] = raw_at<K, CB, 31>(wv);
+            // refill this ring slot once its words are dead
+            load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
 
-            const int sl = wave + i * GEMV_WAVES;         // local slice index
             #pragma unroll
-            for (int row = 0; row < MT; ++row)
+            for (int r = 0; r < MT; ++r)
             {
-                if (MT > 1 && row >= m) break;
-                const u32x4* xp = (const u32x4*) (xs + row * xs_stride + sl * 8);
-                u32x4 xa = xp[0], xb = xp[1];
-                uint32_t x8[8] = { xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w };
+                if (MT > 1 && r >= m) break;
+                const u32x4* xp = (const u32x4*) (xs + r * xs_stride + xo);
+                uint32_t x16[16];
                 #pragma unroll
-                for (int q = 0; q < 16; ++q)
+                for (int v = 0; v < 4; ++v)
                 {
-                    const int xi = (q >> 2) + 4 * (q & 1);      // rows pair_row(q), +1
-                    float& a = acc[row][(q >> 1) & 1];
-                    a = __builtin_amdgcn_fdot2(as_h2(x8[xi]), as_h2(pairs[q]), a, false);
+                    u32x4 t = xp[v];
+                    x16[4 * v] = live ? t.x : 0u;     x16[4 * v + 1] = live ? t.y : 0u;
+                    x16[4 * v + 2] = live ? t.z : 0u; x16[4 * v + 3] = live ? t.w : 0u;
+                }
+                // window w = 8g + jj: column j + 8 (jj >= 4), row 2g + {0, 1, 8, 9}[jj & 3]
+                #pragma unroll
+                for (int w = 0; w < 32; ++w)
+                {
+                    const int g = w >> 3, jj = w & 7;
+                    const int row = 2 * g + (jj & 1) + 8 * ((jj >> 1) & 1);
+                    float& a = acc[r][jj >> 2];
+                    a = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), a, false);
                 }
             }
         }
     }
 
-    // cross-wave reduction (fixed order), columns: tile (lane / 8), col j and j + 8
+    // cross-wave reduction; lane l of tile t owns columns 16t + (l & 7) and + 8
     const int c0 = (lane >> 3) * 16 + (lane & 7);
     #pragma unroll
-    for (int row = 0; row < MT; ++row)
+    for (int r = 0; r < MT; ++r)
     {
-        if (MT > 1 && row >= m) break;
-        red[(wave * MT + row) * 128 + c0] = acc[row][0];
-        red[(wave * MT + row) * 128 + c0 + 8] = acc[row][1];
+        if (MT > 1 && r >= m) break;
+        red[(wave * MT + r) * 128 + c0] = acc[r][0];
+        red[(wave * MT + r) * 128 + c0 + 8] = acc[r][1];
+    }
+    __shared__ float sumx[8];
+    if (CB == 2)
+    {
+        // MUL1 bias term: sum of the rotated input over this workgroup's k range
+        for (int r = wave; r < m; r += GEMV_WAVES)
+        {
+            float v = 0.0f;
+            for (int e = lane; e < SB * 16; e += 64)
+            {
+                const int ks = ks0 + e / 16;
+                v += (float) as_h2(xs[r * xs_stride + (ks / 8 - kc0) * 128 + (ks & 7) * 16 + (e & 15)]).x;
+            }
+            v = wave_sum(v, lane);
+            if (lane == 0) sumx[r] = v;
+        }
     }
     __syncthreads();
 
-    __shared__ int last;
-    if (nsplit > 1)
+    // rows of the chunk: 4 waves x 64 lanes, two columns per lane
+    for (int r = wave; r < m; r += GEMV_WAVES)
     {
-        for (int idx = threadIdx.x; idx < m * 128; idx += GEMV_THREADS)
-        {
-            const int row = idx >> 7, c = idx & 127;
-            float s = red[row * 128 + c];
-            #pragma unroll
-            for (int w = 1; w < GEMV_WAVES; ++w) s += red[(w * MT + row) * 128 + c];
-            partials[((size_t) split * m + row) * n + chunk * 128 + c] = s;
-        }
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0)
-        {
-            int prev = __hip_atomic_fetch_add(counters + chunk, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            last = prev == nsplit - 1;
-            if (last) __hip_atomic_store(counters + chunk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-    }
-
-    // epilogue: one wave per row: sum splits in order, output rotation, store
-    for (int row = wave; row < m; row += GEMV_WAVES)
-    {
-        float v[2];
+        const int c = 2 * lane;
+        float v0 = red[r * 128 + c], v1 = red[r * 128 + c + 1];
         #pragma unroll
-        for (int e = 0; e < 2; ++e)
+        for (int w = 1; w < GEMV_WAVES; ++w)
         {
-            const int c = 2 * lane + e;
-            float s;
-            if (nsplit > 1)
-            {
-                s = 0.0f;
-                for (int sp = 0; sp < nsplit; ++sp)
-                    s += __builtin_nontemporal_load(partials + ((size_t) sp * m + row) * n + chunk * 128 + c);
-            }
-            else
-            {
-                s = red[row * 128 + c];
-                #pragma unroll
-                for (int w = 1; w < GEMV_WAVES; ++w) s += red[(w * MT + row) * 128 + c];
-            }
-            v[e] = s;
+            v0 += red[(w * MT + r) * 128 + c];
+            v1 += red[(w * MT + r) * 128 + c + 1];
         }
-        const int col = chunk * 128 + 2 * lane;
-        store_output(v[0], v[1], C, c_fp32, svh, (size_t) row * n + col, col, lane);
+        if (CB == 2)
+        {
+            const float kinv = (float) as_h(0x1eee), bias = sumx[r] * (float) as_h(0xc931);
+            v0 = v0 * kinv + bias;
+            v1 = v1 * kinv + bias;
+        }
+        if (splits == 1)
+        {
+            const int col = chunk * 128 + c;
+            store_output(v0, v1, C, c_fp32, svh, (size_t) r * n + col, col, lane);
+        }
+        else
+        {
+            float2 pv = { v0, v1 };
+            *(float2*) (partials + (((size_t) chunk * splits + slot) * m + r) * 128 + c) = pv;
+        }
+    }
+}
+
+// Sum the split partials of each column chunk in slot order, output rotation, store.
+// Grid: n / 128 chunks; one wave per row.
+__global__ __launch_bounds__(GEMV_THREADS)
+void gemv_finish(const float* __restrict__ partials, void* __restrict__ C, const uint16_t* __restrict__ svh,
+                 int m, int n, int splits, int c_fp32)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = blockIdx.x;
+    for (int r = wave; r < m; r += GEMV_WAVES)
+    {
+        const int c = 2 * lane;
+        const float* pp = partials + ((size_t) chunk * splits * m + r) * 128 + c;
+        float v0 = 0.0f, v1 = 0.0f;
+        for (int sp0 = 0; sp0 < splits; sp0 += 8)
+        {
+            f32x2 v[8];
+            #pragma unroll
+            for (int j = 0; j < 8; ++j)
+                v[j] = __builtin_nontemporal_load((const f32x2*) (pp + (size_t) min(sp0 + j, splits - 1) * m * 128));
+            #pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (sp0 + j < splits) { v0 += v[j].x; v1 += v[j].y; }
+        }
+        const int col = chunk * 128 + c;
+        store_output(v0, v1, C, c_fp32, svh, (size_t) r * n + col, col, lane);
     }
 }
 
 template <int K, int CB, int MT>
 int launch_gemv_t(const GemvArgs& g, hipStream_t s)
 {
-    const int kchunks = g.k / 128;
-    const int kcps = (kchunks + g.splits - 1) / g.splits;
-    const int nsplit = (kchunks + kcps - 1) / kcps;
-    const size_t lds = (size_t) MT * kcps * 64 * 4 + (size_t) GEMV_WAVES * MT * 128 * 4;
-    dim3 grid(g.n / 128, nsplit);
-    hipLaunchKernelGGL((gemv_kernel<K, CB, MT>), grid, dim3(GEMV_THREADS), lds, s,
-                       g.A, g.trellis, g.C, g.suh, g.svh, g.m, g.k, g.n, g.c_fp32, kcps,
-                       g.partials, g.counters);
+    const int KS = g.k / 16;
+    const int SB = g.slices_per_block;
+    const int splits = KS / SB;
+    const int blocks = splits * (g.n / 128);
+    const size_t lds = (size_t) MT * g.xs_chunks * 128 * 4 + (size_t) GEMV_WAVES * MT * 128 * 4;
+    hipLaunchKernelGGL((gemv_kernel<K, CB, MT>), dim3(blocks), dim3(GEMV_THREADS), lds, s,
+                       g.A, g.trellis, g.C, g.suh, g.svh, g.m, g.k, g.n, g.c_fp32, SB, g.xs_chunks,
+                       g.partials);
+    if (splits > 1)
+        hipLaunchKernelGGL(gemv_finish, dim3(g.n / 128), dim3(GEMV_THREADS), 0, s,
+                           g.partials, g.C, g.svh, g.m, g.n, splits, g.c_fp32);
     return (int) hipGetLastError();
 }
 

@@ -15,9 +15,11 @@ struct GemvArgs
     const uint16_t* svh;        // (n) fp16 or null
     int m, k, n;
     int c_fp32;
-    int splits;                 // requested k-splits (>= 1)
-    float* partials;            // workspace: splits * m * n fp32
-    int* counters;              // workspace: n / 128 ints, zero between calls
+    int slices_per_block;       // SB: k-slices (16 rows x 128 columns) per workgroup, divides k/16
+    int slots;                  // split partials per column chunk: k/16 / SB
+    int xs_chunks;              // rotated 128-row input chunks held in LDS: SB/8 + 2
+    float* partials;            // workspace: slots * m * n fp32
+    int* counters;              // workspace: n / 128 ints (kernels that hand off through counters)
 };
 
 int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
