@@ -39,6 +39,7 @@ def units():
         ("exl3_capi.cpp", "exl3_capi.o", []),
         ("exl3_reconstruct.hip", "exl3_reconstruct.o", []),
         ("exl3_hadamard.hip", "exl3_hadamard.o", []),
+        ("exl3_device.hip", "exl3_device.o", []),
     ]
     for k in range(1, 9):
         u.append(("exl3_gemv.hip", f"exl3_gemv_k{k}.o", [f"-DEXL3_INST_K={k}"]))

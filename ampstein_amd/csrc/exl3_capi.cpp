@@ -65,6 +65,7 @@ struct DeviceState
 {
     bool ready = false;
     int num_cus = 0;
+    int num_xcd = 0;            // > 0 when workgroup b is verified to run on XCD b % num_xcd
     float* partials = nullptr;
     int* counters = nullptr;
 };
@@ -98,6 +99,30 @@ int init_device(int device, DeviceState** out)
             }
             if (hipMemset(c, 0, WS_COUNTERS * sizeof(int)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
                 return fail(EXL3_AMD_EHIP, "counter initialisation failed");
+            // workgroup -> XCD dispatch order (round-robin on MI355X), verified on this device
+            {
+                const int sizes[3] = { 64, 1000, 8192 };
+                int* probe = (int*) p;
+                int nx = 0;
+                bool ok = true;
+                for (int si = 0; si < 3 && ok; ++si)
+                {
+                    int* host = (int*) malloc(sizes[si] * sizeof(int));
+                    if (!host || exl3k_xcd_probe(probe, sizes[si], nullptr) || hipDeviceSynchronize() != hipSuccess ||
+                        hipMemcpy(host, probe, sizes[si] * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+                        ok = false;
+                    if (ok)
+                    {
+                        int mx = 0;
+                        for (int i = 0; i < sizes[si]; ++i) mx = host[i] > mx ? host[i] : mx;
+                        if (si == 0) nx = mx + 1;
+                        for (int i = 0; i < sizes[si] && ok; ++i) ok = host[i] == i % nx;
+                    }
+                    free(host);
+                }
+                d.num_xcd = ok && nx >= 1 ? nx : 0;
+                if (const char* e = getenv("EXL3_AMD_XCD")) if (atoi(e) == 0) d.num_xcd = 0;
+            }
             d.num_cus = cus;
             d.partials = (float*) p;
             d.counters = (int*) c;
@@ -126,19 +151,24 @@ int gemv_plan(int m, int k, int n, int num_cus, GemvArgs& g)
     int per_cu = 2;
     if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
     const long target = (long) per_cu * num_cus;
+    // M = 1 streaming kernel: whole 128-row input chunks per wave (SB multiple of 32)
+    int stream = m == 1 && KS % 32 == 0;
+    if (const char* e = getenv("EXL3_AMD_GEMV_STREAM")) stream = stream && atoi(e) != 0;
+    const int step = stream ? 32 : 1;
     const int lds_budget = 64 * 1024 - 4 * mt * 128 * 4;
     const int max_chunks = lds_budget / (mt * 512);           // rotated 128-row chunks in LDS
     int best = -1;
-    for (int d = 1; d <= KS; ++d)
+    for (int d = step; d <= KS; d += step)
     {
         if (KS % d) continue;
-        if (d / 8 + 2 > max_chunks) break;
+        if (!stream && d / 8 + 2 > max_chunks) break;
         if ((size_t) (KS / d) * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
         if (best < 0 || (long) chunks * (KS / best) > target) best = d;   // fewest blocks >= target
         if ((long) chunks * (KS / d) <= target) break;
     }
-    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && KS % v == 0) best = v; }
+    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && KS % v == 0 && v % step == 0) best = v; }
     if (best < 0) return -1;
+    g.stream_m1 = stream;
     g.slices_per_block = best;
     g.slots = KS / best;
     g.xs_chunks = best / 8 + 2;
@@ -257,6 +287,9 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
         if (gemv_plan(m, k, n, d->num_cus, g)) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: shape exceeds the GEMV workspace");
         g.partials = d->partials;
         g.counters = d->counters;
+        g.xcd = 0;
+        if (g.stream_m1 && d->num_xcd > 0 && (n / 128) % d->num_xcd == 0 && (size_t) (n / 128) * 32 <= WS_COUNTERS)
+            g.xcd = d->num_xcd;
         if ((size_t) n / 128 > WS_COUNTERS) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: n too large for the counter workspace");
         int rc = dispatch_gemv(bits, cb, g, s);
         return rc ? hip_fail(rc, "exl3_gemm") : EXL3_AMD_TAG_GEMV;

@@ -37,7 +37,7 @@
 #endif
 // Prefetch ring depth (k-slices in flight per wave); HBM needs many bytes in flight
 #ifndef EXL3_GEMV_PF
-#define EXL3_GEMV_PF (EXL3_INST_K <= 2 ? 16 : (EXL3_INST_K <= 4 ? 8 : 4))
+#define EXL3_GEMV_PF (EXL3_INST_K <= 4 ? 4 : 2)
 #endif
 
 using namespace exl3;
@@ -88,17 +88,19 @@ __device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int pr
     w[0] = __builtin_nontemporal_load(p + prev_off);
 }
 
-// Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe when the window sits in a
-// single word, else alignbit + mask.
+// Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe, from word hi when the window
+// sits inside it, else from the half-word-shifted word alignbit(wv[hi-1], wv[hi], 16) (one per
+// word, shared by the windows that straddle that word boundary).
 template <int K, int I>
 __device__ __forceinline__ uint32_t state16(const uint32_t* wv)
 {
     constexpr int hi = Win<K>::hi(I), s = Win<K>::s(I);
     if constexpr (s + 16 <= 32) return __builtin_amdgcn_ubfe(wv[hi], s, 16);
-    else return __builtin_amdgcn_alignbit(wv[hi - 1], wv[hi], s) & 0xffffu;
+    else return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(wv[hi - 1], wv[hi], 16), s - 16, 16);
 }
 
 // Codebook word consumed by v_dot2 against (x, x): 3INST/MCG masked halves, MUL1 (h, 0).
+// (3INST goes through mad8_3inst below.)
 template <int CB>
 __device__ __forceinline__ uint32_t raw_weight(uint32_t s)
 {
@@ -108,6 +110,56 @@ __device__ __forceinline__ uint32_t raw_weight(uint32_t s)
         return ((s * 0xCBAC1FEDu) & 0x8fff8fffu) ^ 0x3b603b60u;             // codebook.cuh:69-72
     else
         return __builtin_amdgcn_sad_u8(s * 0x83DCD12Du, 0u, 0x6400u);       // codebook.cuh:78-84
+}
+
+// 3INST for eight clean states: s * 89226354 + 64248484 as one v_mad_u64_u32 each (its low
+// word; ~full rate on gfx950, where mul + add would be two ops), then the mask / xor.
+__device__ __forceinline__ void mad8_3inst(uint32_t* st, uint32_t a, uint32_t b)
+{
+    uint64_t r0, r1, r2, r3, r4, r5, r6, r7;
+    asm("v_mad_u64_u32 %0, vcc, %8, %16, %17\n\t"
+        "v_mad_u64_u32 %1, vcc, %9, %16, %17\n\t"
+        "v_mad_u64_u32 %2, vcc, %10, %16, %17\n\t"
+        "v_mad_u64_u32 %3, vcc, %11, %16, %17\n\t"
+        "v_mad_u64_u32 %4, vcc, %12, %16, %17\n\t"
+        "v_mad_u64_u32 %5, vcc, %13, %16, %17\n\t"
+        "v_mad_u64_u32 %6, vcc, %14, %16, %17\n\t"
+        "v_mad_u64_u32 %7, vcc, %15, %16, %17"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+        : "v"(st[0]), "v"(st[1]), "v"(st[2]), "v"(st[3]), "v"(st[4]), "v"(st[5]), "v"(st[6]), "v"(st[7]),
+          "s"(a), "v"((uint64_t) b)
+        : "vcc");
+    st[0] = (uint32_t) r0; st[1] = (uint32_t) r1; st[2] = (uint32_t) r2; st[3] = (uint32_t) r3;
+    st[4] = (uint32_t) r4; st[5] = (uint32_t) r5; st[6] = (uint32_t) r6; st[7] = (uint32_t) r7;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) st[i] = (st[i] & 0x8fff8fffu) ^ 0x3b603b60u;
+}
+
+template <int K, int CB, int I0>
+__device__ __forceinline__ void raw8(const uint32_t* wv, uint32_t* raw, const uint32_t a3, const uint32_t b3)
+{
+    uint32_t st[8] = { state16<K, I0>(wv), state16<K, I0 + 1>(wv), state16<K, I0 + 2>(wv), state16<K, I0 + 3>(wv),
+                       state16<K, I0 + 4>(wv), state16<K, I0 + 5>(wv), state16<K, I0 + 6>(wv), state16<K, I0 + 7>(wv) };
+    if constexpr (CB == 0)
+    {
+        mad8_3inst(st, a3, b3);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) raw[I0 + i] = st[i];
+    }
+    else
+    {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) raw[I0 + i] = raw_weight<CB>(st[i]);
+    }
+}
+
+template <int K, int CB>
+__device__ __forceinline__ void raw32(const uint32_t* wv, uint32_t* raw, const uint32_t a3, const uint32_t b3)
+{
+    raw8<K, CB, 0>(wv, raw, a3, b3);
+    raw8<K, CB, 8>(wv, raw, a3, b3);
+    raw8<K, CB, 16>(wv, raw, a3, b3);
+    raw8<K, CB, 24>(wv, raw, a3, b3);
 }
 
 template <int K, int CB, int I>
@@ -191,6 +243,7 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
     extern __shared__ uint32_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
     const int KS = k / 16;                                // slices per column chunk
     const int splits = KS / SB;
     const int chunk = blockIdx.x / splits;
@@ -238,22 +291,7 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
             #pragma unroll
             for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
-            raw[0] = raw_at<K, CB, 0>(wv);   raw[1] = raw_at<K, CB, 1>(wv);
-            raw[2] = raw_at<K, CB, 2>(wv);   raw[3] = raw_at<K, CB, 3>(wv);
-            raw[4] = raw_at<K, CB, 4>(wv);   raw[5] = raw_at<K, CB, 5>(wv);
-            raw[6] = raw_at<K, CB, 6>(wv);   raw[7] = raw_at<K, CB, 7>(wv);
-            raw[8] = raw_at<K, CB, 8>(wv);   raw[9] = raw_at<K, CB, 9>(wv);
-            raw[10] = raw_at<K, CB, 10>(wv); raw[11] = raw_at<K, CB, 11>(wv);
-            raw[12] = raw_at<K, CB, 12>(wv); raw[13] = raw_at<K, CB, 13>(wv);
-            raw[14] = raw_at<K, CB, 14>(wv); raw[15] = raw_at<K, CB, 15>(wv);
-            raw[16] = raw_at<K, CB, 16>(wv); raw[17] = raw_at<K, CB, 17>(wv);
-            raw[18] = raw_at<K, CB, 18>(wv); raw[19] = raw_at<K, CB, 19>(wv);
-            raw[20] = raw_at<K, CB, 20>(wv); raw[21] = raw_at<K, CB, 21>(wv);
-            raw[22] = raw_at<K, CB, 22>(wv); raw[23] = raw_at<K, CB, 23>(wv);
-            raw[24] = raw_at<K, CB, 24>(wv); raw[25] = raw_at<K, CB, 25>(wv);
-            raw[26] = raw_at<K, CB, 26>(wv); raw[27] = raw_at<K, CB, 27>(wv);
-            raw[28] = raw_at<K, CB, 28>(wv); raw[29] = raw_at<K, CB, 29>(wv);
-            raw[30] = raw_at<K, CB, 30>(wv); raw[31] = raw_at<K, CB, 31>(wv);
+            raw32<K, CB>(wv, raw, a3, b3);
             // refill this ring slot once its words are dead
             load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
 
@@ -368,6 +406,186 @@ void gemv_finish(const float* __restrict__ partials, void* __restrict__ C, const
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// M = 1 streaming kernel (k % 512 == 0).  Wave w of workgroup (chunk, slot) owns the W = SB/4
+// consecutive k-slices [ks0 + w W, ks0 + (w+1) W), W a multiple of 8, i.e. whole 128-row input
+// chunks, so the waves run independently until the final reduction.  Per input chunk the wave
+// rotates x itself (lane l holds the rotated pair x[2l], x[2l+1] in one VGPR; the next chunk's x
+// and suh are prefetched with the weights), and per k-slice eight v_readlane move that slice's
+// 16 inputs to SGPRs, duplicated into (x, x) pairs by scalar packs; v_dot2 reads them there.
+// No LDS traffic and no barrier in the stream; every load is unconditional (clamped), so the
+// compiler's wait counts stay exact and the PF-deep ring never drains.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t rotate_pair(uint32_t xv, uint32_t sv, bool has_suh, int lane)
+{
+    if (!has_suh) return xv;
+    f16x2 v = as_h2(xv) * as_h2(sv);
+    float v0 = (float) v.x, v1 = (float) v.y;
+    fwht128_wave(v0, v1, lane);
+    f16x2 o = { (f16) (v0 * EXL3_HAD_RSCALE), (f16) (v1 * EXL3_HAD_RSCALE) };
+    return as_u32(o);
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(GEMV_THREADS)
+void gemv1_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ trellis,
+                  void* __restrict__ C, const uint16_t* __restrict__ suh,
+                  const uint16_t* __restrict__ svh, int k, int n, int c_fp32, int SB,
+                  float* __restrict__ partials, int* __restrict__ counters, int xcd)
+{
+    __shared__ float red[GEMV_WAVES][128];
+    __shared__ float sumx_w[GEMV_WAVES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
+    const int KS = k / 16;
+    const int splits = KS / SB;
+    // XCD-local mode: the splits of a chunk run on one XCD (workgroup b on XCD b % xcd), so
+    // they share that XCD's L2 and hand off through an L2 counter instead of a second kernel
+    int chunk, slot;
+    if (xcd > 0)
+    {
+        const int xb = blockIdx.x % xcd, lb = blockIdx.x / xcd;
+        chunk = xb + xcd * (lb / splits);
+        slot = lb % splits;
+    }
+    else
+    {
+        chunk = blockIdx.x / splits;
+        slot = blockIdx.x - chunk * splits;
+    }
+    const int W = SB / GEMV_WAVES;                      // slices per wave, multiple of 8
+    const int a = slot * SB + wave * W;                 // first k-slice of this wave
+    const int nchunks = W / 8;
+    const int tiles_n = n / 16;
+    const size_t rstride = (size_t) tiles_n * 8 * K;    // u32 per k-slice row
+    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
+                         + ((size_t) a * tiles_n + chunk * 8) * (8 * K);
+    const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
+    const bool has_suh = suh != nullptr;
+    const uint32_t* xg = (const uint32_t*) A + lane;                       // x pairs
+    const uint32_t* sg = (const uint32_t*) (has_suh ? suh : A) + lane;     // suh pairs
+
+    constexpr int PF = EXL3_GEMV_PF;
+    static_assert(8 % PF == 0, "prefetch depth must divide 8");
+    const int last = W - 1;
+    // x of the first chunk first (its wait then leaves the weight loads in flight)
+    uint32_t xv = __builtin_nontemporal_load(xg + (size_t) (a / 8) * 64);
+    uint32_t sv = __builtin_nontemporal_load(sg + (size_t) (a / 8) * 64);
+    uint32_t ring[PF][K + 1];
+    #pragma unroll
+    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last) * rstride, prev_off, ring[d]);
+
+    float acc0 = 0.0f, acc1 = 0.0f, sx = 0.0f;
+    for (int c = 0; c < nchunks; ++c)
+    {
+        const uint32_t xr = rotate_pair(xv, sv, has_suh, lane);
+        if (CB == 2)
+        {
+            const f16x2 p = as_h2(xr);
+            sx += wave_sum((float) p.x + (float) p.y, lane);
+        }
+        // prefetch the next chunk's x (clamped: stays inside this wave's range)
+        const int cn = min(c + 1, nchunks - 1);
+        xv = __builtin_nontemporal_load(xg + (size_t) (a / 8 + cn) * 64);
+        sv = __builtin_nontemporal_load(sg + (size_t) (a / 8 + cn) * 64);
+        #pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8)
+        {
+            const int i = c * 8 + s8;
+            const int d = s8 % PF;
+            uint32_t wv[K + 1];
+            #pragma unroll
+            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            uint32_t raw[32];
+            raw32<K, CB>(wv, raw, a3, b3);
+            load_slot<K>(base + (size_t) min(i + PF, last) * rstride, prev_off, ring[d]);
+            // this slice's 16 inputs: lanes 8 s8 .. 8 s8 + 7 hold pairs (x[2q], x[2q+1])
+            uint32_t x16[16];
+            #pragma unroll
+            for (int q = 0; q < 8; ++q)
+            {
+                const uint32_t p = __builtin_amdgcn_readlane(xr, 8 * s8 + q);
+                x16[2 * q] = (p & 0xffffu) | (p << 16);
+                x16[2 * q + 1] = (p >> 16) | (p & 0xffff0000u);
+            }
+            #pragma unroll
+            for (int w = 0; w < 32; ++w)
+            {
+                const int g = w >> 3, jj = w & 7;
+                const int row = 2 * g + (jj & 1) + 8 * ((jj >> 1) & 1);
+                float& acc = (jj >> 2) ? acc1 : acc0;
+                acc = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc, false);
+            }
+        }
+    }
+
+    const int c0 = (lane >> 3) * 16 + (lane & 7);
+    red[wave][c0] = acc0;
+    red[wave][c0 + 8] = acc1;
+    if (lane == 0) sumx_w[wave] = sx;
+    __syncthreads();
+    if (wave == 0)
+    {
+        const int c = 2 * lane;
+        float v0 = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+        float v1 = red[0][c + 1] + red[1][c + 1] + red[2][c + 1] + red[3][c + 1];
+        if (CB == 2)
+        {
+            const float kinv = (float) as_h(0x1eee);
+            const float bias = (sumx_w[0] + sumx_w[1] + sumx_w[2] + sumx_w[3]) * (float) as_h(0xc931);
+            v0 = v0 * kinv + bias;
+            v1 = v1 * kinv + bias;
+        }
+        if (splits == 1)
+        {
+            const int col = chunk * 128 + c;
+            store_output(v0, v1, C, c_fp32, svh, (size_t) col, col, lane);
+        }
+        else
+        {
+            float2 pv = { v0, v1 };
+            float* pp = partials + ((size_t) chunk * splits + slot) * 128 + c;
+            *(float2*) pp = pv;
+            if (xcd > 0)
+            {
+                // release the partial (stores complete in the shared L2), count this split in
+                // the chunk's L2 counter (own 128-byte line); the last arrival sums in slot order
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                int prev = 0;
+                if (lane == 0)
+                    prev = __hip_atomic_fetch_add(counters + chunk * 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                prev = __builtin_amdgcn_readfirstlane(prev);
+                if (prev == splits - 1)
+                {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                    if (lane == 0)
+                        __hip_atomic_store(counters + chunk * 32, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    const float* p0 = partials + (size_t) chunk * splits * 128 + c;
+                    float s0 = 0.0f, s1 = 0.0f;
+                    for (int sp0 = 0; sp0 < splits; sp0 += 8)
+                    {
+                        f32x2 v[8];
+                        #pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                        {
+                            // device-scope load: misses this CU's L1, reads the XCD's L2
+                            const uint64_t* q = (const uint64_t*) (p0 + (size_t) min(sp0 + j, splits - 1) * 128);
+                            const uint64_t u = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            v[j] = __builtin_bit_cast(f32x2, u);
+                        }
+                        #pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (sp0 + j < splits) { s0 += v[j].x; s1 += v[j].y; }
+                    }
+                    const int col = chunk * 128 + c;
+                    store_output(s0, s1, C, c_fp32, svh, (size_t) col, col, lane);
+                }
+            }
+        }
+    }
+}
+
 template <int K, int CB, int MT>
 int launch_gemv_t(const GemvArgs& g, hipStream_t s)
 {
@@ -386,8 +604,24 @@ int launch_gemv_t(const GemvArgs& g, hipStream_t s)
 }
 
 template <int K, int CB>
+int launch_gemv1(const GemvArgs& g, hipStream_t s)
+{
+    const int KS = g.k / 16;
+    const int SB = g.slices_per_block;
+    const int splits = KS / SB;
+    hipLaunchKernelGGL((gemv1_kernel<K, CB>), dim3(splits * (g.n / 128)), dim3(GEMV_THREADS), 0, s,
+                       g.A, g.trellis, g.C, g.suh, g.svh, g.k, g.n, g.c_fp32, SB, g.partials,
+                       g.counters, g.xcd);
+    if (splits > 1 && g.xcd == 0)
+        hipLaunchKernelGGL(gemv_finish, dim3(g.n / 128), dim3(GEMV_THREADS), 0, s,
+                           g.partials, g.C, g.svh, 1, g.n, splits, g.c_fp32);
+    return (int) hipGetLastError();
+}
+
+template <int K, int CB>
 int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 {
+    if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
     if (g.m == 1) return launch_gemv_t<K, CB, 1>(g, s);
     if (g.m <= 4) return launch_gemv_t<K, CB, 4>(g, s);
     return launch_gemv_t<K, CB, 8>(g, s);
