@@ -26,6 +26,20 @@ SIGNATURES = {
     "exl3_amd_reconstruct_had": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_had_r_128": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _f32, _vp]),
     "exl3_amd_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
+    "exl3_amd_mgemm": (_i32, [_vp, _i32, _i32, _i32,             # A, bszm_in, m, k
+                              _vp, _i32,                         # B table, num_B
+                              _vp, _i32, _i32, _i32,             # C, bszm_out, n, c_fp32
+                              _vp, _i32,                         # suh table, num_suh
+                              _vp, ctypes.c_int64,               # A_had, numel
+                              _vp, _i32,                         # svh table, num_svh
+                              _vp, _i32,                         # indices, num_indices
+                              _vp,                               # weights
+                              _f32, _i32, _i32, _i32,            # K, force_shape_idx, mcg, mul1
+                              _i32, _i32, _i32, _i32,            # min/max_index, force_num_sms, num_tokens
+                              _vp, _vp, _i32,                    # size_n_list, c_ptrs, num_c_ptrs
+                              _vp, _i32,                         # n_stride_list, entries
+                              _vp, _i32, _i32,                   # had_src_list, entries, num_had_src
+                              _vp]),
 }
 
 

@@ -68,7 +68,10 @@ struct DeviceState
     int num_xcd = 0;            // > 0 when workgroup b is verified to run on XCD b % num_xcd
     float* partials = nullptr;
     int* counters = nullptr;
+    int64_t* filt_idx = nullptr;      // mgemm expert-range filter output (MGEMM_MAX_FILTER slots)
+    uint16_t* filt_w = nullptr;
 };
+constexpr int MGEMM_MAX_FILTER = 128;   // exl3_gemm_kernel.cuh:82 (index-compaction capacity)
 
 DeviceState g_dev[MAX_DEVICES];
 std::mutex g_mutex;
@@ -99,24 +102,31 @@ int init_device(int device, DeviceState** out)
             }
             if (hipMemset(c, 0, WS_COUNTERS * sizeof(int)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
                 return fail(EXL3_AMD_EHIP, "counter initialisation failed");
+            void* f = nullptr;
+            if (hipMalloc(&f, MGEMM_MAX_FILTER * (sizeof(int64_t) + sizeof(uint16_t))) != hipSuccess)
+                return fail(EXL3_AMD_ENOMEM, "filter workspace allocation failed");
+            d.filt_idx = (int64_t*) f;
+            d.filt_w = (uint16_t*) (d.filt_idx + MGEMM_MAX_FILTER);
             // workgroup -> XCD dispatch order (round-robin on MI355X), verified on this device
             {
-                const int sizes[3] = { 64, 1000, 8192 };
+                const int gx[4] = { 64, 1000, 8192, 64 }, gy[4] = { 1, 1, 1, 9 };
                 int* probe = (int*) p;
                 int nx = 0;
                 bool ok = true;
-                for (int si = 0; si < 3 && ok; ++si)
+                for (int si = 0; si < 4 && ok; ++si)
                 {
-                    int* host = (int*) malloc(sizes[si] * sizeof(int));
-                    if (!host || exl3k_xcd_probe(probe, sizes[si], nullptr) || hipDeviceSynchronize() != hipSuccess ||
-                        hipMemcpy(host, probe, sizes[si] * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+                    const int total = gx[si] * gy[si];
+                    int* host = (int*) malloc(total * sizeof(int));
+                    if (!host || exl3k_xcd_probe(probe, gx[si], gy[si], nullptr) || hipDeviceSynchronize() != hipSuccess ||
+                        hipMemcpy(host, probe, total * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
                         ok = false;
                     if (ok)
                     {
                         int mx = 0;
-                        for (int i = 0; i < sizes[si]; ++i) mx = host[i] > mx ? host[i] : mx;
+                        for (int i = 0; i < total; ++i) mx = host[i] > mx ? host[i] : mx;
                         if (si == 0) nx = mx + 1;
-                        for (int i = 0; i < sizes[si] && ok; ++i) ok = host[i] == i % nx;
+                        // linear workgroup id (x fastest) -> XCD, round-robin
+                        for (int i = 0; i < total && ok; ++i) ok = host[i] == i % nx;
                     }
                     free(host);
                 }
@@ -144,35 +154,73 @@ int current_device(DeviceState** out)
 // GEMV work split (exl3_gemv.hip): SB slices per workgroup, a divisor of k/16 (so no
 // workgroup straddles two column chunks), sized for ~TARGET workgroups per CU within the LDS
 // budget (rotated input + reduction buffer) and the split-partial workspace.
-int gemv_plan(int m, int k, int n, int num_cus, GemvArgs& g)
+int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
 {
     const int mt = m == 1 ? 1 : (m <= 4 ? 4 : 8);
     const int KS = k / 16, chunks = n / 128;
-    int per_cu = 2;
+    int per_cu = 4;
     if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
     const long target = (long) per_cu * num_cus;
-    // M = 1 streaming kernel: whole 128-row input chunks per wave (SB multiple of 32)
-    int stream = m == 1 && KS % 32 == 0;
+    // M = 1 streaming kernel: 1, 2 or 4 slices per wave, or whole 128-row input chunks (SB % 32 == 0)
+    int stream = m == 1;
     if (const char* e = getenv("EXL3_AMD_GEMV_STREAM")) stream = stream && atoi(e) != 0;
-    const int step = stream ? 32 : 1;
+    auto ok_sb = [&](int d) { return KS % d == 0 && (!stream || d == 4 || d == 8 || d == 16 || d % 32 == 0); };
     const int lds_budget = 64 * 1024 - 4 * mt * 128 * 4;
     const int max_chunks = lds_budget / (mt * 512);           // rotated 128-row chunks in LDS
     int best = -1;
-    for (int d = step; d <= KS; d += step)
+    for (int d = stream ? 4 : 1; d <= KS; ++d)
     {
-        if (KS % d) continue;
+        if (!ok_sb(d)) continue;
         if (!stream && d / 8 + 2 > max_chunks) break;
-        if ((size_t) (KS / d) * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
-        if (best < 0 || (long) chunks * (KS / best) > target) best = d;   // fewest blocks >= target
-        if ((long) chunks * (KS / d) <= target) break;
+        if ((size_t) (KS / d) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
+        if (best < 0 || (long) bszm * chunks * (KS / best) > target) best = d;   // fewest blocks >= target
+        if ((long) bszm * chunks * (KS / d) <= target) break;
     }
-    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && KS % v == 0 && v % step == 0) best = v; }
+    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && ok_sb(v)) best = v; }
     if (best < 0) return -1;
+    if ((size_t) (KS / best) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / best > 1) return -1;
     g.stream_m1 = stream;
     g.slices_per_block = best;
     g.slots = KS / best;
     g.xs_chunks = best / 8 + 2;
     return 0;
+}
+
+GemvArgs gemv_args_single(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+                          const uint16_t* suh, const uint16_t* svh, int m, int k, int n)
+{
+    GemvArgs g;
+    memset(&g, 0, sizeof(g));
+    g.A = A; g.trellis = trellis; g.C = C; g.suh = suh; g.svh = svh;
+    g.m = m; g.k = k; g.n = n; g.c_fp32 = c_fp32 ? 1 : 0;
+    g.bszm_in = 1; g.bszm = 1; g.num_tokens = 1;
+    return g;
+}
+
+int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s);
+
+#ifdef EXL3_GEMV_TRACE
+uint64_t* g_trace = nullptr;
+#endif
+
+// Plan the work split, pick the XCD hand-off when the device and shape allow it, launch.
+int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, const char* what)
+{
+    const int chunks = g.n / 128;
+    if (gemv_plan(g.m, g.k, g.n, g.bszm, d->num_cus, g))
+        return fail(EXL3_AMD_EUNSUPPORTED, "%s: shape exceeds the GEMV workspace", what);
+    g.partials = d->partials;
+    g.counters = d->counters;
+    g.counters_half = (int) (WS_COUNTERS / 2);
+#ifdef EXL3_GEMV_TRACE
+    g.trace = g_trace;
+#endif
+    const size_t pairs = (size_t) g.bszm * chunks;
+    g.xcd = 0;
+    if (d->num_xcd > 0 && chunks % d->num_xcd == 0 && pairs * 32 <= WS_COUNTERS / 2)
+        g.xcd = d->num_xcd;
+    int rc = dispatch_gemv(bits, cb, g, s);
+    return rc ? hip_fail(rc, what) : 0;
 }
 
 int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s)
@@ -194,6 +242,10 @@ int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s)
 }  // namespace
 
 extern "C" {
+
+#ifdef EXL3_GEMV_TRACE
+void exl3_amd_debug_set_trace(void* p) { g_trace = (uint64_t*) p; }
+#endif
 
 const char* exl3_amd_last_error(void) { return g_last_error.c_str(); }
 
@@ -273,7 +325,7 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     if (!A || !trellis || !C) return fail(EXL3_AMD_EINVAL, "exl3_gemm: null pointer");
     if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be positive");
     if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
-    if (force_shape_idx < 0 || force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "exl3_gemm: bad force_shape_idx %d", force_shape_idx);
+    if (force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "exl3_gemm: bad force_shape_idx %d", force_shape_idx);
 
     DeviceState* d;
     if (int rc = current_device(&d)) return rc;
@@ -281,20 +333,104 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
 
     if (m <= 8 && force_shape_idx != 2)
     {
-        GemvArgs g;
-        g.A = A; g.trellis = trellis; g.C = C; g.suh = suh; g.svh = svh;
-        g.m = m; g.k = k; g.n = n; g.c_fp32 = c_fp32 ? 1 : 0;
-        if (gemv_plan(m, k, n, d->num_cus, g)) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: shape exceeds the GEMV workspace");
-        g.partials = d->partials;
-        g.counters = d->counters;
-        g.xcd = 0;
-        if (g.stream_m1 && d->num_xcd > 0 && (n / 128) % d->num_xcd == 0 && (size_t) (n / 128) * 32 <= WS_COUNTERS)
-            g.xcd = d->num_xcd;
-        if ((size_t) n / 128 > WS_COUNTERS) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: n too large for the counter workspace");
-        int rc = dispatch_gemv(bits, cb, g, s);
-        return rc ? hip_fail(rc, "exl3_gemm") : EXL3_AMD_TAG_GEMV;
+        GemvArgs g = gemv_args_single(A, trellis, C, c_fp32, suh, svh, m, k, n);
+        int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm");
+        return rc ? rc : EXL3_AMD_TAG_GEMV;
     }
     return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: m > 8 (MFMA GEMM) is not implemented in this build");
+}
+
+int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
+                   const uint64_t* B, int num_B,
+                   void* C, int bszm_out, int n, int c_fp32,
+                   const uint64_t* suh, int num_suh,
+                   uint16_t* A_had, int64_t a_had_numel,
+                   const uint64_t* svh, int num_svh,
+                   const int64_t* indices, int num_indices,
+                   const uint16_t* weights,
+                   float K, int force_shape_idx, int mcg, int mul1,
+                   int min_index, int max_index, int force_num_sms, int num_tokens,
+                   const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
+                   const int* n_stride_list, int num_n_stride,
+                   const int* had_src_list, int num_had_src_list, int num_had_src,
+                   void* stream)
+{
+    (void) A_had; (void) force_num_sms;
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg != 0, mul1 != 0, &bits, &half, &cb, "exl3_mgemm")) return rc;
+    if (bszm_in < 1 || bszm_out < 1 || m < 0 || k < 0 || n < 0 || num_B < 0)
+        return fail(EXL3_AMD_EINVAL, "exl3_mgemm: bad batch or size");
+    if (!A || !B || !suh || !svh || (!C && !c_ptrs)) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: null pointer");
+    const bool sliced = had_src_list != nullptr;
+    if (!sliced && (num_suh != num_B || num_svh != num_B))
+        return fail(EXL3_AMD_EINVAL, "exl3_mgemm: B, suh and svh tables must have the same length");
+    if (sliced && num_svh != num_B) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: B and svh tables must have the same length");
+    if (size_n_list)
+    {
+        if (!c_ptrs) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: size_n_list requires c_ptrs");
+        if (!(num_tokens == 1 && min_index < 0 && !weights))
+            return fail(EXL3_AMD_EINVAL, "exl3_mgemm: per-matrix widths incompatible with multi-token/filtering/weights");
+        bszm_out = num_c_ptrs;
+    }
+    else if (c_ptrs) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: c_ptrs requires size_n_list");
+    int bszm = bszm_in > bszm_out ? bszm_in : bszm_out;
+    if (sliced)
+    {
+        if (!(size_n_list && c_ptrs && n_stride_list))
+            return fail(EXL3_AMD_EINVAL, "exl3_mgemm: sliced mode requires size_n_list, c_ptrs and n_stride_list");
+        if (!(bszm_in == 1 && !indices && !weights && num_tokens == 1 && min_index < 0))
+            return fail(EXL3_AMD_EINVAL, "exl3_mgemm: sliced mode is single-input, unfiltered and single-token");
+        if (num_had_src_list < bszm_out || num_n_stride < bszm_out)
+            return fail(EXL3_AMD_EINVAL, "exl3_mgemm: had_src_list / n_stride_list must have one entry per slice");
+        if (!(num_had_src > 0 && num_suh >= num_had_src))
+            return fail(EXL3_AMD_EINVAL, "exl3_mgemm: sliced mode needs one suh entry per source");
+    }
+    else if (n_stride_list) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: n_stride_list requires had_src_list");
+    const int64_t had_slabs = sliced ? num_had_src : bszm;
+    if (a_had_numel < had_slabs * (int64_t) m * k) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: A_had must hold bszm * m * k elements");
+    if (indices)
+    {
+        if (!(num_indices <= bszm_in || num_indices <= bszm_out))
+            return fail(EXL3_AMD_EINVAL, "mgemm: too many indices for tensor batch");
+        if (bszm_in > num_indices) bszm_in = num_indices;
+        if (bszm_out > num_indices) bszm_out = num_indices;
+    }
+    bszm = bszm_in > bszm_out ? bszm_in : bszm_out;
+    if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: k must be a multiple of 16");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: n must be a multiple of 128");
+    if (num_tokens < 1) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: num_tokens must be positive");
+    if (weights && bszm % num_tokens) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: slots must split evenly into token groups");
+    if (min_index >= 0 && !indices) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: index range filtering requires indices");
+    if (min_index >= 0 && bszm > MGEMM_MAX_FILTER)
+        return fail(EXL3_AMD_EINVAL, "exl3_mgemm: range filtering supports at most %d slots", MGEMM_MAX_FILTER);
+    if (force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: bad force_shape_idx %d", force_shape_idx);
+    if (m == 0 || n == 0 || bszm == 0) return EXL3_AMD_TAG_GEMV;
+    if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: k must be positive");
+    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: k %% 128 != 0 is not implemented in this build");
+    if (m > 8 || force_shape_idx == 2)
+        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: m > 8 (MFMA GEMM) is not implemented in this build");
+
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    hipStream_t s = (hipStream_t) stream;
+
+    GemvArgs g;
+    memset(&g, 0, sizeof(g));
+    g.A = A; g.C = C; g.m = m; g.k = k; g.n = n; g.c_fp32 = c_fp32 ? 1 : 0;
+    g.B_list = B; g.suh_list = suh; g.svh_list = svh;
+    g.indices = indices; g.weights = weights;
+    g.size_n = size_n_list; g.c_list = c_ptrs; g.n_stride = n_stride_list; g.had_src = had_src_list;
+    g.bszm_in = bszm_in; g.bszm = bszm; g.num_tokens = num_tokens;
+    if (min_index >= 0)
+    {
+        int rc = exl3k_mgemm_filter(indices, weights, bszm, min_index, max_index, num_tokens, d->filt_idx, d->filt_w, s);
+        if (rc) return hip_fail(rc, "exl3_mgemm");
+        g.indices = d->filt_idx;
+        if (weights) g.weights = d->filt_w;
+    }
+    int rc = launch_gemv(d, bits, cb, g, s, "exl3_mgemm");
+    return rc ? rc : EXL3_AMD_TAG_GEMV;
 }
 
 }  // extern "C"

@@ -29,6 +29,15 @@ typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
 
 #define EXL3_HAD_RSCALE 0.088388347648f     // 1/sqrt(128) as the reference writes it
 
+// Global-address-space view of a pointer.  Pointers read from memory (pointer tables) or
+// carried in by-value structs are generic to the compiler, whose loads then become flat loads
+// that also count in lgkmcnt (every scalar-load wait then waits for them too).
+#define EXL3_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const EXL3_GLOBAL T* to_global(const T* p) { return (const EXL3_GLOBAL T*) p; }
+template <typename T>
+__device__ __forceinline__ EXL3_GLOBAL T* to_global_w(T* p) { return (EXL3_GLOBAL T*) p; }
+
 namespace exl3 {
 
 __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -226,18 +235,55 @@ __device__ __forceinline__ float xor_shfl(float v, int mask, int lane)
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
 }
 
+// Value of lane (lane ^ M) without LDS: DPP quad permutes (M = 1, 2), two bank-masked row
+// shifts (M = 4), a row rotate (M = 8), gfx950 permlane swaps (M = 16, 32).
+template <int M>
+__device__ __forceinline__ float xor_partner(float v, int lane)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t p;
+    if constexpr (M == 1) p = __builtin_amdgcn_update_dpp(0u, u, 0xB1, 0xf, 0xf, false);       // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) p = __builtin_amdgcn_update_dpp(0u, u, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4)
+    {
+        p = __builtin_amdgcn_update_dpp(0u, u, 0x104, 0xf, 0x5, false);   // row_shl:4 into banks 0, 2
+        p = __builtin_amdgcn_update_dpp(p, u, 0x114, 0xf, 0xa, false);    // row_shr:4 into banks 1, 3
+    }
+    else if constexpr (M == 8) p = __builtin_amdgcn_update_dpp(0u, u, 0x128, 0xf, 0xf, false); // row_ror:8
+    else if constexpr (M == 16)
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        p = (lane & 16) ? r[0] : r[1];
+    }
+    else
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        p = (lane & 32) ? r[0] : r[1];
+    }
+    return __builtin_bit_cast(float, p);
+}
+
+// One butterfly stage: lower lane a + b, upper lane a - b (a = lower element), one rounding each
+// (fma with a +-1 factor is exactly the sum or the difference).
+template <int M>
+__device__ __forceinline__ void fwht_stage(float& v0, float& v1, int lane)
+{
+    const float p0 = xor_partner<M>(v0, lane), p1 = xor_partner<M>(v1, lane);
+    const float sg = (lane & M) ? -1.0f : 1.0f;
+    v0 = __builtin_fmaf(sg, v0, p0);
+    v1 = __builtin_fmaf(sg, v1, p1);
+}
+
 __device__ __forceinline__ void fwht128_wave(float& v0, float& v1, int lane)
 {
     float s = v0 + v1, d = v0 - v1;
     v0 = s; v1 = d;
-    #pragma unroll
-    for (int m = 1; m < 64; m <<= 1)
-    {
-        float p0 = xor_shfl(v0, m, lane);
-        float p1 = xor_shfl(v1, m, lane);
-        if (lane & m) { v0 = p0 - v0; v1 = p1 - v1; }
-        else          { v0 = v0 + p0; v1 = v1 + p1; }
-    }
+    fwht_stage<1>(v0, v1, lane);
+    fwht_stage<2>(v0, v1, lane);
+    fwht_stage<4>(v0, v1, lane);
+    fwht_stage<8>(v0, v1, lane);
+    fwht_stage<16>(v0, v1, lane);
+    fwht_stage<32>(v0, v1, lane);
 }
 
 }  // namespace exl3

@@ -44,6 +44,20 @@ using namespace exl3;
 
 namespace {
 
+// Instrumented builds (-DEXL3_GEMV_TRACE): wave timestamps (s_memrealtime, 100 MHz) taken after
+// `dep` is available, stored by lane 0 with a vector store.
+#ifdef EXL3_GEMV_TRACE
+#define GEMV_STAMP(g, slot_i, dep)                                                              \
+    do {                                                                                        \
+        uint64_t t_;                                                                            \
+        asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_) : "s"(dep));        \
+        if ((threadIdx.x & 63) == 0)                                                            \
+            (g).trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + (slot_i)] = t_; \
+    } while (0)
+#else
+#define GEMV_STAMP(g, slot_i, dep) do { } while (0)
+#endif
+
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = 4;
 
@@ -61,7 +75,7 @@ __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint3
         #pragma unroll
         for (int i = 0; i < K / 4; ++i)
         {
-            u32x4 v = __builtin_nontemporal_load((const u32x4*) p + i);
+            u32x4 v = __builtin_nontemporal_load(to_global((const u32x4*) p) + i);
             w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
         }
     }
@@ -70,14 +84,14 @@ __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint3
         #pragma unroll
         for (int i = 0; i < K / 2; ++i)
         {
-            u32x2 v = __builtin_nontemporal_load((const u32x2*) p + i);
+            u32x2 v = __builtin_nontemporal_load(to_global((const u32x2*) p) + i);
             w[2 * i] = v.x; w[2 * i + 1] = v.y;
         }
     }
     else
     {
         #pragma unroll
-        for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(p + i);
+        for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(to_global(p) + i);
     }
 }
 
@@ -85,7 +99,7 @@ template <int K>
 __device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int prev_off, uint32_t* w)
 {
     load_words<K>(p, w + 1);
-    w[0] = __builtin_nontemporal_load(p + prev_off);
+    w[0] = __builtin_nontemporal_load(to_global(p) + prev_off);
 }
 
 // Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe, from word hi when the window
@@ -165,6 +179,92 @@ __device__ __forceinline__ void raw32(const uint32_t* wv, uint32_t* raw, const u
 template <int K, int CB, int I>
 __device__ __forceinline__ uint32_t raw_at(const uint32_t* wv) { return raw_weight<CB>(state16<K, I>(wv)); }
 
+// ---------------------------------------------------------------------------------------------
+// Per-slot view of one launch (quant/exl3_gemm_kernel.cuh:169-238): slot j computes
+// A[j or 0] @ B[q] with q = indices[j] (or j); table entries give the trellis, the input /
+// output sign vectors, the width, the row stride (sliced mode: column slices of a wider
+// matrix) and the output pointer.  Scalar loads only.
+// ---------------------------------------------------------------------------------------------
+struct MatView
+{
+    const uint16_t* A;
+    const uint16_t* trellis;
+    void* C;
+    const uint16_t* suh;
+    const uint16_t* svh;
+    int n;          // this matrix's width
+    int stride;     // row stride of trellis tiles (in columns) and of C
+    float scale;    // output scale: 1/sqrt(128) (x routing weight)
+};
+
+// Scalar loads of the (uniform) table entries: issued together, one wait.  Absent tables are
+// read at a harmless valid address (the kernel argument block's input pointer) and ignored.
+__device__ __forceinline__ uint32_t s_load_u32(const void* p)
+{
+    uint32_t v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+
+__device__ __forceinline__ bool resolve(const GemvArgs& g, int j, MatView& v)
+{
+    int q = j;
+    if (g.indices)
+    {
+        q = (int) s_load_u32(g.indices + j);      // low word of the int64 index (little endian)
+        if (q < 0) return false;
+    }
+    const void* dummy = g.A;
+    if (g.B_list)
+    {
+        const void* pB = g.B_list + q;
+        const void* pV = g.svh_list + q;
+        const void* pH = g.had_src ? (const void*) (g.had_src + q) : dummy;
+        const void* pN = g.size_n ? (const void*) (g.size_n + q) : dummy;
+        const void* pT = g.n_stride ? (const void*) (g.n_stride + q) : dummy;
+        const void* pC = g.c_list ? (const void*) (g.c_list + q) : dummy;
+        uint64_t b, vs, c;
+        uint32_t h, nn, st;
+        asm volatile("s_load_dwordx2 %0, %6, 0x0\n\t"
+                     "s_load_dwordx2 %1, %7, 0x0\n\t"
+                     "s_load_dword %2, %8, 0x0\n\t"
+                     "s_load_dword %3, %9, 0x0\n\t"
+                     "s_load_dword %4, %10, 0x0\n\t"
+                     "s_load_dwordx2 %5, %11, 0x0\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&s"(b), "=&s"(vs), "=&s"(h), "=&s"(nn), "=&s"(st), "=&s"(c)
+                     : "s"(pB), "s"(pV), "s"(pH), "s"(pN), "s"(pT), "s"(pC)
+                     : "memory");
+        const int src = g.had_src ? (int) h : q;
+        uint64_t u;
+        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(u) : "s"(g.suh_list + src) : "memory");
+        v.trellis = (const uint16_t*) b;
+        v.svh = (const uint16_t*) vs;
+        v.suh = (const uint16_t*) u;
+        v.n = g.size_n ? (int) nn : g.n;
+        v.stride = g.n_stride ? (int) st : v.n;
+        if (g.c_list) v.C = (void*) c;
+        else v.C = (char*) g.C + (size_t) j * g.m * g.n * (g.c_fp32 ? 4 : 2);
+    }
+    else
+    {
+        v.trellis = g.trellis;
+        v.suh = g.suh;
+        v.svh = g.svh;
+        v.n = g.n;
+        v.stride = g.n;
+        v.C = (char*) g.C + (size_t) j * g.m * g.n * (g.c_fp32 ? 4 : 2);
+    }
+    v.A = g.A + (g.bszm_in == 1 ? (size_t) 0 : (size_t) j * g.m * g.k);
+    v.scale = EXL3_HAD_RSCALE;
+    if (g.weights)
+    {
+        const uint32_t w2 = s_load_u32((const uint32_t*) ((uintptr_t) (g.weights + j) & ~(uintptr_t) 3));
+        v.scale = EXL3_HAD_RSCALE * (float) as_h((uint16_t) ((j & 1) ? (w2 >> 16) : w2));
+    }
+    return true;
+}
+
 // Input rotation of chunks [kc0, kc0 + nkc) of rows [0, m) into xs (u32 units: 128
 // duplicated pairs per chunk).  had_hf_r_128_inner<true,false> (hadamard_inner.cuh:93-150):
 // fp16 pre-scale, fp32 butterfly, * 1/sqrt(128), round to fp16.
@@ -176,11 +276,11 @@ __device__ __forceinline__ void rotate_chunks(const uint16_t* __restrict__ A, co
     {
         const int row = job / nkc, c = job % nkc;
         const int col = (kc0 + c) * 128 + 2 * lane;
-        f16x2 v = as_h2(*(const uint32_t*) (A + (size_t) row * k + col));
+        f16x2 v = as_h2(*to_global((const uint32_t*) (A + (size_t) row * k + col)));
         f16x2 o;
         if (suh)
         {
-            v = v * as_h2(*(const uint32_t*) (suh + col));
+            v = v * as_h2(*to_global((const uint32_t*) (suh + col)));
             float v0 = (float) v.x, v1 = (float) v.y;
             fwht128_wave(v0, v1, lane);
             o.x = (f16) (v0 * EXL3_HAD_RSCALE);
@@ -195,20 +295,22 @@ __device__ __forceinline__ void rotate_chunks(const uint16_t* __restrict__ A, co
 
 // Output rotation of one fp32 row chunk held as (v0, v1) = elements 2l, 2l+1, then store.
 // Half output: had_fh_r_128_inner (hadamard_inner.cuh:216-281); float output: had_ff.
-__device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_fp32, const uint16_t* svh,
-                                             size_t idx, int col, int lane)
+// `scale` is 1/sqrt(128), times the routing weight in weighted mode.
+// svp: this lane's svh pair (svh[col], svh[col + 1]), loaded ahead by the caller.
+__device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_fp32, bool has_svh, uint32_t svp,
+                                             size_t idx, int lane, float scale)
 {
-    if (svh)
+    if (has_svh)
     {
         fwht128_wave(v0, v1, lane);
-        v0 *= EXL3_HAD_RSCALE;
-        v1 *= EXL3_HAD_RSCALE;
-        f16x2 s = as_h2(*(const uint32_t*) (svh + col));
+        v0 *= scale;
+        v1 *= scale;
+        f16x2 s = as_h2(svp);
         if (!c_fp32)
         {
             f16x2 h = { (f16) v0, (f16) v1 };
             h = h * s;
-            *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
+            *to_global_w((uint32_t*) ((uint16_t*) C + idx)) = as_u32(h);
             return;
         }
         v0 *= (float) s.x;
@@ -216,50 +318,236 @@ __device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_
     }
     if (c_fp32)
     {
-        float2 o = { v0, v1 };
-        *(float2*) ((float*) C + idx) = o;
+        f32x2 o = { v0, v1 };
+        *to_global_w((f32x2*) ((float*) C + idx)) = o;
     }
     else
     {
         f16x2 h = { (f16) v0, (f16) v1 };
-        *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
+        *to_global_w((uint32_t*) ((uint16_t*) C + idx)) = as_u32(h);
     }
 }
 
 __device__ __forceinline__ float wave_sum(float v, int lane)
 {
-    #pragma unroll
-    for (int msk = 1; msk < 64; msk <<= 1) v += xor_shfl(v, msk, lane);
+    v += xor_partner<1>(v, lane);
+    v += xor_partner<2>(v, lane);
+    v += xor_partner<4>(v, lane);
+    v += xor_partner<8>(v, lane);
+    v += xor_partner<16>(v, lane);
+    v += xor_partner<32>(v, lane);
     return v;
+}
+
+// Device-scope loads: they miss the CU's L1 and read the XCD's L2, where the other
+// workgroups of the chunk (same XCD) left their results.
+__device__ __forceinline__ f32x2 load_l2_f32x2(const float* p)
+{
+    return __builtin_bit_cast(f32x2, __hip_atomic_load(to_global((const uint64_t*) p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint32_t load_l2_u32(const void* p)
+{
+    return __hip_atomic_load(to_global((const uint32_t*) p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// All threads: release this workgroup's stores, count it in *ctr; true in the last arrival of
+// `total` (which then re-arms the counter).  Workgroup scope suffices: every workgroup that
+// counts in one counter runs on the same XCD and meets in its L2, where global atomics execute.
+__device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag)
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        const int prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const bool last = prev == total - 1;
+        if (last) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        *flag = last;
+    }
+    __syncthreads();
+    const bool last = *flag;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    return last;
+}
+
+// Weighted reduction (quant/exl3_gemm_kernel.cuh:286-342) of the 128 columns of one chunk:
+// token group t sums its bszm / num_tokens slots (ascending, inactive slots skipped) into
+// output slab t, groups in increasing t.  fp16 outputs sum in fp16 like the reference.
+__device__ void weighted_reduce(const GemvArgs& g, int chunk, bool via_l2)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int stride = g.bszm / g.num_tokens;
+    const size_t slab = (size_t) g.m * g.n;
+    for (int t = 0; t < g.num_tokens; ++t)
+    {
+        for (int r = wave; r < g.m; r += GEMV_WAVES)
+        {
+            const size_t e = (size_t) r * g.n + chunk * 128 + 2 * lane;
+            if (g.c_fp32)
+            {
+                float* C = (float*) g.C;
+                float s0 = 0.0f, s1 = 0.0f;
+                for (int jj = 0; jj < stride; ++jj)
+                {
+                    const int j = t * stride + jj;
+                    if (g.indices && *to_global(g.indices + j) < 0) continue;
+                    const float* p = C + (size_t) j * slab + e;
+                    f32x2 v = via_l2 ? load_l2_f32x2(p) : *to_global((const f32x2*) p);
+                    s0 += v.x; s1 += v.y;
+                }
+                f32x2 o = { s0, s1 };
+                *to_global_w((f32x2*) (C + (size_t) t * slab + e)) = o;
+            }
+            else
+            {
+                uint16_t* C = (uint16_t*) g.C;
+                f16x2 s = { (f16) 0.0f, (f16) 0.0f };
+                for (int jj = 0; jj < stride; ++jj)
+                {
+                    const int j = t * stride + jj;
+                    if (g.indices && *to_global(g.indices + j) < 0) continue;
+                    const uint16_t* p = C + (size_t) j * slab + e;
+                    s = s + as_h2(via_l2 ? load_l2_u32(p) : *to_global((const uint32_t*) p));
+                }
+                *to_global_w((uint32_t*) (C + (size_t) t * slab + e)) = as_u32(s);
+            }
+        }
+        __syncthreads();   // group t + 1 may read slab t's rows written above by other waves
+    }
+}
+
+// Block epilogue.  res: LDS [m][128] fp32, this workgroup's sums for its k range (all
+// corrections applied).  One split: rotate and store.  Several splits: store the partial to
+// this workgroup's slot; in XCD mode the last workgroup of the (slot j, chunk) pair then sums
+// the partials -- in a fixed order -- rotates and stores.  Weighted mode adds a second hand-off
+// per chunk over all slots, whose last arrival runs the token-group reduction.
+__device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int chunk, int slot, int splits,
+                               const float* res, float* tmp, int* flag, uint32_t svp)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = g.m;
+    const int chunks = g.n / 128;
+    if (splits > 1)
+    {
+        float* pbase = g.partials + ((size_t) j * chunks + chunk) * splits * m * 128;
+        for (int e = threadIdx.x; e < m * 32; e += GEMV_THREADS)
+            *to_global_w((f32x4*) (pbase + (size_t) slot * m * 128 + 4 * e)) = *(const f32x4*) (res + 4 * e);
+        if (!g.xcd) return;
+        GEMV_STAMP(g, 4, 0);
+        if (!arrive_last(g.counters + ((size_t) j * chunks + chunk) * 32, splits, flag)) return;
+        GEMV_STAMP(g, 6, *flag);
+        // sum the slots: threads split into G groups over the m * 64 column pairs; group gi takes
+        // slots gi, gi + G, ...; the groups then combine in order through LDS
+        const int pairs = m * 64;
+        const int G = GEMV_THREADS / pairs > 0 ? GEMV_THREADS / pairs : 1;
+        const int gi = threadIdx.x / pairs;
+        const int pe = threadIdx.x % pairs;
+        if (gi < G)
+        {
+            for (int pe2 = pe; pe2 < pairs; pe2 += GEMV_THREADS)
+            {
+                float s0 = 0.0f, s1 = 0.0f;
+                for (int sp0 = gi; sp0 < splits; sp0 += 8 * G)
+                {
+                    f32x2 vv[8];
+                    #pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        vv[u] = load_l2_f32x2(pbase + (size_t) min(sp0 + u * G, splits - 1) * m * 128 + 2 * pe2);
+                    #pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (sp0 + u * G < splits) { s0 += vv[u].x; s1 += vv[u].y; }
+                }
+                tmp[(gi * pairs + pe2) * 2] = s0;
+                tmp[(gi * pairs + pe2) * 2 + 1] = s1;
+            }
+        }
+        __syncthreads();
+        GEMV_STAMP(g, 7, 0);
+        for (int r = wave; r < m; r += GEMV_WAVES)
+        {
+            float s0 = 0.0f, s1 = 0.0f;
+            for (int q = 0; q < G; ++q)
+            {
+                s0 += tmp[(q * pairs + r * 64 + lane) * 2];
+                s1 += tmp[(q * pairs + r * 64 + lane) * 2 + 1];
+            }
+            const int col = chunk * 128 + 2 * lane;
+            store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale);
+        }
+    }
+    else
+    {
+        for (int r = wave; r < m; r += GEMV_WAVES)
+        {
+            const int col = chunk * 128 + 2 * lane;
+            store_output(res[r * 128 + 2 * lane], res[r * 128 + 2 * lane + 1], v.C, g.c_fp32, v.svh != nullptr,
+                         svp, (size_t) r * v.stride + col, lane, v.scale);
+        }
+    }
+    if (g.weights && g.xcd)
+    {
+        if (!arrive_last(g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
+        weighted_reduce(g, chunk, true);
+    }
+}
+
+// Inactive slot (negative index) in weighted XCD mode: still counted once per chunk.
+__device__ void inactive_arrive(const GemvArgs& g, int chunk, int slot, int* flag)
+{
+    if (!(g.weights && g.xcd) || slot != 0) return;
+    if (!arrive_last(g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
+    weighted_reduce(g, chunk, true);
+}
+
+// Workgroup -> (chunk, split slot).  XCD mode: the splits of a chunk share one XCD.
+__device__ __forceinline__ void block_coords(const GemvArgs& g, int splits, int& chunk, int& slot)
+{
+    if (g.xcd > 0)
+    {
+        const int xb = blockIdx.x % g.xcd, lb = blockIdx.x / g.xcd;
+        chunk = xb + g.xcd * (lb / splits);
+        slot = lb % splits;
+    }
+    else
+    {
+        chunk = blockIdx.x / splits;
+        slot = blockIdx.x - chunk * splits;
+    }
 }
 
 template <int K, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS)
-void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ trellis,
-                 void* __restrict__ C, const uint16_t* __restrict__ suh,
-                 const uint16_t* __restrict__ svh, int m, int k, int n, int c_fp32,
-                 int SB, int xs_chunks, float* __restrict__ partials)
+void gemv_kernel(const GemvArgs g)
 {
     extern __shared__ uint32_t smem[];
+    __shared__ int flag;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
+    const int m = g.m, k = g.k;
     const int KS = k / 16;                                // slices per column chunk
+    const int SB = g.slices_per_block;
     const int splits = KS / SB;
-    const int chunk = blockIdx.x / splits;
-    const int slot = blockIdx.x - chunk * splits;
+    const int j = blockIdx.y;
+    int chunk, slot;
+    block_coords(g, splits, chunk, slot);
+    MatView v;
+    if (!resolve(g, j, v)) { inactive_arrive(g, chunk, slot, &flag); return; }
+    if (chunk * 128 >= v.n) return;
+    // (unconditional load: without svh it reads the input, k >= 128, and is unused)
+    const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
     const int ks0 = slot * SB;
     const int kc0 = ks0 / 8;
     const int nkc = (ks0 + SB - 1) / 8 - kc0 + 1;
-    const int xs_stride = xs_chunks * 128;                // u32 per row
+    const int xs_stride = g.xs_chunks * 128;              // u32 per row
     uint32_t* xs = smem;                                  // [MT][xs_chunks][128] dup pairs
     float* red = (float*) (smem + MT * xs_stride);        // [GEMV_WAVES][MT][128]
 
     // this wave's slices: ks0 + wave + 4 i, i < myn
     const int myn = SB > wave ? (SB - wave + GEMV_WAVES - 1) / GEMV_WAVES : 0;
-    const int tiles_n = n / 16;
+    const int tiles_n = v.stride / 16;
     const size_t kstride = (size_t) GEMV_WAVES * tiles_n * 8 * K;         // u32 between my slices
-    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
+    const uint32_t* base = (const uint32_t*) v.trellis + (size_t) lane * K
                          + ((size_t) (ks0 + min(wave, SB - 1)) * tiles_n + chunk * 8) * (8 * K);
 
     // prefetch ring (unconditional, clamped loads keep the wait counts static)
@@ -271,7 +559,7 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
     for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
 
     // input rotation of the chunks this workgroup touches (overlaps the first loads)
-    rotate_chunks(A, suh, xs, xs_stride, m, k, kc0, nkc);
+    rotate_chunks(v.A, v.suh, xs, xs_stride, m, k, kc0, nkc);
     __syncthreads();
 
     float acc[MT][2];
@@ -302,18 +590,18 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
                 const u32x4* xp = (const u32x4*) (xs + r * xs_stride + xo);
                 uint32_t x16[16];
                 #pragma unroll
-                for (int v = 0; v < 4; ++v)
+                for (int q = 0; q < 4; ++q)
                 {
-                    u32x4 t = xp[v];
-                    x16[4 * v] = live ? t.x : 0u;     x16[4 * v + 1] = live ? t.y : 0u;
-                    x16[4 * v + 2] = live ? t.z : 0u; x16[4 * v + 3] = live ? t.w : 0u;
+                    u32x4 t = xp[q];
+                    x16[4 * q] = live ? t.x : 0u;     x16[4 * q + 1] = live ? t.y : 0u;
+                    x16[4 * q + 2] = live ? t.z : 0u; x16[4 * q + 3] = live ? t.w : 0u;
                 }
                 // window w = 8g + jj: column j + 8 (jj >= 4), row 2g + {0, 1, 8, 9}[jj & 3]
                 #pragma unroll
                 for (int w = 0; w < 32; ++w)
                 {
-                    const int g = w >> 3, jj = w & 7;
-                    const int row = 2 * g + (jj & 1) + 8 * ((jj >> 1) & 1);
+                    const int gq = w >> 3, jj = w & 7;
+                    const int row = 2 * gq + (jj & 1) + 8 * ((jj >> 1) & 1);
                     float& a = acc[r][jj >> 2];
                     a = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), a, false);
                 }
@@ -336,20 +624,23 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
         // MUL1 bias term: sum of the rotated input over this workgroup's k range
         for (int r = wave; r < m; r += GEMV_WAVES)
         {
-            float v = 0.0f;
+            float sv = 0.0f;
             for (int e = lane; e < SB * 16; e += 64)
             {
                 const int ks = ks0 + e / 16;
-                v += (float) as_h2(xs[r * xs_stride + (ks / 8 - kc0) * 128 + (ks & 7) * 16 + (e & 15)]).x;
+                sv += (float) as_h2(xs[r * xs_stride + (ks / 8 - kc0) * 128 + (ks & 7) * 16 + (e & 15)]).x;
             }
-            v = wave_sum(v, lane);
-            if (lane == 0) sumx[r] = v;
+            sv = wave_sum(sv, lane);
+            if (lane == 0) sumx[r] = sv;
         }
     }
     __syncthreads();
 
-    // rows of the chunk: 4 waves x 64 lanes, two columns per lane
-    for (int r = wave; r < m; r += GEMV_WAVES)
+    // rows of the chunk -> res (LDS, reusing the input area): 4 waves x 64 lanes, two columns per lane
+    float* res = (float*) xs;                             // [m][128]
+    float r0[2][2];
+    int nr = 0;
+    for (int r = wave; r < m; r += GEMV_WAVES, ++nr)
     {
         const int c = 2 * lane;
         float v0 = red[r * 128 + c], v1 = red[r * 128 + c + 1];
@@ -365,56 +656,68 @@ void gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ tr
             v0 = v0 * kinv + bias;
             v1 = v1 * kinv + bias;
         }
-        if (splits == 1)
-        {
-            const int col = chunk * 128 + c;
-            store_output(v0, v1, C, c_fp32, svh, (size_t) r * n + col, col, lane);
-        }
-        else
-        {
-            float2 pv = { v0, v1 };
-            *(float2*) (partials + (((size_t) chunk * splits + slot) * m + r) * 128 + c) = pv;
-        }
+        r0[nr][0] = v0; r0[nr][1] = v1;
     }
+    __syncthreads();                                      // xs reads done before res overwrites it
+    nr = 0;
+    for (int r = wave; r < m; r += GEMV_WAVES, ++nr)
+    {
+        res[r * 128 + 2 * lane] = r0[nr][0];
+        res[r * 128 + 2 * lane + 1] = r0[nr][1];
+    }
+    __syncthreads();
+    block_epilogue(g, v, j, chunk, slot, splits, res, red, &flag, svp);
 }
 
-// Sum the split partials of each column chunk in slot order, output rotation, store.
-// Grid: n / 128 chunks; one wave per row.
+// Sum the split partials of each (slot, column chunk) in slot order, output rotation, store.
+// Grid: (n / 128, bszm); one wave per row.  Used when the XCD hand-off is off.
 __global__ __launch_bounds__(GEMV_THREADS)
-void gemv_finish(const float* __restrict__ partials, void* __restrict__ C, const uint16_t* __restrict__ svh,
-                 int m, int n, int splits, int c_fp32)
+void gemv_finish(const GemvArgs g, int splits)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = blockIdx.x;
+    const int chunk = blockIdx.x, j = blockIdx.y;
+    MatView v;
+    if (!resolve(g, j, v) || chunk * 128 >= v.n) return;
+    const int m = g.m;
+    const float* pbase = g.partials + ((size_t) j * (g.n / 128) + chunk) * splits * m * 128;
     for (int r = wave; r < m; r += GEMV_WAVES)
     {
         const int c = 2 * lane;
-        const float* pp = partials + ((size_t) chunk * splits * m + r) * 128 + c;
+        const float* pp = pbase + (size_t) r * 128 + c;
         float v0 = 0.0f, v1 = 0.0f;
         for (int sp0 = 0; sp0 < splits; sp0 += 8)
         {
-            f32x2 v[8];
+            f32x2 vv[8];
             #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                v[j] = __builtin_nontemporal_load((const f32x2*) (pp + (size_t) min(sp0 + j, splits - 1) * m * 128));
+            for (int u = 0; u < 8; ++u)
+                vv[u] = __builtin_nontemporal_load(to_global((const f32x2*) (pp + (size_t) min(sp0 + u, splits - 1) * m * 128)));
             #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (sp0 + j < splits) { v0 += v[j].x; v1 += v[j].y; }
+            for (int u = 0; u < 8; ++u)
+                if (sp0 + u < splits) { v0 += vv[u].x; v1 += vv[u].y; }
         }
         const int col = chunk * 128 + c;
-        store_output(v0, v1, C, c_fp32, svh, (size_t) r * n + col, col, lane);
+        const uint32_t svp = v.svh ? *to_global((const uint32_t*) (v.svh + col)) : 0u;
+        store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale);
     }
 }
 
+// Weighted reduction as its own kernel (XCD hand-off off).  Grid: n / 128.
+__global__ __launch_bounds__(GEMV_THREADS)
+void gemv_weighted_reduce(const GemvArgs g)
+{
+    weighted_reduce(g, blockIdx.x, false);
+}
+
 // ---------------------------------------------------------------------------------------------
-// M = 1 streaming kernel (k % 512 == 0).  Wave w of workgroup (chunk, slot) owns the W = SB/4
-// consecutive k-slices [ks0 + w W, ks0 + (w+1) W), W a multiple of 8, i.e. whole 128-row input
-// chunks, so the waves run independently until the final reduction.  Per input chunk the wave
-// rotates x itself (lane l holds the rotated pair x[2l], x[2l+1] in one VGPR; the next chunk's x
-// and suh are prefetched with the weights), and per k-slice eight v_readlane move that slice's
-// 16 inputs to SGPRs, duplicated into (x, x) pairs by scalar packs; v_dot2 reads them there.
-// No LDS traffic and no barrier in the stream; every load is unconditional (clamped), so the
-// compiler's wait counts stay exact and the PF-deep ring never drains.
+// M = 1 streaming kernel.  Wave w of workgroup (chunk, slot) owns the W = SB/4 consecutive
+// k-slices [ks0 + w W, ks0 + (w+1) W): W in {1, 2, 4} (part of one 128-row input chunk) or a
+// multiple of 8 (whole chunks), so the waves run independently until the final reduction.
+// Per input chunk the wave rotates x itself (lane l holds the rotated pair x[2l], x[2l+1] in
+// one VGPR; the next chunk's x and suh are prefetched with the weights), and per k-slice eight
+// v_readlane move that slice's 16 inputs to SGPRs, duplicated into (x, x) pairs by scalar
+// packs; v_dot2 reads them there.  No LDS traffic and no barrier in the stream; every load is
+// unconditional (clamped), so the compiler's wait counts stay exact and the PF-deep ring never
+// drains.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t rotate_pair(uint32_t xv, uint32_t sv, bool has_suh, int lane)
 {
@@ -426,71 +729,82 @@ __device__ __forceinline__ uint32_t rotate_pair(uint32_t xv, uint32_t sv, bool h
     return as_u32(o);
 }
 
-template <int K, int CB>
+template <int K, int CB, int WS>
 __global__ __launch_bounds__(GEMV_THREADS)
-void gemv1_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ trellis,
-                  void* __restrict__ C, const uint16_t* __restrict__ suh,
-                  const uint16_t* __restrict__ svh, int k, int n, int c_fp32, int SB,
-                  float* __restrict__ partials, int* __restrict__ counters, int xcd)
+void gemv1_kernel(const GemvArgs g)
 {
     __shared__ float red[GEMV_WAVES][128];
+    __shared__ float res[128];
+    __shared__ float tmp[2 * GEMV_THREADS];
     __shared__ float sumx_w[GEMV_WAVES];
+    __shared__ int flag;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
-    const int KS = k / 16;
+    const int KS = g.k / 16;
+    const int SB = g.slices_per_block;
     const int splits = KS / SB;
-    // XCD-local mode: the splits of a chunk run on one XCD (workgroup b on XCD b % xcd), so
-    // they share that XCD's L2 and hand off through an L2 counter instead of a second kernel
+    const int j = blockIdx.y;
     int chunk, slot;
-    if (xcd > 0)
+    block_coords(g, splits, chunk, slot);
+    MatView v;
+    if (!resolve(g, j, v)) { inactive_arrive(g, chunk, slot, &flag); return; }
+    if (chunk * 128 >= v.n) return;
+#ifdef EXL3_GEMV_TRACE
     {
-        const int xb = blockIdx.x % xcd, lb = blockIdx.x / xcd;
-        chunk = xb + xcd * (lb / splits);
-        slot = lb % splits;
+        uint32_t hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n\ts_getreg_b32 %1, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(hw), "=s"(xcc));
+        GEMV_STAMP(g, 0, hw);
+        if ((threadIdx.x & 63) == 0)
+            g.trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + 5] = ((uint64_t) xcc << 32) | hw;
     }
-    else
-    {
-        chunk = blockIdx.x / splits;
-        slot = blockIdx.x - chunk * splits;
-    }
-    const int W = SB / GEMV_WAVES;                      // slices per wave, multiple of 8
+#endif
+
+    // WS: slices per wave when below 8 (W = WS), else 8 (W a multiple of 8)
+    const int W = SB / GEMV_WAVES;
     const int a = slot * SB + wave * W;                 // first k-slice of this wave
-    const int nchunks = W / 8;
-    const int tiles_n = n / 16;
+    const int nchunks = WS < 8 ? 1 : W / 8;
+    constexpr int per = WS;                             // slices per input chunk
+    const int lane0 = WS < 8 ? (a & 7) * 8 : 0;         // x lanes of the first slice
+    const int tiles_n = v.stride / 16;
     const size_t rstride = (size_t) tiles_n * 8 * K;    // u32 per k-slice row
-    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
+    const uint32_t* base = (const uint32_t*) v.trellis + (size_t) lane * K
                          + ((size_t) a * tiles_n + chunk * 8) * (8 * K);
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
-    const bool has_suh = suh != nullptr;
-    const uint32_t* xg = (const uint32_t*) A + lane;                       // x pairs
-    const uint32_t* sg = (const uint32_t*) (has_suh ? suh : A) + lane;     // suh pairs
+    const bool has_suh = v.suh != nullptr;
+    const uint32_t* xg = (const uint32_t*) v.A + lane;                       // x pairs
+    const uint32_t* sg = (const uint32_t*) (has_suh ? v.suh : v.A) + lane;   // suh pairs
 
     constexpr int PF = EXL3_GEMV_PF;
     static_assert(8 % PF == 0, "prefetch depth must divide 8");
     const int last = W - 1;
     // x of the first chunk first (its wait then leaves the weight loads in flight)
-    uint32_t xv = __builtin_nontemporal_load(xg + (size_t) (a / 8) * 64);
-    uint32_t sv = __builtin_nontemporal_load(sg + (size_t) (a / 8) * 64);
+    uint32_t xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8) * 64);
+    uint32_t sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8) * 64);
     uint32_t ring[PF][K + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last) * rstride, prev_off, ring[d]);
+    // svh pair for the epilogue, behind the first weights
+    // (unconditional load: without svh it reads the input, k >= 128, and is unused)
+    const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
 
     float acc0 = 0.0f, acc1 = 0.0f, sx = 0.0f;
     for (int c = 0; c < nchunks; ++c)
     {
         const uint32_t xr = rotate_pair(xv, sv, has_suh, lane);
+        if (c == 0) GEMV_STAMP(g, 1, __builtin_amdgcn_readfirstlane(xr));
         if (CB == 2)
         {
             const f16x2 p = as_h2(xr);
-            sx += wave_sum((float) p.x + (float) p.y, lane);
+            const bool mine = WS == 8 || (lane >= lane0 && lane < lane0 + 8 * per);
+            sx += wave_sum(mine ? (float) p.x + (float) p.y : 0.0f, lane);
         }
         // prefetch the next chunk's x (clamped: stays inside this wave's range)
         const int cn = min(c + 1, nchunks - 1);
-        xv = __builtin_nontemporal_load(xg + (size_t) (a / 8 + cn) * 64);
-        sv = __builtin_nontemporal_load(sg + (size_t) (a / 8 + cn) * 64);
+        xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8 + cn) * 64);
+        sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8 + cn) * 64);
         #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8)
+        for (int s8 = 0; s8 < per; ++s8)
         {
             const int i = c * 8 + s8;
             const int d = s8 % PF;
@@ -500,122 +814,85 @@ void gemv1_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ t
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
             load_slot<K>(base + (size_t) min(i + PF, last) * rstride, prev_off, ring[d]);
-            // this slice's 16 inputs: lanes 8 s8 .. 8 s8 + 7 hold pairs (x[2q], x[2q+1])
+            // this slice's 16 inputs: lanes lane0 + 8 s8 .. + 7 hold pairs (x[2q], x[2q+1])
             uint32_t x16[16];
             #pragma unroll
             for (int q = 0; q < 8; ++q)
             {
-                const uint32_t p = __builtin_amdgcn_readlane(xr, 8 * s8 + q);
+                const uint32_t p = __builtin_amdgcn_readlane(xr, lane0 + 8 * s8 + q);
                 x16[2 * q] = (p & 0xffffu) | (p << 16);
                 x16[2 * q + 1] = (p >> 16) | (p & 0xffff0000u);
             }
             #pragma unroll
             for (int w = 0; w < 32; ++w)
             {
-                const int g = w >> 3, jj = w & 7;
-                const int row = 2 * g + (jj & 1) + 8 * ((jj >> 1) & 1);
+                const int gq = w >> 3, jj = w & 7;
+                const int row = 2 * gq + (jj & 1) + 8 * ((jj >> 1) & 1);
                 float& acc = (jj >> 2) ? acc1 : acc0;
                 acc = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc, false);
             }
         }
     }
 
+    GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(acc0 + acc1)));
     const int c0 = (lane >> 3) * 16 + (lane & 7);
     red[wave][c0] = acc0;
     red[wave][c0 + 8] = acc1;
     if (lane == 0) sumx_w[wave] = sx;
     __syncthreads();
-    if (wave == 0)
+    if (threadIdx.x < 128)
     {
-        const int c = 2 * lane;
-        float v0 = red[0][c] + red[1][c] + red[2][c] + red[3][c];
-        float v1 = red[0][c + 1] + red[1][c + 1] + red[2][c + 1] + red[3][c + 1];
+        const int c = threadIdx.x;
+        float vv = red[0][c] + red[1][c] + red[2][c] + red[3][c];
         if (CB == 2)
         {
             const float kinv = (float) as_h(0x1eee);
             const float bias = (sumx_w[0] + sumx_w[1] + sumx_w[2] + sumx_w[3]) * (float) as_h(0xc931);
-            v0 = v0 * kinv + bias;
-            v1 = v1 * kinv + bias;
+            vv = vv * kinv + bias;
         }
-        if (splits == 1)
-        {
-            const int col = chunk * 128 + c;
-            store_output(v0, v1, C, c_fp32, svh, (size_t) col, col, lane);
-        }
-        else
-        {
-            float2 pv = { v0, v1 };
-            float* pp = partials + ((size_t) chunk * splits + slot) * 128 + c;
-            *(float2*) pp = pv;
-            if (xcd > 0)
-            {
-                // release the partial (stores complete in the shared L2), count this split in
-                // the chunk's L2 counter (own 128-byte line); the last arrival sums in slot order
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                int prev = 0;
-                if (lane == 0)
-                    prev = __hip_atomic_fetch_add(counters + chunk * 32, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                prev = __builtin_amdgcn_readfirstlane(prev);
-                if (prev == splits - 1)
-                {
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                    if (lane == 0)
-                        __hip_atomic_store(counters + chunk * 32, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    const float* p0 = partials + (size_t) chunk * splits * 128 + c;
-                    float s0 = 0.0f, s1 = 0.0f;
-                    for (int sp0 = 0; sp0 < splits; sp0 += 8)
-                    {
-                        f32x2 v[8];
-                        #pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                        {
-                            // device-scope load: misses this CU's L1, reads the XCD's L2
-                            const uint64_t* q = (const uint64_t*) (p0 + (size_t) min(sp0 + j, splits - 1) * 128);
-                            const uint64_t u = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            v[j] = __builtin_bit_cast(f32x2, u);
-                        }
-                        #pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            if (sp0 + j < splits) { s0 += v[j].x; s1 += v[j].y; }
-                    }
-                    const int col = chunk * 128 + c;
-                    store_output(s0, s1, C, c_fp32, svh, (size_t) col, col, lane);
-                }
-            }
-        }
+        res[c] = vv;
     }
+    __syncthreads();
+    block_epilogue(g, v, j, chunk, slot, splits, res, tmp, &flag, svp);
+    GEMV_STAMP(g, 3, flag);
+}
+
+template <typename KernelLaunch>
+int launch_common(const GemvArgs& g, hipStream_t s, KernelLaunch main)
+{
+    const int KS = g.k / 16;
+    const int splits = KS / g.slices_per_block;
+    const int chunks = g.n / 128;
+    main(dim3(splits * chunks, g.bszm));
+    if (!g.xcd)
+    {
+        if (splits > 1)
+            hipLaunchKernelGGL(gemv_finish, dim3(chunks, g.bszm), dim3(GEMV_THREADS), 0, s, g, splits);
+        if (g.weights)
+            hipLaunchKernelGGL(gemv_weighted_reduce, dim3(chunks), dim3(GEMV_THREADS), 0, s, g);
+    }
+    return (int) hipGetLastError();
 }
 
 template <int K, int CB, int MT>
 int launch_gemv_t(const GemvArgs& g, hipStream_t s)
 {
-    const int KS = g.k / 16;
-    const int SB = g.slices_per_block;
-    const int splits = KS / SB;
-    const int blocks = splits * (g.n / 128);
     const size_t lds = (size_t) MT * g.xs_chunks * 128 * 4 + (size_t) GEMV_WAVES * MT * 128 * 4;
-    hipLaunchKernelGGL((gemv_kernel<K, CB, MT>), dim3(blocks), dim3(GEMV_THREADS), lds, s,
-                       g.A, g.trellis, g.C, g.suh, g.svh, g.m, g.k, g.n, g.c_fp32, SB, g.xs_chunks,
-                       g.partials);
-    if (splits > 1)
-        hipLaunchKernelGGL(gemv_finish, dim3(g.n / 128), dim3(GEMV_THREADS), 0, s,
-                           g.partials, g.C, g.svh, g.m, g.n, splits, g.c_fp32);
-    return (int) hipGetLastError();
+    return launch_common(g, s, [&](dim3 grid) {
+        hipLaunchKernelGGL((gemv_kernel<K, CB, MT>), grid, dim3(GEMV_THREADS), lds, s, g);
+    });
 }
 
 template <int K, int CB>
 int launch_gemv1(const GemvArgs& g, hipStream_t s)
 {
-    const int KS = g.k / 16;
-    const int SB = g.slices_per_block;
-    const int splits = KS / SB;
-    hipLaunchKernelGGL((gemv1_kernel<K, CB>), dim3(splits * (g.n / 128)), dim3(GEMV_THREADS), 0, s,
-                       g.A, g.trellis, g.C, g.suh, g.svh, g.k, g.n, g.c_fp32, SB, g.partials,
-                       g.counters, g.xcd);
-    if (splits > 1 && g.xcd == 0)
-        hipLaunchKernelGGL(gemv_finish, dim3(g.n / 128), dim3(GEMV_THREADS), 0, s,
-                           g.partials, g.C, g.svh, 1, g.n, splits, g.c_fp32);
-    return (int) hipGetLastError();
+    const int W = g.slices_per_block / GEMV_WAVES;
+    return launch_common(g, s, [&](dim3 grid) {
+        if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8>), grid, dim3(GEMV_THREADS), 0, s, g);
+    });
 }
 
 template <int K, int CB>

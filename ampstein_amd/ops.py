@@ -186,6 +186,76 @@ def exl3_gemm(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], A_had: Opt
             int(force_shape_idx), _stream(A)))
 
 
+def exl3_mgemm(A: Tensor, B: Tensor, C: Tensor, suh: Tensor, A_had: Tensor, svh: Tensor,
+               indices: Optional[Tensor], weights: Optional[Tensor], K: float,
+               force_shape_idx: int = -1, mcg: int = 0, mul1: int = 0, min_index: int = -1,
+               max_index: int = -1, force_num_sms: int = 0, num_tokens: int = 1,
+               size_n_list: Optional[Tensor] = None, c_ptrs: Optional[Tensor] = None,
+               n_stride_list: Optional[Tensor] = None, had_src_list: Optional[Tensor] = None,
+               num_had_src: int = 0) -> int:
+    """Multi-matrix EXL3 matmul over device pointer tables (exl3_gemm.cu:352-394 semantics).
+    A (bszm_in, m, k) fp16; B / suh / svh int64 tensors of device addresses; C (bszm_out, m, n)
+    fp16 or fp32; indices / weights (.., num_indices) int64 / fp16; optional int32 lists and
+    int64 c_ptrs for per-matrix widths and sliced mode.  Returns the kernel tag."""
+    _dtype(A, torch.half, "A")
+    for t, name in ((B, "B"), (suh, "suh"), (svh, "svh")):
+        _dtype(t, torch.long, name)
+        _need(t.dim() == 1, f"{name} must be 1-dimensional")
+    _need(A.dim() == 3 and C.dim() == 3, "A and C must be 3-dimensional")
+    _need(A.size(1) == C.size(1), "A and C shapes are incompatible")
+    _need(C.dtype in (torch.half, torch.float), "C is incorrect datatype, must be half or float")
+    _cuda(A, B, C, suh, svh, A_had, indices, weights, size_n_list, c_ptrs, n_stride_list, had_src_list)
+    num_indices = 0
+    if indices is not None:
+        _dtype(indices, torch.long, "indices")
+        _need(indices.dim() == 2, "indices must be 2-dimensional")
+        num_indices = indices.size(1)
+    if weights is not None:
+        _dtype(weights, torch.half, "weights")
+        _need(weights.dim() == 2, "weights must be 2-dimensional")
+    for t, name, dt in ((size_n_list, "size_n_list", torch.int32), (c_ptrs, "c_ptrs", torch.long),
+                        (n_stride_list, "n_stride_list", torch.int32), (had_src_list, "had_src_list", torch.int32)):
+        if t is not None:
+            _dtype(t, dt, name)
+    with torch.cuda.device(A.device):
+        return check(_lib.lib().exl3_amd_mgemm(
+            A.data_ptr(), A.size(0), A.size(1), A.size(2),
+            B.data_ptr(), B.size(0),
+            C.data_ptr(), C.size(0), C.size(2), int(C.dtype == torch.float),
+            suh.data_ptr(), suh.size(0),
+            _ptr(A_had), A_had.numel() if A_had is not None else 0,
+            svh.data_ptr(), svh.size(0),
+            _ptr(indices), num_indices, _ptr(weights),
+            float(K), int(force_shape_idx), int(bool(mcg)), int(bool(mul1)),
+            int(min_index), int(max_index), int(force_num_sms), int(num_tokens),
+            _ptr(size_n_list), _ptr(c_ptrs), c_ptrs.size(0) if c_ptrs is not None else 0,
+            _ptr(n_stride_list), n_stride_list.size(0) if n_stride_list is not None else 0,
+            _ptr(had_src_list), had_src_list.size(0) if had_src_list is not None else 0, int(num_had_src),
+            _stream(A)))
+
+
+def mgemm(x: Tensor, B_ptrs: Tensor, C: Tensor, suh_ptrs: Tensor, A_had: Tensor, svh_ptrs: Tensor,
+          K: float, mcg: bool, mul1: bool, opts: Optional[dict] = None) -> Tensor:
+    """torch.mgemm of the engine (amp_torch.cpp:10194-10330): stacked bundle (x broadcast,
+    C (num, m, n)) or, with opts {size_n_list, c_ptrs, n_stride_list, had_src_list,
+    num_had_src}, sliced mode.  Returns C."""
+    o = opts or {}
+    if opts is not None:
+        for key in ("size_n_list", "c_ptrs", "n_stride_list", "had_src_list"):
+            _need(o.get(key) is not None, f"mgemm: opts.{key} missing")
+        _need(isinstance(o.get("num_had_src"), int), "mgemm: num_had_src missing")
+    exl3_mgemm(x, B_ptrs, C, suh_ptrs, A_had, svh_ptrs, None, None, K, -1, int(mcg), int(mul1),
+               -1, -1, 0, 1, o.get("size_n_list"), o.get("c_ptrs"), o.get("n_stride_list"),
+               o.get("had_src_list"), int(o.get("num_had_src", 0)))
+    return C
+
+
+def ptr_array(tensors, device=None) -> Tensor:
+    """int64 device tensor of data pointers (amp_torch.cpp:10333, torch.ptr_array)."""
+    vals = [t if isinstance(t, int) else t.data_ptr() for t in tensors]
+    return torch.tensor(vals, dtype=torch.long, device=device if device is not None else "cuda")
+
+
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
                     mul1: bool = False, mcg: bool = False) -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to

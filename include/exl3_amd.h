@@ -77,13 +77,46 @@ int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
  * NULL (that rotation is skipped).  A_had: caller scratch of A's shape, accepted for interface
  * parity and not written (the rotation is recomputed per workgroup).  k % 128 == 0 and
  * n % 128 == 0 when a rotation is requested, else k % 16 and n % 128.  Returns a kernel tag.
- * force_shape_idx > 0 forces a kernel (1 = GEMV, 2 = MFMA GEMM); 0 = by shape.
+ * force_shape_idx > 0 forces a kernel (1 = GEMV, 2 = MFMA GEMM); <= 0 = by shape.
  * Replaces exl3_gemm (vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:321-350, dispatcher
  * :114-319), bound at src/torch/amp_torch.cpp:11251-11294 (torch.exl3_gemm). */
 int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
                   const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
                   int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
                   void* stream);
+
+/* Multi-matrix GEMV over device pointer tables: slot j (0 <= j < max(bszm_in, bszm_out))
+ * computes C[j] = had(had(A[j or 0] o suh[q]) @ W_hat[q]) o svh[q] with q = indices[j] (or j;
+ * negative = slot skipped).  Tables B, suh, svh hold num_B device addresses (uint64) of
+ * trellis (k/16, n/16, 16K) uint16, suh (k) fp16 and svh (n) fp16.  A (bszm_in, m, k) fp16;
+ * C (bszm_out, m, n) fp16 / fp32.
+ *   weights (fp16 per slot): every output is scaled by its weight, then the slots of each of
+ *     num_tokens groups (bszm / num_tokens consecutive slots) are summed into C[t].
+ *   min_index >= 0: selections outside [min_index, max_index) dropped (one token: compacted,
+ *     several: masked), kept ones rebased by min_index (at most 128 slots).
+ *   size_n_list + c_ptrs (num_c_ptrs entries): per-matrix width and output address.
+ *   sliced mode (had_src_list, n_stride_list, num_had_src): entries are equal-width column
+ *     slices of num_had_src source matrices; B / svh / c_ptrs pre-offset to the slice, the row
+ *     stride of trellis tiles and C is n_stride_list[q], suh is per source had_src_list[q].
+ * All tables and lists are device memory.  A_had: scratch of had_slabs * m * k elements
+ * (checked, not written).  m <= 8; k % 128 == 0; n % 128 == 0.
+ * Replaces exl3_mgemm (vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:396-712, semantics
+ * :352-394, kernel exl3_gemm_kernel.cuh:88-343), declared at src/torch/amp_torch.cpp:3841-3864
+ * and bound at :10194-10330 (torch.mgemm). */
+int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
+                   const uint64_t* B, int num_B,
+                   void* C, int bszm_out, int n, int c_fp32,
+                   const uint64_t* suh, int num_suh,
+                   uint16_t* A_had, int64_t a_had_numel,
+                   const uint64_t* svh, int num_svh,
+                   const int64_t* indices, int num_indices,
+                   const uint16_t* weights,
+                   float K, int force_shape_idx, int mcg, int mul1,
+                   int min_index, int max_index, int force_num_sms, int num_tokens,
+                   const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
+                   const int* n_stride_list, int num_n_stride,
+                   const int* had_src_list, int num_had_src_list, int num_had_src,
+                   void* stream);
 
 #ifdef __cplusplus
 }

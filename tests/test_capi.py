@@ -108,3 +108,44 @@ def test_python_ops_raise_like_torch_check():
         ops.exl3_gemm(torch.empty((1, 64), dtype=torch.half), T, torch.empty((1, 128), dtype=torch.half), None, None, None)
     with pytest.raises(_lib.Exl3Error, match="128"):
         ops.had_r_128(torch.empty((2, 100), dtype=torch.half), torch.empty((2, 100), dtype=torch.half))
+
+
+def mgemm_args(**kw):
+    f = ctypes.c_float
+    order = (("A", 1), ("bszm_in", 1), ("m", 1), ("k", 256), ("B", 1), ("num_B", 2), ("C", 1),
+             ("bszm_out", 2), ("n", 256), ("fp32", 0), ("suh", 1), ("num_suh", 2), ("ahad", 1),
+             ("ahad_n", 1 << 20), ("svh", 1), ("num_svh", 2), ("idx", None), ("num_idx", 0),
+             ("w", None), ("K", f(4.0)), ("force", -1), ("mcg", 0), ("mul1", 0), ("min", -1),
+             ("max", -1), ("sms", 0), ("tokens", 1), ("size_n", None), ("c_ptrs", None),
+             ("num_c", 0), ("stride", None), ("num_stride", 0), ("src", None), ("num_src", 0),
+             ("nsrc", 0), ("stream", None))
+    return [kw.get(name, d) for name, d in order]
+
+
+def test_mgemm_rejects_bad_arguments():
+    """The TORCH_CHECKs of exl3_mgemm_gr (quant/exl3_gemm.cu:424-542) as error codes."""
+    L = _lib.lib()
+    f = ctypes.c_float
+    cases = [
+        (dict(mcg=1, mul1=1), "both"),
+        (dict(num_suh=3), "same length"),
+        (dict(size_n=1), "requires c_ptrs"),
+        (dict(c_ptrs=1, size_n=1, num_c=2, w=1), "incompatible"),
+        (dict(src=1), "sliced mode requires"),
+        (dict(src=1, size_n=1, c_ptrs=1, num_c=2, stride=1, num_stride=2, num_src=2, nsrc=3), "one suh entry"),
+        (dict(src=1, size_n=1, c_ptrs=1, num_c=2, stride=1, num_stride=1, num_src=2, nsrc=1), "one entry per slice"),
+        (dict(stride=1), "n_stride_list requires"),
+        (dict(ahad_n=100), "A_had"),
+        (dict(idx=1, num_idx=3), "too many indices"),
+        (dict(n=200), "n must"),
+        (dict(min=0), "requires indices"),
+        (dict(tokens=0), "num_tokens"),
+        (dict(w=1, idx=1, num_idx=2, tokens=3), "token groups"),
+        (dict(K=f(2.5), mul1=0), "mul1"),
+        (dict(m=9), "not implemented"),
+    ]
+    for kw, text in cases:
+        rc, msg = call_err(L.exl3_amd_mgemm, *mgemm_args(**kw))
+        assert rc < 0 and text in msg, (kw, msg)
+    # nothing to do: empty batch rows
+    assert L.exl3_amd_mgemm(*mgemm_args(m=0)) == _lib.TAG_GEMV
