@@ -1,24 +1,35 @@
 """Benchmark of the EXL3 quantized-linear hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
 
 Workload: Llama-3-8B-shaped decode stack at 4.0 bpw, 3INST
 codebook, M = 1 fp16 activations ~ N(0, 1), random trellis words and +-1 suh / svh per layer;
-32 distinct layers x 7 linears (q, k, v, o, gate, up, down) = 3.49 GB of packed weights,
-far beyond the 256 MB Infinity Cache.  One step = one 32-layer sweep: 224 exl3_gemm calls
-(the decode GEMV) replayed from one HIP graph, as the reference replays its decode step.
+32 distinct layers x 7 linears (q, k, v, o, gate, up, down) = 3.49 GB of packed weights, far
+beyond the 256 MB Infinity Cache.  One step = one 32-layer sweep launched the way the
+engine's decode step launches it (graphdec.uc:168-196): q/k/v as ONE sliced exl3_mgemm,
+o as exl3_gemm, gate/up as ONE stacked exl3_mgemm, down as exl3_gemm -- 128 launches,
+replayed from one HIP graph.
 
-Prints one JSON line: value = packed-weight GB/s of the sweep, plus the roofline of the
-dominant kernel (the K = 4 GEMV; per-launch HIP-event durations), per-shape figures and the
-reference-style CPU path (host trellis reconstruct + Hadamard + ATen CPU matmul) timed on
-this host's cores over a bounded sample.
+Prints one JSON line: value = packed-weight GB/s of the sweep; roofline of the dominant
+kernel (the M = 1 GEMV as the stacked gate/up exl3_mgemm, half of the step's bytes: 32
+back-to-back launches in a graph, HIP events on the replay stream, algorithmic bytes / average
+launch time, inter-launch gaps included); traffic = HBM bytes per launch of that kernel from
+rocprofv3 FETCH_SIZE and WRITE_SIZE passes (child processes, each scaled by the same counter
+on a device copy of known size);
+per-shape figures with one exl3_gemm per linear; the reference-style CPU path (host trellis
+reconstruct + Hadamard + ATen CPU matmul) timed on this host's cores over a bounded sample.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -26,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "EXL3 GEMV GB/s (% HBM peak) at 4bpw M=1; prefill GEMM TFLOPS at M=2048"
+COPY_BYTES = 256 << 20
 
 
 def parse():
@@ -35,27 +47,161 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
     return ap.parse_args()
 
 
-def make_layers(torch, n_layers, K=4):
+# ------------------------------------------------------------------ workload
+def make_stack(torch, n_layers, K=4):
+    """Per layer: name -> bundles.Linear with GPU-generated random trellis words and signs."""
     from ampstein_amd.synth import LLAMA3_8B_SHAPES
+    from ampstein_amd.bundles import Linear
     g = torch.Generator(device="cuda")
     layers = []
     for li in range(n_layers):
-        row = []
+        row = {}
         for si, (name, k, n) in enumerate(LLAMA3_8B_SHAPES):
             g.manual_seed(2000 + 7 * li + si)
             t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16,
                               device="cuda", generator=g)
             s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
             v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
-            row.append((name, k, n, t, s, v))
+            row[name] = Linear(t, s, v, float(K))
         layers.append(row)
     return layers
 
 
+class Sweep:
+    """The decode-step launch sequence over all layers, bundled (engine schedule) or one
+    exl3_gemm per linear.  Each entry: (label, launch(stream_ptr), packed bytes)."""
+
+    def __init__(self, torch, layers, bundled):
+        from ampstein_amd import bundles, _lib
+        self.L = _lib.lib()
+        dev = "cuda"
+        self.x = torch.randn((1, 1, 4096), generator=torch.Generator(device=dev).manual_seed(1), device=dev).half()
+        self.x14 = torch.randn((1, 1, 14336), generator=torch.Generator(device=dev).manual_seed(2), device=dev).half()
+        self.outs = {nm: torch.empty((1, 1, n), dtype=torch.half, device=dev)
+                     for nm, n in (("q", 4096), ("k", 1024), ("v", 1024), ("o", 4096), ("down", 4096))}
+        self.gu = torch.empty((2, 1, 14336), dtype=torch.half, device=dev)
+        self.entries = []
+        for row in layers:
+            if bundled:
+                qkv = bundles.Sliced([row["q"], row["k"], row["v"]], [self.outs["q"], self.outs["k"], self.outs["v"]])
+                gu = bundles.Multi([row["gate"], row["up"]], self.gu)
+                nb = lambda *names: sum(row[n].trellis.numel() * 2 for n in names)
+                self.entries.append(("qkv", self._bundle(qkv), nb("q", "k", "v")))
+                self.entries.append(("o", self._gemm(row["o"], self.x, self.outs["o"]), nb("o")))
+                self.entries.append(("gate_up", self._bundle(gu), nb("gate", "up")))
+                self.entries.append(("down", self._gemm(row["down"], self.x14, self.outs["down"]), nb("down")))
+            else:
+                for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+                    xin = self.x14 if nm == "down" else self.x
+                    out = self.gu[0] if nm in ("gate", "up") else self.outs[nm]
+                    self.entries.append((nm, self._gemm(row[nm], xin, out), row[nm].trellis.numel() * 2))
+        self.bytes = sum(e[2] for e in self.entries)
+
+    def _gemm(self, lin, x, y):
+        L = self.L
+        k, n = lin.in_features, lin.out_features
+
+        def launch(st):
+            rc = L.exl3_amd_gemm(x.data_ptr(), lin.trellis.data_ptr(), y.data_ptr(), 0, lin.suh.data_ptr(), None,
+                                 lin.svh.data_ptr(), 1, k, n, float(lin.K), 0, 0, 0, st)
+            if rc < 0:
+                raise RuntimeError(L.exl3_amd_last_error().decode())
+        return launch
+
+    def _bundle(self, b):
+        def launch(st):
+            b.run(self.x)    # enqueued on torch's current stream, which the caller sets
+        return launch
+
+    def run(self, torch, stream):
+        with torch.cuda.stream(stream):
+            st = stream.cuda_stream
+            for _, fn, _ in self.entries:
+                fn(st)
+
+
+def event_times(torch, sweep, reps=3):
+    """Per-launch HIP-event durations (ms) on the launch stream; the first pass is dropped."""
+    stream = torch.cuda.Stream()
+    recs = []
+    with torch.cuda.stream(stream):
+        for rep in range(reps):
+            for label, fn, nbytes in sweep.entries:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                fn(stream.cuda_stream)
+                e1.record(stream)
+                recs.append((rep, label, nbytes, e0, e1))
+    torch.cuda.synchronize()
+    return [(label, nbytes, e0.elapsed_time(e1)) for rep, label, nbytes, e0, e1 in recs if rep > 0]
+
+
+def dominant_region(torch, layers, reps=3):
+    """The dominant launch of the sweep -- the stacked gate/up exl3_mgemm (58.7 MB, half the
+    step's bytes) -- as its own timed region: one launch per layer (distinct weights), captured
+    in a graph, HIP events around the replays on the replay stream.  Returns (avg us per launch,
+    bytes per launch, launches timed)."""
+    from ampstein_amd import bundles
+    gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
+    x = torch.randn((1, 1, 4096), device="cuda").half()
+    bs = [bundles.Multi([row["gate"], row["up"]], gu_out) for row in layers]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for b in bs:
+            b.run(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for b in bs:
+            b.run(x)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    n = reps * len(bs)
+    nbytes = layers[0]["gate"].trellis.numel() * 4
+    return e0.elapsed_time(e1) * 1e3 / n, nbytes, n
+
+
+def graph_time(torch, sweep, steps, warmup):
+    stream = torch.cuda.Stream()
+    sweep.run(torch, stream)                    # warm the path outside the graph
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _, fn, _ in sweep.entries:
+            fn(stream.cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+
+# ------------------------------------------------------------------ CPU baseline
 def cpu_baseline(seconds: float):
     """Reference CPU path on config 1 (4096 -> 4096, K = 4, 3INST): the oracle's host trellis
     reconstruct to fp16, Hadamard-128 on x (with suh) and on y (with svh), ATen CPU fp32
@@ -85,8 +231,7 @@ def cpu_baseline(seconds: float):
         t_had += (t2 - t1) + (t4 - t3)
         t_mm += t3 - t2
         calls += 1
-    total = t_rec + t_had + t_mm
-    us = total / calls * 1e6
+    us = (t_rec + t_had + t_mm) / calls * 1e6
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -107,100 +252,138 @@ def cpu_baseline(seconds: float):
     }
 
 
+# ------------------------------------------------------------------ HBM traffic (rocprofv3)
+GEMV_KERNEL = "gemv1_kernel"
+
+
+def pmc_child():
+    """Profiled child: a device copy of known size, then two eager bundled sweeps (4 layers)."""
+    import torch
+    from ampstein_amd import ops
+    torch.cuda.set_device(0)
+    ops.init(0)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    from ampstein_amd import bundles
+    layers = make_stack(torch, 4)
+    gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
+    x = torch.randn((1, 1, 4096), device="cuda").half()
+    for _ in range(2):
+        for row in layers:
+            bundles.Multi([row["gate"], row["up"]], gu_out).run(x)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_rows(outdir, counter):
+    rows = []
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+    return rows
+
+
+def measure_traffic(gemv_alg_bytes_per_launch):
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the GEMV launches, each scaled by the
+    same counter's reading on a copy of COPY_BYTES.  Returns the traffic object or None."""
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None
+    res = {}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        outdir = tempfile.mkdtemp(prefix=f"exl3_{counter}_", dir="/tmp")
+        cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", counter, "--output-format", "csv", "-d", outdir,
+               "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
+        p = subprocess.run(cmd, capture_output=True, text=True, env=env, cwd="/tmp")
+        if p.returncode != 0:
+            return {"error": f"rocprofv3 {counter} pass failed (rc {p.returncode})"}
+        rows = _counter_rows(outdir, counter)
+        copy = [v for name, v in rows if "copy" in name.lower()]
+        gemv = [v for name, v in rows if GEMV_KERNEL in name]
+        shutil.rmtree(outdir, ignore_errors=True)
+        if not copy or not gemv:
+            return {"error": f"{counter}: no copy or GEMV dispatches in the profile"}
+        scale = COPY_BYTES / (max(copy) * 1024.0)
+        res[counter] = (sum(gemv) / len(gemv) * 1024.0 * scale, scale, len(gemv))
+    fetch, fscale, n = res["FETCH_SIZE"]
+    write, wscale, _ = res["WRITE_SIZE"]
+    return {"bytes_per_launch": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
+            "copy_scale": {"FETCH_SIZE": round(fscale, 4), "WRITE_SIZE": round(wscale, 4)},
+            "dispatches": n, "algorithmic_bytes_per_launch": round(gemv_alg_bytes_per_launch),
+            "ratio_to_algorithmic": round((fetch + write) / gemv_alg_bytes_per_launch, 4)}
+
+
+# ------------------------------------------------------------------ main
+def summarize_trace(path):
+    """Per (kernel, grid) average durations of a rocprofv3 --kernel-trace csv (this library's
+    kernels only): the figures the roofline's avg_launch_us is checked against."""
+    stats = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if "gemv" not in name and "reconstruct" not in name and "had128" not in name and "gemm" not in name:
+                continue
+            grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
+            d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            stats.setdefault((name, grid), []).append(d)
+    print(f"{'kernel':60s} {'grid (threads x, y)':>22s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}")
+    for (name, grid), ds in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{name[:60]:60s} {str(grid):>22s} {len(ds):6d} {sum(ds) / len(ds) / 1e3:9.2f} "
+              f"{min(ds) / 1e3:9.2f} {max(ds) / 1e3:9.2f}")
+    return 0
+
+
 def main():
     args = parse()
+    if args.summarize_trace:
+        return summarize_trace(args.summarize_trace)
+    if args.pmc_child:
+        return pmc_child()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the EXL3 path runs on a single MI355X; see DESIGN.md for how it would shard)")
+              "(the EXL3 path runs on a single MI355X; a multi-GPU split is design-only in this build)")
         return 2
-    import torch
-    from ampstein_amd import ops, _lib
 
+    # the profiled child launches the stacked gate/up mgemm: 2 x 4096 x 14336 weights at 4 bits
+    alg_per_launch = 2 * 4096 * 14336 / 2
+    traffic = None if args.no_traffic else measure_traffic(alg_per_launch)
+
+    import torch
+    from ampstein_amd import ops
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     ops.init(0)
-    L = _lib.lib()
-    layers = make_layers(torch, args.layers)
-    x4096 = torch.randn((1, 4096), generator=torch.Generator(device="cuda").manual_seed(1),
-                        device="cuda").half()
-    x14336 = torch.randn((1, 14336), generator=torch.Generator(device="cuda").manual_seed(2),
-                         device="cuda").half()
-    outs = {n: torch.empty((1, n), dtype=torch.half, device="cuda") for n in (1024, 4096, 14336)}
-    stream = torch.cuda.current_stream()
+    layers = make_stack(torch, args.layers)
+    bundled = Sweep(torch, layers, bundled=True)
+    separate = Sweep(torch, layers, bundled=False)
 
-    calls = []
-    for row in layers:
-        for name, k, n, t, s, v in row:
-            x = x14336 if k == 14336 else x4096
-            calls.append((name, k, n, x, t, s, v, outs[n]))
-    bytes_per_step = sum(c[4].numel() * 2 for c in calls)
+    # launch durations (HIP events on the launch stream)
+    ev_b = event_times(torch, bundled)
+    ev_s = event_times(torch, separate)
+    dom_us, dom_bytes, dom_n = dominant_region(torch, layers)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
 
-    def launch(c, st):
-        name, k, n, x, t, s, v, y = c
-        rc = L.exl3_amd_gemm(x.data_ptr(), t.data_ptr(), y.data_ptr(), 0, s.data_ptr(), None,
-                             v.data_ptr(), 1, k, n, 4.0, 0, 0, 0, st)
-        if rc < 0:
-            raise RuntimeError(L.exl3_amd_last_error().decode())
+    def per_label(ev):
+        out = {}
+        for label, nbytes, ms in ev:
+            d = out.setdefault(label, [nbytes, []])
+            d[1].append(ms)
+        res = {}
+        for label, (nbytes, mss) in out.items():
+            us = sum(mss) / len(mss) * 1e3
+            res[label] = {"bytes": nbytes, "us": round(us, 2), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                          "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        return res
 
-    # per-launch kernel durations (HIP events on the launch stream), one eager sweep x 3
-    per_shape = {}
-    evs = []
-    for rep in range(3):
-        for c in calls:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            launch(c, stream.cuda_stream)
-            e1.record(stream)
-            evs.append((c, e0, e1, rep))
-    torch.cuda.synchronize()
-    tot_ms = 0.0
-    nmeas = 0
-    for c, e0, e1, rep in evs:
-        if rep == 0:
-            continue   # first pass: cold code / first-touch
-        ms = e0.elapsed_time(e1)
-        d = per_shape.setdefault(c[0], {"k": c[1], "n": c[2], "bytes": c[4].numel() * 2, "ms": []})
-        d["ms"].append(ms)
-        tot_ms += ms
-        nmeas += 1
-    avg_launch_us = tot_ms / nmeas * 1e3
-    avg_bytes = bytes_per_step / len(calls)
+    ms_step, wall = graph_time(torch, bundled, args.steps, args.warmup)
+    value = bundled.bytes / (ms_step * 1e-3) / 1e9
+    ms_sep, _ = graph_time(torch, separate, max(5, args.steps // 5), 2)
 
-    # graph of the whole sweep
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        for c in calls:            # warm the captured path once outside the graph
-            launch(c, cap.cuda_stream)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=cap):
-            for c in calls:
-                launch(c, cap.cuda_stream)
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
-    value = bytes_per_step / (ms_step * 1e-3) / 1e9
-
-    shapes = {}
-    for name, d in per_shape.items():
-        us = sum(d["ms"]) / len(d["ms"]) * 1e3
-        shapes[name] = {"k": d["k"], "n": d["n"], "us": round(us, 2),
-                        "GB_s": round(d["bytes"] / (us * 1e-6) / 1e9, 1),
-                        "frac_hbm": round(d["bytes"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    achieved = avg_bytes / (avg_launch_us * 1e-6) / 1e9
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -214,15 +397,24 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (seeded random trellis words, +-1 suh/svh, N(0,1) fp16 x)",
-        "config": {"workload": "llama3-8b-decode-sweep", "layers": args.layers, "bpw": 4,
-                   "codebook": "3inst", "m": 1, "calls_per_step": len(calls),
-                   "packed_bytes_per_step": bytes_per_step, "launch": "hip-graph replay"},
+        "config": {"workload": "llama3-8b-decode-sweep (configs[1])", "layers": args.layers, "bpw": 4,
+                   "codebook": "3inst", "m": 1, "launches_per_step": len(bundled.entries),
+                   "schedule": "qkv sliced mgemm, o gemm, gate/up stacked mgemm, down gemm",
+                   "packed_bytes_per_step": bundled.bytes, "launch": "hip-graph replay"},
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<K=4,3INST,M=1>",
+        "roofline": {"bound": "hbm",
+                     "kernel": "gemv1_kernel<4,0,8> as the stacked gate/up exl3_mgemm (2 x 4096x14336, grid 896x2)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(avg_launch_us, 3), "algorithmic_bytes_per_launch": round(avg_bytes)},
-        "per_shape": shapes,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_launch"] if traffic and "bytes_per_launch" in traffic else None,
+                     "avg_launch_us": round(dom_us, 3), "algorithmic_bytes_per_launch": dom_bytes,
+                     "launches_timed": dom_n},
+        "traffic_detail": traffic,
+        "per_launch_bundled": per_label(ev_b),
+        "per_shape": per_label(ev_s),
+        "sweep_separate_gemm": {"ms_per_step": round(ms_sep, 4),
+                                "GB_s": round(separate.bytes / (ms_sep * 1e-3) / 1e9, 1),
+                                "launches_per_step": len(separate.entries)},
         "wall_s": round(wall, 3),
     }
     if not args.no_cpu:
