@@ -43,6 +43,7 @@ def units():
     ]
     for k in range(1, 9):
         u.append(("exl3_gemv.hip", f"exl3_gemv_k{k}.o", [f"-DEXL3_INST_K={k}"]))
+        u.append(("exl3_gemm.hip", f"exl3_gemm_k{k}.o", [f"-DEXL3_INST_K={k}"]))
     return u
 
 

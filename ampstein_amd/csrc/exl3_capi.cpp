@@ -223,6 +223,22 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     return rc ? hip_fail(rc, what) : 0;
 }
 
+int dispatch_gemm(int bits, int cb, const GemmArgs& g, hipStream_t s)
+{
+    switch (bits)
+    {
+        case 1: return exl3k_gemm_k1(g, cb, s);
+        case 2: return exl3k_gemm_k2(g, cb, s);
+        case 3: return exl3k_gemm_k3(g, cb, s);
+        case 4: return exl3k_gemm_k4(g, cb, s);
+        case 5: return exl3k_gemm_k5(g, cb, s);
+        case 6: return exl3k_gemm_k6(g, cb, s);
+        case 7: return exl3k_gemm_k7(g, cb, s);
+        case 8: return exl3k_gemm_k8(g, cb, s);
+    }
+    return -1;
+}
+
 int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s)
 {
     switch (bits)
@@ -331,13 +347,27 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     if (int rc = current_device(&d)) return rc;
     hipStream_t s = (hipStream_t) stream;
 
-    if (m <= 8 && force_shape_idx != 2)
+    if ((m <= 8 && force_shape_idx != 2) || force_shape_idx == 1)
     {
+        if (m > 8) return fail(EXL3_AMD_EINVAL, "exl3_gemm: the GEMV kernel takes at most 8 rows");
         GemvArgs g = gemv_args_single(A, trellis, C, c_fp32, suh, svh, m, k, n);
         int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm");
         return rc ? rc : EXL3_AMD_TAG_GEMV;
     }
-    return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: m > 8 (MFMA GEMM) is not implemented in this build");
+    // MFMA GEMM: input rotation into the caller's A_had (exl3_gemm_kernel.cuh writes it there
+    // too), then the tiled kernel
+    if (suh && !A_had) return fail(EXL3_AMD_EINVAL, "exl3_gemm: must supply A_had with suh");
+    if (suh)
+    {
+        int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
+        if (rc) return hip_fail(rc, "exl3_gemm");
+    }
+    GemmArgs gg;
+    gg.A_rot = suh ? A_had : A;
+    gg.trellis = trellis; gg.C = C; gg.svh = svh;
+    gg.m = m; gg.k = k; gg.n = n; gg.c_fp32 = c_fp32 ? 1 : 0;
+    int rc = dispatch_gemm(bits, cb, gg, s);
+    return rc ? hip_fail(rc, "exl3_gemm") : EXL3_AMD_TAG_GEMM;
 }
 
 int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,

@@ -43,6 +43,26 @@ struct GemvArgs
     uint64_t* trace;            // instrumented builds only (EXL3_GEMV_TRACE): per-wave timestamps
 };
 
+// Prefill GEMM (m > 8) over the rotated input.
+struct GemmArgs
+{
+    const uint16_t* A_rot;      // (m, k) fp16: had(A o suh) (the caller's A_had) or A itself
+    const uint16_t* trellis;    // (k/16, n/16, 16K) uint16
+    void* C;                    // (m, n) fp16 or fp32
+    const uint16_t* svh;        // (n) fp16 or null
+    int m, k, n;
+    int c_fp32;
+};
+
+int exl3k_gemm_k1(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k2(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k3(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k4(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k5(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k6(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k7(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k8(const GemmArgs& g, int cb, hipStream_t s);
+
 int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
                       int nt_off, int K, int cb, hipStream_t s);
 int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,

@@ -1,0 +1,96 @@
+"""GPU parity of the MFMA prefill GEMM (exl3_amd_gemm with m > 8, exl3_gemm_kernel semantics:
+the output Hadamard reads fp32 sums) against the CPU oracle's fp64 linear.
+
+Bar: max|y - ref| / max|ref| < 2e-3.  Covers every K and codebook, ragged row counts (row
+blocks of 256 with a partial last block), column-chunk counts that do and do not take the
+XCD-grouped tile order, fp16 / fp32 outputs, and the optional rotations.  A_had must hold the
+rotated input afterwards, bit-exact with had_r_128(A, pre=suh).
+"""
+import numpy as np
+import pytest
+
+from ampstein_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from ampstein_amd import ops
+    ops.init(0)
+    return torch
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def run_gemm(torch, L, x, y_fp32, suh=True, svh=True):
+    from ampstein_amd import ops
+    t, s, v = L.torch()
+    A = torch.from_numpy(x).cuda()
+    A_had = torch.empty_like(A)
+    C = torch.empty((x.shape[0], L.n), dtype=torch.float if y_fp32 else torch.half, device="cuda")
+    tag = ops.exl3_gemm(A, t, C, s if suh else None, A_had, v if svh else None, 0, L.cb == 1, L.cb == 2)
+    return tag, C.cpu().numpy(), A_had.cpu().numpy()
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+@pytest.mark.parametrize("K", list(range(1, 9)))
+def test_gemm_parity_all_bitrates(torch_cuda, orc, K, cb):
+    torch = torch_cuda
+    L = synth.layer(256, 256, K, cb, seed=500 + 10 * K + cb)
+    x = synth.activations(40, 256, seed=K + 3 * cb)
+    tag, y, _ = run_gemm(torch, L, x, False)
+    assert tag == 91
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, K, cb=cb)
+    assert rel_err(y, ref) < TOL
+
+
+@pytest.mark.parametrize("m,k,n", [(9, 128, 128), (256, 512, 1024), (300, 256, 384), (513, 1024, 1024)])
+@pytest.mark.parametrize("y_fp32", [False, True])
+def test_gemm_shapes(torch_cuda, orc, m, k, n, y_fp32):
+    torch = torch_cuda
+    L = synth.layer(k, n, 4, 0, seed=600 + m + k + n)
+    x = synth.activations(m, k, seed=m)
+    tag, y, A_had = run_gemm(torch, L, x, y_fp32)
+    assert tag == 91
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4, cb=0)
+    assert rel_err(y, ref) < TOL
+    assert np.array_equal(A_had.view(np.uint16), orc.had128(x, pre=L.suh).view(np.uint16))
+
+
+@pytest.mark.parametrize("suh,svh", [(False, False), (True, False), (False, True)])
+def test_gemm_optional_rotations(torch_cuda, orc, suh, svh):
+    torch = torch_cuda
+    L = synth.layer(256, 256, 3, 1, seed=77)
+    x = synth.activations(64, 256, seed=77)
+    _, y, _ = run_gemm(torch, L, x, True, suh, svh)
+    ref = orc.linear(x, L.trellis, L.suh if suh else None, L.svh if svh else None, 3, cb=1, y_fp32=True)
+    assert rel_err(y, ref) < TOL
+
+
+def test_gemm_forced_kernel_and_rows(torch_cuda, orc):
+    """force_shape_idx 2 runs the MFMA kernel for m <= 8; 1 forces the GEMV (m <= 8 only)."""
+    torch = torch_cuda
+    from ampstein_amd import ops, _lib
+    L = synth.layer(256, 128, 4, 0, seed=88)
+    x = synth.activations(5, 256, seed=88)
+    t, s, v = L.torch()
+    A = torch.from_numpy(x).cuda()
+    C = torch.empty((5, 128), dtype=torch.float, device="cuda")
+    assert ops.exl3_gemm(A, t, C, s, torch.empty_like(A), v, 2) == 91
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4, cb=0)
+    assert rel_err(C.cpu().numpy(), ref) < TOL
+    A9 = torch.zeros((9, 256), dtype=torch.half, device="cuda")
+    with pytest.raises(_lib.Exl3Error, match="at most 8"):
+        ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, torch.empty_like(A9), v, 1)
+    with pytest.raises(_lib.Exl3Error, match="A_had"):
+        ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, None, v)
