@@ -1,26 +1,26 @@
 // Prefill-shaped EXL3 GEMM for gfx950 (m > 8): C = had(A_had @ W_hat) o svh with fp16 MFMA
 // and fp32 accumulation.  Semantics of exl3_gemm_kernel / exl3_gemm_kernel_inner
 // (quant/exl3_gemm_kernel.cuh:8-84, quant/exl3_gemm_inner.cuh:31-1009): the output Hadamard
-// reads the fp32 sums (had_fh / had_ff, hadamard_inner.cuh:154-281), the input rotation A_had =
+// reads the fp32 sums (had_fh / had_ff, hadamard_inner.cuh:154-281); the input rotation A_had =
 // had_hf(A o suh) is written by the caller-side pre-pass (exl3k_had128).
 //
-// Tiling.  A workgroup (4 waves) owns a 256-row x 128-column output tile; wave w the 32 columns
-// [32w, 32w + 32) of it for all 256 rows: eight v_mfma_f32_32x32x16_f16 accumulators (128
-// fp32 per lane).  Per 16-row k-slice the workgroup stages the A slice (256 x 16 fp16) and the
-// slice's 8 trellis tiles in LDS (double buffer, register prefetch PF slices deep), and every
-// lane decodes exactly the 8 weights of its MFMA B operand -- each weight of the tile once per
-// workgroup.
+// Tiling.  A workgroup (8 waves, 2 per SIMD) owns a 256 x 256 output tile; wave (wm, wn) the
+// 128 rows [128 wm, +128) x 64 columns [64 wn, +64): 4 x 2 v_mfma_f32_32x32x16_f16
+// accumulators.  The k loop runs in stages of 32 (two 16-row trellis slices).  Per stage the
+// workgroup stages the A block (256 x 32 fp16, coalesced 16-byte loads, register prefetch PF
+// stages ahead) and the stage's 2 x 16 trellis tiles in LDS, and decodes every weight of the
+// 32 x 256 B block ONCE into LDS (fp16, MFMA-operand order).  Decode of stage s + 1 runs in
+// the same iteration as the MFMAs of stage s; one barrier per stage.
 //
-// B operand from the trellis.  MFMA lane l holds column l % 32 and k-slots 8(l/32)..+7.  The
-// k order inside a slice is free as long as A uses the same: lane (column c, half h) takes the
-// tile positions 32(c%8) + 4(c/8) + 16h + 8q + j (q < 2, j < 4), which are rows
-// rho_h = {0,1,8,9,2,3,10,11} (h = 0) / {4,5,12,13,6,7,14,15} (h = 1) of column c
-// (make_tc_perm, cpu/moe_mul1.cpp:124-139), a 12-position run of the bit ring: the lane
-// normalises its run to bit 0 with one alignbit per word, then all 8 windows sit at
-// compile-time offsets.  A is staged into LDS in the same permuted k order.
+// Decode.  Thread (column c of the block, half h) produces the 8 weights of rows 8h..8h+7 of
+// column c of one trellis tile, i.e. tile positions 32(c%8) + 4(c/8) + 2h + {0,1,8,9,16,17,
+// 24,25} (make_tc_perm, cpu/moe_mul1.cpp:124-139): a 26-position run of the tile's bit ring.
+// The run is normalised to bit 0 with one alignbit per word, then the 8 windows sit at
+// compile-time offsets.  Weights are the reference's fp16 values exactly: 3INST / MCG lo + hi
+// rounded by one v_pk_add_f16 per pair, MUL1 by one v_pk_fma_f16 (codebook.cuh:57-90).
 //
-// Weights are the reference's fp16 values exactly: 3INST / MCG lo + hi rounded by one
-// v_pk_add_f16 per pair, MUL1 by v_pk_fma_f16 (codebook.cuh:57-90).
+// LDS layouts are XOR-swizzled so that 16 lanes of every ds_read_b128 / ds_write_b128 touch
+// 16 distinct 16-byte bank groups.
 //
 // Compiled once per K (EXL3_INST_K).
 #include "exl3_common.cuh"
@@ -37,17 +37,21 @@ namespace {
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float acc16 __attribute__((ext_vector_type(16)));
 
-constexpr int GT = 256;          // threads per workgroup
+constexpr int GT = 512;          // threads per workgroup (8 waves)
 constexpr int BM = 256;          // rows per workgroup
-constexpr int BN = 128;          // columns per workgroup
-constexpr int PF = 4;            // register prefetch depth, k-slices
+constexpr int BN = 256;          // columns per workgroup
+constexpr int PF = 3;            // register prefetch depth, stages (32 k each)
 
 template <int K> struct GemmLds
 {
     static constexpr int TW = 8 * K + 1;                 // words per staged tile: ring word -1, then 8K
-    static constexpr int A_U32 = BM * 8;                 // one A slice: 256 rows x 16 fp16
-    static constexpr int T_U32 = 8 * TW;                 // 8 tiles
-    static constexpr int BUF = A_U32 + T_U32;
+    static constexpr int A_U32 = BM * 16;                // A block: 256 rows x 32 fp16
+    static constexpr int B_U32 = 2 * BN * 8;             // B block: 2 slices x 256 columns x 16 fp16
+    static constexpr int T_U32 = 2 * 16 * TW;            // 2 slices x 16 tiles
+    static constexpr int A0 = 0;
+    static constexpr int B0 = 2 * A_U32;
+    static constexpr int T0 = B0 + 2 * B_U32;
+    static constexpr int TOTAL = T0 + 2 * T_U32 + 4;     // +4: a run may read one word past the last tile
 };
 
 // 16-bit window at MSB-first bit offset REL of a normalised word run.
@@ -67,7 +71,7 @@ __device__ __forceinline__ uint32_t cb_raw(uint32_t s)
     else return __builtin_amdgcn_sad_u8(s * 0x83DCD12Du, 0u, 0x6400u);                        // codebook.cuh:78-84
 }
 
-// Two decoded weights (slots i, i + 1) packed as the fp16 pair of one B-operand register.
+// Two decoded weights (rows i, i + 1) packed as one fp16 pair.
 template <int CB>
 __device__ __forceinline__ uint32_t weight_pair(uint32_t r0, uint32_t r1)
 {
@@ -85,11 +89,11 @@ __device__ __forceinline__ uint32_t weight_pair(uint32_t r0, uint32_t r1)
     }
 }
 
-// This lane's B operand for one k-slice: 8 weights of column (l % 32), k-slots 8h..8h+7.
+// Weights of rows 8h..8h+7 of one column from its normalised 26-position run.
 template <int K, int CB>
-__device__ __forceinline__ void decode_b(const uint32_t* __restrict__ tl, int sh, uint32_t* b)
+__device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, int sh)
 {
-    constexpr int NW = (11 * K + 16 + 31) / 32;          // normalised words covering the run
+    constexpr int NW = (25 * K + 16 + 31) / 32;
     uint32_t rw[NW + 1], nw[NW + 1];
     #pragma unroll
     for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
@@ -99,14 +103,14 @@ __device__ __forceinline__ void decode_b(const uint32_t* __restrict__ tl, int sh
     uint32_t r[8];
     r[0] = cb_raw<CB>(win16<0 * K>(nw));
     r[1] = cb_raw<CB>(win16<1 * K>(nw));
-    r[2] = cb_raw<CB>(win16<2 * K>(nw));
-    r[3] = cb_raw<CB>(win16<3 * K>(nw));
-    r[4] = cb_raw<CB>(win16<8 * K>(nw));
-    r[5] = cb_raw<CB>(win16<9 * K>(nw));
-    r[6] = cb_raw<CB>(win16<10 * K>(nw));
-    r[7] = cb_raw<CB>(win16<11 * K>(nw));
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = weight_pair<CB>(r[2 * i], r[2 * i + 1]);
+    r[2] = cb_raw<CB>(win16<8 * K>(nw));
+    r[3] = cb_raw<CB>(win16<9 * K>(nw));
+    r[4] = cb_raw<CB>(win16<16 * K>(nw));
+    r[5] = cb_raw<CB>(win16<17 * K>(nw));
+    r[6] = cb_raw<CB>(win16<24 * K>(nw));
+    r[7] = cb_raw<CB>(win16<25 * K>(nw));
+    return (u32x4) { weight_pair<CB>(r[0], r[1]), weight_pair<CB>(r[2], r[3]),
+                     weight_pair<CB>(r[4], r[5]), weight_pair<CB>(r[6], r[7]) };
 }
 
 // Output rotation of one fp32 row chunk (elements 2l, 2l+1) and store: had_fh / had_ff.
@@ -141,21 +145,26 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
     }
 }
 
+// Swizzled LDS offsets (u32 units).  A: row stride 16 u32 (4 chunks of 16 B), chunk ^= (row >> 2) & 3.
+// B: per slice, column stride 8 u32 (2 chunks), chunk ^= (col >> 3) & 1.
+__device__ __forceinline__ int a_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
+__device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ ((col >> 3) & 1)); }
+
 template <int K, int CB>
 __global__ __launch_bounds__(GT, 1)
 void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ trellis, void* __restrict__ C,
                  const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
 {
     using LD = GemmLds<K>;
-    __shared__ __align__(16) uint32_t lds[2 * LD::BUF + 4];   // +4: the last tile's run may read one word past it
+    __shared__ __align__(16) uint32_t lds[LD::TOTAL];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = threadIdx.x;
-    const int KS = k / 16;
-    const int nbn = n / BN, nmb = (M + BM - 1) / BM;
+    const int NST = k / 32;                              // stages
+    const int nbn = (n + BN - 1) / BN, nmb = (M + BM - 1) / BM;   // n % 128 == 0: a last block may be half
 
-    // workgroup -> (column chunk, row block): the row blocks of one column chunk run together on
-    // one XCD (workgroup b on XCD b % 8) when the chunk count allows, sharing its trellis in L2
+    // workgroup -> (column block, row block): the row blocks of one column block run together on
+    // one XCD (workgroup b on XCD b % 8) when the block count allows, sharing its trellis in L2
     int nb, mb;
     if (nbn % 8 == 0)
     {
@@ -169,116 +178,156 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         mb = blockIdx.x % nmb;
     }
 
-    // ---- staging assignment: thread t holds A row t of the block, and (t < 16K) trellis words 4t..4t+3
-    const int arow = min(mb * BM + t, M - 1);
-    const uint32_t* ag = (const uint32_t*) (Ain + (size_t) arow * k);                 // + 8 u32 per slice
-    const int tn = n / 16;
-    const bool tload = t < 16 * K;
-    const uint32_t* tg = (const uint32_t*) trellis + (size_t) nb * 8 * (8 * K) + (tload ? 4 * t : 0);
-    const size_t tstride = (size_t) tn * 8 * K;                                         // u32 per k-slice row
-
-    // ---- decode assignment: column c of tile tt, half h
-    const int h = lane >> 5;
-    const int col32 = lane & 31;
-    const int tt = 2 * wave + (col32 >> 4);
-    const int c = col32 & 15;
-    const int base_pos = 32 * (c & 7) + 4 * (c >> 3) + 16 * h;
-    const int B0 = (base_pos + 1) * K - 16;             // first window's first bit (may be < 0: ring)
-    const int f = B0 - 1 >= 0 ? (B0 - 1) / 32 : -1;     // first staged word (-1: the ring word)
-    const int sh = B0 - 32 * f;                         // 1..32
-    const int toff = LD::A_U32 + tt * LD::TW + 1 + f;   // LDS word of that first word
-
-    uint32_t apf[PF][8];
-    u32x4 tpf[PF];
-    auto load_slice = [&](int s, uint32_t* a, u32x4& tw) {
-        const int sc = min(s, KS - 1);
-        const u32x4 lo = __builtin_nontemporal_load((const u32x4*) (ag + 8 * sc));
-        const u32x4 hi = __builtin_nontemporal_load((const u32x4*) (ag + 8 * sc) + 1);
-        // permuted k order: pairs 0,4,1,5 | 2,6,3,7 (columns rho_0 | rho_1)
-        a[0] = lo.x; a[1] = hi.x; a[2] = lo.y; a[3] = hi.y;
-        a[4] = lo.z; a[5] = hi.z; a[6] = lo.w; a[7] = hi.w;
-        tw = __builtin_nontemporal_load((const u32x4*) (tg + sc * tstride));
-    };
-    // LDS slots of this thread's 4 trellis words (and the ring copy of a tile's last word)
-    int tli[4], tring = -1;
+    // ---- A staging: chunks u = t, t + 512 (row u / 4, 16-byte chunk u % 4 of the row's 64 bytes)
+    int a_lds[2];
+    const u32x4* a_src[2];
     #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int j = 0; j < 2; ++j)
     {
-        const int j = 4 * t + e;
-        const int tile = j / (8 * K), wi = j - tile * (8 * K);
-        tli[e] = LD::A_U32 + tile * LD::TW + 1 + wi;
-        if (wi == 8 * K - 1) tring = LD::A_U32 + tile * LD::TW;
+        const int u = t + GT * j, row = u >> 2, ch = u & 3;
+        a_lds[j] = LD::A0 + a_off(row, ch);
+        a_src[j] = (const u32x4*) (Ain + (size_t) min(mb * BM + row, M - 1) * k + 8 * ch);
     }
-    auto store_slice = [&](uint32_t* buf, const uint32_t* a, const u32x4& tw) {
-        *(u32x4*) (buf + 8 * t) = (u32x4) { a[0], a[1], a[2], a[3] };
-        *(u32x4*) (buf + 8 * t + 4) = (u32x4) { a[4], a[5], a[6], a[7] };
+    // ---- trellis staging: words 4t..4t+3 of the stage's 2 slices x 16 tiles (t < 64K)
+    const bool tload = t < 64 * K;
+    int t_lds[4], t_ring = -1;
+    const uint32_t* t_src;
+    {
+        const int wi = 4 * (tload ? t : 0);
+        const int s2 = wi / (128 * K), wj = wi - s2 * (128 * K);
+        const int tile = wj / (8 * K), wk = wj - tile * (8 * K);
+        #pragma unroll
+        for (int e = 0; e < 4; ++e) t_lds[e] = LD::T0 + (s2 * 16 + tile) * LD::TW + 1 + wk + e;
+        if (wk + 3 == 8 * K - 1) t_ring = LD::T0 + (s2 * 16 + tile) * LD::TW;
+        const int gtile = min(nb * 16 + tile, n / 16 - 1);   // columns past n: a valid tile, results dropped
+        t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * (8 * K) + wk;
+    }
+    const size_t t_stage = (size_t) 2 * (n / 16) * (8 * K);    // u32 per stage (two tile rows)
+
+    // ---- decode assignment: column dc of the block, half dh; both slices of a stage
+    const int dc = t & 255, dh = t >> 8;
+    const int dtile = dc >> 4, dcc = dc & 15;
+    const int dbase = 32 * (dcc & 7) + 4 * (dcc >> 3) + 2 * dh;
+    const int dB0 = (dbase + 1) * K - 16;                // first window's first bit (< 0: ring)
+    const int df = dB0 - 1 >= 0 ? (dB0 - 1) / 32 : -1;
+    const int dsh = dB0 - 32 * df;                       // 1..32
+    const int d_src = LD::T0 + dtile * LD::TW + 1 + df;  // + slice * 16 * TW
+    const int d_dst0 = LD::B0 + b_off(0, dc, dh), d_dst1 = LD::B0 + b_off(1, dc, dh);
+
+    // ---- MFMA operand assignment
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    u32x4 apf[PF][2], tpf[PF];
+    auto load_stage = [&](int s, u32x4* a, u32x4& tw) {
+        const int sc = min(s, NST - 1);
+        a[0] = __builtin_nontemporal_load(a_src[0] + 4 * sc);
+        a[1] = __builtin_nontemporal_load(a_src[1] + 4 * sc);
+        tw = __builtin_nontemporal_load((const u32x4*) (t_src + sc * t_stage));
+    };
+    auto store_stage = [&](int buf, const u32x4* a, const u32x4& tw) {
+        *(u32x4*) (lds + buf * LD::A_U32 + a_lds[0]) = a[0];
+        *(u32x4*) (lds + buf * LD::A_U32 + a_lds[1]) = a[1];
+    };
+    auto store_trellis = [&](int buf, const u32x4& tw) {
         if (tload)
         {
-            buf[tli[0]] = tw.x; buf[tli[1]] = tw.y; buf[tli[2]] = tw.z; buf[tli[3]] = tw.w;
-            if (tring >= 0) buf[tring] = tw.w;          // a tile's last word is always e = 3 (8K % 4 == 0)
+            uint32_t* T = lds + buf * LD::T_U32;
+            T[t_lds[0]] = tw.x; T[t_lds[1]] = tw.y; T[t_lds[2]] = tw.z; T[t_lds[3]] = tw.w;
+            if (t_ring >= 0) T[t_ring] = tw.w;
         }
     };
+    auto decode_stage = [&](int buf) {
+        const uint32_t* T = lds + buf * LD::T_U32;
+        uint32_t* B = lds + buf * LD::B_U32;
+        *(u32x4*) (B + d_dst0) = decode_run<K, CB>(T + d_src, dsh);
+        *(u32x4*) (B + d_dst1) = decode_run<K, CB>(T + d_src + 16 * LD::TW, dsh);
+    };
 
+    // prologue: A(0), trellis(0), trellis(1) staged; B(0) decoded
     #pragma unroll
-    for (int d = 0; d < PF; ++d) load_slice(d, apf[d], tpf[d]);
-    store_slice(lds, apf[0], tpf[0]);
-    load_slice(PF, apf[0], tpf[0]);
+    for (int d = 0; d < PF; ++d) load_stage(d, apf[d], tpf[d]);
+    store_stage(0, apf[0], tpf[0]);
+    store_trellis(0, tpf[0]);
+    store_trellis(1, tpf[1]);
+    __syncthreads();
+    decode_stage(0);
+    // slot 0 now free: A(PF) / trellis(PF); A(1) still waits in slot 1, trellis(2) in slot 2
+    load_stage(PF, apf[0], tpf[0]);
     __syncthreads();
 
-    acc16 acc[8];
+    acc16 acc[4][2];
     #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = (acc16) { };
+    for (int i = 0; i < 4; ++i) { acc[i][0] = (acc16) { }; acc[i][1] = (acc16) { }; }
 
-    for (int s0 = 0; s0 < KS; s0 += PF)
+    for (int s0 = 0; s0 < NST; s0 += PF)
     {
         #pragma unroll
         for (int d = 0; d < PF; ++d)
         {
             const int s = s0 + d;
-            if (s >= KS) break;
-            const uint32_t* buf = lds + (s & 1) * LD::BUF;
-            uint32_t b[4];
-            decode_b<K, CB>(buf + toff, sh, b);
-            const h8v bv = __builtin_bit_cast(h8v, (u32x4) { b[0], b[1], b[2], b[3] });
+            if (s >= NST) break;
+            const int cur = s & 1, nxt = cur ^ 1;
+            // decode B(s + 1) from trellis(s + 1), staged last iteration
+            if (s + 1 < NST) decode_stage(nxt);
+            // MFMAs of stage s
+            const uint32_t* A = lds + LD::A0 + cur * LD::A_U32;
+            const uint32_t* B = lds + LD::B0 + cur * LD::B_U32;
             #pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
+            for (int sl = 0; sl < 2; ++sl)
             {
-                const u32x4 av = *(const u32x4*) (buf + 8 * (mt * 32 + col32) + 4 * h);
-                acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, av), bv, acc[mt], 0, 0, 0);
+                h8v bv[2];
+                #pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    bv[nt] = __builtin_bit_cast(h8v, *(const u32x4*) (B + b_off(sl, 64 * wn + 32 * nt + l32, lh)));
+                #pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                {
+                    const h8v av = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off(128 * wm + 32 * mt + l32, 2 * sl + lh)));
+                    acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[0], acc[mt][0], 0, 0, 0);
+                    acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[1], acc[mt][1], 0, 0, 0);
+                }
             }
-            if (s + 1 < KS)
-            {
-                const int nd = (d + 1) % PF;
-                store_slice(lds + ((s + 1) & 1) * LD::BUF, apf[nd], tpf[nd]);
-                load_slice(s + 1 + PF, apf[nd], tpf[nd]);
-            }
+            // stage A(s + 1) and trellis(s + 2); prefetch further
+            const int n1 = (d + 1) % PF, n2 = (d + 2) % PF;
+            if (s + 1 < NST) store_stage(nxt, apf[n1], tpf[n1]);
+            if (s + 2 < NST) store_trellis(cur, tpf[n2]);
+            load_stage(s + 1 + PF, apf[n1], tpf[n1]);
             __syncthreads();
         }
     }
 
-    // ---- epilogue: per 32-row tile, exchange through LDS so each row's 128 columns meet in one wave
-    float* E = (float*) lds;                              // [32][128] fp32
+    // ---- epilogue: 4 rounds of 64 rows; the 256 columns of each row meet in LDS, each wave then
+    // rotates whole 128-column chunks
+    float* E = (float*) lds;                              // [64][256] fp32
     const bool has_svh = svh != nullptr;
-    const uint32_t svp = has_svh ? *(const uint32_t*) (svh + nb * BN + 2 * lane) : 0u;
     #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
     {
         #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int nt = 0; nt < 2; ++nt)
         {
             #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                E[(8 * j + 4 * h + i) * BN + 32 * wave + col32] = acc[mt][4 * j + i];
+            for (int j = 0; j < 4; ++j)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    E[(32 * wm + 8 * j + 4 * lh + i) * BN + 64 * wn + 32 * nt + l32] = acc[mt][nt][4 * j + i];
+            }
         }
         __syncthreads();
-        #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
+        // 64 rows x 2 chunks = 128 row-chunks, 16 per wave
+        #pragma unroll 2
+        for (int q = 0; q < 16; ++q)
         {
-            const int r = 8 * wave + rr;
-            const int row = mb * BM + mt * 32 + r;
-            const f32x2 v = *(const f32x2*) (E + r * BN + 2 * lane);
-            if (row < M)
-                gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + nb * BN + 2 * lane, lane);
+            const int rc = wave * 16 + q;
+            const int er = rc >> 1, ch = rc & 1;
+            const int row = mb * BM + 128 * (er >> 5) + 32 * mt + (er & 31);
+            const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
+            const int col = nb * BN + 128 * ch + 2 * lane;
+            if (nb * BN + 128 * ch >= n) continue;        // half block: chunk past n (uniform per wave)
+            const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
         }
         __syncthreads();
     }
@@ -287,7 +336,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
 template <int K, int CB>
 int launch_gemm(const GemmArgs& g, hipStream_t s)
 {
-    const int blocks = (g.n / BN) * ((g.m + BM - 1) / BM);
+    const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     hipLaunchKernelGGL((gemm_kernel<K, CB>), dim3(blocks), dim3(GT), 0, s,
                        g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32);
     return (int) hipGetLastError();
