@@ -51,7 +51,8 @@ template <int K> struct GemmLds
     static constexpr int A0 = 0;
     static constexpr int B0 = 2 * A_U32;
     static constexpr int T0 = B0 + 2 * B_U32;
-    static constexpr int TOTAL = T0 + 2 * T_U32 + 4;     // +4: a run may read one word past the last tile
+    static constexpr int DUMMY = T0 + 2 * T_U32 + 4;     // (+4: a run may read one word past the last tile)
+    static constexpr int TOTAL = DUMMY + 8;              // sink for the stores of threads without trellis words
 };
 
 // 16-bit window at MSB-first bit offset REL of a normalised word run.
@@ -63,10 +64,19 @@ __device__ __forceinline__ uint32_t win16(const uint32_t* nw)
     else return __builtin_amdgcn_alignbit(nw[w], nw[w + 1], 48 - off) & 0xffffu;
 }
 
+// 3INST multiply-add as one v_mad_u64_u32 (its low word): ~full rate on gfx950, where mul + add
+// would take two ops.
+__device__ __forceinline__ uint32_t mad_3inst(uint32_t s)
+{
+    uint64_t r;
+    asm("v_mad_u64_u32 %0, vcc, %1, %2, %3" : "=&v"(r) : "v"(s), "s"(89226354u), "v"((uint64_t) 64248484u) : "vcc");
+    return (uint32_t) r;
+}
+
 template <int CB>
 __device__ __forceinline__ uint32_t cb_raw(uint32_t s)
 {
-    if constexpr (CB == 0) return ((s * 89226354u + 64248484u) & 0x8fff8fffu) ^ 0x3b603b60u;   // codebook.cuh:61-63
+    if constexpr (CB == 0) return (mad_3inst(s) & 0x8fff8fffu) ^ 0x3b603b60u;                   // codebook.cuh:61-63
     else if constexpr (CB == 1) return ((s * 0xCBAC1FEDu) & 0x8fff8fffu) ^ 0x3b603b60u;        // codebook.cuh:69-72
     else return __builtin_amdgcn_sad_u8(s * 0x83DCD12Du, 0u, 0x6400u);                        // codebook.cuh:78-84
 }
@@ -190,7 +200,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     }
     // ---- trellis staging: words 4t..4t+3 of the stage's 2 slices x 16 tiles (t < 64K)
     const bool tload = t < 64 * K;
-    int t_lds[4], t_ring = -1;
+    int t_lds[4], t_ring = LD::DUMMY + 4;
     const uint32_t* t_src;
     {
         const int wi = 4 * (tload ? t : 0);
@@ -199,6 +209,11 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         #pragma unroll
         for (int e = 0; e < 4; ++e) t_lds[e] = LD::T0 + (s2 * 16 + tile) * LD::TW + 1 + wk + e;
         if (wk + 3 == 8 * K - 1) t_ring = LD::T0 + (s2 * 16 + tile) * LD::TW;
+        if (!tload)
+        {
+            #pragma unroll
+            for (int e = 0; e < 4; ++e) t_lds[e] = LD::DUMMY + e;
+        }
         const int gtile = min(nb * 16 + tile, n / 16 - 1);   // columns past n: a valid tile, results dropped
         t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * (8 * K) + wk;
     }
@@ -229,20 +244,21 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         *(u32x4*) (lds + buf * LD::A_U32 + a_lds[0]) = a[0];
         *(u32x4*) (lds + buf * LD::A_U32 + a_lds[1]) = a[1];
     };
+    // branch-free: threads without trellis words (and the ring copy of non-final words) write
+    // into a sink past the buffers (stage-relative offsets: buf 1 sinks land in the other sink)
+    const int sink_fix = LD::T_U32;
     auto store_trellis = [&](int buf, const u32x4& tw) {
-        if (tload)
-        {
-            uint32_t* T = lds + buf * LD::T_U32;
-            T[t_lds[0]] = tw.x; T[t_lds[1]] = tw.y; T[t_lds[2]] = tw.z; T[t_lds[3]] = tw.w;
-            if (t_ring >= 0) T[t_ring] = tw.w;
-        }
+        uint32_t* T = lds + buf * LD::T_U32;
+        const int fix = (tload ? 0 : buf * sink_fix);
+        T[t_lds[0] - fix] = tw.x; T[t_lds[1] - fix] = tw.y; T[t_lds[2] - fix] = tw.z; T[t_lds[3] - fix] = tw.w;
+        T[t_ring - (t_ring >= LD::DUMMY ? buf * sink_fix : 0)] = tw.w;
     };
-    auto decode_stage = [&](int buf) {
+    auto decode_slice = [&](int buf, int sl) {
         const uint32_t* T = lds + buf * LD::T_U32;
         uint32_t* B = lds + buf * LD::B_U32;
-        *(u32x4*) (B + d_dst0) = decode_run<K, CB>(T + d_src, dsh);
-        *(u32x4*) (B + d_dst1) = decode_run<K, CB>(T + d_src + 16 * LD::TW, dsh);
+        *(u32x4*) (B + (sl ? d_dst1 : d_dst0)) = decode_run<K, CB>(T + d_src + sl * 16 * LD::TW, dsh);
     };
+    auto decode_stage = [&](int buf) { decode_slice(buf, 0); decode_slice(buf, 1); };
 
     // prologue: A(0), trellis(0), trellis(1) staged; B(0) decoded
     #pragma unroll
@@ -268,31 +284,66 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
             const int s = s0 + d;
             if (s >= NST) break;
             const int cur = s & 1, nxt = cur ^ 1;
-            // decode B(s + 1) from trellis(s + 1), staged last iteration
-            if (s + 1 < NST) decode_stage(nxt);
-            // MFMAs of stage s
+            // per slice: load this stage's MFMA operands from LDS, then decode the same slice of
+            // B(s + 1) from trellis(s + 1) (staged last iteration; past the last stage it decodes
+            // stale words into a buffer nobody reads, keeping the body one basic block) while the
+            // slice's 8 MFMAs run on the operands already in registers
             const uint32_t* A = lds + LD::A0 + cur * LD::A_U32;
             const uint32_t* B = lds + LD::B0 + cur * LD::B_U32;
             #pragma unroll
             for (int sl = 0; sl < 2; ++sl)
             {
-                h8v bv[2];
+                h8v bv[2], av[4];
                 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
                     bv[nt] = __builtin_bit_cast(h8v, *(const u32x4*) (B + b_off(sl, 64 * wn + 32 * nt + l32, lh)));
                 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
-                {
-                    const h8v av = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off(128 * wm + 32 * mt + l32, 2 * sl + lh)));
-                    acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[0], acc[mt][0], 0, 0, 0);
-                    acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[1], acc[mt][1], 0, 0, 0);
-                }
+                    av[mt] = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off(128 * wm + 32 * mt + l32, 2 * sl + lh)));
+                // the decode of this slice of B(s + 1), cut into 8 pieces that ride in the shadow
+                // of the 8 MFMAs (each 32 cycles on the matrix pipe); sched_barrier keeps the cuts
+                constexpr int NW = (25 * K + 16 + 31) / 32;
+                const uint32_t* tl = lds + nxt * LD::T_U32 + d_src + sl * 16 * LD::TW;
+                uint32_t rw[NW + 1], nw[NW + 1], r[8], wp[4];
+                #pragma unroll
+                for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
+#define EXL3_MFMA_STEP(mt, nt) \
+                __builtin_amdgcn_sched_barrier(0); \
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0); \
+                __builtin_amdgcn_sched_barrier(0);
+                EXL3_MFMA_STEP(0, 0)
+                #pragma unroll
+                for (int i = 0; i < NW; ++i) nw[i] = __builtin_amdgcn_alignbit(rw[i], rw[i + 1], 32 - dsh);
+                nw[NW] = 0u;
+                EXL3_MFMA_STEP(0, 1)
+                r[0] = cb_raw<CB>(win16<0 * K>(nw));
+                r[1] = cb_raw<CB>(win16<1 * K>(nw));
+                EXL3_MFMA_STEP(1, 0)
+                r[2] = cb_raw<CB>(win16<8 * K>(nw));
+                r[3] = cb_raw<CB>(win16<9 * K>(nw));
+                EXL3_MFMA_STEP(1, 1)
+                wp[0] = weight_pair<CB>(r[0], r[1]);
+                wp[1] = weight_pair<CB>(r[2], r[3]);
+                EXL3_MFMA_STEP(2, 0)
+                r[4] = cb_raw<CB>(win16<16 * K>(nw));
+                r[5] = cb_raw<CB>(win16<17 * K>(nw));
+                EXL3_MFMA_STEP(2, 1)
+                r[6] = cb_raw<CB>(win16<24 * K>(nw));
+                r[7] = cb_raw<CB>(win16<25 * K>(nw));
+                EXL3_MFMA_STEP(3, 0)
+                wp[2] = weight_pair<CB>(r[4], r[5]);
+                wp[3] = weight_pair<CB>(r[6], r[7]);
+                EXL3_MFMA_STEP(3, 1)
+#undef EXL3_MFMA_STEP
+                *(u32x4*) (lds + nxt * LD::B_U32 + (sl ? d_dst1 : d_dst0)) = (u32x4) { wp[0], wp[1], wp[2], wp[3] };
             }
-            // stage A(s + 1) and trellis(s + 2); prefetch further
+            // stage A(s + 1) and trellis(s + 2) (clamped loads: past the end they rewrite unread
+            // buffers); prefetch further
             const int n1 = (d + 1) % PF, n2 = (d + 2) % PF;
-            if (s + 1 < NST) store_stage(nxt, apf[n1], tpf[n1]);
-            if (s + 2 < NST) store_trellis(cur, tpf[n2]);
+            store_stage(nxt, apf[n1], tpf[n1]);
+            store_trellis(cur, tpf[n2]);
             load_stage(s + 1 + PF, apf[n1], tpf[n1]);
+
             __syncthreads();
         }
     }
