@@ -40,6 +40,20 @@ SIGNATURES = {
                               _vp, _i32,                         # n_stride_list, entries
                               _vp, _i32, _i32,                   # had_src_list, entries, num_had_src
                               _vp]),
+    "exl3_amd_moe_coop": (_i32, [_vp, _i32, _i32, _i32,                 # x, bsz, H, x_stride
+                                 _vp, _vp, _i32,                         # sel, rw, topk
+                                 _i32, _i32, _i32,                       # min/max expert, Hi
+                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,   # tables, n_local
+                                 _vp, _vp, _vp,                          # bias tables
+                                 _f32, _f32, _f32, _i32, _i32, _i32, _f32, _i32,      # Kg Ku Kd mcg mul1 act limit gated
+                                 _vp, ctypes.c_int64, _vp, ctypes.c_int64,            # had_g, had_u
+                                 _vp, _vp, ctypes.c_int64, _i32, _i32,               # gu_g, gu_u, numel, f32, I
+                                 _vp, ctypes.c_int64, _vp, ctypes.c_int64, _i32,     # act_out, d_out, Ho
+                                 _vp, ctypes.c_int64,                    # ctr
+                                 _vp, _i32, _i32, _i32,                  # out, rows_max, H_out, stride
+                                 _vp, _vp, _i32,                         # sh_out, sh_gate_w, n
+                                 _vp, _vp, _vp,                          # bits tables
+                                 _vp]),
 }
 
 

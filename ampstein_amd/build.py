@@ -41,6 +41,8 @@ def units():
         ("exl3_hadamard.hip", "exl3_hadamard.o", []),
         ("exl3_device.hip", "exl3_device.o", []),
     ]
+    for cb in range(3):
+        u.append(("exl3_moe.hip", f"exl3_moe_cb{cb}.o", [f"-DEXL3_MOE_CB={cb}"]))
     for k in range(1, 9):
         u.append(("exl3_gemv.hip", f"exl3_gemv_k{k}.o", [f"-DEXL3_INST_K={k}"]))
         u.append(("exl3_gemm.hip", f"exl3_gemm_k{k}.o", [f"-DEXL3_INST_K={k}"]))

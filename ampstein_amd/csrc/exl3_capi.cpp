@@ -6,6 +6,7 @@
 // bits_k.cuh:178-185).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -461,6 +462,115 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
     }
     int rc = launch_gemv(d, bits, cb, g, s, "exl3_mgemm");
     return rc ? rc : EXL3_AMD_TAG_GEMV;
+}
+
+int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
+                      const int64_t* sel, const uint16_t* rw, int topk,
+                      int min_expert, int max_expert, int Hi,
+                      const uint64_t* g_trellis, const uint64_t* g_suh, const uint64_t* g_svh,
+                      const uint64_t* u_trellis, const uint64_t* u_suh, const uint64_t* u_svh,
+                      const uint64_t* d_trellis, const uint64_t* d_suh, const uint64_t* d_svh, int n_local,
+                      const uint64_t* g_bias, const uint64_t* u_bias, const uint64_t* d_bias,
+                      float Kg, float Ku, float Kd, int mcg, int mul1, int act, float act_limit, int gated,
+                      uint16_t* had_g, int64_t had_g_numel, uint16_t* had_u, int64_t had_u_numel,
+                      void* gu_g, void* gu_u, int64_t gu_numel, int gu_f32, int I,
+                      uint16_t* act_out, int64_t act_out_numel, float* d_out, int64_t d_out_numel, int Ho,
+                      int* ctr, int64_t ctr_numel,
+                      float* out, int rows_max, int H_out, int out_stride,
+                      const float* sh_out, const uint16_t* sh_gate_w, int sh_gate_n,
+                      const uint8_t* bits_g, const uint8_t* bits_u, const uint8_t* bits_d,
+                      void* stream)
+{
+    (void) gu_g; (void) gu_u; (void) gu_f32; (void) d_out;
+    g_last_error.clear();
+    // exl3_moe_coop.cu:185-305 (prepare + run), in the reference's order
+    if (!x || !sel || !rw || !out || !ctr || !had_g || !had_u || !act_out)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: null pointer");
+    if (!g_trellis || !g_suh || !g_svh || !u_trellis || !u_suh || !u_svh || !d_trellis || !d_suh || !d_svh)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: pointer tables must be contiguous int64");
+    if (mcg && mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: specified both mcg and mul1");
+    if (!(Kg >= 1 && Kg <= 8 && Ku >= 1 && Ku <= 8 && Kd >= 1 && Kd <= 8))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: K out of range");
+    if (gated && Kg != Ku) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: gate and up must share a bit width");
+    if (act < 0 || act > 3) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: unknown activation");
+    if (!(Hi % 128 == 0 && I % 128 == 0 && Ho % 128 == 0 && H_out <= Ho && Hi > 0 && I > 0 && Ho > 0))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: Hi/I/Ho shape");
+    int64_t sm = had_g_numel / Hi;
+    sm = std::min<int64_t>(sm, had_u_numel / Hi);
+    sm = std::min<int64_t>(sm, gu_numel / I);
+    sm = std::min<int64_t>(sm, act_out_numel / I);
+    sm = std::min<int64_t>(sm, d_out_numel / Ho);
+    if (sm < 1 || sm > 256) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: scratch must hold 1..256 slots");
+    const int slots_max = (int) sm;
+    const int64_t ctr_len = (int64_t) slots_max * (I / 128) + (int64_t) rows_max * (Ho / 128) + 2 + (slots_max + 1) + slots_max;
+    if (ctr_numel < ctr_len) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: counter scratch too small");
+    if ((bits_g || bits_u || bits_d) && !(bits_g && bits_u && bits_d))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: give all three bit width tables or none");
+    if (bsz < 0 || topk < 1) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: sel/rw must be (bsz, topk)");
+    if (!(H % 4 == 0 && H <= Hi)) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: H/Hi shape");
+    const int slots = bsz * topk;
+    if (!(slots <= slots_max && bsz <= rows_max)) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: batch exceeds the scratch");
+    if (!(min_expert < 0 || max_expert - min_expert <= n_local))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: expert range exceeds tables");
+    if (sh_out)
+    {
+        if (H_out != H) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: shared expert output width must match the routed output");
+        if (sh_gate_w && !(sh_gate_n == H && H % 2 == 0)) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: shared gate width");
+    }
+    const bool dyn = bits_g != nullptr;
+    if (dyn && !mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: mixed bit widths require the mul1 codebook");
+    const float Kgu = gated ? Kg : Ku;
+    if (Kgu != (float) (int) Kgu || Kd != (float) (int) Kd)
+        return fail(Kgu - (int) Kgu == 0.5f && mul1 ? EXL3_AMD_EUNSUPPORTED : EXL3_AMD_EINVAL,
+                    "exl3_moe_coop: half-integer bitrates are not implemented in this build");
+    if (bsz == 0) return 0;
+
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+
+    MoeArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = x; a.x_stride = x_stride; a.sel = sel; a.rw = rw;
+    a.bsz = bsz; a.topk = topk; a.H = H; a.Hi = Hi; a.I = I; a.Ho = Ho; a.H_out = H_out;
+    a.min_expert = min_expert; a.max_expert = max_expert;
+    a.g_trellis = g_trellis; a.g_suh = g_suh; a.g_svh = g_svh;
+    a.u_trellis = u_trellis; a.u_suh = u_suh; a.u_svh = u_svh;
+    a.d_trellis = d_trellis; a.d_suh = d_suh; a.d_svh = d_svh;
+    a.g_bias = g_bias; a.u_bias = u_bias; a.d_bias = d_bias;
+    a.g_bits = bits_g; a.u_bits = bits_u; a.d_bits = bits_d;
+    a.K_gu = (int) Kgu; a.K_d = (int) Kd;
+    a.act = act; a.act_limit = act_limit; a.gated = gated ? 1 : 0;
+    a.had_g = had_g; a.had_u = had_u; a.act_out = act_out;
+    a.runs = ctr + (int64_t) slots_max * (I / 128) + (int64_t) rows_max * (Ho / 128);
+    a.slots_max = slots_max;
+    a.out = out; a.out_stride = out_stride;
+    a.sh_out = sh_out; a.sh_gate_w = sh_out ? sh_gate_w : nullptr;
+
+    // work split: k-splits so every workgroup holds at most EXL3_MOE_SBMAX k-slices and the grid
+    // (sized for one run per slot) reaches a few workgroups per CU
+    const int nproj = gated ? 2 : 1;
+    const long target = 4L * d->num_cus;
+    auto pick = [&](int KS, long base) {
+        int S = (KS + EXL3_MOE_SBMAX - 1) / EXL3_MOE_SBMAX;
+        while (base * S < target && KS / (S + 1) >= 8) ++S;
+        return S;
+    };
+    a.splits_a = pick(Hi / 16, (long) slots * (I / 128) * nproj);
+    a.splits_b = pick(I / 16, (long) slots * (Ho / 128));
+    const size_t pa = (size_t) 2 * a.splits_a * slots * I, pb = (size_t) a.splits_b * slots * Ho;
+    if ((pa + pb) * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe_coop: batch exceeds the library workspace");
+    a.part_a = d->partials;
+    a.part_b = d->partials + pa;
+    const size_t ca = (size_t) slots * (I / 128) * 32, cb_ = (size_t) bsz * (Ho / 128) * 32;
+    if (ca + cb_ > WS_COUNTERS) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe_coop: batch exceeds the counter workspace");
+    a.ctr_a = d->counters;
+    a.ctr_b = d->counters + ca;
+    a.xcd = (d->num_xcd > 0 && (I / 128) % d->num_xcd == 0 && (Ho / 128) % d->num_xcd == 0) ? d->num_xcd : 0;
+
+    const int cb = mcg ? 1 : (mul1 ? 2 : 0);
+    hipStream_t s = (hipStream_t) stream;
+    int rc = cb == 0 ? exl3k_moe_cb0(a, s) : cb == 1 ? exl3k_moe_cb1(a, s) : exl3k_moe_cb2(a, s);
+    return rc ? hip_fail(rc, "exl3_moe_coop") : 0;
 }
 
 }  // extern "C"

@@ -63,6 +63,48 @@ int exl3k_gemm_k6(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k7(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k8(const GemmArgs& g, int cb, hipStream_t s);
 
+// Fused decode-shaped MoE (exl3_moe_coop): route/rotate, gate/up GEMV + activation, down GEMV +
+// routing-weighted sum.  Device pointers throughout; tables indexed by local expert.
+struct MoeArgs
+{
+    const uint16_t* x;          // (bsz, H) fp16, row stride x_stride
+    int x_stride;
+    const int64_t* sel;         // (bsz, topk) expert indices
+    const uint16_t* rw;         // (bsz, topk) fp16 routing weights (0 = inactive slot)
+    int bsz, topk, H, Hi, I, Ho, H_out;
+    int min_expert, max_expert; // min < 0: no range filter
+    const uint64_t *g_trellis, *g_suh, *g_svh;
+    const uint64_t *u_trellis, *u_suh, *u_svh;
+    const uint64_t *d_trellis, *d_suh, *d_svh;
+    const uint64_t *g_bias, *u_bias, *d_bias;      // nullable tables of fp16 vectors
+    const uint8_t *g_bits, *u_bits, *d_bits;       // per-expert widths (mixed K), or null
+    int K_gu, K_d;              // uniform widths when the tables are null
+    int act;                    // 0 SiLU, 1 GELU (tanh), 2 ReLU^2, 3 clamped SwiGLU (gpt-oss)
+    float act_limit;
+    int gated;                  // 0: no gate projection, activation relu(u) * u
+    uint16_t* had_g;            // (slots_max, Hi) rotated gate input
+    uint16_t* had_u;            // (slots_max, Hi) rotated up input
+    uint16_t* act_out;          // (slots_max, I) activation, rotated for the down projection
+    int* runs;                  // run table in the caller's ctr: [n_runs, -, run_start[slots_max+1], order[slots_max]]
+    int slots_max;
+    float* out;                 // (bsz, H_out) fp32, row stride out_stride
+    int out_stride;
+    const float* sh_out;        // shared expert output (bsz, H) fp32, or null
+    const uint16_t* sh_gate_w;  // (H) fp16 shared-expert gate weight, or null
+    // library workspace
+    float* part_a;              // [2][splits_a][slots][I] gate/up partials
+    float* part_b;              // [splits_b][slots][Ho] down partials
+    int* ctr_a;                 // [slots][I/128] x 32 (one 128-byte line each)
+    int* ctr_b;                 // [bsz][Ho/128] x 32
+    int splits_a, splits_b;
+    int xcd;                    // > 0: chunk c runs on XCD c % xcd (workgroup-scope hand-off)
+};
+
+int exl3k_moe_cb0(const MoeArgs& a, hipStream_t s);
+int exl3k_moe_cb1(const MoeArgs& a, hipStream_t s);
+int exl3k_moe_cb2(const MoeArgs& a, hipStream_t s);
+constexpr int EXL3_MOE_SBMAX = 64;     // k-slices per workgroup of the MoE GEMV (LDS bound)
+
 int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
                       int nt_off, int K, int cb, hipStream_t s);
 int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,

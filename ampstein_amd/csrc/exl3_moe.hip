@@ -1,0 +1,654 @@
+// Fused decode-shaped MoE for gfx950 (exl3_moe_coop semantics, quant/exl3_moe_coop_kernel.cuh,
+// quant/exl3_moe_coop.cu): every (token, expert) slot through gate/up, activation and down, with
+// per-expert bit widths (mixed K) or one uniform width.  Three launches:
+//
+//   route   block 0 sorts the active slots by (local expert, slot) and cuts runs of at most 8
+//           slots of one expert into the caller's run table (exl3_moe_coop_kernel.cuh:273-356,
+//           same layout); every wave rotates one 128-chunk of one slot's x row (zero-padded to
+//           Hi, * suh in fp32, Hadamard, fp16) for gate and up; tokens without an active slot get
+//           their output row here (shared-expert term or zeros).
+//   A       one workgroup per (run, 128-column chunk, projection, k-split): the run's slots are
+//           the rows of one multi-row GEMV over the expert's trellis (x in LDS as (x, x) pairs,
+//           the decode of the dense GEMV); the last arrival of a (slot, chunk) sums the split
+//           partials, rotates, * svh, + bias, applies the activation, * down suh, rotates and
+//           stores the down input (:803-845).
+//   B       the same GEMV over the down trellis; the last arrival of a (token, chunk) rotates
+//           each active slot's sum * svh (+ bias), weights it by its routing weight, sums the
+//           slots in the reference's fixed order (:917-999), adds the shared expert and stores.
+//
+// Hand-offs: counters (one 128-byte line each) in the library workspace; chunk c runs on XCD
+// c % 8 when the chunk counts allow, so the hand-off is an L2-local atomic, else device scope.
+// Compiled once per codebook (EXL3_MOE_CB); the bit width is a per-workgroup switch.
+#include "exl3_common.cuh"
+#include "exl3_gemv_core.cuh"
+#include "exl3_kernels.h"
+
+#ifndef EXL3_MOE_CB
+#define EXL3_MOE_CB 0
+#endif
+#ifndef EXL3_GEMV_PF
+#define EXL3_GEMV_PF 2
+#endif
+
+using namespace exl3;
+
+namespace {
+
+constexpr int NT = 256;          // threads per workgroup
+constexpr int NW = NT / 64;      // waves
+constexpr int ROWS = 8;          // slots per run (exl3_moe_coop_kernel.cuh:37)
+constexpr int SBMAX = EXL3_MOE_SBMAX; // k-slices per workgroup (LDS: ROWS x SBMAX x 16 x-pairs)
+constexpr int WKR = 16;          // slot-sum partition of the down epilogue (the reference's 16 warps)
+
+struct SlotInfo
+{
+    int row;
+    int local;
+    float w;
+    bool active;
+};
+
+// exl3_moe_coop_kernel.cuh:250-267
+__device__ __forceinline__ SlotInfo slot_info(const MoeArgs& a, int s)
+{
+    SlotInfo si;
+    si.row = s / a.topk;
+    int64_t e = *to_global(a.sel + s);
+    si.w = (float) as_h(*to_global(a.rw + s));
+    bool ok = si.w != 0.0f;
+    if (a.min_expert >= 0)
+    {
+        ok = ok && e >= a.min_expert && e < a.max_expert;
+        e -= a.min_expert;
+    }
+    si.local = ok ? (int) e : 0;
+    si.active = ok;
+    return si;
+}
+
+__device__ __forceinline__ int token_active_slots(const MoeArgs& a, int row)
+{
+    int n = 0;
+    for (int k = 0; k < a.topk; ++k) n += slot_info(a, row * a.topk + k).active ? 1 : 0;
+    return n;
+}
+
+template <typename T>
+__device__ __forceinline__ const T* tab(const uint64_t* table, int i) { return (const T*) *to_global(table + i); }
+
+__device__ __forceinline__ float h2f(const uint16_t* p, int i) { return (float) as_h(*to_global(p + i)); }
+
+// ---- activations (fp32; exl3_moe_coop_kernel.cuh:91-128).  GELU is the tanh approximation of
+// Hendrycks & Gimpel with its published constants.
+__device__ __forceinline__ float act_silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float act_gelu(float x)
+{
+    const float c = 0.797884560803f;        // sqrt(2 / pi)
+    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float act_relu2(float x) { x = fmaxf(0.0f, x); return x * x; }
+__device__ __forceinline__ float act_oai(float g, float u, float limit)
+{
+    if (limit != 0.0f)
+    {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+    }
+    const float glu = g * (1.0f / (1.0f + __expf(-1.702f * g)));
+    return (u + 1.0f) * glu;
+}
+__device__ __forceinline__ float act_gate(int act, bool gated, float g, float u, float limit)
+{
+    if (act == 3) return act_oai(g, u, limit);
+    float x;
+    if (!gated) x = fmaxf(0.0f, u);
+    else if (act == 0) x = act_silu(g);
+    else if (act == 1) x = act_gelu(g);
+    else x = act_relu2(g);
+    if (limit != 0.0f)
+    {
+        u = fminf(fmaxf(u, -limit), limit);
+        x = fminf(x, limit);
+    }
+    return x * u;
+}
+
+// ---- wave-level row chunk helpers: lane l holds columns 2l, 2l + 1 of a 128-chunk
+
+__device__ __forceinline__ float wave_sum(float v, int lane)
+{
+    v += xor_partner<1>(v, lane);
+    v += xor_partner<2>(v, lane);
+    v += xor_partner<4>(v, lane);
+    v += xor_partner<8>(v, lane);
+    v += xor_partner<16>(v, lane);
+    v += xor_partner<32>(v, lane);
+    return v;
+}
+
+// sigmoid(x_row . sh_gate_w), fp32, by one wave
+__device__ __forceinline__ float shared_gate(const MoeArgs& a, int row, int lane)
+{
+    const uint16_t* xr = a.x + (size_t) row * a.x_stride;
+    float dot = 0.0f;
+    for (int i = 2 * lane; i < a.H; i += 128)
+    {
+        dot += h2f(xr, i) * h2f(a.sh_gate_w, i);
+        if (i + 1 < a.H) dot += h2f(xr, i + 1) * h2f(a.sh_gate_w, i + 1);
+    }
+    dot = wave_sum(dot, lane);
+    return 1.0f / (1.0f + __expf(-dot));
+}
+
+// Token without an active slot: its output chunk is the shared-expert term or zeros (:605-643)
+__device__ void write_empty_row_chunk(const MoeArgs& a, int row, int chunk, int lane)
+{
+    const int col = chunk * 128 + 2 * lane;
+    float o0 = 0.0f, o1 = 0.0f;
+    if (a.sh_out)
+    {
+        const float gv = a.sh_gate_w ? shared_gate(a, row, lane) : 1.0f;
+        const float* sh = a.sh_out + (size_t) row * a.H + col;
+        if (col < a.H) o0 = gv * *to_global(sh);
+        if (col + 1 < a.H) o1 = gv * *to_global(sh + 1);
+    }
+    float* dst = a.out + (size_t) row * a.out_stride + col;
+    if (col < a.H_out) *to_global_w(dst) = o0;
+    if (col + 1 < a.H_out) *to_global_w(dst + 1) = o1;
+}
+
+// Input rotation of one 128-chunk of a slot's x row: zero-padded to Hi, * suh (fp32), Hadamard,
+// fp16 (:646-663)
+__device__ void rotate_chunk(const MoeArgs& a, int row, const uint16_t* suh, int c, uint16_t* dst, int lane)
+{
+    const int col = c * 128 + 2 * lane;
+    const uint16_t* xr = a.x + (size_t) row * a.x_stride;
+    float v0 = col < a.H ? h2f(xr, col) : 0.0f;
+    float v1 = col + 1 < a.H ? h2f(xr, col + 1) : 0.0f;
+    v0 *= h2f(suh, col);
+    v1 *= h2f(suh, col + 1);
+    fwht128_wave(v0, v1, lane);
+    const f16x2 o = { (f16) (v0 * EXL3_HAD_RSCALE), (f16) (v1 * EXL3_HAD_RSCALE) };
+    *to_global_w((uint32_t*) (dst + col)) = as_u32(o);
+}
+
+// ---- run table (exl3_moe_coop_kernel.cuh:273-356): active slots sorted by (local expert, slot),
+// runs of at most ROWS slots of one expert.  Layout [n_runs, -, run_start[slots_max + 1],
+// order[slots_max]].  One workgroup of NT >= slots threads.
+__device__ void build_runs(const MoeArgs& a)
+{
+    __shared__ int sh_local[256];
+    __shared__ int sh_order[256];
+    __shared__ int sh_cnt[NW];
+    __shared__ int sh_nact;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int slots = a.bsz * a.topk;
+    int* run_start = a.runs + 2;
+    int* order = a.runs + 2 + a.slots_max + 1;
+    if (t < slots)
+    {
+        const SlotInfo si = slot_info(a, t);
+        sh_local[t] = si.active ? si.local : -1;
+    }
+    if (t == 0) sh_nact = 0;
+    __syncthreads();
+    if (t < slots && sh_local[t] >= 0)
+    {
+        const int e = sh_local[t];
+        int rank = 0;
+        for (int u = 0; u < slots; ++u)
+        {
+            const int eu = sh_local[u];
+            rank += (eu >= 0 && (eu < e || (eu == e && u < t))) ? 1 : 0;
+        }
+        sh_order[rank] = t;
+        atomicMax(&sh_nact, rank + 1);
+    }
+    __syncthreads();
+    const int n_active = sh_nact;
+    int is_start = 0;
+    if (t < n_active)
+    {
+        const int e_t = sh_local[sh_order[t]];
+        int first = 0;
+        for (int u = 0; u < slots; ++u)
+        {
+            const int eu = sh_local[u];
+            first += (eu >= 0 && eu < e_t) ? 1 : 0;
+        }
+        is_start = (t == 0 || sh_local[sh_order[t - 1]] != e_t || (t - first) % ROWS == 0) ? 1 : 0;
+        *to_global_w(order + t) = sh_order[t];
+    }
+    const uint64_t bal = __ballot(is_start);
+    const int prefix = __popcll(bal & ((1ull << lane) - 1));
+    if (lane == 0) sh_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int base = 0, total = 0;
+    for (int w = 0; w < NW; ++w)
+    {
+        if (w < wave) base += sh_cnt[w];
+        total += sh_cnt[w];
+    }
+    if (is_start) *to_global_w(run_start + base + prefix) = t;
+    if (t == 0)
+    {
+        *to_global_w(run_start + total) = n_active;
+        *to_global_w(a.runs) = total;
+    }
+}
+
+__global__ __launch_bounds__(NT)
+void moe_route_kernel(const MoeArgs a)
+{
+    if (blockIdx.x == 0) build_runs(a);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nproj = a.gated ? 2 : 1;
+    const int chunks = a.Hi / 128;
+    const int slots = a.bsz * a.topk;
+    const int item = blockIdx.x * NW + wave;
+    if (item >= slots * chunks * nproj) return;
+    const int s = item / (chunks * nproj);
+    const int rem = item % (chunks * nproj);
+    const int c = rem / nproj;
+    const bool is_gate = a.gated && (rem % nproj) == 0;
+    const SlotInfo si = slot_info(a, s);
+    if (!si.active)
+    {
+        if (rem % nproj == 0 && s % a.topk == 0 && token_active_slots(a, si.row) == 0)
+            for (int oc = c; oc < a.Ho / 128; oc += chunks) write_empty_row_chunk(a, si.row, oc, lane);
+        return;
+    }
+    const uint16_t* suh = tab<uint16_t>(is_gate ? a.g_suh : a.u_suh, si.local);
+    uint16_t* dst = (is_gate ? a.had_g : a.had_u) + (size_t) s * a.Hi;
+    rotate_chunk(a, si.row, suh, c, dst, lane);
+}
+
+// ---- the multi-row GEMV of one workgroup: rows = the run's slots (x in LDS as (x, x) pairs,
+// xs[r * xs_stride + i] for k-slices [ks0, ks0 + nks)), one 128-column chunk of the expert's
+// trellis.  Same decode and v_dot2 as the dense GEMV.  Leaves res[r][128] fp32 (MUL1 affine
+// correction applied).
+template <int K, int CB>
+__device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
+                         const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);
+    const int myn = nks > wave ? (nks - wave + NW - 1) / NW : 0;
+    const size_t kstride = (size_t) NW * tiles_n * 8 * K;
+    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
+                         + ((size_t) (ks0 + min(wave, nks - 1)) * tiles_n + chunk * 8) * (8 * K);
+    constexpr int PF = EXL3_GEMV_PF;
+    const int last_i = myn > 0 ? myn - 1 : 0;
+    const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
+    uint32_t ring[PF][K + 1];
+    #pragma unroll
+    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+
+    float acc[ROWS][2];
+    #pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.0f;
+
+    for (int i0 = 0; i0 < myn; i0 += PF)
+    {
+        #pragma unroll
+        for (int d = 0; d < PF; ++d)
+        {
+            const int i = i0 + d;
+            const bool live = i < myn;
+            const int xo = (wave + min(i, last_i) * NW) * 16;
+            uint32_t wv[K + 1];
+            #pragma unroll
+            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            uint32_t raw[32];
+            raw32<K, CB>(wv, raw, a3, b3);
+            load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
+            #pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+            {
+                if (r >= nrows) break;
+                const u32x4* xp = (const u32x4*) (xs + r * xs_stride + xo);
+                uint32_t x16[16];
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    u32x4 tq = xp[q];
+                    x16[4 * q] = live ? tq.x : 0u;     x16[4 * q + 1] = live ? tq.y : 0u;
+                    x16[4 * q + 2] = live ? tq.z : 0u; x16[4 * q + 3] = live ? tq.w : 0u;
+                }
+                #pragma unroll
+                for (int w = 0; w < 32; ++w)
+                {
+                    const int gq = w >> 3, jj = w & 7;
+                    const int row = 2 * gq + (jj & 1) + 8 * ((jj >> 1) & 1);
+                    float& acc_ = acc[r][jj >> 2];
+                    acc_ = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc_, false);
+                }
+            }
+        }
+    }
+    const int c0 = (lane >> 3) * 16 + (lane & 7);
+    #pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+    {
+        if (r >= nrows) break;
+        red[(wave * ROWS + r) * 128 + c0] = acc[r][0];
+        red[(wave * ROWS + r) * 128 + c0 + 8] = acc[r][1];
+    }
+    __shared__ float sumx[ROWS];
+    if (CB == 2)
+    {
+        for (int r = wave; r < nrows; r += NW)
+        {
+            float sv = 0.0f;
+            for (int e = lane; e < nks * 16; e += 64) sv += (float) as_h2(xs[r * xs_stride + e]).x;
+            sv = wave_sum(sv, lane);
+            if (lane == 0) sumx[r] = sv;
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nrows * 128; e += NT)
+    {
+        const int r = e >> 7, c = e & 127;
+        float v = 0.0f;
+        #pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[(w * ROWS + r) * 128 + c];
+        if (CB == 2) v = v * (float) as_h(0x1eee) + sumx[r] * (float) as_h(0xc931);
+        res[r * 128 + c] = v;
+    }
+    __syncthreads();
+}
+
+template <int CB>
+__device__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
+                           const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
+{
+    switch (bits)
+    {
+        case 1: moe_gemv<1, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 2: moe_gemv<2, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 3: moe_gemv<3, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 4: moe_gemv<4, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 5: moe_gemv<5, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 6: moe_gemv<6, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 7: moe_gemv<7, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        default: moe_gemv<8, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+    }
+}
+
+// ---- hand-off (all threads): release this workgroup's stores, count it; true in the last of
+// `total` arrivals, which re-arms the counter.  XCD mode: every arrival on the counter runs on
+// one XCD (workgroup scope meets in its L2); else device scope.
+__device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag, bool xcd)
+{
+    if (xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        int prev;
+        if (xcd) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == total - 1;
+        if (last)
+        {
+            if (xcd) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            else __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *flag = last;
+    }
+    __syncthreads();
+    const bool last = *flag;
+    if (last)
+    {
+        if (xcd) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    return last;
+}
+
+// device-scope load (misses L1): data another workgroup of this launch wrote
+__device__ __forceinline__ f32x2 load_l2_f32x2(const float* p)
+{
+    return __builtin_bit_cast(f32x2, __hip_atomic_load(to_global((const uint64_t*) p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// workgroup -> (chunk, rest): chunk c on XCD c % xcd when enabled
+__device__ __forceinline__ void chunk_coords(int xcd, int chunks, int& chunk, int& rest)
+{
+    if (xcd > 0)
+    {
+        const int x = blockIdx.x % xcd, b = blockIdx.x / xcd, cq = chunks / xcd;
+        chunk = x + xcd * (b % cq);
+        rest = b / cq;
+    }
+    else
+    {
+        chunk = blockIdx.x % chunks;
+        rest = blockIdx.x / chunks;
+    }
+}
+
+// x rows of the run (fp16 rows of `src`, row stride `ld`) for k-slices [ks0, ks0 + nks) into LDS
+// as (x, x) pairs
+__device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* rows, int nrows, int ks0, int nks,
+                                        uint32_t* xs, int xs_stride)
+{
+    const int per_row = nks * 8;                          // u32 pairs of fp16 per row
+    for (int e = threadIdx.x; e < nrows * per_row; e += NT)
+    {
+        const int r = e / per_row, i = e - r * per_row;
+        const uint32_t v = *to_global((const uint32_t*) (src + (size_t) rows[r] * ld + ks0 * 16) + i);
+        const f16x2 h = as_h2(v);
+        const f16x2 d0 = { h.x, h.x }, d1 = { h.y, h.y };
+        *(u32x2*) (xs + r * xs_stride + 2 * i) = (u32x2) { as_u32(d0), as_u32(d1) };
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, int& nrows)
+{
+    const int n_runs = *to_global(a.runs);
+    if (run >= n_runs) return false;
+    const int start = *to_global(a.runs + 2 + run), end = *to_global(a.runs + 3 + run);
+    nrows = end - start;
+    if ((int) threadIdx.x < nrows) rows[threadIdx.x] = *to_global(a.runs + 2 + a.slots_max + 1 + start + threadIdx.x);
+    __syncthreads();
+    return true;
+}
+
+template <int CB>
+__global__ __launch_bounds__(NT)
+void moe_a_kernel(const MoeArgs a)
+{
+    extern __shared__ uint32_t smem[];
+    __shared__ int rows[ROWS];
+    __shared__ int flag;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nproj = a.gated ? 2 : 1;
+    const int chunks = a.I / 128;
+    const int slots = a.bsz * a.topk;
+    const int S = a.splits_a;
+    int chunk, rest;
+    chunk_coords(a.xcd, chunks, chunk, rest);
+    const int q = rest % S;
+    const int pr = (rest / S) % nproj;
+    const int run = rest / S / nproj;
+    const bool is_gate = a.gated && pr == 0;
+    int nrows = 0;
+    if (!read_run(a, run, rows, nrows)) return;
+    const int local = slot_info(a, rows[0]).local;
+    const int bits = a.g_bits ? (int) *to_global((is_gate ? a.g_bits : a.u_bits) + local) : a.K_gu;
+    const int KS = a.Hi / 16;
+    const int ks0 = KS * q / S, nks = KS * (q + 1) / S - ks0;
+    const int xs_stride = SBMAX * 16 + 4;
+    uint32_t* xs = smem;
+    float* red = (float*) (smem + ROWS * xs_stride);
+    float* res = red + NW * ROWS * 128;
+    stage_x(is_gate ? a.had_g : a.had_u, a.Hi, rows, nrows, ks0, nks, xs, xs_stride);
+    moe_gemv_k<CB>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0, nks,
+                   xs, xs_stride, nrows, red, res);
+    // split partials: part_a[proj][split][slot][I]
+    for (int e = threadIdx.x; e < nrows * 64; e += NT)
+    {
+        const int r = e >> 6, c2 = e & 63;
+        float* dst = a.part_a + (((size_t) pr * S + q) * slots + rows[r]) * a.I + chunk * 128 + 2 * c2;
+        *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+    }
+    for (int r = 0; r < nrows; ++r)
+    {
+        const int s = rows[r];
+        if (!arrive_last(a.ctr_a + ((size_t) s * chunks + chunk) * 32, nproj * S, &flag, a.xcd > 0)) continue;
+        if (wave == 0)
+        {
+            const int col = chunk * 128 + 2 * lane;
+            auto load_sum = [&](int p, float& v0, float& v1) {
+                v0 = v1 = 0.0f;
+                for (int qq = 0; qq < S; ++qq)
+                {
+                    const f32x2 t = load_l2_f32x2(a.part_a + (((size_t) p * S + qq) * slots + s) * a.I + col);
+                    v0 += t.x; v1 += t.y;
+                }
+            };
+            float u0, u1;
+            load_sum(a.gated ? 1 : 0, u0, u1);
+            fwht128_wave(u0, u1, lane);
+            u0 *= EXL3_HAD_RSCALE; u1 *= EXL3_HAD_RSCALE;
+            const uint16_t* usvh = tab<uint16_t>(a.u_svh, local);
+            u0 *= h2f(usvh, col); u1 *= h2f(usvh, col + 1);
+            if (a.u_bias)
+            {
+                const uint16_t* b = tab<uint16_t>(a.u_bias, local);
+                u0 += h2f(b, col); u1 += h2f(b, col + 1);
+            }
+            float g0 = u0, g1 = u1;
+            if (a.gated)
+            {
+                load_sum(0, g0, g1);
+                fwht128_wave(g0, g1, lane);
+                g0 *= EXL3_HAD_RSCALE; g1 *= EXL3_HAD_RSCALE;
+                const uint16_t* gsvh = tab<uint16_t>(a.g_svh, local);
+                g0 *= h2f(gsvh, col); g1 *= h2f(gsvh, col + 1);
+                if (a.g_bias)
+                {
+                    const uint16_t* b = tab<uint16_t>(a.g_bias, local);
+                    g0 += h2f(b, col); g1 += h2f(b, col + 1);
+                }
+            }
+            float a0 = act_gate(a.act, a.gated, g0, u0, a.act_limit);
+            float a1 = act_gate(a.act, a.gated, g1, u1, a.act_limit);
+            const uint16_t* dsuh = tab<uint16_t>(a.d_suh, local);
+            a0 *= h2f(dsuh, col); a1 *= h2f(dsuh, col + 1);
+            fwht128_wave(a0, a1, lane);
+            const f16x2 o = { (f16) (a0 * EXL3_HAD_RSCALE), (f16) (a1 * EXL3_HAD_RSCALE) };
+            *to_global_w((uint32_t*) (a.act_out + (size_t) s * a.I + col)) = as_u32(o);
+        }
+        __syncthreads();
+    }
+}
+
+template <int CB>
+__global__ __launch_bounds__(NT)
+void moe_b_kernel(const MoeArgs a)
+{
+    extern __shared__ uint32_t smem[];
+    __shared__ int rows[ROWS];
+    __shared__ int flag;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunks = a.Ho / 128;
+    const int slots = a.bsz * a.topk;
+    const int S = a.splits_b;
+    int chunk, rest;
+    chunk_coords(a.xcd, chunks, chunk, rest);
+    const int q = rest % S;
+    const int run = rest / S;
+    int nrows = 0;
+    if (!read_run(a, run, rows, nrows)) return;
+    const int local = slot_info(a, rows[0]).local;
+    const int bits = a.d_bits ? (int) *to_global(a.d_bits + local) : a.K_d;
+    const int KS = a.I / 16;
+    const int ks0 = KS * q / S, nks = KS * (q + 1) / S - ks0;
+    const int xs_stride = SBMAX * 16 + 4;
+    uint32_t* xs = smem;
+    float* red = (float*) (smem + ROWS * xs_stride);
+    float* res = red + NW * ROWS * 128;
+    stage_x(a.act_out, a.I, rows, nrows, ks0, nks, xs, xs_stride);
+    moe_gemv_k<CB>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xs, xs_stride, nrows, red, res);
+    for (int e = threadIdx.x; e < nrows * 64; e += NT)
+    {
+        const int r = e >> 6, c2 = e & 63;
+        float* dst = a.part_b + ((size_t) q * slots + rows[r]) * a.Ho + chunk * 128 + 2 * c2;
+        *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+    }
+    for (int r = 0; r < nrows; ++r)
+    {
+        const int s = rows[r];
+        const int row = s / a.topk;
+        const int expect = token_active_slots(a, row) * S;
+        if (!arrive_last(a.ctr_b + ((size_t) row * chunks + chunk) * 32, expect, &flag, a.xcd > 0)) continue;
+        if (wave == 0)
+        {
+            const int col = chunk * 128 + 2 * lane;
+            float o0 = 0.0f, o1 = 0.0f;
+            // slots k = w, w + 16, ... summed per w, then the partitions in order (:960-979)
+            for (int w = 0; w < WKR; ++w)
+            {
+                float p0 = 0.0f, p1 = 0.0f;
+                for (int k = w; k < a.topk; k += WKR)
+                {
+                    const int sk = row * a.topk + k;
+                    const SlotInfo sj = slot_info(a, sk);
+                    if (!sj.active) continue;
+                    float v0 = 0.0f, v1 = 0.0f;
+                    for (int qq = 0; qq < S; ++qq)
+                    {
+                        const f32x2 t = load_l2_f32x2(a.part_b + ((size_t) qq * slots + sk) * a.Ho + col);
+                        v0 += t.x; v1 += t.y;
+                    }
+                    fwht128_wave(v0, v1, lane);
+                    v0 *= EXL3_HAD_RSCALE; v1 *= EXL3_HAD_RSCALE;
+                    const uint16_t* dsvh = tab<uint16_t>(a.d_svh, sj.local);
+                    v0 *= h2f(dsvh, col); v1 *= h2f(dsvh, col + 1);
+                    if (a.d_bias)
+                    {
+                        const uint16_t* b = tab<uint16_t>(a.d_bias, sj.local);
+                        v0 += h2f(b, col); v1 += h2f(b, col + 1);
+                    }
+                    p0 += sj.w * v0;
+                    p1 += sj.w * v1;
+                }
+                o0 += p0;
+                o1 += p1;
+            }
+            if (a.sh_out)
+            {
+                const float gv = a.sh_gate_w ? shared_gate(a, row, lane) : 1.0f;
+                const float* sh = a.sh_out + (size_t) row * a.H + col;
+                if (col < a.H) o0 += gv * *to_global(sh);
+                if (col + 1 < a.H) o1 += gv * *to_global(sh + 1);
+            }
+            float* dst = a.out + (size_t) row * a.out_stride + col;
+            if (col < a.H_out) *to_global_w(dst) = o0;
+            if (col + 1 < a.H_out) *to_global_w(dst + 1) = o1;
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+// Launch the three stages.  Dynamic LDS: x pairs + the wave reduction + the result rows.
+#define EXL3_CAT2(a, b) a##b
+#define EXL3_CAT(a, b) EXL3_CAT2(a, b)
+
+int EXL3_CAT(exl3k_moe_cb, EXL3_MOE_CB)(const MoeArgs& a, hipStream_t s)
+{
+    const int nproj = a.gated ? 2 : 1;
+    const int slots = a.bsz * a.topk;
+    const size_t lds = ((size_t) ROWS * (SBMAX * 16 + 4) + (size_t) NW * ROWS * 128 + (size_t) ROWS * 128) * 4;
+    const int rot_items = slots * (a.Hi / 128) * nproj;
+    hipLaunchKernelGGL(moe_route_kernel, dim3((rot_items + NW - 1) / NW), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
+    hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+    return (int) hipGetLastError();
+}

@@ -256,6 +256,86 @@ def ptr_array(tensors, device=None) -> Tensor:
     return torch.tensor(vals, dtype=torch.long, device=device if device is not None else "cuda")
 
 
+MOE_ACT = {"silu": 0, "gelu": 1, "relu2": 2, "silu_oai": 3}
+
+
+def moe_coop_ctr_len(slots_max: int, bsz_max: int, I: int, Ho: int) -> int:
+    """int32 scratch length of exl3_moe_coop (exl3_moe_coop.cuh:163-166)."""
+    return slots_max * (I // 128) + bsz_max * (Ho // 128) + 2 + (slots_max + 1) + slots_max
+
+
+def exl3_moe_coop(x: Tensor, sel: Tensor, rw: Tensor, min_expert: int, max_expert: int, Hi: int,
+                  g_trellis: Tensor, g_suh: Tensor, g_svh: Tensor,
+                  u_trellis: Tensor, u_suh: Tensor, u_svh: Tensor,
+                  d_trellis: Tensor, d_suh: Tensor, d_svh: Tensor,
+                  g_bias: Optional[Tensor], u_bias: Optional[Tensor], d_bias: Optional[Tensor],
+                  Kg: float, Ku: float, Kd: float, mcg: bool, mul1: bool, act: int, act_limit: float,
+                  gated: bool, had_g: Tensor, had_u: Tensor, gu_g: Tensor, gu_u: Tensor, act_out: Tensor,
+                  d_out: Tensor, ctr: Tensor, out: Tensor, sh_out: Optional[Tensor] = None,
+                  sh_gate_w: Optional[Tensor] = None, bits_g: Optional[Tensor] = None,
+                  bits_u: Optional[Tensor] = None, bits_d: Optional[Tensor] = None) -> None:
+    """Fused decode-shaped MoE, the tensor front end of exl3_moe_coop (exl3_moe_coop.cu:307-371):
+    out (fp32, rows >= bsz) gets every token's routed experts summed with their routing weights
+    (+ the shared expert).  Pointer tables are int64 device tensors indexed by local expert."""
+    _dtype(x, torch.half, "x")
+    _dtype(sel, torch.long, "sel")
+    _dtype(rw, torch.half, "rw")
+    _need(sel.is_contiguous() and rw.is_contiguous(), "exl3_moe_coop: sel/rw must be contiguous")
+    _need(sel.shape == rw.shape and sel.dim() == 2 and sel.size(0) == x.size(0),
+          "exl3_moe_coop: sel/rw must be (bsz, topk)")
+    _need(x.dim() == 2 and x.stride(1) == 1, "exl3_moe_coop: x must be (bsz, H) with unit column stride")
+    if sh_out is not None:
+        _dtype(sh_out, torch.float, "sh_out")
+        _need(sh_out.is_contiguous() and sh_out.size(-1) == x.size(1) and sh_out.numel() >= x.size(0) * x.size(1),
+              "exl3_moe_coop: shared expert output shape")
+    _dtype(ctr, torch.int32, "ctr")
+    _need(ctr.is_contiguous(), "exl3_moe_coop: ctr must be contiguous")
+    for t in (g_trellis, g_suh, g_svh, u_trellis, u_suh, u_svh, d_trellis, d_suh, d_svh):
+        _need(t.dtype == torch.long and t.is_contiguous(), "exl3_moe_coop: pointer tables must be contiguous int64")
+    for t, name in ((had_g, "had_g"), (had_u, "had_u"), (act_out, "act_out")):
+        _dtype(t, torch.half, name)
+    _dtype(d_out, torch.float, "d_out")
+    _dtype(out, torch.float, "out")
+    _need(gu_u.dtype in (torch.half, torch.float) and gu_g.dtype == gu_u.dtype,
+          "exl3_moe_coop: gate/up scratch dtype mismatch")
+    I, Ho = gu_u.size(-1), d_out.size(-1)
+    for t, w in ((had_g, Hi), (had_u, Hi), (gu_g, I), (gu_u, I), (act_out, I), (d_out, Ho)):
+        _need(t.is_contiguous() and t.size(-1) == w, "exl3_moe_coop: scratch shape")
+    _need(out.dim() >= 2 and out.stride(-1) == 1, "exl3_moe_coop: out shape")
+    if sh_gate_w is not None:
+        _dtype(sh_gate_w, torch.half, "sh_gate_w")
+        _need(sh_gate_w.is_contiguous(), "exl3_moe_coop: shared gate weight must be contiguous")
+    bits = (bits_g, bits_u, bits_d)
+    if any(b is not None for b in bits):
+        _need(all(b is not None for b in bits), "exl3_moe_coop: give all three bit width tables or none")
+        for b in bits:
+            _need(b.dtype == torch.uint8 and b.is_contiguous() and b.numel() >= u_trellis.size(0),
+                  "exl3_moe_coop: bit width tables must be contiguous uint8, one entry per expert")
+    _cuda(x, sel, rw, ctr, out, had_g, had_u, act_out, d_out, gu_g, gu_u, sh_out, sh_gate_w, *bits)
+    for b in (g_bias, u_bias, d_bias):
+        if b is not None:
+            _need(b.dtype == torch.long, "exl3_moe_coop: bias tables must be int64")
+    with torch.cuda.device(x.device):
+        check(_lib.lib().exl3_amd_moe_coop(
+            x.data_ptr(), x.size(0), x.size(1), x.stride(0),
+            sel.data_ptr(), rw.data_ptr(), sel.size(1),
+            int(min_expert), int(max_expert), int(Hi),
+            g_trellis.data_ptr(), g_suh.data_ptr(), g_svh.data_ptr(),
+            u_trellis.data_ptr(), u_suh.data_ptr(), u_svh.data_ptr(),
+            d_trellis.data_ptr(), d_suh.data_ptr(), d_svh.data_ptr(), u_trellis.size(0),
+            _ptr(g_bias), _ptr(u_bias), _ptr(d_bias),
+            float(Kg), float(Ku), float(Kd), int(bool(mcg)), int(bool(mul1)), int(act), float(act_limit),
+            int(bool(gated)),
+            had_g.data_ptr(), had_g.numel(), had_u.data_ptr(), had_u.numel(),
+            gu_g.data_ptr(), gu_u.data_ptr(), min(gu_g.numel(), gu_u.numel()), int(gu_u.dtype == torch.float), I,
+            act_out.data_ptr(), act_out.numel(), d_out.data_ptr(), d_out.numel(), Ho,
+            ctr.data_ptr(), ctr.numel(),
+            out.data_ptr(), out.size(-2), out.size(-1), out.stride(-2),
+            _ptr(sh_out), _ptr(sh_gate_w), sh_gate_w.numel() if sh_gate_w is not None else 0,
+            _ptr(bits_g), _ptr(bits_u), _ptr(bits_d),
+            _stream(x)))
+
+
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
                     mul1: bool = False, mcg: bool = False) -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to

@@ -118,6 +118,37 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
                    const int* had_src_list, int num_had_src_list, int num_had_src,
                    void* stream);
 
+/* Fused decode-shaped MoE: out[t] = sum over token t's active slots k (expert e = sel[t, k],
+ * rw[t, k] != 0, inside [min_expert, max_expert) when min_expert >= 0) of
+ * rw[t, k] * down_e(act(gate_e(x_t), up_e(x_t))) (+ sigmoid-gated shared expert sh_out).
+ * Tables (n_local entries of device addresses): g/u/d trellis, suh, svh (+ optional bias);
+ * bits_g/u/d (uint8 per expert, mul1 only) select mixed widths, else Kg = Ku, Kd.  act: 0 SiLU,
+ * 1 GELU, 2 ReLU^2, 3 clamped SwiGLU; gated = 0: act = relu(u) * u.  Scratch: had_g / had_u
+ * (slots, Hi) fp16, act_out (slots, I) fp16, d_out (slots, Ho) fp32, gu_g / gu_u (slots, I)
+ * (sizes checked; the library keeps its split partials in its own workspace), ctr int32 of at
+ * least slots_max * I/128 + rows_max * Ho/128 + 2 + 2 * slots_max + 1 entries: the run table
+ * (active slots sorted by (expert, slot), runs of <= 8) is written at offset
+ * slots_max * I/128 + rows_max * Ho/128.  out fp32 (rows_max, H_out) row stride out_stride.
+ * Replaces exl3_moe_coop (vendor/exl3/exllamav3_ext/quant/exl3_moe_coop.cu:185-371, kernels
+ * exl3_moe_coop_kernel.cuh:231-1000), declared at src/torch/amp_torch.cpp:7783-7837 and bound
+ * at :7853 (torch.moe_coop). */
+int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
+                      const int64_t* sel, const uint16_t* rw, int topk,
+                      int min_expert, int max_expert, int Hi,
+                      const uint64_t* g_trellis, const uint64_t* g_suh, const uint64_t* g_svh,
+                      const uint64_t* u_trellis, const uint64_t* u_suh, const uint64_t* u_svh,
+                      const uint64_t* d_trellis, const uint64_t* d_suh, const uint64_t* d_svh, int n_local,
+                      const uint64_t* g_bias, const uint64_t* u_bias, const uint64_t* d_bias,
+                      float Kg, float Ku, float Kd, int mcg, int mul1, int act, float act_limit, int gated,
+                      uint16_t* had_g, int64_t had_g_numel, uint16_t* had_u, int64_t had_u_numel,
+                      void* gu_g, void* gu_u, int64_t gu_numel, int gu_f32, int I,
+                      uint16_t* act_out, int64_t act_out_numel, float* d_out, int64_t d_out_numel, int Ho,
+                      int* ctr, int64_t ctr_numel,
+                      float* out, int rows_max, int H_out, int out_stride,
+                      const float* sh_out, const uint16_t* sh_gate_w, int sh_gate_n,
+                      const uint8_t* bits_g, const uint8_t* bits_u, const uint8_t* bits_d,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

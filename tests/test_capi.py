@@ -149,3 +149,48 @@ def test_mgemm_rejects_bad_arguments():
         assert rc < 0 and text in msg, (kw, msg)
     # nothing to do: empty batch rows
     assert L.exl3_amd_mgemm(*mgemm_args(m=0)) == _lib.TAG_GEMV
+
+
+def moe_args(**kw):
+    f = ctypes.c_float
+    order = (("x", 1), ("bsz", 2), ("H", 256), ("xs", 256), ("sel", 1), ("rw", 1), ("topk", 4),
+             ("min", -1), ("max", -1), ("Hi", 256),
+             ("gt", 1), ("gs", 1), ("gv", 1), ("ut", 1), ("us", 1), ("uv", 1), ("dt", 1), ("ds", 1), ("dv", 1),
+             ("n_local", 16), ("gb", None), ("ub", None), ("db", None),
+             ("Kg", f(3.0)), ("Ku", f(3.0)), ("Kd", f(3.0)), ("mcg", 0), ("mul1", 1), ("act", 0),
+             ("limit", f(0.0)), ("gated", 1),
+             ("hg", 1), ("hg_n", 8 * 256), ("hu", 1), ("hu_n", 8 * 256),
+             ("gug", 1), ("guu", 1), ("gu_n", 8 * 256), ("gu32", 1), ("I", 256),
+             ("ao", 1), ("ao_n", 8 * 256), ("do", 1), ("do_n", 8 * 256), ("Ho", 256),
+             ("ctr", 1), ("ctr_n", 1 << 16),
+             ("out", 1), ("rows_max", 2), ("H_out", 256), ("ostride", 256),
+             ("sh", None), ("shg", None), ("shg_n", 0), ("bg", None), ("bu", None), ("bd", None),
+             ("stream", None))
+    return [kw.get(name, d) for name, d in order]
+
+
+def test_moe_coop_rejects_bad_arguments():
+    """The TORCH_CHECKs of exl3_moe_coop_prepare / _run (quant/exl3_moe_coop.cu:185-305)."""
+    L = _lib.lib()
+    f = ctypes.c_float
+    cases = [
+        (dict(mcg=1), "both"),
+        (dict(Kd=f(9.0)), "K out of range"),
+        (dict(Kg=f(2.0)), "share a bit width"),
+        (dict(act=4), "unknown activation"),
+        (dict(I=200), "Hi/I/Ho"),
+        (dict(H_out=512), "Hi/I/Ho"),
+        (dict(hg_n=100), "1..256 slots"),
+        (dict(ctr_n=10), "counter scratch"),
+        (dict(bg=1), "all three"),
+        (dict(H=258), "H/Hi"),
+        (dict(bsz=3), "exceeds the scratch"),
+        (dict(min=0, max=40), "expert range"),
+        (dict(sh=1, H=128), "shared expert output width"),
+        (dict(bg=1, bu=1, bd=1, mul1=0), "mul1"),
+        (dict(gt=None), "pointer tables"),
+    ]
+    for kw, text in cases:
+        rc, msg = call_err(L.exl3_amd_moe_coop, *moe_args(**kw))
+        assert rc < 0 and text in msg, (kw, msg)
+    assert L.exl3_amd_moe_coop(*moe_args(bsz=0)) == 0          # no tokens: nothing to do
