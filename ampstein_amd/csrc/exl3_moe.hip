@@ -141,7 +141,7 @@ __device__ __forceinline__ float shared_gate(const MoeArgs& a, int row, int lane
 }
 
 // Token without an active slot: its output chunk is the shared-expert term or zeros (:605-643)
-__device__ void write_empty_row_chunk(const MoeArgs& a, int row, int chunk, int lane)
+__device__ __forceinline__ void write_empty_row_chunk(const MoeArgs& a, int row, int chunk, int lane)
 {
     const int col = chunk * 128 + 2 * lane;
     float o0 = 0.0f, o1 = 0.0f;
@@ -159,7 +159,7 @@ __device__ void write_empty_row_chunk(const MoeArgs& a, int row, int chunk, int 
 
 // Input rotation of one 128-chunk of a slot's x row: zero-padded to Hi, * suh (fp32), Hadamard,
 // fp16 (:646-663)
-__device__ void rotate_chunk(const MoeArgs& a, int row, const uint16_t* suh, int c, uint16_t* dst, int lane)
+__device__ __forceinline__ void rotate_chunk(const MoeArgs& a, int row, const uint16_t* suh, int c, uint16_t* dst, int lane)
 {
     const int col = c * 128 + 2 * lane;
     const uint16_t* xr = a.x + (size_t) row * a.x_stride;
@@ -175,7 +175,7 @@ __device__ void rotate_chunk(const MoeArgs& a, int row, const uint16_t* suh, int
 // ---- run table (exl3_moe_coop_kernel.cuh:273-356): active slots sorted by (local expert, slot),
 // runs of at most ROWS slots of one expert.  Layout [n_runs, -, run_start[slots_max + 1],
 // order[slots_max]].  One workgroup of NT >= slots threads.
-__device__ void build_runs(const MoeArgs& a)
+__device__ __forceinline__ void build_runs(const MoeArgs& a)
 {
     __shared__ int sh_local[256];
     __shared__ int sh_order[256];
@@ -267,8 +267,8 @@ void moe_route_kernel(const MoeArgs a)
 // xs[r * xs_stride + i] for k-slices [ks0, ks0 + nks)), one 128-column chunk of the expert's
 // trellis.  Same decode and v_dot2 as the dense GEMV.  Leaves res[r][128] fp32 (MUL1 affine
 // correction applied).
-template <int K, int CB>
-__device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
+template <int K, int CB, int MT>
+__device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
                          const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
     const int lane = threadIdx.x & 63;
@@ -278,16 +278,16 @@ __device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks
     const size_t kstride = (size_t) NW * tiles_n * 8 * K;
     const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
                          + ((size_t) (ks0 + min(wave, nks - 1)) * tiles_n + chunk * 8) * (8 * K);
-    constexpr int PF = EXL3_GEMV_PF;
+    constexpr int PF = (MT == 1 && K <= 4) ? 4 : 2;
     const int last_i = myn > 0 ? myn - 1 : 0;
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
     uint32_t ring[PF][K + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
 
-    float acc[ROWS][2];
+    float acc[MT][2];
     #pragma unroll
-    for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    for (int r = 0; r < MT; ++r) acc[r][0] = acc[r][1] = 0.0f;
 
     for (int i0 = 0; i0 < myn; i0 += PF)
     {
@@ -304,9 +304,9 @@ __device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks
             raw32<K, CB>(wv, raw, a3, b3);
             load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
             #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
+            for (int r = 0; r < MT; ++r)
             {
-                if (r >= nrows) break;
+                if (MT > 1 && r >= nrows) break;
                 const u32x4* xp = (const u32x4*) (xs + r * xs_stride + xo);
                 uint32_t x16[16];
                 #pragma unroll
@@ -329,9 +329,9 @@ __device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks
     }
     const int c0 = (lane >> 3) * 16 + (lane & 7);
     #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+    for (int r = 0; r < MT; ++r)
     {
-        if (r >= nrows) break;
+        if (MT > 1 && r >= nrows) break;
         red[(wave * ROWS + r) * 128 + c0] = acc[r][0];
         red[(wave * ROWS + r) * 128 + c0 + 8] = acc[r][1];
     }
@@ -359,20 +359,23 @@ __device__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks
     __syncthreads();
 }
 
-template <int CB>
-__device__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
+template <int CB, int MT>
+__device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
                            const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
+#ifdef EXL3_MOE_ONLY_K
+    moe_gemv<EXL3_MOE_ONLY_K, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); return;
+#endif
     switch (bits)
     {
-        case 1: moe_gemv<1, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 2: moe_gemv<2, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 3: moe_gemv<3, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 4: moe_gemv<4, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 5: moe_gemv<5, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 6: moe_gemv<6, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 7: moe_gemv<7, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        default: moe_gemv<8, CB>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 1: moe_gemv<1, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 2: moe_gemv<2, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 3: moe_gemv<3, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 4: moe_gemv<4, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 5: moe_gemv<5, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 6: moe_gemv<6, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 7: moe_gemv<7, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        default: moe_gemv<8, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
     }
 }
 
@@ -457,7 +460,7 @@ __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, i
     return true;
 }
 
-template <int CB>
+template <int CB, int MT>
 __global__ __launch_bounds__(NT)
 void moe_a_kernel(const MoeArgs a)
 {
@@ -486,7 +489,7 @@ void moe_a_kernel(const MoeArgs a)
     float* red = (float*) (smem + ROWS * xs_stride);
     float* res = red + NW * ROWS * 128;
     stage_x(is_gate ? a.had_g : a.had_u, a.Hi, rows, nrows, ks0, nks, xs, xs_stride);
-    moe_gemv_k<CB>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0, nks,
+    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0, nks,
                    xs, xs_stride, nrows, red, res);
     // split partials: part_a[proj][split][slot][I]
     for (int e = threadIdx.x; e < nrows * 64; e += NT)
@@ -547,7 +550,7 @@ void moe_a_kernel(const MoeArgs a)
     }
 }
 
-template <int CB>
+template <int CB, int MT>
 __global__ __launch_bounds__(NT)
 void moe_b_kernel(const MoeArgs a)
 {
@@ -573,7 +576,7 @@ void moe_b_kernel(const MoeArgs a)
     float* red = (float*) (smem + ROWS * xs_stride);
     float* res = red + NW * ROWS * 128;
     stage_x(a.act_out, a.I, rows, nrows, ks0, nks, xs, xs_stride);
-    moe_gemv_k<CB>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xs, xs_stride, nrows, red, res);
+    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xs, xs_stride, nrows, red, res);
     for (int e = threadIdx.x; e < nrows * 64; e += NT)
     {
         const int r = e >> 6, c2 = e & 63;
@@ -648,7 +651,16 @@ int EXL3_CAT(exl3k_moe_cb, EXL3_MOE_CB)(const MoeArgs& a, hipStream_t s)
     const size_t lds = ((size_t) ROWS * (SBMAX * 16 + 4) + (size_t) NW * ROWS * 128 + (size_t) ROWS * 128) * 4;
     const int rot_items = slots * (a.Hi / 128) * nproj;
     hipLaunchKernelGGL(moe_route_kernel, dim3((rot_items + NW - 1) / NW), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
-    hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+    // one slot per run when every token has distinct picks (one token): single-row GEMV
+    if (a.bsz == 1)
+    {
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+    }
+    else
+    {
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+    }
     return (int) hipGetLastError();
 }

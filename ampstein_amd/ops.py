@@ -17,6 +17,8 @@ from __future__ import annotations
 
 from typing import Optional
 
+import os
+
 import torch
 
 from . import _lib
@@ -24,7 +26,7 @@ from ._lib import check
 
 Tensor = torch.Tensor
 
-RECON_FUSED_ROWS = 2048      # amp_torch.cpp:11203-11209 (AMP_RECON_FUSED_ROWS default)
+RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", "2048"))   # amp_torch.cpp:11203-11209
 
 
 def _ptr(t: Optional[Tensor]):
@@ -337,7 +339,7 @@ def exl3_moe_coop(x: Tensor, sel: Tensor, rw: Tensor, min_expert: int, max_exper
 
 
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
-                    mul1: bool = False, mcg: bool = False) -> Tensor:
+                    mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None) -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to
     fp16 once, then one dense GEMM.  rows >= 2048: original-basis W and y = x @ W; otherwise
     y = had(had(x o suh) @ W_hat) o svh.  The dense GEMM is torch.mm (hipBLASLt)."""
@@ -348,7 +350,7 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
     rows = x.size(0)
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device)
     w = torch.empty((k, n), dtype=x.dtype, device=x.device)
-    if rows >= RECON_FUSED_ROWS:
+    if rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows):
         reconstruct_had_slice(w, trellis, suh, svh, K, mcg, mul1, 0)
         torch.mm(x, w, out=y)
     else:

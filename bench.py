@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-prefill", action="store_true", help="skip the M = 2048 prefill GEMM line")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE expert GEMV line")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
@@ -199,6 +201,136 @@ def graph_time(torch, sweep, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+
+# ------------------------------------------------------------------ prefill GEMM
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def timed(torch, fn, reps=5):
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def prefill_bench(torch):
+    """M = 2048 fp16 x N(0,1) against 8192->28672 and 28672->8192 at 4 bpw (3INST).  Paths:
+    recon = the reference's routing for rows >= 2048 (amp_torch.cpp:11149-11230: our
+    reconstruct_had, then one hipBLASLt fp16 GEMM); recon_rotated = its rows < 2048 branch
+    (input/output Hadamard around W_hat); fused = our MFMA kernel (exl3_gemm, m > 8)."""
+    from ampstein_amd import ops
+    M = 2048
+    res = {}
+    g = torch.Generator(device="cuda")
+    for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
+        g.manual_seed(4000 + si)
+        t = torch.randint(-32768, 32768, (k // 16, n // 16, 64), dtype=torch.int16, device="cuda", generator=g)
+        s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
+        v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
+        x = torch.randn((M, k), device="cuda", generator=g).half()
+        ah = torch.empty_like(x)
+        C = torch.empty((M, n), dtype=torch.half, device="cuda")
+        flops = 2.0 * M * k * n
+        row = {}
+        for name, fn in (("recon", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=2048)),
+                         ("recon_rotated", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30)),
+                         ("fused", lambda: ops.exl3_gemm(x, t, C, s, ah, v))):
+            us = timed(torch, fn)
+            row[name] = {"us": round(us, 1), "TFLOPS": round(flops / us / 1e6, 1),
+                         "frac_mfma_peak": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+        res[f"{k}x{n}"] = row
+        del t, s, v, x, ah, C
+        torch.cuda.empty_cache()
+    best = {name: sum(2.0 * M * int(sh.split("x")[0]) * int(sh.split("x")[1]) for sh in res) /
+            sum(res[sh][name]["us"] for sh in res) / 1e6 for name in ("recon", "recon_rotated", "fused")}
+    path = max(best, key=best.get)
+    return {"metric": "prefill GEMM TFLOPS at M=2048 (configs[3], 4 bpw 3INST)", "m": M,
+            "value": round(best[path], 1), "unit": "TFLOPS", "path": path,
+            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best[path] / MFMA_F16_PEAK_TFLOPS, 4),
+            "paths_TFLOPS": {k2: round(v2, 1) for k2, v2 in best.items()}, "per_shape": res}
+
+
+# ------------------------------------------------------------------ MoE expert GEMV (configs[4])
+def moe_bench(torch, reps=8):
+    """256 experts, gate/up 4096->2048, down 2048->4096, K per expert from {2,3,4} (seeded), mul1;
+    router logits N(0,1), softmax top-8; M in {1, 8, 16}.  Algorithmic bytes = packed bytes of the
+    distinct routed experts.  `reps` different routings rotate through one graph so the routed
+    experts change between calls (the 256 MB MALL cannot hold them)."""
+    import numpy as np
+    from ampstein_amd import ops
+    E, Hi, I, Ho, topk = 256, 4096, 2048, 4096, 8
+    rng = np.random.default_rng(5000)
+    Ks = rng.choice([2, 3, 4], E)
+    g = torch.Generator(device="cuda")
+    mats = []
+    for e in range(E):
+        trio = []
+        for pi, (k, n) in enumerate(((Hi, I), (Hi, I), (I, Ho))):
+            g.manual_seed(6000 + 3 * e + pi)
+            t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * int(Ks[e])), dtype=torch.int16, device="cuda",
+                              generator=g)
+            s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
+            v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
+            trio.append((t, s, v))
+        mats.append(trio)
+    P = lambda vals: torch.tensor(vals, dtype=torch.long, device="cuda")
+    tabs = [P([mats[e][pi][j].data_ptr() for e in range(E)]) for pi in range(3) for j in range(3)]
+    bits = torch.tensor(Ks, dtype=torch.uint8, device="cuda")
+    per_expert = {e: int(Ks[e]) * (2 * Hi * I + I * Ho) // 8 for e in range(E)}
+    res = {}
+    for M in (1, 8, 16):
+        slots = M * topk
+        routs = []
+        for r in range(reps):
+            logits = rng.standard_normal((M, E))
+            p = np.exp(logits - logits.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            sel = np.argsort(-p, axis=1, kind="stable")[:, :topk]
+            rw = np.take_along_axis(p, sel, 1).astype(np.float16)
+            routs.append((torch.from_numpy(sel.astype(np.int64)).cuda(), torch.from_numpy(rw).cuda(),
+                          sum(per_expert[int(e)] for e in set(sel.reshape(-1).tolist()))))
+        x = torch.randn((M, Hi), device="cuda", generator=g).half()
+        z = lambda *sh, dt=torch.half: torch.zeros(sh, dtype=dt, device="cuda")
+        had_g, had_u, act_out = z(slots, Hi), z(slots, Hi), z(slots, I)
+        gu = z(slots, I, dt=torch.float)
+        d_out = z(slots, Ho, dt=torch.float)
+        ctr = torch.zeros(ops.moe_coop_ctr_len(slots, M, I, Ho), dtype=torch.int32, device="cuda")
+        out = z(M, Ho, dt=torch.float)
+
+        def call(sel, rw):
+            ops.exl3_moe_coop(x, sel, rw, -1, -1, Hi, *tabs, None, None, None, 4.0, 4.0, 4.0, False, True, 0, 0.0,
+                              True, had_g, had_u, gu, gu, act_out, d_out, ctr, out, None, None, bits, bits, bits)
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            for sel, rw, _ in routs:
+                call(sel, rw)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for sel, rw, _ in routs:
+                call(sel, rw)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(4):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (4 * reps)
+        nbytes = sum(r[2] for r in routs) / reps
+        res[f"M{M}"] = {"us_per_call": round(us, 2), "routed_bytes": round(nbytes), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"metric": "MoE mixed-K expert GEMV GB/s (configs[4]: 256 experts, K in {2,3,4}, mul1, top-8)",
+            "launches_per_call": 3, "per_m": res}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -417,6 +549,12 @@ def main():
                                 "launches_per_step": len(separate.entries)},
         "wall_s": round(wall, 3),
     }
+    del bundled, separate, layers
+    torch.cuda.empty_cache()
+    if not args.no_prefill:
+        out["prefill"] = prefill_bench(torch)
+    if not args.no_moe:
+        out["moe"] = moe_bench(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
