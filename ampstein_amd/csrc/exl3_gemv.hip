@@ -37,6 +37,10 @@
 #define EXL3_INST_K 4
 #endif
 // Prefetch ring depth (k-slices in flight per wave); HBM needs many bytes in flight
+// dot products of the M = 1 stream on MFMA (1) or v_dot2 (0)
+#ifndef EXL3_GEMV_MFMA
+#define EXL3_GEMV_MFMA 1
+#endif
 #ifndef EXL3_GEMV_PF
 #define EXL3_GEMV_PF (EXL3_INST_K <= 4 ? 4 : 2)
 #endif
@@ -672,6 +676,14 @@ void gemv1_kernel(const GemvArgs g)
     const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
 
     float acc0 = 0.0f, acc1 = 0.0f, sx = 0.0f;
+#if EXL3_GEMV_MFMA
+    // Dot products on the matrix pipe: v_mfma_f32_4x4x4_16b_f16 with A = two decoded words of
+    // this lane (lo, hi of windows w, w + 1) and B = (x_r, x_r, x_r+1, x_r+1), the same for every
+    // lane: lane l's own dot accumulates in element l % 4 of the 4 x 4 block result.  The x pairs
+    // come from LDS (broadcast reads, no VALU); 2 accumulators per column break the chains.
+    __shared__ __align__(16) uint32_t xdup[GEMV_WAVES][2][128];
+    f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
+#endif
     for (int c = 0; c < nchunks; ++c)
     {
         const uint32_t xr = rotate_pair(xv, sv, has_suh, lane);
@@ -682,6 +694,15 @@ void gemv1_kernel(const GemvArgs g)
             const bool mine = WS == 8 || (lane >= lane0 && lane < lane0 + 8 * per);
             sx += wave_sum(mine ? (float) p.x + (float) p.y : 0.0f, lane);
         }
+#if EXL3_GEMV_MFMA
+        uint32_t* xd = xdup[wave][c & 1];
+        {
+            const f16x2 p = as_h2(xr);
+            const f16x2 d0 = { p.x, p.x }, d1 = { p.y, p.y };
+            *(u32x2*) (xd + 2 * lane) = (u32x2) { as_u32(d0), as_u32(d1) };
+        }
+        __builtin_amdgcn_wave_barrier();
+#endif
         // prefetch the next chunk's x (clamped: stays inside this wave's range)
         const int cn = min(c + 1, nchunks - 1);
         xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8 + cn) * 64);
@@ -697,6 +718,27 @@ void gemv1_kernel(const GemvArgs g)
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
             load_slot<K>(base + (size_t) min(i + PF, last) * rstride, prev_off, ring[d]);
+#if EXL3_GEMV_MFMA
+            // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
+            const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            #pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+            {
+                #pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    const u32x2 xb = *(const u32x2*) (xs + 2 * gq + 8 * h);
+                    const h4 bx = __builtin_bit_cast(h4, xb);
+                    // windows w = 8 gq + 2 h (+1): column a; + 4: column b
+                    const int w = 8 * gq + 2 * h;
+                    const h4 wa = __builtin_bit_cast(h4, (u32x2) { raw[w], raw[w + 1] });
+                    const h4 wb = __builtin_bit_cast(h4, (u32x2) { raw[w + 4], raw[w + 5] });
+                    accv[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wa, bx, accv[h], 0, 0, 0);
+                    accv[2 + h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wb, bx, accv[2 + h], 0, 0, 0);
+                }
+            }
+#else
             // this slice's 16 inputs: lanes lane0 + 8 s8 .. + 7 hold pairs (x[2q], x[2q+1])
             uint32_t x16[16];
             #pragma unroll
@@ -714,8 +756,17 @@ void gemv1_kernel(const GemvArgs g)
                 float& acc = (jj >> 2) ? acc1 : acc0;
                 acc = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc, false);
             }
+#endif
         }
     }
+#if EXL3_GEMV_MFMA
+    {
+        const int e = lane & 3;
+        auto pick = [&](const f32x4& v) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; };
+        acc0 = pick(accv[0]) + pick(accv[1]);
+        acc1 = pick(accv[2]) + pick(accv[3]);
+    }
+#endif
 
     GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(acc0 + acc1)));
     const int c0 = (lane >> 3) * 16 + (lane & 7);
