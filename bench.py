@@ -458,7 +458,7 @@ def summarize_trace(path):
     with open(path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if "gemv" not in name and "reconstruct" not in name and "had128" not in name and "gemm" not in name:
+            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_")):
                 continue
             grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
             d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
