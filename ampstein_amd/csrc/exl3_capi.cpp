@@ -114,6 +114,9 @@ int init_device(int device, DeviceState** out)
                 int* probe = (int*) p;
                 int nx = 0;
                 bool ok = true;
+                // the probe's launch status is read with hipGetLastError: drop any error an earlier
+                // call of the host process (not this library) left pending
+                (void) hipGetLastError();
                 for (int si = 0; si < 4 && ok; ++si)
                 {
                     const int total = gx[si] * gy[si];
@@ -126,9 +129,15 @@ int init_device(int device, DeviceState** out)
                         int mx = 0;
                         for (int i = 0; i < total; ++i) mx = host[i] > mx ? host[i] : mx;
                         if (si == 0) nx = mx + 1;
-                        // linear workgroup id (x fastest) -> XCD, round-robin
-                        for (int i = 0; i < total && ok; ++i) ok = host[i] == i % nx;
+                        // linear workgroup id (x fastest) -> XCD, round-robin from wherever the
+                        // previous dispatch on the queue left off: workgroups b and b + nx share an
+                        // XCD, which is all the hand-off needs
+                        for (int i = 0; i < total && ok; ++i) ok = host[i] == (host[0] + i) % nx;
                     }
+                    if (getenv("EXL3_AMD_DEBUG") && host)
+                        fprintf(stderr, "exl3_amd: xcd probe %d (%dx%d): ok %d nx %d first %d %d %d %d %d %d %d %d %d\n", si,
+                                gx[si], gy[si], (int) ok, nx, host[0], host[1], host[2], host[3], host[4], host[5], host[6],
+                                host[7], host[8]);
                     free(host);
                 }
                 d.num_xcd = ok && nx >= 1 ? nx : 0;
@@ -145,8 +154,12 @@ int init_device(int device, DeviceState** out)
     return 0;
 }
 
+// Every entry point that launches comes through here.  The launchers report their launch
+// status with hipGetLastError, so a stale error left by other code in the process is dropped
+// first: it would otherwise be reported as this call's failure.
 int current_device(DeviceState** out)
 {
+    (void) hipGetLastError();
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(EXL3_AMD_EHIP, "hipGetDevice failed");
     return init_device(dev, out);
@@ -272,6 +285,15 @@ int exl3_amd_init(int device)
 {
     DeviceState* d;
     return init_device(device, &d);
+}
+
+int exl3_amd_device_info(int device, int* num_cus, int* num_xcd)
+{
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    if (num_cus) *num_cus = d->num_cus;
+    if (num_xcd) *num_xcd = d->num_xcd;
+    return 0;
 }
 
 int exl3_amd_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n_packed, int n,

@@ -1,7 +1,8 @@
 // Device-side helpers of the C-ABI layer:
 //  - topology probe: which XCD (accelerator complex die, each with its own L2) runs each
 //    workgroup.  The GEMV's XCD-local split-k hand-off relies on MI355X dispatching linear
-//    workgroup b to XCD b % 8; exl3_amd_init verifies that on the device before enabling it.
+//    workgroup b to XCD (b + c) % 8, c fixed per launch, so workgroups b and b + 8 share an XCD;
+//    exl3_amd_init verifies that on the device before enabling it.
 //  - mgemm expert-range filter (quant/exl3_gemm_kernel.cuh:98-143): selections outside
 //    [min_index, max_index) are removed (one token: compacted) or masked to -1 (several tokens),
 //    retained indices rebased by min_index.

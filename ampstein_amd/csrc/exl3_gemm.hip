@@ -174,7 +174,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     const int nbn = (n + BN - 1) / BN, nmb = (M + BM - 1) / BM;   // n % 128 == 0: a last block may be half
 
     // workgroup -> (column block, row block): the row blocks of one column block run together on
-    // one XCD (workgroup b on XCD b % 8) when the block count allows, sharing its trellis in L2
+    // one XCD (workgroups b and b + 8 on one XCD) when the block count allows, sharing its trellis in L2
     int nb, mb;
     if (nbn % 8 == 0)
     {

@@ -36,7 +36,7 @@ struct GemvArgs
     int slices_per_block;       // SB: k-slices (16 rows x 128 columns) per workgroup, divides k/16
     int slots;                  // split partials per column chunk: k/16 / SB
     int xs_chunks;              // rotated 128-row input chunks held in LDS (LDS kernel)
-    int xcd;                    // > 0: XCD-local hand-off through L2 counters (workgroup b on XCD b % xcd)
+    int xcd;                    // > 0: XCD-local hand-off through L2 counters (workgroups b and b + xcd on one XCD)
     float* partials;            // workspace: bszm * slots * m * n fp32
     int* counters;              // workspace: zeroed; [0, half) per (slot, chunk), [half, ..) per chunk
     int counters_half;

@@ -48,6 +48,12 @@ int exl3_amd_version(void);
  * Replaces DevCtx::get_locks (vendor/exl3/exllamav3_ext/quant/exl3_devctx.cu:81-93). */
 int exl3_amd_init(int device);
 
+/* Topology the library planned for on `device` (initialising it if needed): compute units and
+ * the number of XCDs whose round-robin workgroup dispatch was verified on the device (0: the
+ * XCD-local split-k hand-off is off and a finish kernel sums the partials).  No counterpart in
+ * the reference; for tests and benchmarks. */
+int exl3_amd_device_info(int device, int* num_cus, int* num_xcd);
+
 /* W_hat (k, n) fp16 = decoded trellis columns [n_offset, n_offset + n) of a packed tensor
  * whose full width is n_packed, in the Hadamard basis.  k % 16 == 0, n % 128 == 0,
  * n_offset % 128 == 0.  Bit-exact with the reference.
