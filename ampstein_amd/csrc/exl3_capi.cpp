@@ -190,6 +190,14 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
         if (best < 0 || (long) bszm * chunks * (KS / best) > target) best = d;   // fewest blocks >= target
         if ((long) bszm * chunks * (KS / d) <= target) break;
     }
+    // M = 1 stream: 8 k-slices per wave (16 from k = 8192), the best split measured on MI355X for
+    // the Llama-3-8B shapes (4096 x {1024, 4096, 14336}, 14336 x 4096) at 1-3.5 waves per SIMD
+    if (stream)
+    {
+        const int pref = k >= 8192 ? 64 : 32;
+        for (int d = pref; d >= 4; d /= 2)
+            if (ok_sb(d) && ((size_t) (KS / d) * bszm * m * n * 4 <= WS_PARTIAL_BYTES || KS / d == 1)) { best = d; break; }
+    }
     if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && ok_sb(v)) best = v; }
     if (best < 0) return -1;
     if ((size_t) (KS / best) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / best > 1) return -1;
@@ -233,6 +241,35 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     g.xcd = 0;
     if (d->num_xcd > 0 && chunks % d->num_xcd == 0 && pairs * 32 <= WS_COUNTERS / 2)
         g.xcd = d->num_xcd;
+    // M = 1 balanced stream: one wave per SIMD slot at 4 waves per SIMD, equal runs of slices
+    // (exl3_gemv.hip gemv1p_kernel).  Needs the XCD-local hand-off and per-slot tables of at
+    // most 16 slots without indices or routing weights.
+    // Opt-in (EXL3_AMD_GEMV_P1=1) until its GPU run is cleared.
+    bool p1 = g.m == 1 && g.stream_m1 && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16;
+    {
+        const char* e = getenv("EXL3_AMD_GEMV_P1");
+        p1 = p1 && e && atoi(e) != 0;
+    }
+    if (p1)
+    {
+        const int xg = d->num_xcd;
+        const long units = (long) g.bszm * chunks;                       // upper bound (widths <= n)
+        const long slices = units * (g.k / 16);
+        int lmin = 2;
+        if (const char* e = getenv("EXL3_AMD_P1_LMIN")) { int v = atoi(e); if (v > 0) lmin = v; }
+        long waves = (slices + lmin - 1) / lmin;
+        const long max_waves = (long) d->num_cus * 4 * 4;
+        if (const char* e = getenv("EXL3_AMD_P1_WAVES")) { long v = atol(e); if (v > 0) waves = v; }
+        waves = std::min(std::max(waves, (long) 4 * xg), max_waves);
+        const long per_group = (waves / 4 + xg - 1) / xg;
+        // unit counters: [0, units); partial slots: at most waves + 2 units pieces of 128 floats
+        if (units * 32 <= (long) (WS_COUNTERS / 2) && (size_t) (per_group * xg * 4 + 2 * units) * 512 <= WS_PARTIAL_BYTES)
+        {
+            g.xcd = xg;
+            g.stream_m1 = 2;
+            g.p1_blocks = (int) (per_group * xg);
+        }
+    }
     int rc = dispatch_gemv(bits, cb, g, s);
     return rc ? hip_fail(rc, what) : 0;
 }
