@@ -1,6 +1,6 @@
 // Standalone Hadamard-128 rotation (had_r_128, quant/hadamard.cu:125-210) for gfx950.
-// y[r, 128c .. 128c+127] = H128(x[r, chunk] (o pre)) * scale / sqrt(128) (o post), one wave64
-// per 128-element chunk (lane l holds elements 2l, 2l+1), in place allowed.
+// y[r, 128c .. 128c+127] = H128(x[r, chunk] (o pre)) * scale / sqrt(128) (o post), 16 lanes per
+// 128-element chunk, in place allowed (a chunk is read whole before it is written).
 // fp16 data: had_hf_r_128_inner (pre/post scales are fp16 multiplies, fp32 butterfly);
 // fp32 data: had_ff_r_128_inner (scales applied in fp32).
 #include "exl3_common.cuh"
@@ -10,53 +10,136 @@ using namespace exl3;
 
 namespace {
 
+// Lane mapping: 16 lanes per 128-element chunk, lane g of the group holds elements 8g .. 8g+7
+// (one 16-byte fp16 load, two for fp32), so a wave rotates 4 chunks per step with coalesced
+// loads.  Butterfly stages in the reference's order, widths 1, 2, 4 in-lane and 8, 16, 32, 64
+// across lanes (DPP xor 1, 2, 4, 8 inside the 16-lane row): every stage writes a + b / a - b with
+// one fp32 rounding, so the result is bit-identical to any other placement of the same stages.
+__device__ __forceinline__ void fwht8_inlane(float* e)
+{
+    #pragma unroll
+    for (int w = 1; w < 8; w <<= 1)
+    {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            if (i & w) continue;
+            const float a = e[i], b = e[i + w];
+            e[i] = a + b;
+            e[i + w] = a - b;
+        }
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void fwht8_stage(float* e, int lane)
+{
+    const float sg = (lane & M) ? -1.0f : 1.0f;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        const float p = xor_partner<M>(e[i], lane);
+        e[i] = __builtin_fmaf(sg, e[i], p);
+    }
+}
+
 template <bool FP32>
 __global__ __launch_bounds__(256)
-void had128_kernel(const void* __restrict__ in, void* __restrict__ out, int rows, int cols,
+void had128_kernel(const void* __restrict__ in, void* __restrict__ out, long jobs, int cols,
                    const uint16_t* __restrict__ pre, const uint16_t* __restrict__ post, float r_scale)
 {
     const int lane = threadIdx.x & 63;
+    const int g = lane & 15;
     const int chunks = cols / 128;
-    const long job = (long) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (job >= (long) rows * chunks) return;
-    const int row = (int) (job / chunks), c = (int) (job % chunks);
-    const int col = c * 128 + 2 * lane;
-    const size_t idx = (size_t) row * cols + col;
-    float v0, v1;
-    if constexpr (FP32)
+    const long step = (long) gridDim.x * 16;
+    for (long base = ((long) blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; base < jobs; base += step)
     {
-        float2 v = *(const float2*) ((const float*) in + idx);
-        v0 = v.x; v1 = v.y;
-        if (pre)
+        const long job = base + (lane >> 4);
+        const bool valid = job < jobs;
+        const long jc = valid ? job : jobs - 1;
+        const long row = jc / chunks;
+        const int c = (int) (jc - row * chunks);
+        const int col = c * 128 + 8 * g;
+        const size_t idx = (size_t) row * cols + col;
+        float e[8];
+        if constexpr (FP32)
         {
-            f16x2 s = as_h2(*(const uint32_t*) (pre + col));
-            v0 *= (float) s.x; v1 *= (float) s.y;
+            const f32x4* src = (const f32x4*) ((const float*) in + idx);
+            const f32x4 a = __builtin_nontemporal_load(to_global(src)), b = __builtin_nontemporal_load(to_global(src) + 1);
+            e[0] = a.x; e[1] = a.y; e[2] = a.z; e[3] = a.w; e[4] = b.x; e[5] = b.y; e[6] = b.z; e[7] = b.w;
+            if (pre)
+            {
+                const u32x4 sv = *to_global((const u32x4*) (pre + col));
+                const uint32_t sw[4] = { sv.x, sv.y, sv.z, sv.w };
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    const f16x2 s2 = as_h2(sw[q]);
+                    e[2 * q] *= (float) s2.x;
+                    e[2 * q + 1] *= (float) s2.y;
+                }
+            }
         }
-    }
-    else
-    {
-        f16x2 v = as_h2(*(const uint32_t*) ((const uint16_t*) in + idx));
-        if (pre) v = v * as_h2(*(const uint32_t*) (pre + col));
-        v0 = (float) v.x; v1 = (float) v.y;
-    }
-    fwht128_wave(v0, v1, lane);
-    v0 *= r_scale;
-    v1 *= r_scale;
-    if constexpr (FP32)
-    {
-        if (post)
+        else
         {
-            f16x2 s = as_h2(*(const uint32_t*) (post + col));
-            v0 *= (float) s.x; v1 *= (float) s.y;
+            const u32x4 v = __builtin_nontemporal_load(to_global((const u32x4*) ((const uint16_t*) in + idx)));
+            uint32_t vw[4] = { v.x, v.y, v.z, v.w };
+            if (pre)
+            {
+                const u32x4 sv = *to_global((const u32x4*) (pre + col));
+                const uint32_t sw[4] = { sv.x, sv.y, sv.z, sv.w };
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) vw[q] = as_u32(as_h2(vw[q]) * as_h2(sw[q]));    // fp16 multiply
+            }
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const f16x2 h = as_h2(vw[q]);
+                e[2 * q] = (float) h.x;
+                e[2 * q + 1] = (float) h.y;
+            }
         }
-        float2 o = { v0, v1 };
-        *(float2*) ((float*) out + idx) = o;
-    }
-    else
-    {
-        f16x2 h = { (f16) v0, (f16) v1 };
-        if (post) h = h * as_h2(*(const uint32_t*) (post + col));
-        *(uint32_t*) ((uint16_t*) out + idx) = as_u32(h);
+        fwht8_inlane(e);
+        fwht8_stage<1>(e, lane);
+        fwht8_stage<2>(e, lane);
+        fwht8_stage<4>(e, lane);
+        fwht8_stage<8>(e, lane);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] *= r_scale;
+        if (!valid) continue;
+        if constexpr (FP32)
+        {
+            if (post)
+            {
+                const u32x4 sv = *to_global((const u32x4*) (post + col));
+                const uint32_t sw[4] = { sv.x, sv.y, sv.z, sv.w };
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    const f16x2 s2 = as_h2(sw[q]);
+                    e[2 * q] *= (float) s2.x;
+                    e[2 * q + 1] *= (float) s2.y;
+                }
+            }
+            f32x4* dst = (f32x4*) ((float*) out + idx);
+            __builtin_nontemporal_store((f32x4) { e[0], e[1], e[2], e[3] }, to_global_w(dst));
+            __builtin_nontemporal_store((f32x4) { e[4], e[5], e[6], e[7] }, to_global_w(dst) + 1);
+        }
+        else
+        {
+            uint32_t ow[4];
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) ow[q] = as_u32((f16x2) { (f16) e[2 * q], (f16) e[2 * q + 1] });
+            if (post)
+            {
+                const u32x4 sv = *to_global((const u32x4*) (post + col));
+                const uint32_t sw[4] = { sv.x, sv.y, sv.z, sv.w };
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) ow[q] = as_u32(as_h2(ow[q]) * as_h2(sw[q]));  // fp16 multiply
+            }
+            __builtin_nontemporal_store((u32x4) { ow[0], ow[1], ow[2], ow[3] },
+                                        to_global_w((u32x4*) ((uint16_t*) out + idx)));
+        }
     }
 }
 
@@ -68,8 +151,10 @@ int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
     const float r_scale = scale * 0.088388347648f;
     const long jobs = (long) rows * (cols / 128);
     if (jobs == 0) return 0;
-    dim3 grid((unsigned) ((jobs + 3) / 4));
-    if (fp32) hipLaunchKernelGGL(had128_kernel<true>, grid, dim3(256), 0, s, in, out, rows, cols, pre, post, r_scale);
-    else      hipLaunchKernelGGL(had128_kernel<false>, grid, dim3(256), 0, s, in, out, rows, cols, pre, post, r_scale);
+    // 16 chunks per workgroup per step; at most 8 workgroups per CU (grid-stride beyond)
+    const long want = (jobs + 15) / 16;
+    dim3 grid((unsigned) (want < 2048 ? want : 2048));
+    if (fp32) hipLaunchKernelGGL(had128_kernel<true>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale);
+    else      hipLaunchKernelGGL(had128_kernel<false>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale);
     return (int) hipGetLastError();
 }
