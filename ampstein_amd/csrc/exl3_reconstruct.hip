@@ -97,6 +97,50 @@ void reconstruct_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ t
     }
 }
 
+// ---------------------------------------------------------------------------- reconstruct_t
+// W_hat transposed, (n, k) row-major: the layout the recon GEMM reads fastest (both operands
+// k-contiguous).  Same grid as reconstruct_kernel: wave w decodes k-slice 4 blockIdx.y + w of the
+// chunk; lane (tile t, j) holds the 16 rows of columns j and j + 8 of its tile, i.e. 32-byte runs
+// of two transposed rows.  The workgroup's 128 columns x 64 k meet in LDS and leave as whole
+// 128-byte lines (8 threads per transposed row).
+template <int K, int CB>
+__global__ __launch_bounds__(256)
+void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict__ trellis,
+                          int k, int tiles_n, int nt_off)
+{
+    __shared__ __align__(16) uint32_t sh[128][32 + 4];    // [column][64 k as 32 pairs] (+pad)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kt = blockIdx.y * 4 + wave;
+    const int chunk = blockIdx.x;
+    const int nks = min(4, k / 16 - blockIdx.y * 4);     // k-slices of this workgroup
+    if (wave < nks)
+    {
+        const DecodeRegs r = make_decode_regs<CB>();
+        uint32_t p[16];
+        decode_slice<K, CB>(trellis, tiles_n, kt, nt_off + chunk * 8, lane, p, r);
+        // pair q holds rows pair_row(q), +1 of column pair_col(j, q): column j = pairs 0,4,8,12
+        // (rows 0-7) and 1,5,9,13 (rows 8-15); column j + 8 = pairs 2,6,10,14 and 3,7,11,15
+        const int ca = (lane >> 3) * 16 + (lane & 7);
+        *(u32x4*) &sh[ca][8 * wave] = (u32x4) { p[0], p[4], p[8], p[12] };
+        *(u32x4*) &sh[ca][8 * wave + 4] = (u32x4) { p[1], p[5], p[9], p[13] };
+        *(u32x4*) &sh[ca + 8][8 * wave] = (u32x4) { p[2], p[6], p[10], p[14] };
+        *(u32x4*) &sh[ca + 8][8 * wave + 4] = (u32x4) { p[3], p[7], p[11], p[15] };
+    }
+    __syncthreads();
+    // 128 rows x (nks x 32 bytes): thread t writes 16-byte piece t % 8 of rows t / 8 + 32 i
+    const int piece = threadIdx.x & 7;
+    if (piece < 2 * nks)
+    {
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const int row = (threadIdx.x >> 3) + 32 * i;
+            const u32x4 v = *(const u32x4*) &sh[row][4 * piece];
+            *to_global_w((u32x4*) (WT + (size_t) (chunk * 128 + row) * k + blockIdx.y * 64 + 8 * piece)) = v;
+        }
+    }
+}
+
 // -------------------------------------------------------------------------- reconstruct_had
 // One 128x128 block per workgroup.  LDS holds the block as 128 rows x 64 dwords with the
 // dword index of (row R, column pair cp) swizzled to cp ^ (2 * ((R >> 2) & 31)): conflict-free
@@ -212,6 +256,15 @@ int launch_reconstruct_t(uint16_t* W, const uint16_t* trellis, int k, int n, int
 }
 
 template <int K, int CB>
+int launch_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
+                          int nt_off, hipStream_t s)
+{
+    dim3 grid(n / 128, (k / 16 + 3) / 4);
+    hipLaunchKernelGGL((reconstruct_t_kernel<K, CB>), grid, dim3(256), 0, s, WT, trellis, k, tiles_n, nt_off);
+    return (int) hipGetLastError();
+}
+
+template <int K, int CB>
 int launch_reconstruct_had_t(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
                              const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
                              hipStream_t s)
@@ -264,4 +317,10 @@ int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* 
                           int K, int cb, hipStream_t s)
 {
     EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_had_t, W, trellis, suh, svh, k, n, tiles_n, nt_off, s)
+}
+
+int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
+                         int nt_off, int K, int cb, hipStream_t s)
+{
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, s)
 }

