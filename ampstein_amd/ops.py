@@ -26,7 +26,15 @@ from ._lib import check
 
 Tensor = torch.Tensor
 
-RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", "2048"))   # amp_torch.cpp:11203-11209
+# Row count from which exl3_gemm_recon reconstructs the weight in the original basis (one fused
+# W, y = x @ W) instead of rotating x and y around W_hat.  The reference switches at 2048 rows
+# (amp_torch.cpp:11203-11209, models.uc:36-37); on MI355X the rotated form is faster at every
+# measured size (reconstruct_had is ALU-bound, the activation rotations are HBM-bound and short),
+# so by default it is always taken.  AMP_RECON_FUSED_ROWS=2048 restores the reference's routing.
+RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", str(1 << 30)))
+# Tuned dense GEMM for the recon path (PyTorch TunableOp: hipBLASLt and rocBLAS solutions timed
+# per shape on first use): 8-20 % faster than the default heuristic at M = 2048.
+RECON_TUNED_GEMM = os.environ.get("AMP_RECON_TUNABLE", "1") != "0"
 
 
 def _ptr(t: Optional[Tensor]):
@@ -360,11 +368,29 @@ def exl3_moe_coop(x: Tensor, sel: Tensor, rw: Tensor, min_expert: int, max_exper
             _stream(x)))
 
 
+def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
+    """out = a @ b on the dense GEMM library, with TunableOp scoped to this call (the caller's
+    process-wide setting is restored)."""
+    tun = getattr(torch.cuda, "tunable", None)
+    if not RECON_TUNED_GEMM or tun is None:
+        torch.mm(a, b, out=out)
+        return
+    was = tun.is_enabled()
+    if not was:
+        tun.enable(True)
+    try:
+        torch.mm(a, b, out=out)
+    finally:
+        if not was:
+            tun.enable(False)
+
+
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
                     mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None) -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to
     fp16 once, then one dense GEMM.  rows >= 2048: original-basis W and y = x @ W; otherwise
-    y = had(had(x o suh) @ W_hat) o svh.  The dense GEMM is torch.mm (hipBLASLt)."""
+    y = had(had(x o suh) @ W_hat) o svh.  The dense GEMM is torch.mm on hipBLASLt / rocBLAS,
+    tuned per shape (_recon_mm)."""
     _need(trellis.dim() == 3, "exl3_gemm_recon: trellis must be 3-D")
     k, n = trellis.size(0) * 16, trellis.size(1) * 16
     _need(x.dim() == 2 and x.size(1) == k and suh.numel() == k and svh.numel() == n and n <= 32768,
@@ -374,7 +400,7 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
     w = torch.empty((k, n), dtype=x.dtype, device=x.device)
     if rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows):
         reconstruct_had_slice(w, trellis, suh, svh, K, mcg, mul1, 0)
-        torch.mm(x, w, out=y)
+        _recon_mm(x, w, y)
     else:
         # W_hat stored transposed: the GEMM then reads both operands k-contiguous (~15 %
         # faster in hipBLASLt on MI355X at M = 2048)
@@ -382,7 +408,7 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
         had_r_128(x, xh, suh, None, 1.0)
         wt = w.view(n, k)
         reconstruct_t(wt, trellis, K, mcg, mul1)
-        torch.mm(xh, wt.t(), out=y)
+        _recon_mm(xh, wt.t(), y)
         had_r_128(y, y, None, svh, 1.0)
     return y
 
