@@ -263,13 +263,38 @@ void moe_route_kernel(const MoeArgs a)
     rotate_chunk(a, si.row, suh, c, dst, lane);
 }
 
+// Where a run's x rows come from: rows[r] of `src`, row stride `ld` (fp16).
+struct XSrc
+{
+    const uint16_t* src;
+    int ld;
+    const int* rows;
+};
+
+// x rows of the run (fp16 rows of `src`, row stride `ld`) for k-slices [ks0, ks0 + nks) into LDS
+// as (x, x) pairs
+__device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* rows, int nrows, int ks0, int nks,
+                                        uint32_t* xs, int xs_stride)
+{
+    const int per_row = nks * 8;                          // u32 pairs of fp16 per row
+    for (int e = threadIdx.x; e < nrows * per_row; e += NT)
+    {
+        const int r = e / per_row, i = e - r * per_row;
+        const uint32_t v = *to_global((const uint32_t*) (src + (size_t) rows[r] * ld + ks0 * 16) + i);
+        const f16x2 h = as_h2(v);
+        const f16x2 d0 = { h.x, h.x }, d1 = { h.y, h.y };
+        *(u32x2*) (xs + r * xs_stride + 2 * i) = (u32x2) { as_u32(d0), as_u32(d1) };
+    }
+    __syncthreads();
+}
+
 // ---- the multi-row GEMV of one workgroup: rows = the run's slots (x in LDS as (x, x) pairs,
 // xs[r * xs_stride + i] for k-slices [ks0, ks0 + nks)), one 128-column chunk of the expert's
 // trellis.  Same decode and v_dot2 as the dense GEMV.  Leaves res[r][128] fp32 (MUL1 affine
 // correction applied).
 template <int K, int CB, int MT>
 __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
-                         const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
+                         const XSrc& xsrc, uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -284,6 +309,8 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
     uint32_t ring[PF][K + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+    // the x rows after the weight prefetch: both latencies overlap
+    stage_x(xsrc.src, xsrc.ld, xsrc.rows, min(nrows, MT), ks0, nks, xs, xs_stride);   // LDS holds MT rows
 
     float acc[MT][2];
     #pragma unroll
@@ -332,8 +359,8 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
     for (int r = 0; r < MT; ++r)
     {
         if (MT > 1 && r >= nrows) break;
-        red[(wave * ROWS + r) * 128 + c0] = acc[r][0];
-        red[(wave * ROWS + r) * 128 + c0 + 8] = acc[r][1];
+        red[(wave * MT + r) * 128 + c0] = acc[r][0];
+        red[(wave * MT + r) * 128 + c0 + 8] = acc[r][1];
     }
     __shared__ float sumx[ROWS];
     if (CB == 2)
@@ -352,7 +379,7 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
         const int r = e >> 7, c = e & 127;
         float v = 0.0f;
         #pragma unroll
-        for (int w = 0; w < NW; ++w) v += red[(w * ROWS + r) * 128 + c];
+        for (int w = 0; w < NW; ++w) v += red[(w * MT + r) * 128 + c];
         if (CB == 2) v = v * (float) as_h(0x1eee) + sumx[r] * (float) as_h(0xc931);
         res[r * 128 + c] = v;
     }
@@ -361,21 +388,21 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
 
 template <int CB, int MT>
 __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
-                           const uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
+                           const XSrc& xsrc, uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
 #ifdef EXL3_MOE_ONLY_K
-    moe_gemv<EXL3_MOE_ONLY_K, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); return;
+    moe_gemv<EXL3_MOE_ONLY_K, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); return;
 #endif
     switch (bits)
     {
-        case 1: moe_gemv<1, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 2: moe_gemv<2, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 3: moe_gemv<3, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 4: moe_gemv<4, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 5: moe_gemv<5, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 6: moe_gemv<6, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        case 7: moe_gemv<7, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
-        default: moe_gemv<8, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xs, xs_stride, nrows, red, res); break;
+        case 1: moe_gemv<1, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 2: moe_gemv<2, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 3: moe_gemv<3, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 4: moe_gemv<4, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 5: moe_gemv<5, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 6: moe_gemv<6, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        case 7: moe_gemv<7, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        default: moe_gemv<8, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
     }
 }
 
@@ -432,23 +459,6 @@ __device__ __forceinline__ void chunk_coords(int xcd, int chunks, int& chunk, in
     }
 }
 
-// x rows of the run (fp16 rows of `src`, row stride `ld`) for k-slices [ks0, ks0 + nks) into LDS
-// as (x, x) pairs
-__device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* rows, int nrows, int ks0, int nks,
-                                        uint32_t* xs, int xs_stride)
-{
-    const int per_row = nks * 8;                          // u32 pairs of fp16 per row
-    for (int e = threadIdx.x; e < nrows * per_row; e += NT)
-    {
-        const int r = e / per_row, i = e - r * per_row;
-        const uint32_t v = *to_global((const uint32_t*) (src + (size_t) rows[r] * ld + ks0 * 16) + i);
-        const f16x2 h = as_h2(v);
-        const f16x2 d0 = { h.x, h.x }, d1 = { h.y, h.y };
-        *(u32x2*) (xs + r * xs_stride + 2 * i) = (u32x2) { as_u32(d0), as_u32(d1) };
-    }
-    __syncthreads();
-}
-
 __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, int& nrows)
 {
     const int n_runs = *to_global(a.runs);
@@ -486,11 +496,11 @@ void moe_a_kernel(const MoeArgs a)
     const int ks0 = KS * q / S, nks = KS * (q + 1) / S - ks0;
     const int xs_stride = SBMAX * 16 + 4;
     uint32_t* xs = smem;
-    float* red = (float*) (smem + ROWS * xs_stride);
-    float* res = red + NW * ROWS * 128;
-    stage_x(is_gate ? a.had_g : a.had_u, a.Hi, rows, nrows, ks0, nks, xs, xs_stride);
+    float* red = (float*) (smem + MT * xs_stride);     // LDS sized for MT rows (moe_lds_bytes)
+    float* res = red + NW * MT * 128;
+    const XSrc xsrc = { is_gate ? a.had_g : a.had_u, a.Hi, rows };
     moe_gemv_k<CB, MT>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0, nks,
-                   xs, xs_stride, nrows, red, res);
+                   xsrc, xs, xs_stride, nrows, red, res);
     // split partials: part_a[proj][split][slot][I]
     for (int e = threadIdx.x; e < nrows * 64; e += NT)
     {
@@ -573,10 +583,10 @@ void moe_b_kernel(const MoeArgs a)
     const int ks0 = KS * q / S, nks = KS * (q + 1) / S - ks0;
     const int xs_stride = SBMAX * 16 + 4;
     uint32_t* xs = smem;
-    float* red = (float*) (smem + ROWS * xs_stride);
-    float* res = red + NW * ROWS * 128;
-    stage_x(a.act_out, a.I, rows, nrows, ks0, nks, xs, xs_stride);
-    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xs, xs_stride, nrows, red, res);
+    float* red = (float*) (smem + MT * xs_stride);     // LDS sized for MT rows (moe_lds_bytes)
+    float* res = red + NW * MT * 128;
+    const XSrc xsrc = { a.act_out, a.I, rows };
+    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
     for (int e = threadIdx.x; e < nrows * 64; e += NT)
     {
         const int r = e >> 6, c2 = e & 63;
@@ -648,19 +658,21 @@ int EXL3_CAT(exl3k_moe_cb, EXL3_MOE_CB)(const MoeArgs& a, hipStream_t s)
 {
     const int nproj = a.gated ? 2 : 1;
     const int slots = a.bsz * a.topk;
-    const size_t lds = ((size_t) ROWS * (SBMAX * 16 + 4) + (size_t) NW * ROWS * 128 + (size_t) ROWS * 128) * 4;
+    // x rows + the wave reduction + the result rows, for MT rows: the single-row variant needs
+    // 6.7 KB instead of 53 KB, so LDS no longer caps it at 3 workgroups per CU
+    auto moe_lds_bytes = [](int mt) { return ((size_t) mt * (SBMAX * 16 + 4) + (size_t) NW * mt * 128 + (size_t) mt * 128) * 4; };
     const int rot_items = slots * (a.Hi / 128) * nproj;
     hipLaunchKernelGGL(moe_route_kernel, dim3((rot_items + NW - 1) / NW), dim3(NT), 0, s, a);
     // one slot per run when every token has distinct picks (one token): single-row GEMV
     if (a.bsz == 1)
     {
-        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
-        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), moe_lds_bytes(1), s, a);
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), moe_lds_bytes(1), s, a);
     }
     else
     {
-        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), lds, s, a);
-        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), lds, s, a);
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), moe_lds_bytes(ROWS), s, a);
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), moe_lds_bytes(ROWS), s, a);
     }
     return (int) hipGetLastError();
 }
