@@ -242,6 +242,9 @@ __device__ __forceinline__ uint32_t load_l2_u32(const void* p)
 // counts in one counter runs on the same XCD and meets in its L2, where global atomics execute.
 __device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag)
 {
+    // the workgroup-scope release waits for LDS only: wait for this thread's global stores to be
+    // acknowledged by the L2 before the counter can move
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (threadIdx.x == 0)
@@ -717,7 +720,10 @@ void gemv1_kernel(const GemvArgs g)
             for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
-            load_slot<K>(base + (size_t) min(i + PF, last) * rstride, prev_off, ring[d]);
+            // refill with slice i + PF; past the last slice it re-reads slice i, just consumed and
+            // cache-hot, so the hand-off's wait for the partial stores (loads and stores retire in
+            // order) does not wait on HBM.  Unconditional, so the wait counts stay static.
+            load_slot<K>(base + (size_t) (i + PF <= last ? i + PF : i) * rstride, prev_off, ring[d]);
 #if EXL3_GEMV_MFMA
             // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
             const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;

@@ -411,6 +411,9 @@ __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, in
 // one XCD (workgroup scope meets in its L2); else device scope.
 __device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag, bool xcd)
 {
+    // the workgroup-scope release waits for LDS only: wait for this thread's global stores to be
+    // acknowledged by the L2 before the counter can move
+    if (xcd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
