@@ -78,12 +78,51 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     return LIB
 
 
+ADAPTER_DIR = os.path.join(PKG, "adapter")
+
+
+def adapter_path() -> str:
+    import sysconfig
+    return os.path.join(LIB_DIR, "exl3_amd_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_adapter(verbose: bool = False) -> str:
+    """The at::Tensor adapter (adapter/exl3_amd_adapter.cpp) and its Python module: host-only
+    C++ (no device code) built by the host compiler against torch's ROCm headers, linked to
+    libexl3_amd.so (rpath $ORIGIN).  __HIP_PLATFORM_AMD__ is the define hipcc itself passes;
+    the HIP runtime headers that torch's headers include need it."""
+    import sysconfig
+    from torch.utils import cpp_extension as ce
+    out = adapter_path()
+    inc = ce.include_paths(device_type="cuda") + [sysconfig.get_paths()["include"], ADAPTER_DIR,
+                                                    os.path.join(ROOT, "include")]
+    libdirs = ce.library_paths(device_type="cuda")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-fPIC", "-shared", "-std=c++17", "-D__HIP_PLATFORM_AMD__=1",
+           "-DTORCH_EXTENSION_NAME=exl3_amd_torch", "-D_GLIBCXX_USE_CXX11_ABI=1",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", "-DUSE_ROCM=1", "-w"]
+    cmd += [f"-I{d}" for d in inc]
+    cmd += [os.path.join(ADAPTER_DIR, "exl3_amd_adapter.cpp"), os.path.join(ADAPTER_DIR, "exl3_amd_torch.cpp")]
+    cmd += [f"-L{d}" for d in libdirs] + [f"-L{LIB_DIR}", "-lexl3_amd", "-lc10", "-lc10_hip", "-ltorch",
+                                          "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+                                          "-Wl,-rpath,$ORIGIN"]
+    tmp = out + ".tmp"
+    t0 = time.time()
+    p = subprocess.run(cmd + ["-o", tmp], capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"adapter build failed:\n{p.stderr[-6000:]}")
+    shutil.move(tmp, out)
+    if verbose:
+        print(f"  {os.path.basename(out)}: {time.time() - t0:.1f}s", flush=True)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     args = ap.parse_args(argv)
     t0 = time.time()
     path = build(args.j, verbose=True)
+    build_adapter(verbose=True)
     print(f"built {path} in {time.time() - t0:.1f}s")
 
 

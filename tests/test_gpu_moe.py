@@ -39,8 +39,9 @@ def routing(rng, bsz, n_experts, topk):
 
 
 def run(torch, es, x, sel, rw, *, mn=-1, mx=-1, act=0, limit=0.0, gated=True, mixed=True, H_out=None,
-        sh_out=None, sh_gate_w=None, bias=False, slots_max=None, rows_max=None):
+        sh_out=None, sh_gate_w=None, bias=False, slots_max=None, rows_max=None, moe_fn=None):
     from ampstein_amd import ops
+    moe_fn = moe_fn or ops.exl3_moe_coop
     bsz, topk = sel.shape
     H = x.shape[1]
     H_out = H_out or es.Ho
@@ -56,7 +57,7 @@ def run(torch, es, x, sel, rw, *, mn=-1, mx=-1, act=0, limit=0.0, gated=True, mi
     out = torch.full((rows_max, H_out), float("nan"), dtype=torch.float, device="cuda")
     T = es.tables
     K = es.K[0]
-    ops.exl3_moe_coop(dev(x), dev(sel), dev(rw), mn, mx, es.Hi,
+    moe_fn(dev(x), dev(sel), dev(rw), mn, mx, es.Hi,
                       T["g_trellis"], T["g_suh"], T["g_svh"], T["u_trellis"], T["u_suh"], T["u_svh"],
                       T["d_trellis"], T["d_suh"], T["d_svh"],
                       T.get("g_bias") if bias else None, T.get("u_bias") if bias else None,
