@@ -99,6 +99,7 @@ struct MoeArgs
     int* ctr_b;                 // [bsz][Ho/128] x 32
     int splits_a, splits_b;
     int xcd;                    // > 0: chunk c runs on XCD c % xcd (workgroup-scope hand-off)
+    int run_lo, run_hi;         // this launch takes the runs of run_lo + 1 .. run_hi slots
 };
 
 int exl3k_moe_cb0(const MoeArgs& a, hipStream_t s);

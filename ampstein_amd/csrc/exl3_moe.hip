@@ -1,6 +1,6 @@
 // Fused decode-shaped MoE for gfx950 (exl3_moe_coop semantics, quant/exl3_moe_coop_kernel.cuh,
 // quant/exl3_moe_coop.cu): every (token, expert) slot through gate/up, activation and down, with
-// per-expert bit widths (mixed K) or one uniform width.  Three launches:
+// per-expert bit widths (mixed K) or one uniform width.  Three stages:
 //
 //   route   block 0 sorts the active slots by (local expert, slot) and cuts runs of at most 8
 //           slots of one expert into the caller's run table (exl3_moe_coop_kernel.cuh:273-356,
@@ -15,6 +15,9 @@
 //   B       the same GEMV over the down trellis; the last arrival of a (token, chunk) rotates
 //           each active slot's sum * svh (+ bias), weights it by its routing weight, sums the
 //           slots in the reference's fixed order (:917-999), adds the shared expert and stores.
+// A and B each launch once per run size class: single-slot runs with the one-row body (126
+// VGPRs, 4 waves per SIMD), larger runs with the eight-row body.  A token's slots can sit in
+// both classes; its down hand-off counter then collects arrivals from both launches.
 //
 // Hand-offs: counters (one 128-byte line each) in the library workspace; chunk c runs on XCD
 // c % 8 when the chunk counts allow, so the hand-off is an L2-local atomic, else device scope.
@@ -28,6 +31,9 @@
 #endif
 #ifndef EXL3_GEMV_PF
 #define EXL3_GEMV_PF 2
+#endif
+#ifndef EXL3_MOE_PF1
+#define EXL3_MOE_PF1 4          // k-slices in flight per wave, single-row body, K <= 4
 #endif
 
 using namespace exl3;
@@ -272,18 +278,46 @@ struct XSrc
 };
 
 // x rows of the run (fp16 rows of `src`, row stride `ld`) for k-slices [ks0, ks0 + nks) into LDS
-// as (x, x) pairs
+// as (x, x) pairs.  16-byte loads, two per thread in flight before either is consumed: one
+// memory round trip per 2 x 256 x 8 halves instead of one per pair.
 __device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* rows, int nrows, int ks0, int nks,
                                         uint32_t* xs, int xs_stride)
 {
-    const int per_row = nks * 8;                          // u32 pairs of fp16 per row
-    for (int e = threadIdx.x; e < nrows * per_row; e += NT)
+    constexpr int B = 2;
+    const int per_row = nks * 2;                          // 16-byte groups (8 halves) per row
+    const int total = nrows * per_row;
+    for (int e0 = 0; e0 < total; e0 += NT * B)
     {
-        const int r = e / per_row, i = e - r * per_row;
-        const uint32_t v = *to_global((const uint32_t*) (src + (size_t) rows[r] * ld + ks0 * 16) + i);
-        const f16x2 h = as_h2(v);
-        const f16x2 d0 = { h.x, h.x }, d1 = { h.y, h.y };
-        *(u32x2*) (xs + r * xs_stride + 2 * i) = (u32x2) { as_u32(d0), as_u32(d1) };
+        u32x4 v[B];
+        #pragma unroll
+        for (int j = 0; j < B; ++j)
+        {
+            const int e = min(e0 + j * NT + (int) threadIdx.x, total - 1);
+            const int r = e / per_row, i = e - r * per_row;
+            v[j] = *to_global((const u32x4*) (src + (size_t) rows[r] * ld + ks0 * 16) + i);
+        }
+        #pragma unroll
+        for (int j = 0; j < B; ++j)
+        {
+            const int e = e0 + j * NT + (int) threadIdx.x;
+            const int r = e / per_row, i = e - r * per_row;
+            if (e < total)
+            {
+                uint32_t* d = xs + r * xs_stride + 8 * i;
+                const uint32_t w[4] = { v[j].x, v[j].y, v[j].z, v[j].w };
+                uint32_t o[8];
+                #pragma unroll
+                for (int t = 0; t < 4; ++t)
+                {
+                    const f16x2 h = as_h2(w[t]);
+                    const f16x2 d0 = { h.x, h.x }, d1 = { h.y, h.y };
+                    o[2 * t] = as_u32(d0);
+                    o[2 * t + 1] = as_u32(d1);
+                }
+                *(u32x4*) d = (u32x4) { o[0], o[1], o[2], o[3] };
+                *(u32x4*) (d + 4) = (u32x4) { o[4], o[5], o[6], o[7] };
+            }
+        }
     }
     __syncthreads();
 }
@@ -303,12 +337,18 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
     const size_t kstride = (size_t) NW * tiles_n * 8 * K;
     const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
                          + ((size_t) (ks0 + min(wave, nks - 1)) * tiles_n + chunk * 8) * (8 * K);
-    constexpr int PF = (MT == 1 && K <= 4) ? 4 : 2;
+    constexpr int PF = (MT == 1 && K <= 4) ? EXL3_MOE_PF1 : 2;
     const int last_i = myn > 0 ? myn - 1 : 0;
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
     uint32_t ring[PF][K + 1];
+    // issued in ring order (the scheduler may not interleave them): the loop head's wait for
+    // ring[0] then leaves PF - 1 slices in flight on every path into it
     #pragma unroll
-    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+    for (int d = 0; d < PF; ++d)
+    {
+        load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // the x rows after the weight prefetch: both latencies overlap
     stage_x(xsrc.src, xsrc.ld, xsrc.rows, min(nrows, MT), ks0, nks, xs, xs_stride);   // LDS holds MT rows
 
@@ -493,6 +533,7 @@ void moe_a_kernel(const MoeArgs a)
     const bool is_gate = a.gated && pr == 0;
     int nrows = 0;
     if (!read_run(a, run, rows, nrows)) return;
+    if (nrows <= a.run_lo || nrows > a.run_hi) return;  // another launch's size class
     const int local = slot_info(a, rows[0]).local;
     const int bits = a.g_bits ? (int) *to_global((is_gate ? a.g_bits : a.u_bits) + local) : a.K_gu;
     const int KS = a.Hi / 16;
@@ -501,15 +542,21 @@ void moe_a_kernel(const MoeArgs a)
     uint32_t* xs = smem;
     float* red = (float*) (smem + MT * xs_stride);     // LDS sized for MT rows (moe_lds_bytes)
     float* res = red + NW * MT * 128;
-    const XSrc xsrc = { is_gate ? a.had_g : a.had_u, a.Hi, rows };
-    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0, nks,
-                   xsrc, xs, xs_stride, nrows, red, res);
-    // split partials: part_a[proj][split][slot][I]
-    for (int e = threadIdx.x; e < nrows * 64; e += NT)
+    // MT rows per pass (a run larger than MT, possible only in the single-row launch of a
+    // one-token batch with a repeated expert, takes several passes over the weights)
+    for (int r0 = 0; r0 < (MT == 1 ? nrows : 1); r0 += MT)
     {
-        const int r = e >> 6, c2 = e & 63;
-        float* dst = a.part_a + (((size_t) pr * S + q) * slots + rows[r]) * a.I + chunk * 128 + 2 * c2;
-        *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+        const int nr = min(MT, nrows - r0);
+        const XSrc xsrc = { is_gate ? a.had_g : a.had_u, a.Hi, rows + r0 };
+        moe_gemv_k<CB, MT>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0,
+                           nks, xsrc, xs, xs_stride, nr, red, res);
+        // split partials: part_a[proj][split][slot][I]
+        for (int e = threadIdx.x; e < nr * 64; e += NT)
+        {
+            const int r = e >> 6, c2 = e & 63;
+            float* dst = a.part_a + (((size_t) pr * S + q) * slots + rows[r0 + r]) * a.I + chunk * 128 + 2 * c2;
+            *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+        }
     }
     for (int r = 0; r < nrows; ++r)
     {
@@ -580,6 +627,7 @@ void moe_b_kernel(const MoeArgs a)
     const int run = rest / S;
     int nrows = 0;
     if (!read_run(a, run, rows, nrows)) return;
+    if (nrows <= a.run_lo || nrows > a.run_hi) return;  // another launch's size class
     const int local = slot_info(a, rows[0]).local;
     const int bits = a.d_bits ? (int) *to_global(a.d_bits + local) : a.K_d;
     const int KS = a.I / 16;
@@ -588,13 +636,18 @@ void moe_b_kernel(const MoeArgs a)
     uint32_t* xs = smem;
     float* red = (float*) (smem + MT * xs_stride);     // LDS sized for MT rows (moe_lds_bytes)
     float* res = red + NW * MT * 128;
-    const XSrc xsrc = { a.act_out, a.I, rows };
-    moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
-    for (int e = threadIdx.x; e < nrows * 64; e += NT)
+    for (int r0 = 0; r0 < (MT == 1 ? nrows : 1); r0 += MT)
     {
-        const int r = e >> 6, c2 = e & 63;
-        float* dst = a.part_b + ((size_t) q * slots + rows[r]) * a.Ho + chunk * 128 + 2 * c2;
-        *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+        const int nr = min(MT, nrows - r0);
+        const XSrc xsrc = { a.act_out, a.I, rows + r0 };
+        moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xsrc, xs, xs_stride,
+                           nr, red, res);
+        for (int e = threadIdx.x; e < nr * 64; e += NT)
+        {
+            const int r = e >> 6, c2 = e & 63;
+            float* dst = a.part_b + ((size_t) q * slots + rows[r0 + r]) * a.Ho + chunk * 128 + 2 * c2;
+            *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
+        }
     }
     for (int r = 0; r < nrows; ++r)
     {
@@ -666,16 +719,18 @@ int EXL3_CAT(exl3k_moe_cb, EXL3_MOE_CB)(const MoeArgs& a, hipStream_t s)
     auto moe_lds_bytes = [](int mt) { return ((size_t) mt * (SBMAX * 16 + 4) + (size_t) NW * mt * 128 + (size_t) mt * 128) * 4; };
     const int rot_items = slots * (a.Hi / 128) * nproj;
     hipLaunchKernelGGL(moe_route_kernel, dim3((rot_items + NW - 1) / NW), dim3(NT), 0, s, a);
-    // one slot per run when every token has distinct picks (one token): single-row GEMV
-    if (a.bsz == 1)
-    {
-        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), moe_lds_bytes(1), s, a);
-        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), moe_lds_bytes(1), s, a);
-    }
-    else
-    {
-        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.I / 128) * nproj * a.splits_a), dim3(NT), moe_lds_bytes(ROWS), s, a);
-        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(slots * (a.Ho / 128) * a.splits_b), dim3(NT), moe_lds_bytes(ROWS), s, a);
-    }
+    // Runs by size class, each with the GEMV body of its row count: VGPRs (126 for one row, 204
+    // for eight) set the waves per SIMD, and most runs of a decode batch hold a single slot.  A
+    // one-token batch has distinct picks but for repeats, so its single-row launch takes every
+    // run (a repeat costs a second pass) and the eight-row launch is skipped.
+    const int gridA = slots * (a.I / 128) * nproj * a.splits_a, gridB = slots * (a.Ho / 128) * a.splits_b;
+    const bool multi = a.bsz > 1;
+    MoeArgs c1 = a, c8 = a;
+    c1.run_lo = 0; c1.run_hi = multi ? 1 : ROWS;
+    c8.run_lo = 1; c8.run_hi = ROWS;
+    hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(gridA), dim3(NT), moe_lds_bytes(1), s, c1);
+    if (multi) hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(gridA), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+    hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(gridB), dim3(NT), moe_lds_bytes(1), s, c1);
+    if (multi) hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(gridB), dim3(NT), moe_lds_bytes(ROWS), s, c8);
     return (int) hipGetLastError();
 }

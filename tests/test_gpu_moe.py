@@ -163,3 +163,18 @@ def test_moe_repeat_deterministic(torch_cuda, experts_mixed):
     y1, _ = run(torch_cuda, experts_mixed, x, sel, rw)
     y2, _ = run(torch_cuda, experts_mixed, x, sel, rw)
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("bsz", [1, 4])
+def test_moe_repeated_expert(torch_cuda, experts_mixed, bsz):
+    """A token that picks one expert twice: the run holds both slots (one token: the single-row
+    launch takes it in two passes; several tokens: the multi-row launch)."""
+    rng = np.random.default_rng(19 + bsz)
+    sel, rw = routing(rng, bsz, 16, 8)
+    sel[0, 1] = sel[0, 0]
+    sel[bsz - 1, 5] = sel[bsz - 1, 2]
+    x = rng.standard_normal((bsz, 256)).astype(np.float16)
+    y, runs = run(torch_cuda, experts_mixed, x, sel, rw)
+    ref = moe_ref.reference(experts_mixed, x, sel, rw, -1, -1, 0, True, 0.0, 1024)
+    assert rel_err(y, ref) < TOL
+    check_runs(runs, sel, rw, -1, -1)
