@@ -101,14 +101,16 @@ def reconstruct_slice(unpacked: Tensor, packed: Tensor, K: float, mcg: bool, mul
 
 
 def reconstruct_t(unpacked_t: Tensor, packed: Tensor, K: float, mcg: bool = False,
-                  mul1: bool = False) -> None:
-    """W_hat transposed into `unpacked_t` (n, k) fp16: the k-contiguous layout the recon GEMM
-    reads fastest.  Values bit-exact with reconstruct (no reference counterpart: the reference
-    keeps W (k, n) for cuBLAS, amp_torch.cpp:11199-11214)."""
+                  mul1: bool = False, n_offset: int = 0) -> None:
+    """W_hat columns [n_offset, n_offset + unpacked_t.size(0)) transposed into `unpacked_t`
+    (rows, k) fp16: the k-contiguous layout the recon GEMM reads fastest.  Values bit-exact
+    with reconstruct (no reference counterpart: the reference keeps W (k, n) for cuBLAS,
+    amp_torch.cpp:11199-11214)."""
     bits, half = bits_from_K(K)
     _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
     _need(packed.dim() == 3 and unpacked_t.dim() == 2, "reconstruct: bad tensor ranks")
-    _need(unpacked_t.size(1) == packed.size(0) * 16 and unpacked_t.size(0) == packed.size(1) * 16,
+    _need(unpacked_t.size(1) == packed.size(0) * 16 and n_offset >= 0
+          and n_offset + unpacked_t.size(0) <= packed.size(1) * 16,
           "unpacked and packed shapes are incompatible")
     _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
     _dtype(unpacked_t, torch.half, "unpacked")
@@ -119,7 +121,7 @@ def reconstruct_t(unpacked_t: Tensor, packed: Tensor, K: float, mcg: bool = Fals
     with torch.cuda.device(unpacked_t.device):
         check(_lib.lib().exl3_amd_reconstruct_t(
             unpacked_t.data_ptr(), packed.data_ptr(), unpacked_t.size(1), packed.size(1) * 16,
-            unpacked_t.size(0), 0, float(K), int(bool(mcg)), int(bool(mul1)), _stream(unpacked_t)))
+            unpacked_t.size(0), int(n_offset), float(K), int(bool(mcg)), int(bool(mul1)), _stream(unpacked_t)))
 
 
 def reconstruct(unpacked: Tensor, packed: Tensor, K: float, mcg: bool = False,
@@ -405,8 +407,8 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
         # W_hat stored transposed: the GEMM then reads both operands k-contiguous (~15 %
         # faster in hipBLASLt on MI355X at M = 2048)
         xh = torch.empty_like(x)
-        had_r_128(x, xh, suh, None, 1.0)
         wt = w.view(n, k)
+        had_r_128(x, xh, suh, None, 1.0)
         reconstruct_t(wt, trellis, K, mcg, mul1)
         _recon_mm(xh, wt.t(), y)
         had_r_128(y, y, None, svh, 1.0)

@@ -108,6 +108,10 @@ def test_reconstruct_t_bit_exact(torch_cuda, orc, K, cb):
     ops.reconstruct_t(WT, t, K, cb == 1, cb == 2)
     ref = orc.reconstruct(L.trellis, K, cb=cb)
     assert np.array_equal(WT.cpu().numpy().view(np.uint16), np.ascontiguousarray(ref.T).view(np.uint16))
+    # a column block (the recon pipeline's unit): columns [128, 384) into rows 0..255
+    WB = torch.empty((256, 256), dtype=torch.half, device="cuda")
+    ops.reconstruct_t(WB, t, K, cb == 1, cb == 2, n_offset=128)
+    assert np.array_equal(WB.cpu().numpy().view(np.uint16), np.ascontiguousarray(ref[:, 128:].T).view(np.uint16))
 
 
 @pytest.mark.parametrize("branch", ["rotated", "fused_w"])
@@ -122,5 +126,6 @@ def test_gemm_recon(torch_cuda, orc, branch, K, cb):
     t, s, v = L.torch()
     y = ops.exl3_gemm_recon(torch.from_numpy(x).cuda(), t, s, v, float(K), mul1=cb == 2, mcg=cb == 1,
                             fused_rows=0 if branch == "fused_w" else 1 << 30)
+    torch.cuda.synchronize()
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, K, cb=cb)
     assert rel_err(y.cpu().numpy(), ref) < TOL
