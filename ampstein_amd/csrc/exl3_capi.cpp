@@ -39,6 +39,7 @@ int hip_fail(int rc, const char* what)
 }
 
 // Bitrate K: integer 1..8, or 1.5 / 2.5 / 3.5 with the mul1 codebook (bits_k.cuh:178-185).
+// *bits receives the rate code: the integer bitrate, or 16 + b for b + 1/2.
 // both_ok: the reconstruct entry points take mcg over mul1 when both are set
 // (reconstruct.cu:181-184); exl3_gemm rejects the combination (exl3_gemm.cu:179).
 int parse_K(float K, int mcg, int mul1, int* bits, int* half, int* cb, const char* what, bool both_ok = false)
@@ -48,12 +49,11 @@ int parse_K(float K, int mcg, int mul1, int* bits, int* half, int* cb, const cha
     if (!(b >= 1 && b <= 8 && (f == 0.0f || (f == 0.5f && b <= 3))))
         return fail(EXL3_AMD_EINVAL, "%s: unsupported EXL3 bitrate %g (integer 1..8, or 1.5 / 2.5 / 3.5)", what, (double) K);
     if (mcg && mul1 && !both_ok) return fail(EXL3_AMD_EINVAL, "%s: specified both mcg and mul1", what);
-    *bits = b;
     *half = f == 0.5f;
+    *bits = *half ? 16 + b : b;         // the kernels' rate code (exl3_common.cuh kbits / khalf)
     *cb = mcg ? 1 : (mul1 ? 2 : 0);
     if (*half && mul1) *cb = 2;
     if (*half && !mul1) return fail(EXL3_AMD_EINVAL, "%s: half-integer bitrates require the mul1 codebook", what);
-    if (*half) return fail(EXL3_AMD_EUNSUPPORTED, "%s: half-integer bitrates are not implemented in this build", what);
     return 0;
 }
 
@@ -413,6 +413,7 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
+    if (half) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: half-integer bitrates are not implemented in this build");
     if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: negative size");
     if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
     if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
@@ -468,6 +469,7 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
     g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg != 0, mul1 != 0, &bits, &half, &cb, "exl3_mgemm")) return rc;
+    if (half) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: half-integer bitrates are not implemented in this build");
     if (bszm_in < 1 || bszm_out < 1 || m < 0 || k < 0 || n < 0 || num_B < 0)
         return fail(EXL3_AMD_EINVAL, "exl3_mgemm: bad batch or size");
     if (!A || !B || !suh || !svh || (!C && !c_ptrs)) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: null pointer");

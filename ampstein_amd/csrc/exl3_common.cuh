@@ -177,9 +177,30 @@ EXL3_QUAD_SPEC(1, 1, 0, 0) EXL3_QUAD_SPEC(1, 1, 0, 1) EXL3_QUAD_SPEC(1, 1, 1, 0)
 // half of alignbit(wv[hi-1], wv[hi], s & 15) with s the right shift of the window's end;
 // windows whose shifts differ by 16 share one alignbit, and s & 15 == 0 costs nothing.
 // ---------------------------------------------------------------------------------------------
-template <int K> struct Win
+// Rate codes: K = 1..8 is the integer bitrate; K = 16 + b (b = 1..3) is b + 1/2 (mul1 only,
+// bits_k.cuh:8-27).  A 16x16 tile holds tile_words(K) u32.
+__host__ __device__ constexpr int kbits(int K) { return K & 15; }
+__host__ __device__ constexpr bool khalf(int K) { return K >= 16; }
+__host__ __device__ constexpr int tile_words(int K) { return 8 * kbits(K) + (khalf(K) ? 4 : 0); }
+
+template <int K, bool H = khalf(K)> struct Win
 {
     static constexpr int e(int i) { return (i + 1) * K + 32; }
+    static constexpr int hi(int i) { return (e(i) - 1) / 32; }
+    static constexpr int s(int i) { return (hi(i) + 1) * 32 - e(i); }
+    static constexpr int sb(int i) { return s(i) & 15; }
+    static constexpr int h(int i) { return s(i) >> 4; }
+};
+
+// Half-integer rates (K = 16 + b): a tile holds 8b + 4 words, and lane j of the tile (j = lane
+// % 8) decodes positions 32j..32j+31, whose windows end at tile bits S_j + r(i),
+// S_j = j (32b + 16), r(i) = (i/2)(2b + 1) + (i odd ? 2b + 1 : b) (exl3_dq.cuh:254-285).  The
+// lane's frame wv[0..b] holds bits [S_j - 16, S_j + 32b + 16) (load_frame_half), so window i
+// ends at frame bit r(i) + 16; windows inside wv[0] (e <= 32) need no left word.
+template <int K> struct Win<K, true>
+{
+    static constexpr int B = K & 15;
+    static constexpr int e(int i) { return (i >> 1) * (2 * B + 1) + ((i & 1) ? 2 * B + 1 : B) + 16; }
     static constexpr int hi(int i) { return (e(i) - 1) / 32; }
     static constexpr int s(int i) { return (hi(i) + 1) * 32 - e(i); }
     static constexpr int sb(int i) { return s(i) & 15; }
@@ -191,7 +212,24 @@ __device__ __forceinline__ uint32_t win_reg(const uint32_t* wv)
 {
     constexpr int hi = Win<K>::hi(I), sb = Win<K>::sb(I);
     if constexpr (sb == 0) return wv[hi];
-    else return __builtin_amdgcn_alignbit(wv[hi - 1], wv[hi], sb);
+    else return __builtin_amdgcn_alignbit(wv[hi > 0 ? hi - 1 : 0], wv[hi], sb);
+}
+
+// Frame of a half-rate lane (see Win<K, true>): the b + 2 words from word jb + j/2 - 1 of the
+// tile (lane 0: the ring wraps to the tile's last word), shifted left by 16 bits for even j so
+// that the frame starts at word 0, bit 0 (MSB-first).
+template <int K>
+__device__ __forceinline__ void load_frame_half(const uint32_t* __restrict__ tile, int j, uint32_t* wv)
+{
+    constexpr int B = kbits(K);
+    const int b = j * B + (j >> 1) - 1;
+    uint32_t raw[B + 2];
+    raw[0] = __builtin_nontemporal_load(tile + (b < 0 ? tile_words(K) - 1 : b));
+    #pragma unroll
+    for (int i = 1; i < B + 2; ++i) raw[i] = __builtin_nontemporal_load(tile + b + i);
+    const uint32_t sh = (j & 1) ? 0u : 16u;
+    #pragma unroll
+    for (int i = 0; i <= B; ++i) wv[i] = __builtin_amdgcn_alignbit(raw[i], raw[i + 1], sh);
 }
 
 // Decode the lane's 32 windows into 16 packed pairs: out[q] = (window 2q, window 2q+1).

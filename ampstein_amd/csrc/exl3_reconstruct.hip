@@ -50,11 +50,21 @@ __device__ __forceinline__ void decode_slice(const uint16_t* __restrict__ trelli
                                              int kt, int nt0, int lane, uint32_t* pairs,
                                              const DecodeRegs& r)
 {
-    const uint32_t* base = (const uint32_t*) trellis
-                         + ((size_t) kt * tiles_n + nt0) * (8 * K) + (size_t) lane * K;
-    uint32_t wv[K + 1];
-    load_lane_words<K>(base, wv + 1);
-    wv[0] = ring_prev(wv[K], lane);
+    constexpr int KB = kbits(K);
+    uint32_t wv[KB + 1];
+    if constexpr (khalf(K))
+    {
+        const uint32_t* tile = (const uint32_t*) trellis
+                             + ((size_t) kt * tiles_n + nt0 + (lane >> 3)) * tile_words(K);
+        load_frame_half<K>(tile, lane & 7, wv);
+    }
+    else
+    {
+        const uint32_t* base = (const uint32_t*) trellis
+                             + ((size_t) kt * tiles_n + nt0) * (8 * K) + (size_t) lane * K;
+        load_lane_words<K>(base, wv + 1);
+        wv[0] = ring_prev(wv[K], lane);
+    }
     decode_lane32<K, CB>(wv, pairs, r);
 }
 
@@ -277,32 +287,35 @@ int launch_reconstruct_had_t(uint16_t* W, const uint16_t* trellis, const uint16_
 }  // namespace
 
 #define EXL3_DISPATCH_K_CB(K, CB, FN, ...)                                        \
-    switch (CB * 16 + K)                                                          \
+    switch (CB * 32 + K)                                                          \
     {                                                                             \
-        case 0 * 16 + 1: return FN<1, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 2: return FN<2, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 3: return FN<3, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 4: return FN<4, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 5: return FN<5, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 6: return FN<6, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 7: return FN<7, 0>(__VA_ARGS__);                            \
-        case 0 * 16 + 8: return FN<8, 0>(__VA_ARGS__);                            \
-        case 1 * 16 + 1: return FN<1, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 2: return FN<2, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 3: return FN<3, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 4: return FN<4, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 5: return FN<5, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 6: return FN<6, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 7: return FN<7, 1>(__VA_ARGS__);                            \
-        case 1 * 16 + 8: return FN<8, 1>(__VA_ARGS__);                            \
-        case 2 * 16 + 1: return FN<1, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 2: return FN<2, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 3: return FN<3, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 4: return FN<4, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 5: return FN<5, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 6: return FN<6, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 7: return FN<7, 2>(__VA_ARGS__);                            \
-        case 2 * 16 + 8: return FN<8, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 17: return FN<17, 2>(__VA_ARGS__);                          \
+        case 2 * 32 + 18: return FN<18, 2>(__VA_ARGS__);                          \
+        case 2 * 32 + 19: return FN<19, 2>(__VA_ARGS__);                          \
+        case 0 * 32 + 1: return FN<1, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 2: return FN<2, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 3: return FN<3, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 4: return FN<4, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 5: return FN<5, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 6: return FN<6, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 7: return FN<7, 0>(__VA_ARGS__);                            \
+        case 0 * 32 + 8: return FN<8, 0>(__VA_ARGS__);                            \
+        case 1 * 32 + 1: return FN<1, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 2: return FN<2, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 3: return FN<3, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 4: return FN<4, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 5: return FN<5, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 6: return FN<6, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 7: return FN<7, 1>(__VA_ARGS__);                            \
+        case 1 * 32 + 8: return FN<8, 1>(__VA_ARGS__);                            \
+        case 2 * 32 + 1: return FN<1, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 2: return FN<2, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 3: return FN<3, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 4: return FN<4, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 5: return FN<5, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 6: return FN<6, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 7: return FN<7, 2>(__VA_ARGS__);                            \
+        case 2 * 32 + 8: return FN<8, 2>(__VA_ARGS__);                            \
     }                                                                             \
     return -1;
 

@@ -53,6 +53,31 @@ def test_reconstruct_bit_exact(torch_cuda, orc, K, cb):
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("K", [1.5, 2.5, 3.5])
+def test_reconstruct_half_rate_bit_exact(torch_cuda, orc, K):
+    """Half-integer bitrates (mul1, 16K + 8 u16 per tile): reconstruct, a column slice,
+    the transposed layout and the original-basis form, bit for bit against the oracle."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    b = int(K)
+    L = synth.layer(256, 384, K, 2, seed=int(40 * K))
+    t, s, v = L.torch()
+    ref = orc.reconstruct(L.trellis, b, half=True, cb=2)
+    W = torch.empty((256, 384), dtype=torch.half, device="cuda")
+    ops.reconstruct(W, t, K, mul1=True)
+    assert np.array_equal(W.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+    Ws = torch.empty((256, 256), dtype=torch.half, device="cuda")
+    ops.reconstruct_slice(Ws, t, K, False, True, 128)
+    assert np.array_equal(Ws.cpu().numpy().view(np.uint16), ref[:, 128:].view(np.uint16))
+    WT = torch.empty((384, 256), dtype=torch.half, device="cuda")
+    ops.reconstruct_t(WT, t, K, False, True)
+    assert np.array_equal(WT.cpu().numpy().view(np.uint16), np.ascontiguousarray(ref.T).view(np.uint16))
+    ref_had = orc.reconstruct_had(L.trellis, L.suh, L.svh, b, half=True, cb=2)
+    Wh = torch.empty((256, 384), dtype=torch.half, device="cuda")
+    ops.reconstruct_had_slice(Wh, t, s, v, K, False, True, 0)
+    assert np.array_equal(Wh.cpu().numpy().view(np.uint16), ref_had.view(np.uint16))
+
+
 def test_reconstruct_slice_bit_exact(torch_cuda, orc):
     torch = torch_cuda
     from ampstein_amd import ops
