@@ -302,6 +302,9 @@ int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s)
         case 6: return exl3k_gemv_k6(g, cb, s);
         case 7: return exl3k_gemv_k7(g, cb, s);
         case 8: return exl3k_gemv_k8(g, cb, s);
+        case 17: return exl3k_gemv_k17(g, cb, s);
+        case 18: return exl3k_gemv_k18(g, cb, s);
+        case 19: return exl3k_gemv_k19(g, cb, s);
     }
     return -1;
 }
@@ -413,7 +416,6 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
-    if (half) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: half-integer bitrates are not implemented in this build");
     if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: negative size");
     if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
     if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
@@ -442,6 +444,19 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
         int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
         if (rc) return hip_fail(rc, "exl3_gemm");
     }
+    if (half)
+    {
+        // half rates: the tiled kernel decodes integer rates only; the GEMV takes the rows in
+        // groups of 8 (callers route large row counts to the reconstruct + dense GEMM path)
+        const size_t elt = c_fp32 ? 4 : 2;
+        for (int r0 = 0; r0 < m; r0 += 8)
+        {
+            GemvArgs g = gemv_args_single(A + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt, c_fp32,
+                                          suh, svh, std::min(8, m - r0), k, n);
+            if (int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm")) return rc;
+        }
+        return EXL3_AMD_TAG_GEMV;
+    }
     GemmArgs gg;
     gg.A_rot = suh ? A_had : A;
     gg.trellis = trellis; gg.C = C; gg.svh = svh;
@@ -469,7 +484,6 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
     g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg != 0, mul1 != 0, &bits, &half, &cb, "exl3_mgemm")) return rc;
-    if (half) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: half-integer bitrates are not implemented in this build");
     if (bszm_in < 1 || bszm_out < 1 || m < 0 || k < 0 || n < 0 || num_B < 0)
         return fail(EXL3_AMD_EINVAL, "exl3_mgemm: bad batch or size");
     if (!A || !B || !suh || !svh || (!C && !c_ptrs)) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: null pointer");

@@ -224,9 +224,9 @@ __device__ __forceinline__ void load_frame_half(const uint32_t* __restrict__ til
     constexpr int B = kbits(K);
     const int b = j * B + (j >> 1) - 1;
     uint32_t raw[B + 2];
-    raw[0] = __builtin_nontemporal_load(tile + (b < 0 ? tile_words(K) - 1 : b));
+    raw[0] = __builtin_nontemporal_load(to_global(tile) + (b < 0 ? tile_words(K) - 1 : b));
     #pragma unroll
-    for (int i = 1; i < B + 2; ++i) raw[i] = __builtin_nontemporal_load(tile + b + i);
+    for (int i = 1; i < B + 2; ++i) raw[i] = __builtin_nontemporal_load(to_global(tile) + b + i);
     const uint32_t sh = (j & 1) ? 0u : 16u;
     #pragma unroll
     for (int i = 0; i <= B; ++i) wv[i] = __builtin_amdgcn_alignbit(raw[i], raw[i + 1], sh);

@@ -436,17 +436,18 @@ void gemv_kernel(const GemvArgs g)
     // this wave's slices: ks0 + wave + 4 i, i < myn
     const int myn = SB > wave ? (SB - wave + GEMV_WAVES - 1) / GEMV_WAVES : 0;
     const int tiles_n = v.stride / 16;
-    const size_t kstride = (size_t) GEMV_WAVES * tiles_n * 8 * K;         // u32 between my slices
-    const uint32_t* base = (const uint32_t*) v.trellis + (size_t) lane * K
-                         + ((size_t) (ks0 + min(wave, SB - 1)) * tiles_n + chunk * 8) * (8 * K);
+    constexpr int KB = kbits(K);                          // whole words per lane (rate code K)
+    const size_t kstride = (size_t) GEMV_WAVES * tiles_n * tile_words(K);   // u32 between my slices
+    const uint32_t* base = (const uint32_t*) v.trellis + lane_word_off<K>(lane)
+                         + ((size_t) (ks0 + min(wave, SB - 1)) * tiles_n + chunk * 8) * tile_words(K);
 
     // prefetch ring (unconditional, clamped loads keep the wait counts static)
     constexpr int PF = EXL3_GEMV_PF;
     const int last_i = myn > 0 ? myn - 1 : 0;
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;   // ring predecessor of my first word
-    uint32_t ring[PF][K + 1];
+    uint32_t ring[PF][KB + 1];
     #pragma unroll
-    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+    for (int d = 0; d < PF; ++d) load_slot_k<K>(base + (size_t) min(d, last_i) * kstride, prev_off, lane, ring[d]);
 
     // input rotation of the chunks this workgroup touches (overlaps the first loads)
     rotate_chunks(v.A, v.suh, xs, xs_stride, m, k, kc0, nkc);
@@ -465,13 +466,13 @@ void gemv_kernel(const GemvArgs g)
             const bool live = i < myn;
             const int ks = ks0 + wave + min(i, last_i) * GEMV_WAVES;
             const int xo = (ks / 8 - kc0) * 128 + (ks & 7) * 16;
-            uint32_t wv[K + 1];
+            uint32_t wv[KB + 1];
             #pragma unroll
-            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
             // refill this ring slot once its words are dead
-            load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
+            load_slot_k<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, lane, ring[d]);
 
             #pragma unroll
             for (int r = 0; r < MT; ++r)
@@ -657,9 +658,10 @@ void gemv1_kernel(const GemvArgs g)
     constexpr int per = WS;                             // slices per input chunk
     const int lane0 = WS < 8 ? (a & 7) * 8 : 0;         // x lanes of the first slice
     const int tiles_n = v.stride / 16;
-    const size_t rstride = (size_t) tiles_n * 8 * K;    // u32 per k-slice row
-    const uint32_t* base = (const uint32_t*) v.trellis + (size_t) lane * K
-                         + ((size_t) a * tiles_n + chunk * 8) * (8 * K);
+    constexpr int KB = kbits(K);                        // whole words per lane (rate code K)
+    const size_t rstride = (size_t) tiles_n * tile_words(K);    // u32 per k-slice row
+    const uint32_t* base = (const uint32_t*) v.trellis + lane_word_off<K>(lane)
+                         + ((size_t) a * tiles_n + chunk * 8) * tile_words(K);
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
     const bool has_suh = v.suh != nullptr;
     const uint32_t* xg = (const uint32_t*) v.A + lane;                       // x pairs
@@ -671,9 +673,9 @@ void gemv1_kernel(const GemvArgs g)
     // x of the first chunk first (its wait then leaves the weight loads in flight)
     uint32_t xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8) * 64);
     uint32_t sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8) * 64);
-    uint32_t ring[PF][K + 1];
+    uint32_t ring[PF][KB + 1];
     #pragma unroll
-    for (int d = 0; d < PF; ++d) load_slot<K>(base + (size_t) min(d, last) * rstride, prev_off, ring[d]);
+    for (int d = 0; d < PF; ++d) load_slot_k<K>(base + (size_t) min(d, last) * rstride, prev_off, lane, ring[d]);
     // svh pair for the epilogue, behind the first weights
     // (unconditional load: without svh it reads the input, k >= 128, and is unused)
     const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
@@ -715,15 +717,15 @@ void gemv1_kernel(const GemvArgs g)
         {
             const int i = c * 8 + s8;
             const int d = s8 % PF;
-            uint32_t wv[K + 1];
+            uint32_t wv[KB + 1];
             #pragma unroll
-            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
             // refill with slice i + PF; past the last slice it re-reads slice i, just consumed and
             // cache-hot, so the hand-off's wait for the partial stores (loads and stores retire in
             // order) does not wait on HBM.  Unconditional, so the wait counts stay static.
-            load_slot<K>(base + (size_t) (i + PF <= last ? i + PF : i) * rstride, prev_off, ring[d]);
+            load_slot_k<K>(base + (size_t) (i + PF <= last ? i + PF : i) * rstride, prev_off, lane, ring[d]);
 #if EXL3_GEMV_MFMA
             // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
             const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;
@@ -1149,11 +1151,12 @@ int launch_gemv1(const GemvArgs& g, hipStream_t s)
 template <int K, int CB>
 int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 {
-    if (g.m == 1 && g.stream_m1 == 2)
-    {
-        hipLaunchKernelGGL((gemv1p_kernel<K, CB>), dim3(g.p1_blocks), dim3(GEMV_THREADS), 0, s, g);
-        return (int) hipGetLastError();
-    }
+    if constexpr (!khalf(K))
+        if (g.m == 1 && g.stream_m1 == 2)
+        {
+            hipLaunchKernelGGL((gemv1p_kernel<K, CB>), dim3(g.p1_blocks), dim3(GEMV_THREADS), 0, s, g);
+            return (int) hipGetLastError();
+        }
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
     if (g.m == 1) return launch_gemv_t<K, CB, 1>(g, s);
     if (g.m <= 4) return launch_gemv_t<K, CB, 4>(g, s);
@@ -1167,6 +1170,9 @@ int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 
 int EXL3_CAT(exl3k_gemv_k, EXL3_INST_K)(const GemvArgs& g, int cb, hipStream_t s)
 {
+#if EXL3_INST_K >= 16
+    return cb == 2 ? launch_gemv_m<EXL3_INST_K, 2>(g, s) : -1;     // half rates: mul1 only
+#else
     switch (cb)
     {
         case 0: return launch_gemv_m<EXL3_INST_K, 0>(g, s);
@@ -1174,4 +1180,5 @@ int EXL3_CAT(exl3k_gemv_k, EXL3_INST_K)(const GemvArgs& g, int cb, hipStream_t s
         case 2: return launch_gemv_m<EXL3_INST_K, 2>(g, s);
     }
     return -1;
+#endif
 }

@@ -48,6 +48,19 @@ __device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int pr
     w[0] = __builtin_nontemporal_load(to_global(p) + prev_off);
 }
 
+// Slot load for any rate code.  Integer K: load_slot, p = the lane's first word (chunk base +
+// lane_word_off).  Half rates: p = the 8-tile chunk's first word, the lane's frame of K + 1
+// words (exl3_common.cuh load_frame_half); prev_off is unused.
+template <int K>
+__device__ __forceinline__ constexpr int lane_word_off(int lane) { return khalf(K) ? 0 : lane * K; }
+
+template <int K>
+__device__ __forceinline__ void load_slot_k(const uint32_t* __restrict__ p, int prev_off, int lane, uint32_t* w)
+{
+    if constexpr (khalf(K)) load_frame_half<K>(p + (lane >> 3) * tile_words(K), lane & 7, w);
+    else load_slot<K>(p, prev_off, w);
+}
+
 // Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe, from word hi when the window
 // sits inside it, else from the half-word-shifted word alignbit(wv[hi-1], wv[hi], 16) (one per
 // word, shared by the windows that straddle that word boundary).

@@ -130,3 +130,6 @@ int exl3k_gemv_k5(const GemvArgs& g, int cb, hipStream_t s);
 int exl3k_gemv_k6(const GemvArgs& g, int cb, hipStream_t s);
 int exl3k_gemv_k7(const GemvArgs& g, int cb, hipStream_t s);
 int exl3k_gemv_k8(const GemvArgs& g, int cb, hipStream_t s);
+int exl3k_gemv_k17(const GemvArgs& g, int cb, hipStream_t s);     // 1.5 bits (mul1)
+int exl3k_gemv_k18(const GemvArgs& g, int cb, hipStream_t s);     // 2.5
+int exl3k_gemv_k19(const GemvArgs& g, int cb, hipStream_t s);     // 3.5
