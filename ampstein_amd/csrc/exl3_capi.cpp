@@ -614,9 +614,9 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     const bool dyn = bits_g != nullptr;
     if (dyn && !mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe_coop: mixed bit widths require the mul1 codebook");
     const float Kgu = gated ? Kg : Ku;
-    if (Kgu != (float) (int) Kgu || Kd != (float) (int) Kd)
-        return fail(Kgu - (int) Kgu == 0.5f && mul1 ? EXL3_AMD_EUNSUPPORTED : EXL3_AMD_EINVAL,
-                    "exl3_moe_coop: half-integer bitrates are not implemented in this build");
+    int kgu_code, kd_code, half_, cbk;              // rate codes (integer, or 16 + b for b + 1/2)
+    if (int rc = parse_K(Kgu, mcg, mul1, &kgu_code, &half_, &cbk, "exl3_moe_coop")) return rc;
+    if (int rc = parse_K(Kd, mcg, mul1, &kd_code, &half_, &cbk, "exl3_moe_coop")) return rc;
     if (bsz == 0) return 0;
 
     DeviceState* d;
@@ -632,7 +632,7 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     a.d_trellis = d_trellis; a.d_suh = d_suh; a.d_svh = d_svh;
     a.g_bias = g_bias; a.u_bias = u_bias; a.d_bias = d_bias;
     a.g_bits = bits_g; a.u_bits = bits_u; a.d_bits = bits_d;
-    a.K_gu = (int) Kgu; a.K_d = (int) Kd;
+    a.K_gu = kgu_code; a.K_d = kd_code;
     a.act = act; a.act_limit = act_limit; a.gated = gated ? 1 : 0;
     a.had_g = had_g; a.had_u = had_u; a.act_out = act_out;
     a.runs = ctr + (int64_t) slots_max * (I / 128) + (int64_t) rows_max * (Ho / 128);

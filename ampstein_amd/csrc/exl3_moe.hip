@@ -334,19 +334,20 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);
     const int myn = nks > wave ? (nks - wave + NW - 1) / NW : 0;
-    const size_t kstride = (size_t) NW * tiles_n * 8 * K;
-    const uint32_t* base = (const uint32_t*) trellis + (size_t) lane * K
-                         + ((size_t) (ks0 + min(wave, nks - 1)) * tiles_n + chunk * 8) * (8 * K);
-    constexpr int PF = (MT == 1 && K <= 4) ? EXL3_MOE_PF1 : 2;
+    constexpr int KB = kbits(K);                          // whole words per lane (rate code K)
+    const size_t kstride = (size_t) NW * tiles_n * tile_words(K);
+    const uint32_t* base = (const uint32_t*) trellis + lane_word_off<K>(lane)
+                         + ((size_t) (ks0 + min(wave, nks - 1)) * tiles_n + chunk * 8) * tile_words(K);
+    constexpr int PF = (MT == 1 && KB <= 4) ? EXL3_MOE_PF1 : 2;
     const int last_i = myn > 0 ? myn - 1 : 0;
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
-    uint32_t ring[PF][K + 1];
+    uint32_t ring[PF][KB + 1];
     // issued in ring order (the scheduler may not interleave them): the loop head's wait for
     // ring[0] then leaves PF - 1 slices in flight on every path into it
     #pragma unroll
     for (int d = 0; d < PF; ++d)
     {
-        load_slot<K>(base + (size_t) min(d, last_i) * kstride, prev_off, ring[d]);
+        load_slot_k<K>(base + (size_t) min(d, last_i) * kstride, prev_off, lane, ring[d]);
         __builtin_amdgcn_sched_barrier(0);
     }
     // the x rows after the weight prefetch: both latencies overlap
@@ -364,12 +365,12 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
             const int i = i0 + d;
             const bool live = i < myn;
             const int xo = (wave + min(i, last_i) * NW) * 16;
-            uint32_t wv[K + 1];
+            uint32_t wv[KB + 1];
             #pragma unroll
-            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
+            for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
-            load_slot<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, ring[d]);
+            load_slot_k<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, lane, ring[d]);
             #pragma unroll
             for (int r = 0; r < MT; ++r)
             {
@@ -426,23 +427,35 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
     __syncthreads();
 }
 
-template <int CB, int MT>
+// HS: the half-rate variant (rate codes 16 + b, mul1 only), a launch of its own so that the
+// integer-rate kernels keep their register budget.
+template <int CB, int MT, bool HS>
 __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
                            const XSrc& xsrc, uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
 #ifdef EXL3_MOE_ONLY_K
     moe_gemv<EXL3_MOE_ONLY_K, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); return;
 #endif
-    switch (bits)
+    if constexpr (HS)
     {
-        case 1: moe_gemv<1, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 2: moe_gemv<2, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 3: moe_gemv<3, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 4: moe_gemv<4, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 5: moe_gemv<5, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 6: moe_gemv<6, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        case 7: moe_gemv<7, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
-        default: moe_gemv<8, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        if (bits == 17) moe_gemv<17, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
+        else if (bits == 18) moe_gemv<18, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
+        else moe_gemv<19, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
+        return;
+    }
+    else
+    {
+        switch (bits)
+        {
+            case 1: moe_gemv<1, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 2: moe_gemv<2, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 3: moe_gemv<3, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 4: moe_gemv<4, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 5: moe_gemv<5, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 6: moe_gemv<6, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            case 7: moe_gemv<7, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+            default: moe_gemv<8, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); break;
+        }
     }
 }
 
@@ -513,7 +526,7 @@ __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, i
     return true;
 }
 
-template <int CB, int MT>
+template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT)
 void moe_a_kernel(const MoeArgs a)
 {
@@ -548,7 +561,7 @@ void moe_a_kernel(const MoeArgs a)
     {
         const int nr = min(MT, nrows - r0);
         const XSrc xsrc = { is_gate ? a.had_g : a.had_u, a.Hi, rows + r0 };
-        moe_gemv_k<CB, MT>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0,
+        moe_gemv_k<CB, MT, HS>(bits, tab<uint16_t>(is_gate ? a.g_trellis : a.u_trellis, local), a.I / 16, chunk, ks0,
                            nks, xsrc, xs, xs_stride, nr, red, res);
         // split partials: part_a[proj][split][slot][I]
         for (int e = threadIdx.x; e < nr * 64; e += NT)
@@ -610,7 +623,7 @@ void moe_a_kernel(const MoeArgs a)
     }
 }
 
-template <int CB, int MT>
+template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT)
 void moe_b_kernel(const MoeArgs a)
 {
@@ -640,7 +653,7 @@ void moe_b_kernel(const MoeArgs a)
     {
         const int nr = min(MT, nrows - r0);
         const XSrc xsrc = { a.act_out, a.I, rows + r0 };
-        moe_gemv_k<CB, MT>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xsrc, xs, xs_stride,
+        moe_gemv_k<CB, MT, HS>(bits, tab<uint16_t>(a.d_trellis, local), a.Ho / 16, chunk, ks0, nks, xsrc, xs, xs_stride,
                            nr, red, res);
         for (int e = threadIdx.x; e < nr * 64; e += NT)
         {
@@ -728,9 +741,29 @@ int EXL3_CAT(exl3k_moe_cb, EXL3_MOE_CB)(const MoeArgs& a, hipStream_t s)
     MoeArgs c1 = a, c8 = a;
     c1.run_lo = 0; c1.run_hi = multi ? 1 : ROWS;
     c8.run_lo = 1; c8.run_hi = ROWS;
-    hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1>), dim3(gridA), dim3(NT), moe_lds_bytes(1), s, c1);
-    if (multi) hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS>), dim3(gridA), dim3(NT), moe_lds_bytes(ROWS), s, c8);
-    hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1>), dim3(gridB), dim3(NT), moe_lds_bytes(1), s, c1);
-    if (multi) hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS>), dim3(gridB), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+#if EXL3_MOE_CB == 2
+    if (a.K_gu >= 16 && !a.g_bits)
+    {
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1, true>), dim3(gridA), dim3(NT), moe_lds_bytes(1), s, c1);
+        if (multi) hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS, true>), dim3(gridA), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+    }
+    else
+#endif
+    {
+        hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, 1, false>), dim3(gridA), dim3(NT), moe_lds_bytes(1), s, c1);
+        if (multi) hipLaunchKernelGGL((moe_a_kernel<EXL3_MOE_CB, ROWS, false>), dim3(gridA), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+    }
+#if EXL3_MOE_CB == 2
+    if (a.K_d >= 16 && !a.d_bits)
+    {
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1, true>), dim3(gridB), dim3(NT), moe_lds_bytes(1), s, c1);
+        if (multi) hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS, true>), dim3(gridB), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+    }
+    else
+#endif
+    {
+        hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, 1, false>), dim3(gridB), dim3(NT), moe_lds_bytes(1), s, c1);
+        if (multi) hipLaunchKernelGGL((moe_b_kernel<EXL3_MOE_CB, ROWS, false>), dim3(gridB), dim3(NT), moe_lds_bytes(ROWS), s, c8);
+    }
     return (int) hipGetLastError();
 }

@@ -46,14 +46,15 @@ class ExpertSet:
     def __init__(self, torch, orc, n, Hi, I, Ho, Ks, cb, seed, bias=False):
         rng = np.random.default_rng(seed)
         self.n, self.Hi, self.I, self.Ho, self.cb = n, Hi, I, Ho, cb
-        self.K = [int(k) for k in Ks]
+        self.K = [float(k) if float(k) != int(k) else int(k) for k in Ks]     # b + 0.5: half rate (mul1)
         self.layers = []
         for e in range(n):
             g = synth.layer(Hi, I, self.K[e], cb, seed=seed * 1000 + 3 * e)
             u = synth.layer(Hi, I, self.K[e], cb, seed=seed * 1000 + 3 * e + 1)
             d = synth.layer(I, Ho, self.K[e], cb, seed=seed * 1000 + 3 * e + 2)
             self.layers.append((g, u, d))
-        self.W = [tuple(orc.reconstruct(L.trellis, L.K, cb=cb).astype(np.float64) for L in trio) for trio in self.layers]
+        self.W = [tuple(orc.reconstruct(L.trellis, int(L.K), half=L.K != int(L.K), cb=cb).astype(np.float64)
+                        for L in trio) for trio in self.layers]
         self.dev = [tuple(L.torch() for L in trio) for trio in self.layers]
         P = lambda v: torch.tensor(v, dtype=torch.long, device="cuda")
         self.tables = {}
@@ -61,7 +62,7 @@ class ExpertSet:
             self.tables[name + "_trellis"] = P([self.dev[e][pi][0].data_ptr() for e in range(n)])
             self.tables[name + "_suh"] = P([self.dev[e][pi][1].data_ptr() for e in range(n)])
             self.tables[name + "_svh"] = P([self.dev[e][pi][2].data_ptr() for e in range(n)])
-        self.bits = {name: torch.tensor(self.K, dtype=torch.uint8, device="cuda") for name in "gud"}
+        self.bits = {name: torch.tensor([int(k) for k in self.K], dtype=torch.uint8, device="cuda") for name in "gud"}
         self.bias_np = None
         if bias:
             self.bias_np = [tuple((rng.standard_normal(w) * 0.1).astype(np.float16) for w in (I, I, Ho)) for _ in range(n)]

@@ -178,3 +178,17 @@ def test_moe_repeated_expert(torch_cuda, experts_mixed, bsz):
     ref = moe_ref.reference(experts_mixed, x, sel, rw, -1, -1, 0, True, 0.0, 1024)
     assert rel_err(y, ref) < TOL
     check_runs(runs, sel, rw, -1, -1)
+
+
+@pytest.mark.parametrize("K", [1.5, 2.5, 3.5])
+def test_moe_half_rate(torch_cuda, orc, K):
+    """Uniform half-integer bitrate (mul1): gate/up and down at K + 0.5 bits."""
+    es = moe_ref.ExpertSet(torch_cuda, orc, 8, 256, 1024, 1024, [K] * 8, 2, seed=int(4 * K))
+    rng = np.random.default_rng(int(10 * K))
+    for bsz in (1, 4):
+        sel, rw = routing(rng, bsz, 8, 4)
+        x = rng.standard_normal((bsz, 256)).astype(np.float16)
+        y, runs = run(torch_cuda, es, x, sel, rw, mixed=False)
+        ref = moe_ref.reference(es, x, sel, rw, -1, -1, 0, True, 0.0, 1024)
+        assert rel_err(y, ref) < TOL, bsz
+        check_runs(runs, sel, rw, -1, -1)
