@@ -245,7 +245,8 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     // (exl3_gemv.hip gemv1p_kernel).  Needs the XCD-local hand-off and per-slot tables of at
     // most 16 slots without indices or routing weights.
     // Opt-in (EXL3_AMD_GEMV_P1=1) until its GPU run is cleared.
-    bool p1 = g.m == 1 && g.stream_m1 && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16;
+    bool p1 = g.m == 1 && g.stream_m1 && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
+              g.row0 == 0 && g.slab_m <= 1;
     {
         const char* e = getenv("EXL3_AMD_GEMV_P1");
         p1 = p1 && e && atoi(e) != 0;
@@ -533,8 +534,8 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
     if (m == 0 || n == 0 || bszm == 0) return EXL3_AMD_TAG_GEMV;
     if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: k must be positive");
     if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: k %% 128 != 0 is not implemented in this build");
-    if (m > 8 || force_shape_idx == 2)
-        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: m > 8 (MFMA GEMM) is not implemented in this build");
+    if (m > 8 && weights)
+        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: m > 8 with routing weights is not implemented in this build");
 
     DeviceState* d;
     if (int rc = current_device(&d)) return rc;
@@ -554,8 +555,16 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         g.indices = d->filt_idx;
         if (weights) g.weights = d->filt_w;
     }
-    int rc = launch_gemv(d, bits, cb, g, s, "exl3_mgemm");
-    return rc ? rc : EXL3_AMD_TAG_GEMV;
+    // more than 8 rows: the GEMV in row groups of 8 (slab strides stay those of all m rows)
+    g.slab_m = m;
+    for (int r0 = 0; r0 < m; r0 += 8)
+    {
+        GemvArgs gr = g;
+        gr.m = std::min(8, m - r0);
+        gr.row0 = r0;
+        if (int rc = launch_gemv(d, bits, cb, gr, s, "exl3_mgemm")) return rc;
+    }
+    return EXL3_AMD_TAG_GEMV;
 }
 
 int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,

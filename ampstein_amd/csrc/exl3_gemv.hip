@@ -95,6 +95,8 @@ __device__ __forceinline__ uint32_t s_load_u32(const void* p)
 
 __device__ __forceinline__ bool resolve(const GemvArgs& g, int j, MatView& v)
 {
+    const size_t rows = g.slab_m ? g.slab_m : g.m;       // rows per slab
+    const size_t elt = g.c_fp32 ? 4 : 2;
     int q = j;
     if (g.indices)
     {
@@ -131,7 +133,7 @@ __device__ __forceinline__ bool resolve(const GemvArgs& g, int j, MatView& v)
         v.n = g.size_n ? (int) nn : g.n;
         v.stride = g.n_stride ? (int) st : v.n;
         if (g.c_list) v.C = (void*) c;
-        else v.C = (char*) g.C + (size_t) j * g.m * g.n * (g.c_fp32 ? 4 : 2);
+        else v.C = (char*) g.C + (size_t) j * rows * g.n * elt;
     }
     else
     {
@@ -140,9 +142,11 @@ __device__ __forceinline__ bool resolve(const GemvArgs& g, int j, MatView& v)
         v.svh = g.svh;
         v.n = g.n;
         v.stride = g.n;
-        v.C = (char*) g.C + (size_t) j * g.m * g.n * (g.c_fp32 ? 4 : 2);
+        v.C = (char*) g.C + (size_t) j * rows * g.n * elt;
     }
-    v.A = g.A + (g.bszm_in == 1 ? (size_t) 0 : (size_t) j * g.m * g.k);
+    // rows [row0, row0 + m) of the slab (row groups of a call with more than 8 rows)
+    v.C = (char*) v.C + (size_t) g.row0 * v.stride * elt;
+    v.A = g.A + (g.bszm_in == 1 ? (size_t) 0 : (size_t) j * rows * g.k) + (size_t) g.row0 * g.k;
     v.scale = EXL3_HAD_RSCALE;
     if (g.weights)
     {

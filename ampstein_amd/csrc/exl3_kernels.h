@@ -31,6 +31,8 @@ struct GemvArgs
     int bszm_in;                // input slabs: 1 = broadcast
     int bszm;                   // slots (grid.y)
     int num_tokens;             // weighted reduction groups
+    int slab_m;                 // rows per A / C slab (0: m); a launch may cover rows [row0, row0 + m)
+    int row0;
     // work split (host planner)
     int stream_m1;              // 2: M = 1 balanced stream, 1: M = 1 streaming kernel, 0: LDS kernel
     int p1_blocks;              // balanced stream: workgroups (a multiple of xcd)

@@ -73,14 +73,16 @@ def test_mgemm_stacked(torch_cuda, orc, n, m, y_fp32, K, cb):
 
 
 @pytest.mark.parametrize("width", [256, 128])
-def test_mgemm_sliced_qkv(torch_cuda, orc, width):
-    """q 1024 / k 256 / v 256 cut into equal-width column slices (models.uc:367-430)."""
+@pytest.mark.parametrize("m", [1, 12])
+def test_mgemm_sliced_qkv(torch_cuda, orc, width, m):
+    """q 1024 / k 256 / v 256 cut into equal-width column slices (models.uc:367-430); 12 rows
+    run as row groups of 8 and 4 with the slices' row stride."""
     torch = torch_cuda
     from ampstein_amd import ops
     widths = [1024, 256, 256]
     bd = Bundle(torch, 1024, widths, 4, 0, seed=70)
-    x = synth.activations(1, 1024, seed=3)
-    outs = [torch.full((1, w), float("nan"), dtype=torch.half, device="cuda") for w in widths]
+    x = synth.activations(m, 1024, seed=3)
+    outs = [torch.full((m, w), float("nan"), dtype=torch.half, device="cuda") for w in widths]
     t_ptr, svh_ptr, c_ptr, strides, srcs = [], [], [], [], []
     for i, w in enumerate(widths):
         t, s, v = bd.dev[i]
@@ -94,14 +96,37 @@ def test_mgemm_sliced_qkv(torch_cuda, orc, width):
     ns = len(t_ptr)
     P = lambda v: torch.tensor(v, dtype=torch.long, device="cuda")
     I = lambda v: torch.tensor(v, dtype=torch.int32, device="cuda")
-    carrier = torch.zeros((ns, 1, width), dtype=torch.half, device="cuda")
-    A_had = torch.zeros((3, 1, 1024), dtype=torch.half, device="cuda")
+    carrier = torch.zeros((ns, m, width), dtype=torch.half, device="cuda")
+    A_had = torch.zeros((3, m, 1024), dtype=torch.half, device="cuda")
     opts = {"size_n_list": I([width] * ns), "c_ptrs": P(c_ptr), "n_stride_list": I(strides),
             "had_src_list": I(srcs), "num_had_src": 3}
     ops.mgemm(cuda_x(torch, x[None]), P(t_ptr), carrier, bd.suh, A_had, P(svh_ptr), 4, False, False, opts)
     torch.cuda.synchronize()
     for i in range(3):
         assert rel_err(outs[i].cpu().numpy(), bd.ref(orc, i, x, False)) < TOL, i
+
+
+@pytest.mark.parametrize("n", [1024, 384])
+@pytest.mark.parametrize("m", [9, 20])
+@pytest.mark.parametrize("slabs", [1, 3])
+@pytest.mark.parametrize("y_fp32", [False, True])
+def test_mgemm_many_rows(torch_cuda, orc, n, m, slabs, y_fp32):
+    """More than 8 rows per matrix (batched decode): row groups of 8 over one broadcast input or
+    one input slab per matrix, with an index that skips a slot."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    bd = Bundle(torch, 256, [n] * 3, 4, 0, seed=130 + n)
+    xs = [synth.activations(m, 256, seed=m + 17 * i) for i in range(slabs)]
+    A = cuda_x(torch, np.stack(xs))
+    C = torch.full((3, m, n), 7.0, dtype=torch.float if y_fp32 else torch.half, device="cuda")
+    idx = torch.tensor([[1, -1, 0]], dtype=torch.long, device="cuda")
+    A_had = torch.empty((3, m, 256), dtype=torch.half, device="cuda")
+    ops.exl3_mgemm(A, bd.B, C, bd.suh, A_had, bd.svh, idx, None, 4)
+    torch.cuda.synchronize()
+    got = C.cpu().numpy()
+    assert rel_err(got[0], bd.ref(orc, 1, xs[0], y_fp32)) < TOL
+    assert np.all(got[1] == 7.0)
+    assert rel_err(got[2], bd.ref(orc, 0, xs[2 if slabs == 3 else 0], y_fp32)) < TOL
 
 
 @pytest.mark.parametrize("n", [1024, 384])
