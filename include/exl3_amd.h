@@ -92,6 +92,8 @@ int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
  * parity and not written (the rotation is recomputed per workgroup).  k % 128 == 0 and
  * n % 128 == 0 when a rotation is requested, else k % 16 and n % 128.  Returns a kernel tag.
  * force_shape_idx > 0 forces a kernel (1 = GEMV, 2 = MFMA GEMM); <= 0 = by shape.
+ * K: 1..8, or 1.5 / 2.5 / 3.5 with mul1; at a half rate more than 8 rows run the GEMV in
+ * row groups of 8 (tag 90).
  * Replaces exl3_gemm (vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:321-350, dispatcher
  * :114-319), bound at src/torch/amp_torch.cpp:11251-11294 (torch.exl3_gemm). */
 int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
@@ -113,7 +115,8 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
  *     slices of num_had_src source matrices; B / svh / c_ptrs pre-offset to the slice, the row
  *     stride of trellis tiles and C is n_stride_list[q], suh is per source had_src_list[q].
  * All tables and lists are device memory.  A_had: scratch of had_slabs * m * k elements
- * (checked, not written).  m <= 8; k % 128 == 0; n % 128 == 0.
+ * (checked, not written).  k % 128 == 0; n % 128 == 0.  More than 8 rows run as row groups
+ * of 8 (not with weights).
  * Replaces exl3_mgemm (vendor/exl3/exllamav3_ext/quant/exl3_gemm.cu:396-712, semantics
  * :352-394, kernel exl3_gemm_kernel.cuh:88-343), declared at src/torch/amp_torch.cpp:3841-3864
  * and bound at :10194-10330 (torch.mgemm). */
