@@ -69,6 +69,7 @@ struct DeviceState
     int num_xcd = 0;            // > 0 when workgroup b is verified to run on XCD b % num_xcd
     float* partials = nullptr;
     int* counters = nullptr;
+    uint32_t* sink = nullptr;           // 8 KiB, zeroed, never written after init
     int64_t* filt_idx = nullptr;      // mgemm expert-range filter output (MGEMM_MAX_FILTER slots)
     uint16_t* filt_w = nullptr;
 };
@@ -106,6 +107,11 @@ int init_device(int device, DeviceState** out)
             void* f = nullptr;
             if (hipMalloc(&f, MGEMM_MAX_FILTER * (sizeof(int64_t) + sizeof(uint16_t))) != hipSuccess)
                 return fail(EXL3_AMD_ENOMEM, "filter workspace allocation failed");
+            void* sk = nullptr;
+            if (hipMalloc(&sk, 8192) != hipSuccess) return fail(EXL3_AMD_ENOMEM, "sink allocation failed");
+            if (hipMemset(sk, 0, 8192) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+                return fail(EXL3_AMD_EHIP, "sink initialisation failed");
+            d.sink = (uint32_t*) sk;
             d.filt_idx = (int64_t*) f;
             d.filt_w = (uint16_t*) (d.filt_idx + MGEMM_MAX_FILTER);
             // workgroup -> XCD dispatch order (round-robin on MI355X), verified on this device
@@ -234,6 +240,7 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     g.partials = d->partials;
     g.counters = d->counters;
     g.counters_half = (int) (WS_COUNTERS / 2);
+    g.sink = d->sink;
 #ifdef EXL3_GEMV_TRACE
     g.trace = g_trace;
 #endif

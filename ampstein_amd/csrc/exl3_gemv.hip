@@ -667,6 +667,7 @@ void gemv1_kernel(const GemvArgs g)
     const uint32_t* base = (const uint32_t*) v.trellis + lane_word_off<K>(lane)
                          + ((size_t) a * tiles_n + chunk * 8) * tile_words(K);
     const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
+    const uint32_t* sinkp = g.sink + 64 + lane_word_off<K>(lane);      // +64: room for prev_off = -1
     const bool has_suh = v.suh != nullptr;
     const uint32_t* xg = (const uint32_t*) v.A + lane;                       // x pairs
     const uint32_t* sg = (const uint32_t*) (has_suh ? v.suh : v.A) + lane;   // suh pairs
@@ -726,10 +727,11 @@ void gemv1_kernel(const GemvArgs g)
             for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
-            // refill with slice i + PF; past the last slice it re-reads slice i, just consumed and
-            // cache-hot, so the hand-off's wait for the partial stores (loads and stores retire in
-            // order) does not wait on HBM.  Unconditional, so the wait counts stay static.
-            load_slot_k<K>(base + (size_t) (i + PF <= last ? i + PF : i) * rstride, prev_off, lane, ring[d]);
+            // refill with slice i + PF; past the last slice it reads the 8 KiB sink, which every
+            // wave's tail reads and nothing writes (L2-resident: no HBM traffic, and the hand-off's
+            // wait for the partial stores does not wait on HBM).  Unconditional, so the wait
+            // counts stay static.
+            load_slot_k<K>(i + PF <= last ? base + (size_t) (i + PF) * rstride : sinkp, prev_off, lane, ring[d]);
 #if EXL3_GEMV_MFMA
             // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
             const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;

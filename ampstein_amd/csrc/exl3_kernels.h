@@ -40,6 +40,7 @@ struct GemvArgs
     int slots;                  // split partials per column chunk: k/16 / SB
     int xs_chunks;              // rotated 128-row input chunks held in LDS (LDS kernel)
     int xcd;                    // > 0: XCD-local hand-off through L2 counters (workgroups b and b + xcd on one XCD)
+    const uint32_t* sink;       // workspace: 8 KiB never written, target of the stream's past-the-end prefetches
     float* partials;            // workspace: bszm * slots * m * n fp32
     int* counters;              // workspace: zeroed; [0, half) per (slot, chunk), [half, ..) per chunk
     int counters_half;
