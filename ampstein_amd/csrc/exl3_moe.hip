@@ -459,38 +459,39 @@ __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, in
     }
 }
 
-// ---- hand-off (all threads): release this workgroup's stores, count it; true in the last of
-// `total` arrivals, which re-arms the counter.  XCD mode: every arrival on the counter runs on
-// one XCD (workgroup scope meets in its L2); else device scope.
-__device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag, bool xcd)
+// Hand-off of every row of a run at once: each thread waits for its partial stores, the
+// workgroup releases them, then thread r < nrows counts row r in counter ctr_r (total arrivals
+// total_r), re-arming it when its arrival is the last; last[r] tells the epilogue which rows this
+// workgroup completes.  One counter round trip for the run instead of one per row.
+template <typename CtrOf>
+__device__ __forceinline__ void arrive_rows(int nrows, CtrOf ctr_of, int* last, bool xcd)
 {
-    // the workgroup-scope release waits for LDS only: wait for this thread's global stores to be
-    // acknowledged by the L2 before the counter can move
     if (xcd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
-    if (threadIdx.x == 0)
+    if ((int) threadIdx.x < nrows)
     {
+        int total;
+        int* ctr = ctr_of((int) threadIdx.x, total);
         int prev;
         if (xcd) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == total - 1;
-        if (last)
+        const bool done = prev == total - 1;
+        if (done)
         {
             if (xcd) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             else __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        *flag = last;
+        last[threadIdx.x] = done;
     }
     __syncthreads();
-    const bool last = *flag;
-    if (last)
-    {
-        if (xcd) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    return last;
+}
+
+__device__ __forceinline__ void acquire_handoff(bool xcd)
+{
+    if (xcd) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 // device-scope load (misses L1): data another workgroup of this launch wrote
@@ -532,7 +533,6 @@ void moe_a_kernel(const MoeArgs a)
 {
     extern __shared__ uint32_t smem[];
     __shared__ int rows[ROWS];
-    __shared__ int flag;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nproj = a.gated ? 2 : 1;
     const int chunks = a.I / 128;
@@ -571,11 +571,15 @@ void moe_a_kernel(const MoeArgs a)
             *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
         }
     }
-    for (int r = 0; r < nrows; ++r)
+    // completed (slot, chunk) rows: one wave each
+    __shared__ int last[ROWS];
+    arrive_rows(nrows, [&](int r, int& total) { total = nproj * S; return a.ctr_a + ((size_t) rows[r] * chunks + chunk) * 32; },
+                last, a.xcd > 0);
+    for (int r = wave; r < nrows; r += NW)
     {
+        if (!last[r]) continue;
+        acquire_handoff(a.xcd > 0);
         const int s = rows[r];
-        if (!arrive_last(a.ctr_a + ((size_t) s * chunks + chunk) * 32, nproj * S, &flag, a.xcd > 0)) continue;
-        if (wave == 0)
         {
             const int col = chunk * 128 + 2 * lane;
             auto load_sum = [&](int p, float& v0, float& v1) {
@@ -619,7 +623,6 @@ void moe_a_kernel(const MoeArgs a)
             const f16x2 o = { (f16) (a0 * EXL3_HAD_RSCALE), (f16) (a1 * EXL3_HAD_RSCALE) };
             *to_global_w((uint32_t*) (a.act_out + (size_t) s * a.I + col)) = as_u32(o);
         }
-        __syncthreads();
     }
 }
 
@@ -629,7 +632,6 @@ void moe_b_kernel(const MoeArgs a)
 {
     extern __shared__ uint32_t smem[];
     __shared__ int rows[ROWS];
-    __shared__ int flag;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int chunks = a.Ho / 128;
     const int slots = a.bsz * a.topk;
@@ -662,13 +664,19 @@ void moe_b_kernel(const MoeArgs a)
             *to_global_w((f32x2*) dst) = *(const f32x2*) (res + r * 128 + 2 * c2);
         }
     }
-    for (int r = 0; r < nrows; ++r)
+    // completed (token, chunk) outputs: one wave each (a token with two slots in this run
+    // arrives twice; only one arrival can be the last)
+    __shared__ int last[ROWS];
+    arrive_rows(nrows, [&](int r, int& total) {
+                    const int row = rows[r] / a.topk;
+                    total = token_active_slots(a, row) * S;
+                    return a.ctr_b + ((size_t) row * chunks + chunk) * 32; },
+                last, a.xcd > 0);
+    for (int r = wave; r < nrows; r += NW)
     {
-        const int s = rows[r];
-        const int row = s / a.topk;
-        const int expect = token_active_slots(a, row) * S;
-        if (!arrive_last(a.ctr_b + ((size_t) row * chunks + chunk) * 32, expect, &flag, a.xcd > 0)) continue;
-        if (wave == 0)
+        if (!last[r]) continue;
+        acquire_handoff(a.xcd > 0);
+        const int row = rows[r] / a.topk;
         {
             const int col = chunk * 128 + 2 * lane;
             float o0 = 0.0f, o1 = 0.0f;
@@ -713,7 +721,6 @@ void moe_b_kernel(const MoeArgs a)
             if (col < a.H_out) *to_global_w(dst) = o0;
             if (col + 1 < a.H_out) *to_global_w(dst + 1) = o1;
         }
-        __syncthreads();
     }
 }
 
