@@ -385,6 +385,47 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
     }
 }
 
+// One wave's epilogue of an M = 1 chunk (no routing weights): v0, v1 are this workgroup's sums
+// of columns 2 lane, 2 lane + 1 (corrections applied).  One split: rotate and store.  Several:
+// store the partial to this workgroup's slot; in XCD mode count it in the chunk's counter (the
+// wave waits for its stores first: the workgroup-scope release orders LDS only) and, in the last
+// arrival, sum the slots in order, rotate and store.  Wave-level only: the workgroup's other
+// waves have ended.
+__device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int chunk, int slot, int splits,
+                               float v0, float v1, uint32_t svp)
+{
+    const int lane = threadIdx.x & 63;
+    const int col = chunk * 128 + 2 * lane;
+    if (splits == 1)
+    {
+        store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+        return;
+    }
+    float* pbase = g.partials + ((size_t) j * (g.n / 128) + chunk) * splits * 128;
+    *to_global_w((f32x2*) (pbase + (size_t) slot * 128 + 2 * lane)) = (f32x2) { v0, v1 };
+    if (!g.xcd) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    int* ctr = g.counters + ((size_t) j * (g.n / 128) + chunk) * 32;
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != splits - 1) return;
+    if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int p0 = 0; p0 < splits; p0 += 8)
+    {
+        f32x2 vv[8];
+        #pragma unroll
+        for (int u = 0; u < 8; ++u) vv[u] = load_l2_f32x2(pbase + (size_t) min(p0 + u, splits - 1) * 128 + 2 * lane);
+        #pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (p0 + u < splits) { s0 += vv[u].x; s1 += vv[u].y; }
+    }
+    store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+}
+
 // Inactive slot (negative index) in weighted XCD mode: still counted once per chunk.
 __device__ void inactive_arrive(const GemvArgs& g, int chunk, int slot, int* flag)
 {
@@ -788,6 +829,24 @@ void gemv1_kernel(const GemvArgs g)
     red[wave][c0 + 8] = acc1;
     if (lane == 0) sumx_w[wave] = sx;
     __syncthreads();
+    if (!g.weights)
+    {
+        // one wave finishes the chunk; the other three end here, so their registers take the
+        // next workgroups' waves instead of idling through the hand-off
+        if (wave != 0) return;
+        float v0 = red[0][2 * lane] + red[1][2 * lane] + red[2][2 * lane] + red[3][2 * lane];
+        float v1 = red[0][2 * lane + 1] + red[1][2 * lane + 1] + red[2][2 * lane + 1] + red[3][2 * lane + 1];
+        if (CB == 2)
+        {
+            const float kinv = (float) as_h(0x1eee);
+            const float bias = (sumx_w[0] + sumx_w[1] + sumx_w[2] + sumx_w[3]) * (float) as_h(0xc931);
+            v0 = v0 * kinv + bias;
+            v1 = v1 * kinv + bias;
+        }
+        finish_m1_wave(g, v, j, chunk, slot, splits, v0, v1, svp);
+        GEMV_STAMP(g, 3, 0);
+        return;
+    }
     if (threadIdx.x < 128)
     {
         const int c = threadIdx.x;
