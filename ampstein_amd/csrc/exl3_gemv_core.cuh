@@ -126,6 +126,27 @@ __device__ __forceinline__ void raw8(const uint32_t* wv, uint32_t* raw, const ui
     }
 }
 
+// MUL1 weights of windows 2q, 2q + 1 packed into one word: low half 0x6400 + byte sum of
+// window 2q's product, high half that of window 2q + 1 (v_sad_u8 then v_sad_hi_u8, which adds
+// its byte sum shifted left by 16): the fp16 pair (1024 + s_2q, 1024 + s_2q+1).
+template <int K, int Q>
+__device__ __forceinline__ uint32_t mul1_pair(const uint32_t* wv)
+{
+    const uint32_t p0 = state16<K, 2 * Q>(wv) * 0x83DCD12Du, p1 = state16<K, 2 * Q + 1>(wv) * 0x83DCD12Du;
+    return __builtin_amdgcn_sad_hi_u8(p1, 0u, __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u));
+}
+
+template <int K>
+__device__ __forceinline__ void mul1_pairs(const uint32_t* wv, uint32_t* pk)
+{
+    pk[0] = mul1_pair<K, 0>(wv);   pk[1] = mul1_pair<K, 1>(wv);   pk[2] = mul1_pair<K, 2>(wv);
+    pk[3] = mul1_pair<K, 3>(wv);   pk[4] = mul1_pair<K, 4>(wv);   pk[5] = mul1_pair<K, 5>(wv);
+    pk[6] = mul1_pair<K, 6>(wv);   pk[7] = mul1_pair<K, 7>(wv);   pk[8] = mul1_pair<K, 8>(wv);
+    pk[9] = mul1_pair<K, 9>(wv);   pk[10] = mul1_pair<K, 10>(wv); pk[11] = mul1_pair<K, 11>(wv);
+    pk[12] = mul1_pair<K, 12>(wv); pk[13] = mul1_pair<K, 13>(wv); pk[14] = mul1_pair<K, 14>(wv);
+    pk[15] = mul1_pair<K, 15>(wv);
+}
+
 template <int K, int CB>
 __device__ __forceinline__ void raw32(const uint32_t* wv, uint32_t* raw, const uint32_t a3, const uint32_t b3)
 {

@@ -278,8 +278,9 @@ struct XSrc
 };
 
 // x rows of the run (fp16 rows of `src`, row stride `ld`) for k-slices [ks0, ks0 + nks) into LDS
-// as (x, x) pairs.  16-byte loads, two per thread in flight before either is consumed: one
+// as (x, x) pairs (DUP) or as they are (the MUL1 body dots packed weight pairs).  16-byte loads, two per thread in flight before either is consumed: one
 // memory round trip per 2 x 256 x 8 halves instead of one per pair.
+template <bool DUP>
 __device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* rows, int nrows, int ks0, int nks,
                                         uint32_t* xs, int xs_stride)
 {
@@ -301,7 +302,8 @@ __device__ __forceinline__ void stage_x(const uint16_t* src, int ld, const int* 
         {
             const int e = e0 + j * NT + (int) threadIdx.x;
             const int r = e / per_row, i = e - r * per_row;
-            if (e < total)
+            if (e < total && !DUP) *(u32x4*) (xs + r * xs_stride + 4 * i) = v[j];
+            if (e < total && DUP)
             {
                 uint32_t* d = xs + r * xs_stride + 8 * i;
                 const uint32_t w[4] = { v[j].x, v[j].y, v[j].z, v[j].w };
@@ -351,7 +353,7 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
         __builtin_amdgcn_sched_barrier(0);
     }
     // the x rows after the weight prefetch: both latencies overlap
-    stage_x(xsrc.src, xsrc.ld, xsrc.rows, min(nrows, MT), ks0, nks, xs, xs_stride);   // LDS holds MT rows
+    stage_x<CB != 2>(xsrc.src, xsrc.ld, xsrc.rows, min(nrows, MT), ks0, nks, xs, xs_stride);   // LDS holds MT rows
 
     float acc[MT][2];
     #pragma unroll
@@ -368,6 +370,39 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
             uint32_t wv[KB + 1];
             #pragma unroll
             for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+            if constexpr (CB == 2)
+            {
+                // MUL1: the weights of rows 2g and 2g + 1 of a column packed in one word by
+                // v_sad_u8 / v_sad_hi_u8 (each half 0x6400 + byte sum, codebook.cuh:78-84),
+                // dotted with the x pair (x_2g, x_2g+1): one v_dot2 per two weights
+                uint32_t pk[16];
+                mul1_pairs<K>(wv, pk);
+                load_slot_k<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, lane, ring[d]);
+                #pragma unroll
+                for (int r = 0; r < MT; ++r)
+                {
+                    if (MT > 1 && r >= nrows) break;
+                    const u32x4* xp = (const u32x4*) (xs + r * xs_stride + xo / 2);
+                    uint32_t x8[8];
+                    #pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                    {
+                        u32x4 tq = xp[q];
+                        x8[4 * q] = live ? tq.x : 0u;     x8[4 * q + 1] = live ? tq.y : 0u;
+                        x8[4 * q + 2] = live ? tq.z : 0u; x8[4 * q + 3] = live ? tq.w : 0u;
+                    }
+                    #pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                    {
+                        const int w = 2 * q, gq = w >> 3, jj = w & 7;
+                        const int pr = gq + 4 * ((jj >> 1) & 1);        // x pair of rows 2 pr, 2 pr + 1
+                        float& acc_ = acc[r][jj >> 2];
+                        acc_ = __builtin_amdgcn_fdot2(as_h2(x8[pr]), as_h2(pk[q]), acc_, false);
+                    }
+                }
+            }
+            else
+            {
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
             load_slot_k<K>(base + (size_t) min(i + PF, last_i) * kstride, prev_off, lane, ring[d]);
@@ -393,6 +428,7 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
                     acc_ = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc_, false);
                 }
             }
+            }
         }
     }
     const int c0 = (lane >> 3) * 16 + (lane & 7);
@@ -409,7 +445,11 @@ __device__ __forceinline__ void moe_gemv(const uint16_t* trellis, int tiles_n, i
         for (int r = wave; r < nrows; r += NW)
         {
             float sv = 0.0f;
-            for (int e = lane; e < nks * 16; e += 64) sv += (float) as_h2(xs[r * xs_stride + e]).x;
+            for (int e = lane; e < nks * 8; e += 64)
+            {
+                const f16x2 h = as_h2(xs[r * xs_stride + e]);
+                sv += (float) h.x + (float) h.y;
+            }
             sv = wave_sum(sv, lane);
             if (lane == 0) sumx[r] = sv;
         }
@@ -528,7 +568,7 @@ __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, i
 }
 
 template <int CB, int MT, bool HS>
-__global__ __launch_bounds__(NT)
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_a_kernel(const MoeArgs a)
 {
     extern __shared__ uint32_t smem[];
@@ -627,7 +667,7 @@ void moe_a_kernel(const MoeArgs a)
 }
 
 template <int CB, int MT, bool HS>
-__global__ __launch_bounds__(NT)
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_b_kernel(const MoeArgs a)
 {
     extern __shared__ uint32_t smem[];
