@@ -662,7 +662,10 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     // work split: k-splits so every workgroup holds at most EXL3_MOE_SBMAX k-slices and the grid
     // (sized for one run per slot) reaches a few workgroups per CU
     const int nproj = gated ? 2 : 1;
-    const long target = 4L * d->num_cus;
+    // 2 workgroups per CU: the one-token batch (8 slots) then splits gate/up and down k in 2
+    // (measured 1, 2, 4, 8 per CU: 51.9, 51.6, 53.6, 68.4 us)
+    long target = 2L * d->num_cus;
+    if (const char* e = getenv("EXL3_AMD_MOE_WG_PER_CU")) { int v = atoi(e); if (v > 0) target = (long) v * d->num_cus; }
     auto pick = [&](int KS, long base) {
         int S = (KS + EXL3_MOE_SBMAX - 1) / EXL3_MOE_SBMAX;
         while (base * S < target && KS / (S + 1) >= 8) ++S;
