@@ -158,22 +158,24 @@ void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict_
 // pass (32 lanes, 4 columns each).
 __device__ __forceinline__ int rh_dw(int R, int cp) { return R * 64 + (cp ^ (((R >> 2) & 31) << 1)); }
 
-__device__ __forceinline__ f16x2 shfl_h2(f16x2 v, int src_lane)
-{
-    return as_h2(__builtin_amdgcn_ds_bpermute(src_lane << 2, as_u32(v)));
-}
 
 // fp16 lane stages xor 1..16 within a 32-lane half: lower lane a + b, upper (-b) + a
-// (shuffle_had_h2x32, hadamard_inner.cuh:83-93).
+// (shuffle_had_h2x32, hadamard_inner.cuh:83-93).  The partner value moves by DPP / permlane
+// (exl3_common.cuh xor_partner), not through LDS.
+template <int M>
+__device__ __forceinline__ f16x2 had_h2_stage(f16x2 v, int lane)
+{
+    const f16x2 p = as_h2(__builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, as_u32(v)), lane)));
+    return (lane & M) ? (p + (-v)) : (v + p);
+}
+
 __device__ __forceinline__ f16x2 had_h2x32(f16x2 v, int lane)
 {
-    #pragma unroll
-    for (int m = 1; m < 32; m <<= 1)
-    {
-        f16x2 p = shfl_h2(v, lane ^ m);
-        v = (lane & m) ? (p + (-v)) : (v + p);
-    }
-    return v;
+    v = had_h2_stage<1>(v, lane);
+    v = had_h2_stage<2>(v, lane);
+    v = had_h2_stage<4>(v, lane);
+    v = had_h2_stage<8>(v, lane);
+    return had_h2_stage<16>(v, lane);
 }
 
 template <int K, int CB>
