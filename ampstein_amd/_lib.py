@@ -56,6 +56,23 @@ SIGNATURES = {
                                  _vp, _vp, _i32,                         # sh_out, sh_gate_w, n
                                  _vp, _vp, _vp,                          # bits tables
                                  _vp]),
+    "exl3_amd_moe_max_concurrency": (_i32, [_i32]),
+    "exl3_amd_moe": (_i32, [_vp, _i32, _i32, _vp,                       # hidden, bsz, hidden_dim, output
+                            _vp, _i32, _vp, _vp, _i32,                  # expert_count (+len), token/weight_sorted, n
+                            _vp, _vp, _i32, _i32,                       # temp_state_g/u, concurrency, max_tokens
+                            _vp, _vp, _i32,                             # temp_intermediate_g/u, intermediate_dim
+                            _i32, _f32, _f32, _f32,                     # act, K gate/up/down
+                            _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,   # tables, num_ptrs
+                            _i32, _i32, _i32, _i32, _i32, _i32,         # codebook flags
+                            _f32, _i32,                                 # act_limit, num_active
+                            _vp, ctypes.c_int64, _i32, _vp,             # output_scratch (rows, cols), fused_base
+                            _i32, _i32, _i32,                           # count_lo, count_hi, m_tile
+                            _vp, _vp, _vp, _i32,                        # bits tables, len
+                            _vp]),
+    "exl3_amd_moe_gather": (_i32, [_vp, _i32, _i32, _vp, _i32,          # out, tokens, hidden, scratch, cols
+                                   _vp, _i32, _vp,                      # flat_expert, num_assign, inv_order
+                                   _vp, _i32, _vp, _i32,                # expert_start (+len), slot_base (+len)
+                                   _vp, _i32, _vp, _vp]),               # slot_kind, num_experts, weight_sorted
 }
 
 

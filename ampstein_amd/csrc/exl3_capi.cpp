@@ -689,4 +689,192 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     return rc ? hip_fail(rc, "exl3_moe_coop") : 0;
 }
 
+
+int exl3_amd_moe_max_concurrency(int device)
+{
+    g_last_error.clear();
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    return d->num_cus / 8;                           // exl3_moe.cu:15-19 (MOE_SMS_PER_EXPERT = 8)
+}
+
+int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* output_state,
+                 const int64_t* expert_count, int expert_count_len,
+                 const int64_t* token_sorted, const uint16_t* weight_sorted, int num_assign,
+                 uint16_t* temp_state_g, uint16_t* temp_state_u, int concurrency, int max_tokens_per_expert,
+                 uint16_t* temp_intermediate_g, uint16_t* temp_intermediate_u, int intermediate_dim,
+                 int act_function, float K_gate, float K_up, float K_down,
+                 const uint64_t* gate_ptrs_trellis, const uint64_t* gate_ptrs_suh, const uint64_t* gate_ptrs_svh,
+                 const uint64_t* up_ptrs_trellis, const uint64_t* up_ptrs_suh, const uint64_t* up_ptrs_svh,
+                 const uint64_t* down_ptrs_trellis, const uint64_t* down_ptrs_suh, const uint64_t* down_ptrs_svh,
+                 int num_ptrs,
+                 int gate_mcg, int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1,
+                 float act_limit, int num_active,
+                 float* output_scratch, int64_t scratch_rows, int scratch_cols, const int64_t* fused_base,
+                 int count_lo, int count_hi, int m_tile,
+                 const uint8_t* bits_g, const uint8_t* bits_u, const uint8_t* bits_d, int bits_len,
+                 void* stream)
+{
+    g_last_error.clear();
+    // exl3_moe.cu:186-323, in the reference's order
+    if (num_active == 0) return 0;
+    if (output_scratch)
+    {
+        if (!fused_base) return fail(EXL3_AMD_EINVAL, "exl3_moe: output_scratch needs fused_base");
+        if (scratch_cols != hidden_dim) return fail(EXL3_AMD_EINVAL, "exl3_moe: output_scratch must be [slots, hidden]");
+    }
+    if (!hidden_state || !output_state || !expert_count || !token_sorted || !weight_sorted || !temp_state_g ||
+        !temp_state_u || !temp_intermediate_g || !temp_intermediate_u)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: null pointer");
+    if (bsz < 1 || expert_count_len < 1 || num_assign % bsz != 0)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: token_sorted must hold bsz * num_experts_per_tok entries");
+    const int num_experts = expert_count_len - 1;
+    if (concurrency < 1 || max_tokens_per_expert < 1 || intermediate_dim < 1)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: temp buffer shapes");
+    if (!(gate_mcg == up_mcg && up_mcg == down_mcg && gate_mul1 == up_mul1 && up_mul1 == down_mul1))
+        return fail(EXL3_AMD_EINVAL, "MoE kernel: gate/up/down must share the same codebook");
+    if (gate_mcg == gate_mul1) return fail(EXL3_AMD_EINVAL, "MoE kernel: Only mcg and mul1 codebooks are supported");
+    auto k2 = [](float K) { return (int) (2.0f * K); };
+    const int K2g = k2(K_gate), K2u = k2(K_up), K2d = k2(K_down);
+    if (!gate_mul1 && (K2g % 2 || K2u % 2 || K2d % 2))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: half-integer bitrates require the mul1 codebook");
+    if (bits_g || bits_u || bits_d)
+    {
+        if (!(bits_g && bits_u && bits_d)) return fail(EXL3_AMD_EINVAL, "exl3_moe: give all three bit width tables or none");
+        if (bits_len < num_experts)
+            return fail(EXL3_AMD_EINVAL, "exl3_moe: bit width tables must be contiguous uint8, one entry per expert");
+        if (!gate_mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe: mixed bit widths require the mul1 codebook");
+    }
+    if (!gate_ptrs_trellis || !gate_ptrs_suh || !gate_ptrs_svh || !up_ptrs_trellis || !up_ptrs_suh ||
+        !up_ptrs_svh || !down_ptrs_trellis || !down_ptrs_suh || !down_ptrs_svh)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: null pointer table");
+    if (num_ptrs != num_experts) return fail(EXL3_AMD_EINVAL, "Number of gate tensors doesn't match num_experts");
+
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    if (concurrency * 8 > d->num_cus) return fail(EXL3_AMD_EINVAL, "Concurrency too high for device num_sms");
+    if (m_tile > 16)
+    {
+        if (!gate_mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe: row tiles above 16 are instantiated for the mul1 codebook only");
+        if (max_tokens_per_expert < m_tile) return fail(EXL3_AMD_EINVAL, "exl3_moe: temp buffers hold fewer rows than the tile");
+    }
+    // this build's limits: 128-multiples (every row is rotated in 128-chunks), integer rates in
+    // the MFMA tiles, the plan's expert count
+    if (hidden_dim % 128 || intermediate_dim % 128)
+        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: hidden and intermediate sizes must be multiples of 128");
+    if (K2g % 2 || K2u % 2 || K2d % 2)
+        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: half-integer bitrates are not implemented in the MFMA tiles");
+    if (!bits_g && !(K2g >= 2 && K2g <= 16 && K2u >= 2 && K2u <= 16 && K2d >= 2 && K2d <= 16))
+        return fail(EXL3_AMD_EINVAL, "exl3_moe: bitrate out of range");
+    if (num_experts > 4096) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: more than 4096 experts");
+
+    const int64_t pool64 = (int64_t) concurrency * max_tokens_per_expert;
+    const int pool = (int) std::min<int64_t>(pool64, (int64_t) num_assign);   // rows a pass can hold
+    const int rt_cap = pool / 256 + std::min(num_experts, pool) + 1;
+    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 24 * (size_t) rt_cap + 24;
+    if (ws_ints * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: pool exceeds the library workspace");
+
+    MoesArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = hidden_state; a.out = output_state; a.scratch = output_scratch; a.fused_base = fused_base;
+    a.expert_count = expert_count; a.token_sorted = token_sorted; a.weight_sorted = weight_sorted;
+    a.num_experts = num_experts; a.num_assign = num_assign; a.H = hidden_dim; a.I = intermediate_dim;
+    a.max_tokens = max_tokens_per_expert; a.count_lo = count_lo; a.count_hi = count_hi;
+    a.pool_rows = pool;
+    a.ts_g = temp_state_g; a.ts_u = temp_state_u; a.ti_g = temp_intermediate_g; a.ti_u = temp_intermediate_u;
+    a.g_trellis = gate_ptrs_trellis; a.g_suh = gate_ptrs_suh; a.g_svh = gate_ptrs_svh;
+    a.u_trellis = up_ptrs_trellis; a.u_suh = up_ptrs_suh; a.u_svh = up_ptrs_svh;
+    a.d_trellis = down_ptrs_trellis; a.d_suh = down_ptrs_suh; a.d_svh = down_ptrs_svh;
+    a.bits_g = bits_g; a.bits_u = bits_u; a.bits_d = bits_d;
+    a.K_g = K2g / 2; a.K_u = K2u / 2; a.K_d = K2d / 2;
+    a.act = act_function; a.gated = act_function != 2;      // MOE_ACT_RELU2_NOGATE skips the gate
+    a.act_limit = act_limit;
+    int* ws = (int*) d->partials;
+    a.rowinfo = ws;
+    a.rt = ws + 3 * (size_t) pool;
+    a.lists = a.rt + 3 * (size_t) rt_cap;
+    a.counts = a.lists + 24 * (size_t) rt_cap;
+    a.rt_cap = rt_cap;
+
+    typedef int (*group_fn)(const GemmGroupArgs&, int, hipStream_t);
+    static const group_fn gfn[8] = { exl3k_gemm_group_k1, exl3k_gemm_group_k2, exl3k_gemm_group_k3, exl3k_gemm_group_k4,
+                                     exl3k_gemm_group_k5, exl3k_gemm_group_k6, exl3k_gemm_group_k7, exl3k_gemm_group_k8 };
+    const int cb = gate_mul1 ? 2 : 1;
+    hipStream_t s = (hipStream_t) stream;
+    // one grouped launch per (phase, bitrate) that can occur: the list counts sit on the device
+    auto gemm_phase = [&](int phase) -> int {
+        for (int K = 1; K <= 8; ++K)
+        {
+            GemmGroupArgs g;
+            memset(&g, 0, sizeof(g));
+            g.rt = a.rt;
+            g.nrt = rt_cap;
+            int mats = 0;
+            auto add = [&](int m, const uint16_t* A, uint16_t* C, const uint64_t* tab, int Km) {
+                if (!bits_g && Km != K) return;
+                g.A[mats] = A; g.C[mats] = C; g.tab[mats] = tab;
+                g.list[mats] = a.lists + (size_t) (m * 8 + K - 1) * rt_cap;
+                g.count[mats] = a.counts + m * 8 + K - 1;
+                ++mats;
+            };
+            if (phase == 0)
+            {
+                if (a.gated) add(0, a.ts_g, a.ti_g, a.g_trellis, a.K_g);
+                add(1, a.ts_u, a.ti_u, a.u_trellis, a.K_u);
+                g.k = hidden_dim; g.n = intermediate_dim;
+            }
+            else
+            {
+                add(2, a.ti_g, a.ts_g, a.d_trellis, a.K_d);
+                g.k = intermediate_dim; g.n = hidden_dim;
+            }
+            if (!mats) continue;
+            g.mats = mats;
+            if (int rc = gfn[K - 1](g, cb, s)) return rc;
+        }
+        return 0;
+    };
+    const int cus = d->num_cus;
+    for (int row0 = 0; row0 < num_assign; row0 += pool)
+    {
+        int rc = exl3k_moes_plan(a, row0, s);
+        if (!rc) rc = exl3k_moes_gather(a, cus, s);
+        if (!rc) rc = gemm_phase(0);
+        if (!rc) rc = exl3k_moes_act(a, cus, s);
+        if (!rc) rc = gemm_phase(1);
+        if (!rc) rc = exl3k_moes_out(a, cus, s);
+        if (rc) return hip_fail(rc, "exl3_moe");
+    }
+    return 0;
+}
+
+int exl3_amd_moe_gather(float* output_state, int tokens, int hidden_dim,
+                        const float* output_scratch, int scratch_cols,
+                        const int64_t* flat_expert, int num_assign, const int64_t* inv_order,
+                        const int64_t* expert_start, int expert_start_len,
+                        const int64_t* slot_base, int slot_base_len,
+                        const int64_t* slot_kind, int num_experts,
+                        const uint16_t* weight_sorted, void* stream)
+{
+    g_last_error.clear();
+    // exl3_moe.cu:480-527
+    if (!output_state || !output_scratch || !flat_expert || !inv_order || !expert_start || !slot_base ||
+        !slot_kind || !weight_sorted)
+        return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: null pointer");
+    if (scratch_cols != hidden_dim) return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: output_scratch must be [slots, hidden]");
+    if (tokens < 0 || (tokens > 0 && num_assign % tokens != 0)) return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: assignments / tokens");
+    if (!(slot_base_len >= num_experts && expert_start_len >= num_experts)) return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: table sizes");
+    if (!tokens) return 0;
+    const int topk = num_assign / tokens;
+    if (topk > 32) return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: top-k too large");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    MoesGatherArgs g;
+    g.out = output_state; g.scratch = output_scratch; g.flat_expert = flat_expert; g.inv_order = inv_order;
+    g.expert_start = expert_start; g.slot_base = slot_base; g.slot_kind = slot_kind; g.weight_sorted = weight_sorted;
+    g.tokens = tokens; g.H = hidden_dim; g.topk = topk; g.num_experts = num_experts;
+    int rc = exl3k_moes_sum(g, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "exl3_moe_gather") : 0;
+}
+
 }  // extern "C"

@@ -23,6 +23,8 @@
 // 16 distinct 16-byte bank groups.
 //
 // Compiled once per K (EXL3_INST_K).
+#include <cstring>
+
 #include "exl3_common.cuh"
 #include "exl3_kernels.h"
 
@@ -160,10 +162,10 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
 __device__ __forceinline__ int a_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
 __device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ ((col >> 3) & 1)); }
 
-template <int K, int CB>
+template <int K, int CB, bool GROUP>
 __global__ __launch_bounds__(GT, 1)
 void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ trellis, void* __restrict__ C,
-                 const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+                 const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, GemmGroupArgs grp)
 {
     using LD = GemmLds<K>;
     __shared__ __align__(16) uint32_t lds[LD::TOTAL];
@@ -171,12 +173,32 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = threadIdx.x;
     const int NST = k / 32;                              // stages
-    const int nbn = (n + BN - 1) / BN, nmb = (M + BM - 1) / BM;   // n % 128 == 0: a last block may be half
+    const int nbn = (n + BN - 1) / BN;                   // n % 128 == 0: a last block may be half
 
     // workgroup -> (column block, row block): the row blocks of one column block run together on
     // one XCD (workgroups b and b + 8 on one XCD) when the block count allows, sharing its trellis in L2
     int nb, mb;
-    if (nbn % 8 == 0)
+    if constexpr (GROUP)
+    {
+        // grouped launch: one row tile of one expert per workgroup (uniform early exit past the
+        // list: no barrier has been reached)
+        nb = blockIdx.x % nbn;
+        const int t2 = blockIdx.x / nbn;
+        const int mat = t2 % grp.mats, li = t2 / grp.mats;
+        if (li >= *(mat ? grp.count[1] : grp.count[0])) return;
+        const int tid = (mat ? grp.list[1] : grp.list[0])[li];
+        const int e = grp.rt[3 * tid], row0 = grp.rt[3 * tid + 1];
+        M = grp.rt[3 * tid + 2];
+        Ain = (mat ? grp.A[1] : grp.A[0]) + (size_t) row0 * k;
+        C = (mat ? grp.C[1] : grp.C[0]) + (size_t) row0 * n;
+        trellis = (const uint16_t*) (mat ? grp.tab[1] : grp.tab[0])[e];
+        svh = nullptr;
+        c_fp32 = 0;
+        mb = 0;
+    }
+    const int nmb = (M + BM - 1) / BM;
+    if constexpr (GROUP) { }           // (nb, mb) from the row tile above
+    else if (nbn % 8 == 0)
     {
         const int x = blockIdx.x % 8, r = blockIdx.x / 8;
         nb = x + 8 * (r / nmb);
@@ -388,8 +410,21 @@ template <int K, int CB>
 int launch_gemm(const GemmArgs& g, hipStream_t s)
 {
     const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_kernel<K, CB>), dim3(blocks), dim3(GT), 0, s,
-                       g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32);
+    GemmGroupArgs none;
+    memset(&none, 0, sizeof(none));
+    hipLaunchKernelGGL((gemm_kernel<K, CB, false>), dim3(blocks), dim3(GT), 0, s,
+                       g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, none);
+    return (int) hipGetLastError();
+}
+
+template <int K, int CB>
+int launch_gemm_group(const GemmGroupArgs& g, hipStream_t s)
+{
+    const long blocks = (long) g.nrt * g.mats * ((g.n + BN - 1) / BN);
+    if (blocks <= 0) return 0;
+    hipLaunchKernelGGL((gemm_kernel<K, CB, true>), dim3((unsigned) blocks), dim3(GT), 0, s,
+                       (const uint16_t*) nullptr, (const uint16_t*) nullptr, (void*) nullptr,
+                       (const uint16_t*) nullptr, 0, g.k, g.n, 0, g);
     return (int) hipGetLastError();
 }
 
@@ -405,6 +440,17 @@ int EXL3_CAT(exl3k_gemm_k, EXL3_INST_K)(const GemmArgs& g, int cb, hipStream_t s
         case 0: return launch_gemm<EXL3_INST_K, 0>(g, s);
         case 1: return launch_gemm<EXL3_INST_K, 1>(g, s);
         case 2: return launch_gemm<EXL3_INST_K, 2>(g, s);
+    }
+    return -1;
+}
+
+int EXL3_CAT(exl3k_gemm_group_k, EXL3_INST_K)(const GemmGroupArgs& g, int cb, hipStream_t s)
+{
+    // the token-sorted MoE takes the mcg and mul1 codebooks only (exl3_moe.cu:242)
+    switch (cb)
+    {
+        case 1: return launch_gemm_group<EXL3_INST_K, 1>(g, s);
+        case 2: return launch_gemm_group<EXL3_INST_K, 2>(g, s);
     }
     return -1;
 }

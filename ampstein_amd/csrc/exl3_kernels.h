@@ -67,6 +67,75 @@ int exl3k_gemm_k6(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k7(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k8(const GemmArgs& g, int cb, hipStream_t s);
 
+// Grouped GEMM of the token-sorted MoE: one launch runs every row tile of one bitrate.  A row
+// tile is (expert, first row, rows <= 256) of the compacted row pool; workgroup b runs column
+// block b % nbn of list entry (b / nbn) / mats of matrix set (b / nbn) % mats and exits when the
+// entry is past count.  No output rotation; fp16 output rows.
+struct GemmGroupArgs
+{
+    const uint16_t* A[2];       // (pool rows, k) fp16, per matrix set
+    uint16_t* C[2];             // (pool rows, n) fp16
+    const uint64_t* tab[2];     // trellis address per expert
+    const int* rt;              // row tiles: (expert, first row, rows) triples
+    const int* list[2];         // row-tile ids at this bitrate, per matrix set
+    const int* count[2];        // entries in list[i]
+    int mats;                   // 1 or 2
+    int k, n;
+    int nrt;                    // row-tile capacity of the launch
+};
+
+int exl3k_gemm_group_k1(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k2(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k3(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k4(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k5(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k6(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k7(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k8(const GemmGroupArgs& g, int cb, hipStream_t s);
+
+// Token-sorted MoE (exl3_moe_sorted.hip).  Pool rows are the caller's temp buffers; the plan
+// tables live in the library workspace.
+struct MoesArgs
+{
+    const uint16_t* x;          // (bsz, H) fp16
+    float* out;                 // (bsz, H) fp32, accumulated into (atomic mode)
+    float* scratch;             // (slots, H) fp32 or null: deterministic slot mode
+    const int64_t* fused_base;  // slot of each expert's first row (slot mode)
+    const int64_t* expert_count;    // (num_experts + 1), the last entry ignored
+    const int64_t* token_sorted;    // (num_assign) token of each sorted assignment
+    const uint16_t* weight_sorted;  // (num_assign) fp16 routing weight
+    int num_experts, num_assign, H, I;
+    int max_tokens, count_lo, count_hi;
+    int pool_rows;              // rows of the temp buffers (concurrency x max_tokens)
+    uint16_t *ts_g, *ts_u;      // (pool_rows, H) fp16
+    uint16_t *ti_g, *ti_u;      // (pool_rows, I) fp16
+    const uint64_t *g_trellis, *g_suh, *g_svh, *u_trellis, *u_suh, *u_svh, *d_trellis, *d_suh, *d_svh;
+    const uint8_t *bits_g, *bits_u, *bits_d;
+    int K_g, K_u, K_d;          // integer bitrates when there are no tables
+    int act, gated;
+    float act_limit;
+    int* rowinfo;               // workspace: (sorted position or -1, expert, row within expert) per pool row
+    int* rt;                    // workspace: row tiles (expert, first pool row, rows)
+    int* lists;                 // workspace: 3 x 8 lists of row-tile ids, rt_cap each
+    int* counts;                // workspace: 3 x 8 list lengths
+    int rt_cap;
+};
+
+struct MoesGatherArgs
+{
+    float* out;                 // (tokens, H) fp32
+    const float* scratch;       // (slots, H) fp32
+    const int64_t *flat_expert, *inv_order, *expert_start, *slot_base, *slot_kind;
+    const uint16_t* weight_sorted;
+    int tokens, H, topk, num_experts;
+};
+
+int exl3k_moes_plan(const MoesArgs& a, int pass_row0, hipStream_t s);
+int exl3k_moes_gather(const MoesArgs& a, int cus, hipStream_t s);
+int exl3k_moes_act(const MoesArgs& a, int cus, hipStream_t s);
+int exl3k_moes_out(const MoesArgs& a, int cus, hipStream_t s);
+int exl3k_moes_sum(const MoesGatherArgs& a, hipStream_t s);
+
 // Fused decode-shaped MoE (exl3_moe_coop): route/rotate, gate/up GEMV + activation, down GEMV +
 // routing-weighted sum.  Device pointers throughout; tables indexed by local expert.
 struct MoeArgs

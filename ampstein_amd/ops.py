@@ -370,6 +370,111 @@ def exl3_moe_coop(x: Tensor, sel: Tensor, rw: Tensor, min_expert: int, max_exper
             _stream(x)))
 
 
+def exl3_moe_max_concurrency(device: int = 0) -> int:
+    """exl3_moe_max_concurrency (exl3_moe.cu:15-19): the temp buffers' first dimension."""
+    return check(_lib.lib().exl3_amd_moe_max_concurrency(int(device)))
+
+
+def exl3_moe(hidden_state: Tensor, output_state: Tensor, expert_count: Tensor, token_sorted: Tensor,
+             weight_sorted: Tensor, temp_state_g: Tensor, temp_state_u: Tensor,
+             temp_intermediate_g: Tensor, temp_intermediate_u: Tensor, act_function: int,
+             K_gate: float, K_up: float, K_down: float,
+             gate_ptrs_trellis: Tensor, gate_ptrs_suh: Tensor, gate_ptrs_svh: Tensor,
+             up_ptrs_trellis: Tensor, up_ptrs_suh: Tensor, up_ptrs_svh: Tensor,
+             down_ptrs_trellis: Tensor, down_ptrs_suh: Tensor, down_ptrs_svh: Tensor,
+             gate_mcg: bool, gate_mul1: bool, up_mcg: bool, up_mul1: bool, down_mcg: bool, down_mul1: bool,
+             act_limit: float, num_active: int, output_scratch: Optional[Tensor] = None,
+             fused_base: Optional[Tensor] = None, count_lo: int = 0, count_hi: int = 1 << 30,
+             m_tile: int = 16, bits_g: Optional[Tensor] = None, bits_u: Optional[Tensor] = None,
+             bits_d: Optional[Tensor] = None) -> None:
+    """Token-sorted fused MoE, the tensor front end of exl3_moe (exl3_moe.cu:137-418): the experts
+    with count_lo <= count <= count_hi (and count <= max_tokens_per_expert) run gate / up / act /
+    down on their gathered rows and add weight * result into output_state (fp32, zeroed by the
+    caller), or store it in their slots of output_scratch (then exl3_moe_gather sums in order)."""
+    if num_active == 0:
+        return
+    if output_scratch is not None:
+        _need(fused_base is not None, "exl3_moe: output_scratch needs fused_base")
+        _dtype(output_scratch, torch.float, "output_scratch")
+        _dtype(fused_base, torch.long, "fused_base")
+        _need(output_scratch.is_contiguous() and output_scratch.dim() == 2
+              and output_scratch.size(1) == hidden_state.size(1), "exl3_moe: output_scratch must be [slots, hidden]")
+    _dtype(hidden_state, torch.half, "hidden_state")
+    _need(hidden_state.dim() == 2 and hidden_state.is_contiguous(), "hidden_state must be 2-dimensional")
+    _dtype(output_state, torch.float, "output_state")
+    _need(output_state.shape == hidden_state.shape and output_state.is_contiguous(),
+          "output_state and hidden_state shapes differ")
+    _dtype(expert_count, torch.long, "expert_count")
+    _need(expert_count.dim() == 1, "expert_count must be 1-dimensional")
+    _dtype(token_sorted, torch.long, "token_sorted")
+    _need(token_sorted.dim() == 1 and token_sorted.shape == weight_sorted.shape,
+          "token_sorted and weight_sorted shapes differ")
+    _dtype(weight_sorted, torch.half, "weight_sorted")
+    for t, name in ((temp_state_g, "temp_state_g"), (temp_state_u, "temp_state_u"),
+                    (temp_intermediate_g, "temp_intermediate_g"), (temp_intermediate_u, "temp_intermediate_u")):
+        _dtype(t, torch.half, name)
+        _need(t.dim() == 3 and t.is_contiguous(), f"{name} must be 3-dimensional")
+    _need(temp_state_g.size(2) == hidden_state.size(1), "temp_state_g and hidden_state shapes differ")
+    _need(temp_state_g.shape == temp_state_u.shape, "temp_state_g and temp_state_u shapes differ")
+    _need(temp_intermediate_g.shape == temp_intermediate_u.shape, "temp_intermediate shapes differ")
+    _need(temp_intermediate_g.size(1) == temp_state_g.size(1), "temp_intermediate_g and temp_state_g shapes differ")
+    tables = (gate_ptrs_trellis, gate_ptrs_suh, gate_ptrs_svh, up_ptrs_trellis, up_ptrs_suh, up_ptrs_svh,
+              down_ptrs_trellis, down_ptrs_suh, down_ptrs_svh)
+    for t in tables:
+        _need(t.dtype == torch.long and t.dim() == 1 and t.is_contiguous() and t.shape == gate_ptrs_trellis.shape,
+              "exl3_moe: pointer tables must be contiguous int64 of one length")
+    bits = (bits_g, bits_u, bits_d)
+    if any(b is not None for b in bits):
+        _need(all(b is not None for b in bits), "exl3_moe: give all three bit width tables or none")
+        for b in bits:
+            _need(b.dtype == torch.uint8 and b.is_contiguous() and b.numel() >= expert_count.numel() - 1,
+                  "exl3_moe: bit width tables must be contiguous uint8, one entry per expert")
+    _cuda(hidden_state, output_state, expert_count, token_sorted, weight_sorted, temp_state_g,
+          temp_intermediate_g, output_scratch, fused_base, *bits)
+    with torch.cuda.device(hidden_state.device):
+        check(_lib.lib().exl3_amd_moe(
+            hidden_state.data_ptr(), hidden_state.size(0), hidden_state.size(1), output_state.data_ptr(),
+            expert_count.data_ptr(), expert_count.numel(), token_sorted.data_ptr(), weight_sorted.data_ptr(),
+            token_sorted.numel(),
+            temp_state_g.data_ptr(), temp_state_u.data_ptr(), temp_state_g.size(0), temp_state_g.size(1),
+            temp_intermediate_g.data_ptr(), temp_intermediate_u.data_ptr(), temp_intermediate_g.size(2),
+            int(act_function), float(K_gate), float(K_up), float(K_down),
+            *[t.data_ptr() for t in tables], gate_ptrs_trellis.numel(),
+            int(bool(gate_mcg)), int(bool(gate_mul1)), int(bool(up_mcg)), int(bool(up_mul1)),
+            int(bool(down_mcg)), int(bool(down_mul1)),
+            float(act_limit), int(num_active),
+            _ptr(output_scratch), output_scratch.size(0) if output_scratch is not None else 0,
+            output_scratch.size(1) if output_scratch is not None else 0, _ptr(fused_base),
+            int(count_lo), int(count_hi), int(m_tile),
+            _ptr(bits_g), _ptr(bits_u), _ptr(bits_d), bits_g.numel() if bits_g is not None else 0,
+            _stream(hidden_state)))
+
+
+def exl3_moe_gather(output_state: Tensor, output_scratch: Tensor, flat_expert: Tensor, inv_order: Tensor,
+                    expert_start: Tensor, slot_base: Tensor, slot_kind: Tensor, weight_sorted: Tensor) -> None:
+    """exl3_moe_gather (exl3_moe.cu:480-527): every token's top-k slots summed in k order into
+    its fp32 output row."""
+    _dtype(output_state, torch.float, "output_state")
+    _dtype(output_scratch, torch.float, "output_scratch")
+    for t, name in ((flat_expert, "flat_expert"), (inv_order, "inv_order"), (expert_start, "expert_start"),
+                    (slot_base, "slot_base"), (slot_kind, "slot_kind")):
+        _dtype(t, torch.long, name)
+    _dtype(weight_sorted, torch.half, "weight_sorted")
+    _need(output_state.is_contiguous() and output_state.dim() == 2, "exl3_moe_gather: output_state")
+    _need(output_scratch.is_contiguous() and output_scratch.dim() == 2
+          and output_scratch.size(1) == output_state.size(1), "exl3_moe_gather: output_scratch must be [slots, hidden]")
+    _need(all(t.is_contiguous() for t in (flat_expert, inv_order, expert_start, slot_base, slot_kind, weight_sorted)),
+          "exl3_moe_gather: index tensors must be contiguous")
+    _cuda(output_state, output_scratch, flat_expert, inv_order, expert_start, slot_base, slot_kind, weight_sorted)
+    with torch.cuda.device(output_state.device):
+        check(_lib.lib().exl3_amd_moe_gather(
+            output_state.data_ptr(), output_state.size(0), output_state.size(1),
+            output_scratch.data_ptr(), output_scratch.size(1),
+            flat_expert.data_ptr(), flat_expert.numel(), inv_order.data_ptr(),
+            expert_start.data_ptr(), expert_start.numel(), slot_base.data_ptr(), slot_base.numel(),
+            slot_kind.data_ptr(), slot_kind.numel(), weight_sorted.data_ptr(), _stream(output_state)))
+
+
 def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
     """out = a @ b on the dense GEMM library, with TunableOp scoped to this call (the caller's
     process-wide setting is restored)."""

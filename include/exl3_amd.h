@@ -166,6 +166,60 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
                       const uint8_t* bits_g, const uint8_t* bits_u, const uint8_t* bits_d,
                       void* stream);
 
+/* Workgroup groups the reference's token-sorted MoE would run on this device (num_cus / 8): the
+ * caller sizes the temp buffers' first dimension with it.  Replaces exl3_moe_max_concurrency
+ * (vendor/exl3/exllamav3_ext/quant/exl3_moe.cu:15-19).  Returns >= 0, or a negative error code. */
+int exl3_amd_moe_max_concurrency(int device);
+
+/* Token-sorted fused MoE for prefill-sized batches.  For every expert e whose token count c
+ * (expert_count[e], expert_count_len = num_experts + 1, last entry ignored) satisfies
+ * 0 < c <= max_tokens_per_expert and count_lo <= c <= count_hi, and every one of its
+ * assignments (token_sorted / weight_sorted, sorted by expert, num_assign = bsz * top-k):
+ *     y = w * (had(down_e(had(act(had(gate_e(h)) o svh_g, had(up_e(h)) o svh_u) o suh_d))) o svh_d)
+ * with h = had(x[token] o suh_g / suh_u), is added atomically to output_state[token] (fp32,
+ * (bsz, hidden_dim)), or, with output_scratch (scratch_rows x scratch_cols fp32) and fused_base
+ * (int64 per expert), stored in slot fused_base[e] + (row of the assignment within e).
+ * act_function: 0 SiLU, 1 GELU, 2 non-gated ReLU^2 (gate skipped), else identity; act_limit != 0
+ * clamps.  Temp buffers: temp_state_g / _u (concurrency, max_tokens_per_expert, hidden_dim) fp16,
+ * temp_intermediate_g / _u (concurrency, max_tokens_per_expert, intermediate_dim) fp16, used as
+ * one pool of rows (more routed rows than the pool holds run in passes).  mcg or mul1 codebook;
+ * bits_g/u/d (uint8 per expert, mul1) select per-expert integer widths.  Unlike the reference,
+ * every in-range expert runs in one set of launches (no group barriers); half-integer rates
+ * return EXL3_AMD_EUNSUPPORTED.
+ * Replaces exl3_moe (vendor/exl3/exllamav3_ext/quant/exl3_moe.cu:137-418, kernel
+ * exl3_moe_kernel.cuh:78-313), declared at src/torch/amp_torch.cpp:7796-7837 and bound at :9269
+ * (torch.moe_fused). */
+int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* output_state,
+                 const int64_t* expert_count, int expert_count_len,
+                 const int64_t* token_sorted, const uint16_t* weight_sorted, int num_assign,
+                 uint16_t* temp_state_g, uint16_t* temp_state_u, int concurrency, int max_tokens_per_expert,
+                 uint16_t* temp_intermediate_g, uint16_t* temp_intermediate_u, int intermediate_dim,
+                 int act_function, float K_gate, float K_up, float K_down,
+                 const uint64_t* gate_ptrs_trellis, const uint64_t* gate_ptrs_suh, const uint64_t* gate_ptrs_svh,
+                 const uint64_t* up_ptrs_trellis, const uint64_t* up_ptrs_suh, const uint64_t* up_ptrs_svh,
+                 const uint64_t* down_ptrs_trellis, const uint64_t* down_ptrs_suh, const uint64_t* down_ptrs_svh,
+                 int num_ptrs,
+                 int gate_mcg, int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1,
+                 float act_limit, int num_active,
+                 float* output_scratch, int64_t scratch_rows, int scratch_cols, const int64_t* fused_base,
+                 int count_lo, int count_hi, int m_tile,
+                 const uint8_t* bits_g, const uint8_t* bits_u, const uint8_t* bits_d, int bits_len,
+                 void* stream);
+
+/* Fixed-order reduction of exl3_amd_moe's slots: for every token, output_state[token] +=
+ * sum over its top-k assignments a (in k order) of output_scratch[slot(a)] * wt(a), with
+ * e = flat_expert[a], slot = slot_base[e] + inv_order[a] - expert_start[e] when slot_kind[e]
+ * != 0 (kind 2: wt = weight_sorted[inv_order[a]], else 1).  top-k <= 32.
+ * Replaces exl3_moe_gather (vendor/exl3/exllamav3_ext/quant/exl3_moe.cu:420-531), declared at
+ * src/torch/amp_torch.cpp:7783-7794 and bound at :9359 (torch.moe_gather). */
+int exl3_amd_moe_gather(float* output_state, int tokens, int hidden_dim,
+                        const float* output_scratch, int scratch_cols,
+                        const int64_t* flat_expert, int num_assign, const int64_t* inv_order,
+                        const int64_t* expert_start, int expert_start_len,
+                        const int64_t* slot_base, int slot_base_len,
+                        const int64_t* slot_kind, int num_experts,
+                        const uint16_t* weight_sorted, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

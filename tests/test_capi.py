@@ -194,3 +194,57 @@ def test_moe_coop_rejects_bad_arguments():
         rc, msg = call_err(L.exl3_amd_moe_coop, *moe_args(**kw))
         assert rc < 0 and text in msg, (kw, msg)
     assert L.exl3_amd_moe_coop(*moe_args(bsz=0)) == 0          # no tokens: nothing to do
+
+
+def _moe_args(**kw):
+    """exl3_amd_moe argument list (fake non-null addresses: every call here fails validation
+    before any device access)."""
+    a = dict(hidden=1, bsz=4, hidden_dim=256, out=1, count=1, count_len=9, tok=1, w=1, n=8,
+             tsg=1, tsu=1, conc=1, max_tok=16, tig=1, tiu=1, I=256, act=0, Kg=3.0, Ku=3.0, Kd=3.0,
+             tables=[1] * 9, num_ptrs=8, cbs=[1, 0, 1, 0, 1, 0], limit=0.0, num_active=3,
+             scratch=None, scratch_rows=0, scratch_cols=0, fused_base=None, lo=0, hi=1 << 30, m_tile=16,
+             bits=[None, None, None], bits_len=0)
+    a.update(kw)
+    f = ctypes.c_float
+    return [a["hidden"], a["bsz"], a["hidden_dim"], a["out"], a["count"], a["count_len"], a["tok"], a["w"], a["n"],
+            a["tsg"], a["tsu"], a["conc"], a["max_tok"], a["tig"], a["tiu"], a["I"], a["act"],
+            f(a["Kg"]), f(a["Ku"]), f(a["Kd"]), *a["tables"], a["num_ptrs"], *a["cbs"], f(a["limit"]),
+            a["num_active"], a["scratch"], a["scratch_rows"], a["scratch_cols"], a["fused_base"],
+            a["lo"], a["hi"], a["m_tile"], *a["bits"], a["bits_len"], None]
+
+
+def test_moe_sorted_rejects_bad_arguments():
+    """exl3_moe's checks (exl3_moe.cu:186-323) in the reference's order and wording."""
+    L = _lib.lib()
+    assert L.exl3_amd_moe(*_moe_args(num_active=0, hidden=None)) == 0       # nothing to do: returns first
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(scratch=1, scratch_cols=256))
+    assert rc == _lib.EINVAL and "needs fused_base" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(scratch=1, scratch_cols=128, fused_base=1))
+    assert rc == _lib.EINVAL and "[slots, hidden]" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(cbs=[1, 0, 0, 1, 1, 0]))
+    assert rc == _lib.EINVAL and "same codebook" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(cbs=[0, 0, 0, 0, 0, 0]))
+    assert rc == _lib.EINVAL and "Only mcg and mul1" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(Kg=2.5))
+    assert rc == _lib.EINVAL and "half-integer" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(bits=[1, None, None], cbs=[0, 1, 0, 1, 0, 1]))
+    assert rc == _lib.EINVAL and "all three" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(bits=[1, 1, 1], bits_len=8))
+    assert rc == _lib.EINVAL and "mul1" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(num_ptrs=7))
+    assert rc == _lib.EINVAL and "num_experts" in msg
+    rc, msg = call_err(L.exl3_amd_moe, *_moe_args(n=9))
+    assert rc == _lib.EINVAL and "bsz" in msg
+
+
+def test_moe_gather_rejects_bad_arguments():
+    L = _lib.lib()
+    rc, msg = call_err(L.exl3_amd_moe_gather, 1, 4, 256, 1, 128, 1, 8, 1, 1, 4, 1, 4, 1, 4, 1, None)
+    assert rc == _lib.EINVAL and "[slots, hidden]" in msg
+    rc, msg = call_err(L.exl3_amd_moe_gather, 1, 4, 256, 1, 256, 1, 9, 1, 1, 4, 1, 4, 1, 4, 1, None)
+    assert rc == _lib.EINVAL and "assignments / tokens" in msg
+    rc, msg = call_err(L.exl3_amd_moe_gather, 1, 4, 256, 1, 256, 1, 8, 1, 1, 3, 1, 4, 1, 4, 1, None)
+    assert rc == _lib.EINVAL and "table sizes" in msg
+    rc, msg = call_err(L.exl3_amd_moe_gather, 1, 1, 256, 1, 256, 1, 33, 1, 1, 4, 1, 4, 1, 4, 1, None)
+    assert rc == _lib.EINVAL and "top-k" in msg
+    assert L.exl3_amd_moe_gather(1, 0, 256, 1, 256, 1, 0, 1, 1, 4, 1, 4, 1, 4, 1, None) == 0
