@@ -41,6 +41,7 @@ def units():
         ("exl3_hadamard.hip", "exl3_hadamard.o", []),
         ("exl3_device.hip", "exl3_device.o", []),
         ("exl3_moe_sorted.hip", "exl3_moe_sorted.o", []),
+        ("exl3_decode_ops.hip", "exl3_decode_ops.o", []),
     ]
     for cb in range(3):
         u.append(("exl3_moe.hip", f"exl3_moe_cb{cb}.o", [f"-DEXL3_MOE_CB={cb}"]))

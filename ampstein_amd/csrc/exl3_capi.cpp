@@ -255,7 +255,7 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     // (exl3_gemv.hip gemv1p_kernel).  Needs the XCD-local hand-off and per-slot tables of at
     // most 16 slots without indices or routing weights.
     // Opt-in (EXL3_AMD_GEMV_P1=1) until its GPU run is cleared.
-    bool p1 = g.m == 1 && g.stream_m1 && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
+    bool p1 = g.m == 1 && g.stream_m1 && !g.A_up && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
               g.row0 == 0 && g.slab_m <= 1;
     {
         const char* e = getenv("EXL3_AMD_GEMV_P1");
@@ -770,7 +770,16 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
 
     const int64_t pool64 = (int64_t) concurrency * max_tokens_per_expert;
     const int pool = (int) std::min<int64_t>(pool64, (int64_t) num_assign);   // rows a pass can hold
-    const int rt_cap = pool / 256 + std::min(num_experts, pool) + 1;
+    // rows per MFMA tile from the mean rows per expert: one tile covers most experts, with
+    // little padding (the weights are decoded once per tile)
+    const int mean_rows = num_assign / std::max(num_experts, 1);
+    int tile_rows = mean_rows <= 40 ? 64 : (mean_rows <= 160 ? 128 : 256);
+    if (const char* e = getenv("EXL3_AMD_MOE_TILE_ROWS"))
+    {
+        const int v = atoi(e);
+        if (v == 64 || v == 128 || v == 256) tile_rows = v;
+    }
+    const int rt_cap = pool / tile_rows + std::min(num_experts, pool) + 1;
     const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 24 * (size_t) rt_cap + 24;
     if (ws_ints * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: pool exceeds the library workspace");
 
@@ -795,6 +804,7 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     a.lists = a.rt + 3 * (size_t) rt_cap;
     a.counts = a.lists + 24 * (size_t) rt_cap;
     a.rt_cap = rt_cap;
+    a.tile_rows = tile_rows;
 
     typedef int (*group_fn)(const GemmGroupArgs&, int, hipStream_t);
     static const group_fn gfn[8] = { exl3k_gemm_group_k1, exl3k_gemm_group_k2, exl3k_gemm_group_k3, exl3k_gemm_group_k4,
@@ -809,6 +819,7 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
             memset(&g, 0, sizeof(g));
             g.rt = a.rt;
             g.nrt = rt_cap;
+            g.tile_rows = tile_rows;
             int mats = 0;
             auto add = [&](int m, const uint16_t* A, uint16_t* C, const uint64_t* tab, int Km) {
                 if (!bits_g && Km != K) return;
@@ -875,6 +886,69 @@ int exl3_amd_moe_gather(float* output_state, int tokens, int hidden_dim,
     g.tokens = tokens; g.H = hidden_dim; g.topk = topk; g.num_experts = num_experts;
     int rc = exl3k_moes_sum(g, (hipStream_t) stream);
     return rc ? hip_fail(rc, "exl3_moe_gather") : 0;
+}
+
+
+int exl3_amd_rms_norm_res(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* y, uint16_t* n,
+                          int64_t rows, int dim, float eps, void* stream)
+{
+    g_last_error.clear();
+    // amp_torch.cpp:10106-10131 and amp_kernels.cu:371-381
+    if (rows < 0 || dim < 0) return fail(EXL3_AMD_EINVAL, "rms_norm_res: negative size");
+    if (rows == 0 || dim == 0) return 0;
+    if (dim % 4) return fail(EXL3_AMD_EINVAL, "rms_norm_res: last dim (%d) must be a multiple of 4", dim);
+    if (!x || !r || !w || !y || !n) return fail(EXL3_AMD_EINVAL, "rms_norm_res: null pointer");
+    if (((uintptr_t) x | (uintptr_t) r | (uintptr_t) w | (uintptr_t) y | (uintptr_t) n) & 7)
+        return fail(EXL3_AMD_EINVAL, "rms_norm_res: tensors must be 8-byte aligned");
+    if (rows > 0x7fffffff) return fail(EXL3_AMD_EINVAL, "rms_norm_res: too many rows");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    int rc = exl3k_rms_norm_res(x, r, w, y, n, (long) rows, dim, eps, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "rms_norm_res") : 0;
+}
+
+int exl3_amd_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t numel, void* stream)
+{
+    g_last_error.clear();
+    if (numel <= 0) return 0;
+    if (!g || !u || !out) return fail(EXL3_AMD_EINVAL, "silu_mul: null pointer");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    int rc = exl3k_silu_mul(g, u, out, (long) numel, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "silu_mul") : 0;
+}
+
+int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* act,
+                           const uint16_t* trellis, void* C, int c_fp32,
+                           const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                           int m, int k, int n, float K, int mcg, int mul1, void* stream)
+{
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
+    if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: negative size");
+    if (m == 0 || n == 0) return EXL3_AMD_TAG_GEMV;
+    if (!gate || !up || !act || !trellis || !C) return fail(EXL3_AMD_EINVAL, "exl3_gemm_silu_mul: null pointer");
+    if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
+    if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be positive");
+    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    if (m == 1)
+    {
+        GemvArgs g = gemv_args_single(gate, trellis, C, c_fp32, suh, svh, m, k, n);
+        GemvArgs probe = g;
+        if (!gemv_plan(m, k, n, 1, d->num_cus, probe) && probe.stream_m1 == 1)
+        {
+            g.A_up = up;                             // silu(gate) * up formed in the input load
+            int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm_silu_mul");
+            return rc ? rc : EXL3_AMD_TAG_GEMV;
+        }
+    }
+    if (int rc = exl3k_silu_mul(gate, up, act, (long) m * k, s)) return hip_fail(rc, "exl3_gemm_silu_mul");
+    return exl3_amd_gemm(act, trellis, C, c_fp32, suh, A_had, svh, m, k, n, K, mcg, mul1, 0, stream);
 }
 
 }  // extern "C"

@@ -273,6 +273,9 @@ __device__ __forceinline__ float xor_shfl(float v, int mask, int lane)
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
 }
 
+// silu(x) = x / (1 + exp(-x)) in fp32 (amp_silu_mul_kernel, src/torch/amp_kernels.cu:235-251).
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
 // Value of lane (lane ^ M) without LDS: DPP quad permutes (M = 1, 2), two bank-masked row
 // shifts (M = 4), a row rotate (M = 8), gfx950 permlane swaps (M = 16, 32).
 template <int M>

@@ -44,17 +44,18 @@ constexpr int BM = 256;          // rows per workgroup
 constexpr int BN = 256;          // columns per workgroup
 constexpr int PF = 3;            // register prefetch depth, stages (32 k each)
 
-template <int K> struct GemmLds
+template <int K, int RB> struct GemmLds
 {
     static constexpr int TW = 8 * K + 1;                 // words per staged tile: ring word -1, then 8K
-    static constexpr int A_U32 = BM * 16;                // A block: 256 rows x 32 fp16
+    static constexpr int A_U32 = RB * 16;                // A block: RB rows x 32 fp16
     static constexpr int B_U32 = 2 * BN * 8;             // B block: 2 slices x 256 columns x 16 fp16
     static constexpr int T_U32 = 2 * 16 * TW;            // 2 slices x 16 tiles
     static constexpr int A0 = 0;
     static constexpr int B0 = 2 * A_U32;
     static constexpr int T0 = B0 + 2 * B_U32;
     static constexpr int DUMMY = T0 + 2 * T_U32 + 4;     // (+4: a run may read one word past the last tile)
-    static constexpr int TOTAL = DUMMY + 8;              // sink for the stores of threads without trellis words
+    // (+8: sink for the stores of threads without trellis words; at least the epilogue's 64 x 256 fp32)
+    static constexpr int TOTAL = DUMMY + 8 > 64 * BN ? DUMMY + 8 : 64 * BN;
 };
 
 // 16-bit window at MSB-first bit offset REL of a normalised word run.
@@ -162,12 +163,14 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
 __device__ __forceinline__ int a_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
 __device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ ((col >> 3) & 1)); }
 
-template <int K, int CB, bool GROUP>
+template <int K, int CB, bool GROUP, int RB>
 __global__ __launch_bounds__(GT, 1)
 void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ trellis, void* __restrict__ C,
                  const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, GemmGroupArgs grp)
 {
-    using LD = GemmLds<K>;
+    using LD = GemmLds<K, RB>;
+    constexpr int MT = RB / 64;                          // 32-row MFMA tiles per wave (2 waves along m)
+    constexpr int AJ = RB >= 256 ? 2 : 1;                // A chunks staged per thread
     __shared__ __align__(16) uint32_t lds[LD::TOTAL];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -196,7 +199,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         c_fp32 = 0;
         mb = 0;
     }
-    const int nmb = (M + BM - 1) / BM;
+    const int nmb = (M + RB - 1) / RB;
     if constexpr (GROUP) { }           // (nb, mb) from the row tile above
     else if (nbn % 8 == 0)
     {
@@ -211,14 +214,15 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     }
 
     // ---- A staging: chunks u = t, t + 512 (row u / 4, 16-byte chunk u % 4 of the row's 64 bytes)
+    // (RB = 64: threads t and t + 256 stage the same chunk, an identical duplicate store)
     int a_lds[2];
     const u32x4* a_src[2];
     #pragma unroll
     for (int j = 0; j < 2; ++j)
     {
-        const int u = t + GT * j, row = u >> 2, ch = u & 3;
+        const int u = (t + GT * (j % AJ)) % (RB * 4), row = u >> 2, ch = u & 3;
         a_lds[j] = LD::A0 + a_off(row, ch);
-        a_src[j] = (const u32x4*) (Ain + (size_t) min(mb * BM + row, M - 1) * k + 8 * ch);
+        a_src[j] = (const u32x4*) (Ain + (size_t) min(mb * RB + row, M - 1) * k + 8 * ch);
     }
     // ---- trellis staging: words 4t..4t+3 of the stage's 2 slices x 16 tiles (t < 64K)
     const bool tload = t < 64 * K;
@@ -259,12 +263,12 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     auto load_stage = [&](int s, u32x4* a, u32x4& tw) {
         const int sc = min(s, NST - 1);
         a[0] = __builtin_nontemporal_load(a_src[0] + 4 * sc);
-        a[1] = __builtin_nontemporal_load(a_src[1] + 4 * sc);
+        if constexpr (AJ == 2) a[1] = __builtin_nontemporal_load(a_src[1] + 4 * sc);
         tw = __builtin_nontemporal_load((const u32x4*) (t_src + sc * t_stage));
     };
     auto store_stage = [&](int buf, const u32x4* a, const u32x4& tw) {
         *(u32x4*) (lds + buf * LD::A_U32 + a_lds[0]) = a[0];
-        *(u32x4*) (lds + buf * LD::A_U32 + a_lds[1]) = a[1];
+        if constexpr (AJ == 2) *(u32x4*) (lds + buf * LD::A_U32 + a_lds[1]) = a[1];
     };
     // branch-free: threads without trellis words (and the ring copy of non-final words) write
     // into a sink past the buffers (stage-relative offsets: buf 1 sinks land in the other sink)
@@ -294,9 +298,9 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     load_stage(PF, apf[0], tpf[0]);
     __syncthreads();
 
-    acc16 acc[4][2];
+    acc16 acc[MT][2];
     #pragma unroll
-    for (int i = 0; i < 4; ++i) { acc[i][0] = (acc16) { }; acc[i][1] = (acc16) { }; }
+    for (int i = 0; i < MT; ++i) { acc[i][0] = (acc16) { }; acc[i][1] = (acc16) { }; }
 
     for (int s0 = 0; s0 < NST; s0 += PF)
     {
@@ -315,13 +319,13 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
             #pragma unroll
             for (int sl = 0; sl < 2; ++sl)
             {
-                h8v bv[2], av[4];
+                h8v bv[2], av[MT];
                 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
                     bv[nt] = __builtin_bit_cast(h8v, *(const u32x4*) (B + b_off(sl, 64 * wn + 32 * nt + l32, lh)));
                 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-                    av[mt] = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off(128 * wm + 32 * mt + l32, 2 * sl + lh)));
+                for (int mt = 0; mt < MT; ++mt)
+                    av[mt] = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off((RB / 2) * wm + 32 * mt + l32, 2 * sl + lh)));
                 // the decode of this slice of B(s + 1), cut into 8 pieces that ride in the shadow
                 // of the 8 MFMAs (each 32 cycles on the matrix pipe); sched_barrier keeps the cuts
                 constexpr int NW = (25 * K + 16 + 31) / 32;
@@ -331,7 +335,8 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
                 for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
 #define EXL3_MFMA_STEP(mt, nt) \
                 __builtin_amdgcn_sched_barrier(0); \
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0); \
+                if constexpr ((mt) < MT) \
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0); \
                 __builtin_amdgcn_sched_barrier(0);
                 EXL3_MFMA_STEP(0, 0)
                 #pragma unroll
@@ -370,12 +375,12 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         }
     }
 
-    // ---- epilogue: 4 rounds of 64 rows; the 256 columns of each row meet in LDS, each wave then
+    // ---- epilogue: MT rounds of 64 rows; the 256 columns of each row meet in LDS, each wave then
     // rotates whole 128-column chunks
     float* E = (float*) lds;                              // [64][256] fp32
     const bool has_svh = svh != nullptr;
     #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
     {
         #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
@@ -395,7 +400,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         {
             const int rc = wave * 16 + q;
             const int er = rc >> 1, ch = rc & 1;
-            const int row = mb * BM + 128 * (er >> 5) + 32 * mt + (er & 31);
+            const int row = mb * RB + (RB / 2) * (er >> 5) + 32 * mt + (er & 31);
             const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
             const int col = nb * BN + 128 * ch + 2 * lane;
             if (nb * BN + 128 * ch >= n) continue;        // half block: chunk past n (uniform per wave)
@@ -412,7 +417,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s)
     const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     GemmGroupArgs none;
     memset(&none, 0, sizeof(none));
-    hipLaunchKernelGGL((gemm_kernel<K, CB, false>), dim3(blocks), dim3(GT), 0, s,
+    hipLaunchKernelGGL((gemm_kernel<K, CB, false, BM>), dim3(blocks), dim3(GT), 0, s,
                        g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, none);
     return (int) hipGetLastError();
 }
@@ -422,9 +427,14 @@ int launch_gemm_group(const GemmGroupArgs& g, hipStream_t s)
 {
     const long blocks = (long) g.nrt * g.mats * ((g.n + BN - 1) / BN);
     if (blocks <= 0) return 0;
-    hipLaunchKernelGGL((gemm_kernel<K, CB, true>), dim3((unsigned) blocks), dim3(GT), 0, s,
-                       (const uint16_t*) nullptr, (const uint16_t*) nullptr, (void*) nullptr,
-                       (const uint16_t*) nullptr, 0, g.k, g.n, 0, g);
+    const dim3 grid((unsigned) blocks), block(GT);
+    const uint16_t* nul = nullptr;
+    if (g.tile_rows == 64)
+        hipLaunchKernelGGL((gemm_kernel<K, CB, true, 64>), grid, block, 0, s, nul, nul, (void*) nullptr, nul, 0, g.k, g.n, 0, g);
+    else if (g.tile_rows == 128)
+        hipLaunchKernelGGL((gemm_kernel<K, CB, true, 128>), grid, block, 0, s, nul, nul, (void*) nullptr, nul, 0, g.k, g.n, 0, g);
+    else
+        hipLaunchKernelGGL((gemm_kernel<K, CB, true, 256>), grid, block, 0, s, nul, nul, (void*) nullptr, nul, 0, g.k, g.n, 0, g);
     return (int) hipGetLastError();
 }
 

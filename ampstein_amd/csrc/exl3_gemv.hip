@@ -665,7 +665,15 @@ __device__ __forceinline__ uint32_t rotate_pair(uint32_t xv, uint32_t sv, bool h
     return as_u32(o);
 }
 
-template <int K, int CB, int WS>
+// Fused SwiGLU input (ACT): the pair of silu(gate) * up, rounded to fp16 as silu_mul does.
+__device__ __forceinline__ uint32_t silu_mul_pair(uint32_t gv, uint32_t uv)
+{
+    const f16x2 gh = as_h2(gv), uh = as_h2(uv);
+    const f16x2 o = { (f16) (silu_f32((float) gh.x) * (float) uh.x), (f16) (silu_f32((float) gh.y) * (float) uh.y) };
+    return as_u32(o);
+}
+
+template <int K, int CB, int WS, bool ACT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemv1_kernel(const GemvArgs g)
 {
@@ -712,6 +720,7 @@ void gemv1_kernel(const GemvArgs g)
     const bool has_suh = v.suh != nullptr;
     const uint32_t* xg = (const uint32_t*) v.A + lane;                       // x pairs
     const uint32_t* sg = (const uint32_t*) (has_suh ? v.suh : v.A) + lane;   // suh pairs
+    const uint32_t* ug = (const uint32_t*) (ACT ? g.A_up : v.A) + lane;      // up pairs (fused SwiGLU)
 
     constexpr int PF = EXL3_GEMV_PF;
     static_assert(8 % PF == 0, "prefetch depth must divide 8");
@@ -719,6 +728,8 @@ void gemv1_kernel(const GemvArgs g)
     // x of the first chunk first (its wait then leaves the weight loads in flight)
     uint32_t xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8) * 64);
     uint32_t sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8) * 64);
+    uint32_t uv = 0u;
+    if constexpr (ACT) uv = __builtin_nontemporal_load(to_global(ug) + (size_t) (a / 8) * 64);
     uint32_t ring[PF][KB + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_slot_k<K>(base + (size_t) min(d, last) * rstride, prev_off, lane, ring[d]);
@@ -737,7 +748,7 @@ void gemv1_kernel(const GemvArgs g)
 #endif
     for (int c = 0; c < nchunks; ++c)
     {
-        const uint32_t xr = rotate_pair(xv, sv, has_suh, lane);
+        const uint32_t xr = rotate_pair(ACT ? silu_mul_pair(xv, uv) : xv, sv, has_suh, lane);
         if (c == 0) GEMV_STAMP(g, 1, __builtin_amdgcn_readfirstlane(xr));
         if (CB == 2)
         {
@@ -758,6 +769,7 @@ void gemv1_kernel(const GemvArgs g)
         const int cn = min(c + 1, nchunks - 1);
         xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8 + cn) * 64);
         sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8 + cn) * 64);
+        if constexpr (ACT) uv = __builtin_nontemporal_load(to_global(ug) + (size_t) (a / 8 + cn) * 64);
         #pragma unroll
         for (int s8 = 0; s8 < per; ++s8)
         {
@@ -1206,10 +1218,18 @@ int launch_gemv1(const GemvArgs& g, hipStream_t s)
 {
     const int W = g.slices_per_block / GEMV_WAVES;
     return launch_common(g, s, [&](dim3 grid) {
-        if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8>), grid, dim3(GEMV_THREADS), 0, s, g);
+        if (g.A_up)
+        {
+            if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1, true>), grid, dim3(GEMV_THREADS), 0, s, g);
+            else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2, true>), grid, dim3(GEMV_THREADS), 0, s, g);
+            else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4, true>), grid, dim3(GEMV_THREADS), 0, s, g);
+            else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8, true>), grid, dim3(GEMV_THREADS), 0, s, g);
+            return;
+        }
+        if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1, false>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2, false>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4, false>), grid, dim3(GEMV_THREADS), 0, s, g);
+        else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8, false>), grid, dim3(GEMV_THREADS), 0, s, g);
     });
 }
 
@@ -1223,6 +1243,7 @@ int launch_gemv_m(const GemvArgs& g, hipStream_t s)
             return (int) hipGetLastError();
         }
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
+    if (g.A_up) return -1;             // the fused SwiGLU input exists in the M = 1 stream kernel only
     if (g.m == 1) return launch_gemv_t<K, CB, 1>(g, s);
     if (g.m <= 4) return launch_gemv_t<K, CB, 4>(g, s);
     return launch_gemv_t<K, CB, 8>(g, s);

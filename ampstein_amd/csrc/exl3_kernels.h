@@ -12,6 +12,7 @@
 struct GemvArgs
 {
     const uint16_t* A;          // (bszm_in, m, k) fp16
+    const uint16_t* A_up;       // non-null: the input is fp16(silu(A) * A_up) (M = 1 stream kernel only)
     const uint16_t* trellis;    // (k/16, n/16, 16K) uint16 (single matrix)
     void* C;                    // (bszm, m, n) fp16 or fp32
     const uint16_t* suh;        // (k) fp16 or null (single matrix)
@@ -82,6 +83,7 @@ struct GemmGroupArgs
     int mats;                   // 1 or 2
     int k, n;
     int nrt;                    // row-tile capacity of the launch
+    int tile_rows;              // rows per tile: 64, 128 or 256
 };
 
 int exl3k_gemm_group_k1(const GemmGroupArgs& g, int cb, hipStream_t s);
@@ -119,6 +121,7 @@ struct MoesArgs
     int* lists;                 // workspace: 3 x 8 lists of row-tile ids, rt_cap each
     int* counts;                // workspace: 3 x 8 list lengths
     int rt_cap;
+    int tile_rows;              // rows per row tile (64, 128 or 256)
 };
 
 struct MoesGatherArgs
@@ -129,6 +132,10 @@ struct MoesGatherArgs
     const uint16_t* weight_sorted;
     int tokens, H, topk, num_experts;
 };
+
+int exl3k_rms_norm_res(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* y, uint16_t* n,
+                       long rows, int dim, float eps, hipStream_t s);
+int exl3k_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long n, hipStream_t s);
 
 int exl3k_moes_plan(const MoesArgs& a, int pass_row0, hipStream_t s);
 int exl3k_moes_gather(const MoesArgs& a, int cus, hipStream_t s);

@@ -6,7 +6,7 @@
 //   plan     one workgroup: per-expert starts in the sorted assignment list, the experts this
 //            launch takes (0 < count <= max_tokens_per_expert, count_lo <= count <= count_hi),
 //            their rows compacted into a pool (the caller's temp buffers, concurrency x
-//            max_tokens_per_expert rows), row tiles of <= 256 rows of one expert, and per
+//            max_tokens_per_expert rows), row tiles of <= 64 / 128 / 256 rows of one expert, and per
 //            (matrix, bitrate) lists of row tiles;
 //   gather   pool row r <- had(x[token] o suh) for gate and up (had_hf_r_128_inner);
 //   GEMM     grouped MFMA GEMM (exl3_gemm.hip, GROUP instance) per bitrate, gate and up together;
@@ -171,8 +171,9 @@ void moes_plan_kernel(MoesArgs a, int pass_row0)
         }
     }
     __syncthreads();
+    const int TR = a.tile_rows;
     #pragma unroll
-    for (int i = 0; i < 4; ++i) if (4 * t + i < E) s_nt[4 * t + i] = (n_r[i] + 255) / 256;
+    for (int i = 0; i < 4; ++i) if (4 * t + i < E) s_nt[4 * t + i] = (n_r[i] + TR - 1) / TR;
     __syncthreads();
     scan_excl(s_nt, E, s_tmp);
     // row tiles and the per (matrix, bitrate) lists
@@ -185,12 +186,12 @@ void moes_plan_kernel(MoesArgs a, int pass_row0)
         kb[0] = a.bits_g ? (int) a.bits_g[e] : a.K_g;
         kb[1] = a.bits_u ? (int) a.bits_u[e] : a.K_u;
         kb[2] = a.bits_d ? (int) a.bits_d[e] : a.K_d;
-        for (int j = 0; j * 256 < n_r[i]; ++j)
+        for (int j = 0; j * TR < n_r[i]; ++j)
         {
             const int tid = s_nt[e] + j;
             a.rt[3 * tid] = e;
-            a.rt[3 * tid + 1] = lo_r[i] - w0 + 256 * j;
-            a.rt[3 * tid + 2] = min(256, n_r[i] - 256 * j);
+            a.rt[3 * tid + 1] = lo_r[i] - w0 + TR * j;
+            a.rt[3 * tid + 2] = min(TR, n_r[i] - TR * j);
             #pragma unroll
             for (int m = 0; m < 3; ++m)
             {

@@ -475,6 +475,68 @@ def exl3_moe_gather(output_state: Tensor, output_scratch: Tensor, flat_expert: T
             slot_kind.data_ptr(), slot_kind.numel(), weight_sorted.data_ptr(), _stream(output_state)))
 
 
+def rms_norm_res(x: Tensor, r: Tensor, weight: Tensor, eps: float, y: Optional[Tensor] = None,
+                 n: Optional[Tensor] = None):
+    """Fused residual add + RMSNorm (amp_torch.cpp:10073-10160): returns [y, n] with
+    y = x + r (fp16) and n = rmsnorm(y) * weight.  y / n are allocated unless given (a captured
+    decode step passes persistent buffers; y may be x itself)."""
+    for t, name in ((x, "x"), (r, "r"), (weight, "weight")):
+        _dtype(t, torch.half, name)
+    dim = weight.numel()
+    _need(x.dim() >= 1 and r.dim() >= 1 and x.size(-1) == dim and r.size(-1) == dim and r.numel() == x.numel(),
+          "rms_norm_res: weight/last-dim mismatch")
+    _need(dim % 4 == 0, f"rms_norm_res: last dim ({dim}) must be a multiple of 4")
+    y = torch.empty_like(x) if y is None else y
+    n = torch.empty_like(x) if n is None else n
+    _cuda(x, r, weight, y, n)
+    with torch.cuda.device(x.device):
+        check(_lib.lib().exl3_amd_rms_norm_res(x.data_ptr(), r.data_ptr(), weight.data_ptr(), y.data_ptr(),
+                                               n.data_ptr(), x.numel() // max(dim, 1), dim, float(eps), _stream(x)))
+    return [y, n]
+
+
+def silu_mul(g: Tensor, u: Tensor, out: Optional[Tensor] = None) -> Tensor:
+    """silu(g) * u elementwise in fp32, rounded to fp16 (amp_torch.cpp:4960-5005)."""
+    _dtype(g, torch.half, "silu_mul: gate")
+    _dtype(u, torch.half, "silu_mul: up")
+    _need(g.numel() == u.numel(), "silu_mul: gate/up size mismatch")
+    out = torch.empty_like(g) if out is None else out
+    _cuda(g, u, out)
+    with torch.cuda.device(g.device):
+        check(_lib.lib().exl3_amd_silu_mul(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(), _stream(g)))
+    return out
+
+
+def exl3_gemm_silu_mul(gate: Tensor, up: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor],
+                       svh: Optional[Tensor], mcg: bool = False, mul1: bool = False,
+                       act: Optional[Tensor] = None, A_had: Optional[Tensor] = None) -> int:
+    """C = exl3_gemm(silu_mul(gate, up)) (graphdec.uc:206-217) in one call; one launch at one
+    row (the GEMV forms the SwiGLU product in its input load).  act / A_had: scratch of gate's
+    shape (allocated when absent)."""
+    _need(B.dim() == 3, "B must be 3-dimensional")
+    _dtype(gate, torch.half, "gate")
+    _dtype(up, torch.half, "up")
+    _need(gate.shape == up.shape, "silu_mul: gate/up size mismatch")
+    _need(gate.size(-1) == B.size(0) * 16, "A and B shapes are incompatible")
+    _need(C.size(-1) == B.size(1) * 16, "C and B shapes are incompatible")
+    _trellis_dtype(B, "B")
+    _need(C.dtype in (torch.half, torch.float), "C is incorrect datatype, must be half or float")
+    tile = B.size(2)
+    half_k = tile % 16 != 0
+    _need(not half_k or (tile % 16 == 8 and mul1), "exl3_gemm: half-integer bitrates require the mul1 codebook")
+    K = tile // 16 + (0.5 if half_k else 0.0)
+    mcg_i, mul1_i = _codebook_flags(mcg, mul1)
+    act = torch.empty_like(gate) if act is None else act
+    A_had = torch.empty_like(gate) if A_had is None else A_had
+    m = gate.numel() // gate.size(-1)
+    _cuda(gate, up, act, B, C, suh, svh, A_had)
+    with torch.cuda.device(gate.device):
+        return check(_lib.lib().exl3_amd_gemm_silu_mul(
+            gate.data_ptr(), up.data_ptr(), act.data_ptr(), B.data_ptr(), C.data_ptr(), int(C.dtype == torch.float),
+            _ptr(suh), A_had.data_ptr(), _ptr(svh), m, gate.size(-1), C.size(-1), float(K), mcg_i, mul1_i,
+            _stream(gate)))
+
+
 def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
     """out = a @ b on the dense GEMM library, with TunableOp scoped to this call (the caller's
     process-wide setting is restored)."""

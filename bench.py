@@ -203,6 +203,41 @@ def graph_time(torch, sweep, steps, warmup):
     return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
 
 
+# ------------------------------------------------------------------ captured decode step
+def decode_step_bench(torch, layers, steps=20):
+    """The linear part of the Llama-3-8B decode step with its neighbours (graphdec.uc:151-230:
+    rms_norm_res, q/k/v sliced mgemm, o gemm, rms_norm_res, gate/up stacked mgemm, SwiGLU + down,
+    final norm) captured into one graph over the same 32 layers; attention is outside the path
+    (the q projection feeds o).  Fused: the down GEMV forms silu(gate) * up in its input load."""
+    from ampstein_amd.decode import DecodeStack, LayerWeights
+    H = 4096
+    ones = torch.ones(H, dtype=torch.half, device="cuda")
+    lw = [LayerWeights(q=r["q"], k=r["k"], v=r["v"], o=r["o"], gate=r["gate"], up=r["up"], down=r["down"],
+                       input_norm=ones, post_norm=ones) for r in layers]
+    nbytes = sum(r[n].trellis.numel() * 2 for r in layers for n in ("q", "k", "v", "o", "gate", "up", "down"))
+    x = torch.randn((1, H), device="cuda").half()
+    res = {}
+    for name, fuse in (("fused_swiglu", True), ("separate_silu_mul", False)):
+        st = DecodeStack(lw, ones, fuse_swiglu=fuse)
+        st.capture()
+        for _ in range(3):
+            st(x)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            st.graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        res[name] = {"us_per_step": round(us, 1), "us_per_layer": round(us / len(layers), 2),
+                     "launches_per_layer": 6 if fuse else 7, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del st
+    return {"what": "32-layer decode step without attention: norms + linears + SwiGLU, one graph",
+            "packed_bytes": nbytes, **res}
+
+
 # ------------------------------------------------------------------ prefill GEMM (configs[3])
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -329,8 +364,43 @@ def moe_bench(torch, reps=8):
         nbytes = sum(r[2] for r in routs) / reps
         res[f"M{M}"] = {"us_per_call": round(us, 2), "routed_bytes": round(nbytes), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    # token-sorted prefill MoE (exl3_moe) on the same experts: T tokens, pool = every assignment
+    pre = {}
+    conc = ops.exl3_moe_max_concurrency(torch.cuda.current_device())
+    for T in (512, 2048):
+        logits = rng.standard_normal((T, E))
+        sel = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+        p = np.exp(logits - logits.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        rw = np.take_along_axis(p, sel, 1).astype(np.float16)
+        flat = sel.reshape(-1)
+        order = np.argsort(flat, kind="stable")
+        count = np.bincount(flat, minlength=E + 1).astype(np.int64)
+        max_tok = -(-T * topk // conc)
+        dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        cnt, tok, ws = dv(count), dv((order // topk).astype(np.int64)), dv(rw.reshape(-1)[order])
+        x = torch.randn((T, Hi), device="cuda", generator=g).half()
+        out = torch.zeros((T, Ho), dtype=torch.float, device="cuda")
+        tsg, tsu = (torch.empty((conc, max_tok, Hi), dtype=torch.half, device="cuda") for _ in range(2))
+        tig, tiu = (torch.empty((conc, max_tok, I), dtype=torch.half, device="cuda") for _ in range(2))
+        active = int((count[:E] > 0).sum())
+
+        def call():
+            ops.exl3_moe(x, out, cnt, tok, ws, tsg, tsu, tig, tiu, 0, 0.0, 0.0, 0.0, *tabs,
+                         False, True, False, True, False, True, 0.0, active, None, None, 0, 1 << 30, 16,
+                         bits, bits, bits)
+        us = timed(torch, call, reps=5)
+        flops = 2.0 * T * topk * (2 * Hi * I + I * Ho)
+        nbytes = sum(per_expert[e] for e in range(E) if count[e] > 0)
+        pre[f"T{T}"] = {"us_per_call": round(us, 1), "TFLOPS": round(flops / us / 1e6, 1),
+                        "frac_mfma_peak": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
+                        "routed_bytes": nbytes, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "active_experts": active, "max_rows_per_expert": int(count[:E].max())}
+        del tsg, tsu, tig, tiu, out, x
+        torch.cuda.empty_cache()
     return {"metric": "MoE mixed-K expert GEMV GB/s (configs[4]: 256 experts, K in {2,3,4}, mul1, top-8)",
-            "launches_per_call": {"M1": 3, "M8": 5, "M16": 5}, "per_m": res}
+            "launches_per_call": {"M1": 3, "M8": 5, "M16": 5}, "per_m": res,
+            "prefill_token_sorted": {"op": "exl3_moe (token-sorted, grouped MFMA GEMM)", "per_T": pre}}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -549,7 +619,9 @@ def main():
                                 "launches_per_step": len(separate.entries)},
         "wall_s": round(wall, 3),
     }
-    del bundled, separate, layers
+    del bundled, separate
+    out["decode_step"] = decode_step_bench(torch, layers)
+    del layers
     torch.cuda.empty_cache()
     if not args.no_prefill:
         out["prefill"] = prefill_bench(torch)

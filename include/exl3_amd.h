@@ -220,6 +220,30 @@ int exl3_amd_moe_gather(float* output_state, int tokens, int hidden_dim,
                         const int64_t* slot_kind, int num_experts,
                         const uint16_t* weight_sorted, void* stream);
 
+/* Fused residual add + RMSNorm over rows of dim (a multiple of 4) fp16 values:
+ * y = fp16(x + r) (the updated residual stream; y may alias x),
+ * n = fp16(fp16(y * rsqrt(mean(y^2) + eps)) * w).  Pointers 8-byte aligned.
+ * Replaces amp_rms_norm_res_fp16 (src/torch/amp_kernels.cu:367-397, kernel :279-365), bound at
+ * src/torch/amp_torch.cpp:10081 (torch.rms_norm_res). */
+int exl3_amd_rms_norm_res(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* y, uint16_t* n,
+                          int64_t rows, int dim, float eps, void* stream);
+
+/* out = fp16(silu(g) * u) elementwise, fp32 math.  Replaces amp_silu_mul_fp16
+ * (src/torch/amp_kernels.cu:253-268, kernel :235-251), bound at src/torch/amp_torch.cpp:4966
+ * (torch.silu_mul). */
+int exl3_amd_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t numel, void* stream);
+
+/* C = exl3_gemm(silu(gate) * up) in one call: the decode step's SwiGLU + down projection
+ * (graphdec.uc:206-217 calls torch.silu_mul, then torch.exl3_gemm).  With one row the M = 1
+ * stream kernel forms silu(gate) * up, rounded to fp16 as silu_mul does, while loading its input
+ * (one launch, act untouched); otherwise silu_mul writes act (m, k) and exl3_gemm reads it.
+ * Same results as the two calls.  No counterpart in the reference (a fusion of two of its calls).
+ * Returns the exl3_gemm tag. */
+int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* act,
+                           const uint16_t* trellis, void* C, int c_fp32,
+                           const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                           int m, int k, int n, float K, int mcg, int mul1, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
