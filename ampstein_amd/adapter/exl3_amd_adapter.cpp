@@ -14,6 +14,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <algorithm>
+#include <cstdio>
 
 #include "exl3_amd.h"
 #include "exl3_amd_adapter.h"
@@ -296,4 +297,137 @@ void exl3_moe_coop(const at::Tensor& x, const at::Tensor& sel, const at::Tensor&
         sh_gate_w.has_value() && sh_gate_w->defined() ? (int) sh_gate_w->numel() : 0,
         opt_ptr<const uint8_t>(bits_g), opt_ptr<const uint8_t>(bits_u), opt_ptr<const uint8_t>(bits_d),
         cur_stream(x)));
+}
+
+int exl3_moe_max_concurrency(int device)
+{
+    return check(exl3_amd_moe_max_concurrency(device));
+}
+
+void exl3_moe_gather(at::Tensor output_state, const at::Tensor& output_scratch, const at::Tensor& flat_expert,
+                     const at::Tensor& inv_order, const at::Tensor& expert_start, const at::Tensor& slot_base,
+                     const at::Tensor& slot_kind, const at::Tensor& weight_sorted)
+{
+    // exl3_moe.cu:491-517
+    check_dtype(output_state, at::kFloat, "output_state");
+    check_dtype(output_scratch, at::kFloat, "output_scratch");
+    check_dtype(flat_expert, at::kLong, "flat_expert");
+    check_dtype(inv_order, at::kLong, "inv_order");
+    check_dtype(expert_start, at::kLong, "expert_start");
+    check_dtype(slot_base, at::kLong, "slot_base");
+    check_dtype(slot_kind, at::kLong, "slot_kind");
+    check_dtype(weight_sorted, at::kHalf, "weight_sorted");
+    TORCH_CHECK(output_state.is_contiguous() && output_state.dim() == 2, "exl3_moe_gather: output_state");
+    TORCH_CHECK(output_scratch.is_contiguous() && output_scratch.dim() == 2 &&
+                output_scratch.size(1) == output_state.size(1), "exl3_moe_gather: output_scratch must be [slots, hidden]");
+    TORCH_CHECK(flat_expert.is_contiguous() && inv_order.is_contiguous() && expert_start.is_contiguous() &&
+                slot_base.is_contiguous() && slot_kind.is_contiguous() && weight_sorted.is_contiguous(),
+                "exl3_moe_gather: index tensors must be contiguous");
+    for (const at::Tensor* t : std::initializer_list<const at::Tensor*> { &output_state, &output_scratch, &flat_expert,
+                                 &inv_order, &expert_start, &slot_base, &slot_kind, &weight_sorted })
+        check_on_device(*t, "exl3_moe_gather operand");
+    const c10::OptionalDeviceGuard guard(output_state.device());
+    check(exl3_amd_moe_gather((float*) output_state.data_ptr(), (int) output_state.size(0), (int) output_state.size(1),
+                              (const float*) output_scratch.data_ptr(), (int) output_scratch.size(1),
+                              (const int64_t*) flat_expert.data_ptr(), (int) flat_expert.numel(),
+                              (const int64_t*) inv_order.data_ptr(), (const int64_t*) expert_start.data_ptr(),
+                              (int) expert_start.numel(), (const int64_t*) slot_base.data_ptr(), (int) slot_base.numel(),
+                              (const int64_t*) slot_kind.data_ptr(), (int) slot_kind.numel(),
+                              (const uint16_t*) weight_sorted.data_ptr(), cur_stream(output_state)));
+}
+
+void exl3_moe(const at::Tensor& hidden_state, const at::Tensor& output_state, const at::Tensor& expert_count,
+              const at::Tensor& token_sorted, const at::Tensor& weight_sorted, const at::Tensor& temp_state_g,
+              const at::Tensor& temp_state_u, const at::Tensor& temp_intermediate_g,
+              const at::Tensor& temp_intermediate_u, const int act_function, const float K_gate, const float K_up,
+              const float K_down, const at::Tensor& gate_ptrs_trellis, const at::Tensor& gate_ptrs_suh,
+              const at::Tensor& gate_ptrs_svh, const at::Tensor& up_ptrs_trellis, const at::Tensor& up_ptrs_suh,
+              const at::Tensor& up_ptrs_svh, const at::Tensor& down_ptrs_trellis, const at::Tensor& down_ptrs_suh,
+              const at::Tensor& down_ptrs_svh, const bool gate_mcg, const bool gate_mul1, const bool up_mcg,
+              const bool up_mul1, const bool down_mcg, const bool down_mul1, const float act_limit,
+              const int num_active, const c10::optional<at::Tensor>& output_scratch,
+              const c10::optional<at::Tensor>& fused_base, const int count_lo, const int count_hi, const int m_tile,
+              const c10::optional<at::Tensor>& bits_g, const c10::optional<at::Tensor>& bits_u,
+              const c10::optional<at::Tensor>& bits_d)
+{
+    // exl3_moe.cu:186-235: tensor checks; the rest are made by the C ABI in the same order
+    if (num_active == 0) return;
+    const bool scr = output_scratch.has_value() && output_scratch->defined();
+    if (scr)
+    {
+        TORCH_CHECK(fused_base.has_value() && fused_base->defined(), "exl3_moe: output_scratch needs fused_base");
+        check_dtype(*output_scratch, at::kFloat, "output_scratch");
+        check_dtype(*fused_base, at::kLong, "fused_base");
+        TORCH_CHECK(output_scratch->is_contiguous() && output_scratch->dim() == 2 &&
+                    output_scratch->size(1) == hidden_state.size(1), "exl3_moe: output_scratch must be [slots, hidden]");
+    }
+    check_dtype(hidden_state, at::kHalf, "hidden_state");
+    TORCH_CHECK(hidden_state.dim() == 2 && hidden_state.is_contiguous(), "hidden_state must be 2-dimensional");
+    check_dtype(output_state, at::kFloat, "output_state");
+    TORCH_CHECK(output_state.sizes() == hidden_state.sizes(), "output_state and hidden_state shapes differ");
+    check_dtype(expert_count, at::kLong, "expert_count");
+    TORCH_CHECK(expert_count.dim() == 1, "expert_count must be 1-dimensional");
+    check_dtype(token_sorted, at::kLong, "token_sorted");
+    TORCH_CHECK(token_sorted.dim() == 1 && token_sorted.sizes() == weight_sorted.sizes(),
+                "token_sorted and weight_sorted shapes differ");
+    check_dtype(weight_sorted, at::kHalf, "weight_sorted");
+    for (const at::Tensor* t : { &temp_state_g, &temp_state_u, &temp_intermediate_g, &temp_intermediate_u })
+    {
+        check_dtype(*t, at::kHalf, "temp buffer");
+        TORCH_CHECK(t->dim() == 3 && t->is_contiguous(), "exl3_moe: temp buffers must be contiguous and 3-dimensional");
+    }
+    TORCH_CHECK(temp_state_g.size(2) == hidden_state.size(1) && temp_state_g.sizes() == temp_state_u.sizes(),
+                "temp_state shapes differ");
+    TORCH_CHECK(temp_intermediate_g.sizes() == temp_intermediate_u.sizes() &&
+                temp_intermediate_g.size(1) == temp_state_g.size(1), "temp_intermediate shapes differ");
+    for (const at::Tensor* t : { &gate_ptrs_trellis, &gate_ptrs_suh, &gate_ptrs_svh, &up_ptrs_trellis, &up_ptrs_suh,
+                                 &up_ptrs_svh, &down_ptrs_trellis, &down_ptrs_suh, &down_ptrs_svh })
+        TORCH_CHECK(t->scalar_type() == at::kLong && t->dim() == 1 && t->is_contiguous() &&
+                    t->sizes() == gate_ptrs_trellis.sizes(), "exl3_moe: pointer tables must be contiguous int64 of one length");
+    const int nb = (int) (bits_g.has_value() && bits_g->defined()) + (int) (bits_u.has_value() && bits_u->defined()) +
+                   (int) (bits_d.has_value() && bits_d->defined());
+    TORCH_CHECK(nb == 0 || nb == 3, "exl3_moe: give all three bit width tables or none");
+    for (const c10::optional<at::Tensor>* b : { &bits_g, &bits_u, &bits_d })
+        if (b->has_value() && (*b)->defined())
+            TORCH_CHECK((*b)->scalar_type() == at::kByte && (*b)->is_contiguous() && (*b)->numel() >= expert_count.numel() - 1,
+                        "exl3_moe: bit width tables must be contiguous uint8, one entry per expert");
+    for (const at::Tensor* t : { &hidden_state, &output_state, &expert_count, &token_sorted, &weight_sorted,
+                                 &temp_state_g, &temp_intermediate_g })
+        check_on_device(*t, "exl3_moe operand");
+    const c10::OptionalDeviceGuard guard(hidden_state.device());
+    check(exl3_amd_moe(
+        (const uint16_t*) hidden_state.data_ptr(), (int) hidden_state.size(0), (int) hidden_state.size(1),
+        (float*) output_state.data_ptr(), (const int64_t*) expert_count.data_ptr(), (int) expert_count.numel(),
+        (const int64_t*) token_sorted.data_ptr(), (const uint16_t*) weight_sorted.data_ptr(), (int) token_sorted.numel(),
+        (uint16_t*) temp_state_g.data_ptr(), (uint16_t*) temp_state_u.data_ptr(), (int) temp_state_g.size(0),
+        (int) temp_state_g.size(1), (uint16_t*) temp_intermediate_g.data_ptr(), (uint16_t*) temp_intermediate_u.data_ptr(),
+        (int) temp_intermediate_g.size(2), act_function, K_gate, K_up, K_down,
+        (const uint64_t*) gate_ptrs_trellis.data_ptr(), (const uint64_t*) gate_ptrs_suh.data_ptr(),
+        (const uint64_t*) gate_ptrs_svh.data_ptr(), (const uint64_t*) up_ptrs_trellis.data_ptr(),
+        (const uint64_t*) up_ptrs_suh.data_ptr(), (const uint64_t*) up_ptrs_svh.data_ptr(),
+        (const uint64_t*) down_ptrs_trellis.data_ptr(), (const uint64_t*) down_ptrs_suh.data_ptr(),
+        (const uint64_t*) down_ptrs_svh.data_ptr(), (int) gate_ptrs_trellis.numel(),
+        gate_mcg, gate_mul1, up_mcg, up_mul1, down_mcg, down_mul1, act_limit, num_active,
+        scr ? (float*) output_scratch->data_ptr() : nullptr, scr ? output_scratch->size(0) : 0,
+        scr ? (int) output_scratch->size(1) : 0, scr ? (const int64_t*) fused_base->data_ptr() : nullptr,
+        count_lo, count_hi, m_tile, opt_ptr<const uint8_t>(bits_g), opt_ptr<const uint8_t>(bits_u),
+        opt_ptr<const uint8_t>(bits_d), nb ? (int) bits_g->numel() : 0, cur_stream(hidden_state)));
+}
+
+// amp_kernels.cu:253-268 / :367-397 return a HIP status (0 = launched); a rejected argument
+// prints the library's message, as the reference prints its dim check, and returns -1.
+extern "C" int amp_silu_mul_fp16(const void* g, const void* u, void* out, long n, void* stream)
+{
+    const int rc = exl3_amd_silu_mul((const uint16_t*) g, (const uint16_t*) u, (uint16_t*) out, n, stream);
+    if (rc < 0) fprintf(stderr, "amp_silu_mul: %s\n", exl3_amd_last_error());
+    return rc < 0 ? -1 : 0;
+}
+
+extern "C" int amp_rms_norm_res_fp16(const void* x, const void* r, const void* w, void* y, void* n, long rows,
+                                     int dim, double eps, void* stream)
+{
+    const int rc = exl3_amd_rms_norm_res((const uint16_t*) x, (const uint16_t*) r, (const uint16_t*) w,
+                                         (uint16_t*) y, (uint16_t*) n, rows, dim, (float) eps, stream);
+    if (rc < 0) fprintf(stderr, "amp_rms_norm_res: %s\n", exl3_amd_last_error());
+    return rc < 0 ? -1 : 0;
 }

@@ -2,6 +2,9 @@
 // exactly as amp_torch.cpp's bindings call them.  c10::Error raised by an operator reaches
 // Python as RuntimeError.
 #include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
+
+#include <algorithm>
 
 #include "exl3_amd_adapter.h"
 
@@ -40,4 +43,20 @@ PYBIND11_MODULE(exl3_amd_torch, m)
                             gated, had_g, had_u, gu_g, gu_u, act_out, d_out, ctr, out, sh_out, sh_gate_w, bits_g,
                             bits_u, bits_d);
           });
+    m.def("exl3_moe_max_concurrency", &exl3_moe_max_concurrency);
+    m.def("exl3_moe_gather", &exl3_moe_gather);
+    m.def("exl3_moe", &exl3_moe);
+    m.def("rms_norm_res", [](const at::Tensor& x, const at::Tensor& r, const at::Tensor& w, at::Tensor y,
+                             at::Tensor n, double eps) {
+        const long dim = w.numel();
+        const int rc = amp_rms_norm_res_fp16(x.data_ptr(), r.data_ptr(), w.data_ptr(), y.data_ptr(), n.data_ptr(),
+                                             x.numel() / std::max(dim, 1L), (int) dim, eps,
+                                             (void*) c10::hip::getCurrentHIPStream(x.device().index()).stream());
+        TORCH_CHECK(rc == 0, "rms_norm_res: launch failed");
+    });
+    m.def("silu_mul", [](const at::Tensor& g, const at::Tensor& u, at::Tensor out) {
+        const int rc = amp_silu_mul_fp16(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(),
+                                         (void*) c10::hip::getCurrentHIPStream(g.device().index()).stream());
+        TORCH_CHECK(rc == 0, "silu_mul: launch failed");
+    });
 }

@@ -1,7 +1,7 @@
 """The at::Tensor adapter (ampstein_amd/adapter/exl3_amd_adapter.cpp): the operators ampstein's
 bindings call, with amp_torch.cpp's C++ signatures, over the C ABI.
 
-CPU: the module loads, exposes the six operators, and raises c10::Error (RuntimeError) on bad
+CPU: the module loads, exposes the operators, and raises c10::Error (RuntimeError) on bad
 arguments before any launch, as the vendored TORCH_CHECKs do (tests/bindings_errors.uc of the
 reference requires every binding to raise on bad arguments).
 GPU: each operator against the CPU oracle on seeded inputs, to the bars of the direct tests
@@ -14,7 +14,8 @@ import torch
 from ampstein_amd import synth, torch_adapter
 
 TOL = 2e-3
-OPS = ("exl3_gemm", "exl3_mgemm", "exl3_moe_coop", "had_r_128", "reconstruct", "reconstruct_had_slice")
+OPS = ("exl3_gemm", "exl3_mgemm", "exl3_moe_coop", "had_r_128", "reconstruct", "reconstruct_had_slice",
+       "exl3_moe", "exl3_moe_gather", "exl3_moe_max_concurrency", "rms_norm_res", "silu_mul")
 
 
 @pytest.fixture(scope="module")
@@ -159,3 +160,66 @@ def test_adapter_exl3_moe_coop(ad, orc):
     ref = moe_ref.reference(es, x, sel, rw, -1, -1, 0, True, 0.0, 1024)
     assert rel_err(y, ref) < TOL
     check_runs(runs, sel, rw, -1, -1)
+
+
+def test_adapter_moe_rejects_bad_arguments(ad):
+    h = lambda *s: torch.zeros(s, dtype=torch.half)
+    L = lambda *s: torch.zeros(s, dtype=torch.long)
+    tabs = [L(4) for _ in range(9)]
+    with pytest.raises(RuntimeError, match="output_scratch needs fused_base"):
+        ad.exl3_moe(h(2, 128), torch.zeros((2, 128)), L(5), L(4), h(4), h(1, 4, 128), h(1, 4, 128), h(1, 4, 128),
+                    h(1, 4, 128), 0, 3.0, 3.0, 3.0, *tabs, True, False, True, False, True, False, 0.0, 1,
+                    torch.zeros((4, 128)), None, 0, 1 << 30, 16, None, None, None)
+    with pytest.raises(RuntimeError, match="output_state is incorrect datatype"):
+        ad.exl3_moe(h(2, 128), h(2, 128), L(5), L(4), h(4), h(1, 4, 128), h(1, 4, 128), h(1, 4, 128),
+                    h(1, 4, 128), 0, 3.0, 3.0, 3.0, *tabs, True, False, True, False, True, False, 0.0, 1,
+                    None, None, 0, 1 << 30, 16, None, None, None)
+    with pytest.raises(RuntimeError, match="weight_sorted is incorrect datatype"):
+        ad.exl3_moe_gather(torch.zeros((2, 128)), torch.zeros((4, 128)), L(4), L(4), L(3), L(3), L(3), L(4))
+
+
+@pytest.mark.gpu
+def test_adapter_exl3_moe_and_gather(ad, orc):
+    """Slot mode through the adapter: bit-identical to the same call through the C ABI's
+    Python front end, then the fixed-order gather (also bit-identical)."""
+    from ampstein_amd import ops
+    from tests.moe_ref import ExpertSet
+    from tests.test_gpu_moe_sorted import routing
+    E, H, I, T, topk = 6, 256, 256, 24, 2
+    es = ExpertSet(torch, orc, E, H, I, H, [3] * E, 1, seed=5)
+    x = torch.from_numpy(np.random.default_rng(2).standard_normal((T, H)).astype(np.float16)).cuda()
+    flat, order, inv, tok, ws, count, start = routing(T, E, topk, seed=4)
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    fb = dv(start[:E])
+    tb = es.tables
+    tabs = [tb[n] for n in ("g_trellis", "g_suh", "g_svh", "u_trellis", "u_suh", "u_svh", "d_trellis", "d_suh", "d_svh")]
+    outs = []
+    for fn in (ad.exl3_moe, ops.exl3_moe):
+        tmp = [torch.zeros((1, 64, w), dtype=torch.half, device="cuda") for w in (H, H, I, I)]
+        out = torch.zeros((T, H), dtype=torch.float, device="cuda")
+        scr = torch.zeros((T * topk, H), dtype=torch.float, device="cuda")
+        fn(x, out, dv(count), dv(tok), dv(ws), *tmp, 0, 3.0, 3.0, 3.0, *tabs, True, False, True, False, True, False,
+           0.0, E, scr, fb, 0, 1 << 30, 16, None, None, None)
+        kind = dv(np.ones(E, np.int64))
+        g = ad.exl3_moe_gather if fn is ad.exl3_moe else ops.exl3_moe_gather
+        g(out, scr, dv(flat), dv(inv), dv(start), fb, kind, dv(ws))
+        torch.cuda.synchronize()
+        outs.append((scr.cpu().numpy(), out.cpu().numpy()))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert np.abs(outs[0][1]).max() > 0
+    assert ad.exl3_moe_max_concurrency(0) == ops.exl3_moe_max_concurrency(0)
+
+
+@pytest.mark.gpu
+def test_adapter_decode_neighbours(ad):
+    from ampstein_amd import ops
+    rng = np.random.default_rng(8)
+    x, r = (torch.from_numpy(rng.standard_normal((2, 1024)).astype(np.float16)).cuda() for _ in range(2))
+    w = torch.from_numpy((rng.standard_normal(1024) * 0.1 + 1).astype(np.float16)).cuda()
+    y, n = torch.empty_like(x), torch.empty_like(x)
+    ad.rms_norm_res(x, r, w, y, n, 1e-6)
+    y2, n2 = ops.rms_norm_res(x, r, w, 1e-6)
+    assert torch.equal(y, y2) and torch.equal(n, n2)
+    out = torch.empty_like(x)
+    ad.silu_mul(x, r, out)
+    assert torch.equal(out, ops.silu_mul(x, r))
