@@ -528,7 +528,7 @@ def summarize_trace(path):
     with open(path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_")):
+            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "rms_norm", "silu_mul")):
                 continue
             grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
             d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
