@@ -18,6 +18,10 @@ __device__ __forceinline__ float wave_sum64(float v)
     return v;
 }
 
+// Chunks per thread kept in registers between the two passes (dim <= 4 * 4 * 1024 = 16384);
+// wider rows re-read the rest of y from memory.
+constexpr int NORM_REG_CHUNKS = 4;
+
 __global__ __launch_bounds__(1024)
 void rms_norm_res_kernel(const uint16_t* x, const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
                          uint16_t* y, uint16_t* __restrict__ n, int dim, float eps)
@@ -26,7 +30,11 @@ void rms_norm_res_kernel(const uint16_t* x, const uint16_t* __restrict__ r, cons
     const int row = blockIdx.x, t = threadIdx.x, cnt = dim >> 2;
     const size_t off = (size_t) row * dim;
     float acc = 0.0f;
-    for (int c = t; c < cnt; c += blockDim.x)
+    u32x2 yk[NORM_REG_CHUNKS], wk[NORM_REG_CHUNKS];
+    #pragma unroll
+    for (int q = 0; q < NORM_REG_CHUNKS; ++q) { yk[q] = (u32x2) { 0u, 0u }; wk[q] = yk[q]; }
+    int q = 0;
+    for (int c = t; c < cnt; c += blockDim.x, ++q)
     {
         const u32x2 xv = *to_global((const u32x2*) (x + off) + c);
         const u32x2 rv = *to_global((const u32x2*) (r + off) + c);
@@ -34,7 +42,15 @@ void rms_norm_res_kernel(const uint16_t* x, const uint16_t* __restrict__ r, cons
         // fp32 add of two fp16 values rounded once: the fp16 sum exactly
         const f16x2 h0 = { (f16) ((float) x0.x + (float) r0.x), (f16) ((float) x0.y + (float) r0.y) };
         const f16x2 h1 = { (f16) ((float) x1.x + (float) r1.x), (f16) ((float) x1.y + (float) r1.y) };
-        *((u32x2*) (y + off) + c) = (u32x2) { as_u32(h0), as_u32(h1) };
+        const u32x2 hv = { as_u32(h0), as_u32(h1) };
+        *((u32x2*) (y + off) + c) = hv;
+        #pragma unroll
+        for (int j = 0; j < NORM_REG_CHUNKS; ++j)
+            if (j == q)
+            {
+                yk[j] = hv;
+                wk[j] = *to_global((const u32x2*) w + c);       // the weights, before the barrier
+            }
         const float a = (float) h0.x, b = (float) h0.y, cc = (float) h1.x, d = (float) h1.y;
         acc += a * a + b * b;
         acc += cc * cc + d * d;
@@ -50,10 +66,21 @@ void rms_norm_res_kernel(const uint16_t* x, const uint16_t* __restrict__ r, cons
     }
     __syncthreads();
     const float scale = wsum[0];
-    for (int c = t; c < cnt; c += blockDim.x)
+    q = 0;
+    for (int c = t; c < cnt; c += blockDim.x, ++q)
     {
-        const u32x2 yv = *((const u32x2*) (y + off) + c);
-        const u32x2 wv = *to_global((const u32x2*) w + c);
+        u32x2 yv, wv;
+        if (q < NORM_REG_CHUNKS)
+        {
+            #pragma unroll
+            for (int j = 0; j < NORM_REG_CHUNKS; ++j)
+                if (j == q) { yv = yk[j]; wv = wk[j]; }
+        }
+        else
+        {
+            yv = *((const u32x2*) (y + off) + c);
+            wv = *to_global((const u32x2*) w + c);
+        }
         const f16x2 y0 = as_h2(yv.x), y1 = as_h2(yv.y);
         // normalise in fp32, round to fp16, then the fp16 weight multiply
         const f16x2 n0 = (f16x2) { (f16) ((float) y0.x * scale), (f16) ((float) y0.y * scale) } * as_h2(wv.x);
