@@ -227,3 +227,25 @@ def test_exl3_moe_gather_exact():
     ops.exl3_moe_gather(out, T_(scratch), T_(flat), T_(inv), T_(start), T_(slot_base), T_(kind), T_(weight_sorted))
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), exp.astype(np.float32))
+
+
+def test_exl3_moe_edges(orc):
+    """No expert in range leaves the output alone; one token; a pool of 5 rows so that experts
+    straddle pass boundaries (rows of one expert in two passes)."""
+    E, H, I = 4, 128, 256
+    es = ExpertSet(torch, orc, E, H, I, H, [2, 3, 4, 2], 2, seed=90)
+    x1 = np.random.default_rng(1).standard_normal((1, H)).astype(np.float16)
+    rt1 = routing(1, E, 2, seed=2)
+    Ks = [2, 3, 4, 2]
+    out, _, _, elig = run_moe(es, x1, rt1, 8, 1, 0, 1 << 30, 0, 0.0, Ks)
+    ref, _ = model(es, x1, rt1[0], rt1[3], rt1[4], rt1[5], rt1[6], 8, 0, 1 << 30, 0, 0.0)
+    assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 2e-3
+    x = np.random.default_rng(3).standard_normal((12, H)).astype(np.float16)
+    rt = routing(12, E, 2, seed=4)
+    out, _, _, elig = run_moe(es, x, rt, 5, 1, 100, 200, 0, 0.0, Ks)       # count range excludes all
+    assert elig == [] or float(out.abs().max()) == 0.0
+    # max_tok 13 holds every expert (24 assignments over 4 experts), pool = 13 rows -> 2 passes
+    out, _, _, elig = run_moe(es, x, rt, 13, 1, 0, 1 << 30, 1, 0.0, Ks)
+    ref, _ = model(es, x, rt[0], rt[3], rt[4], rt[5], rt[6], 13, 0, 1 << 30, 1, 0.0)
+    assert len(elig) == E
+    assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 2e-3
