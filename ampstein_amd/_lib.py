@@ -61,6 +61,8 @@ SIGNATURES = {
     "exl3_amd_silu_mul": (_i32, [_vp, _vp, _vp, ctypes.c_int64, _vp]),
     "exl3_amd_gemm_silu_mul": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_gemm_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _i32, _i32, _i32, _f32, _i32, _i32, _vp, _vp, _vp, _f32, _vp]),
     "exl3_amd_moe": (_i32, [_vp, _i32, _i32, _vp,                       # hidden, bsz, hidden_dim, output
                             _vp, _i32, _vp, _vp, _i32,                  # expert_count (+len), token/weight_sorted, n
                             _vp, _vp, _i32, _i32,                       # temp_state_g/u, concurrency, max_tokens

@@ -255,7 +255,7 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     // (exl3_gemv.hip gemv1p_kernel).  Needs the XCD-local hand-off and per-slot tables of at
     // most 16 slots without indices or routing weights.
     // Opt-in (EXL3_AMD_GEMV_P1=1) until its GPU run is cleared.
-    bool p1 = g.m == 1 && g.stream_m1 && !g.A_up && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
+    bool p1 = g.m == 1 && g.stream_m1 && !g.A_up && !g.norm_h && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
               g.row0 == 0 && g.slab_m <= 1;
     {
         const char* e = getenv("EXL3_AMD_GEMV_P1");
@@ -950,6 +950,48 @@ int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* a
     }
     if (int rc = exl3k_silu_mul(gate, up, act, (long) m * k, s)) return hip_fail(rc, "exl3_gemm_silu_mul");
     return exl3_amd_gemm(act, trellis, C, c_fp32, suh, A_had, svh, m, k, n, K, mcg, mul1, 0, stream);
+}
+
+
+int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, const uint16_t* trellis, uint16_t* C,
+                       const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                       int m, int k, int n, float K, int mcg, int mul1,
+                       uint16_t* h, const uint16_t* w, uint16_t* r, float eps, void* stream)
+{
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
+    if (m < 1 || k < 1 || n < 1) return fail(EXL3_AMD_EINVAL, "exl3_gemm_norm: sizes must be positive");
+    if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
+    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
+    if (!A || !trellis || !C || !h || !w || !r || (up && !act)) return fail(EXL3_AMD_EINVAL, "exl3_gemm_norm: null pointer");
+    if (((uintptr_t) C | (uintptr_t) h | (uintptr_t) w | (uintptr_t) r) & 15)
+        return fail(EXL3_AMD_EINVAL, "exl3_gemm_norm: C, h, w and r must be 16-byte aligned");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    if (m == 1)
+    {
+        GemvArgs g = gemv_args_single(A, trellis, C, 0, suh, svh, m, k, n);
+        GemvArgs probe = g;
+        const bool plan_ok = !gemv_plan(m, k, n, 1, d->num_cus, probe) && probe.stream_m1 == 1;
+        const int chunks = n / 128;
+        const bool handoff = probe.slots == 1 || (d->num_xcd > 0 && chunks % d->num_xcd == 0 && chunks * 32 <= (int) (WS_COUNTERS / 2));
+        if (plan_ok && handoff)
+        {
+            g.A_up = up;
+            g.norm_h = h; g.norm_w = w; g.norm_r = r; g.norm_eps = eps;
+            g.norm_ctr = d->counters + WS_COUNTERS - 32;
+            int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm_norm");
+            return rc ? rc : EXL3_AMD_TAG_GEMV;
+        }
+    }
+    int tag = up ? exl3_amd_gemm_silu_mul(A, up, act, trellis, C, 0, suh, A_had, svh, m, k, n, K, mcg, mul1, stream)
+                 : exl3_amd_gemm(A, trellis, C, 0, suh, A_had, svh, m, k, n, K, mcg, mul1, 0, stream);
+    if (tag < 0) return tag;
+    if (int rc = exl3_amd_rms_norm_res(h, C, w, h, r, m, n, eps, stream)) return rc;
+    return tag;
 }
 
 }  // extern "C"

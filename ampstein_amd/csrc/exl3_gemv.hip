@@ -385,6 +385,90 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
     }
 }
 
+// Fused residual add + RMSNorm of the whole output row (rms_norm_res, amp_kernels.cu:279-365),
+// run by the one wave that completes the row's last column chunk: h = fp16(h + C) in place,
+// r = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * w).  Lane l holds columns 8 l .. 8 l + 7 of each
+// 512-column block; up to 8 blocks stay in registers between the two passes.
+constexpr int NORM_RC = 8;
+
+__device__ __noinline__ void fused_norm_wave(const uint16_t* C, uint16_t* h, const uint16_t* wn, uint16_t* rn,
+                                             int n, float eps)
+{
+    const int lane = threadIdx.x & 63;
+    float acc = 0.0f;
+    u32x4 yk[NORM_RC];
+    auto add_block = [&](int col, u32x4& out) {
+        const u32x4 cv = *to_global((const u32x4*) (C + col));
+        const u32x4 hv = *to_global((const u32x4*) (h + col));
+        const uint32_t cw[4] = { cv.x, cv.y, cv.z, cv.w }, hw[4] = { hv.x, hv.y, hv.z, hv.w };
+        uint32_t yw[4];
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const f16x2 a = as_h2(hw[q]), b = as_h2(cw[q]);
+            const f16x2 y = { (f16) ((float) a.x + (float) b.x), (f16) ((float) a.y + (float) b.y) };
+            yw[q] = as_u32(y);
+            acc += (float) y.x * (float) y.x + (float) y.y * (float) y.y;
+        }
+        out = (u32x4) { yw[0], yw[1], yw[2], yw[3] };
+        *to_global_w((u32x4*) (h + col)) = out;
+    };
+    #pragma unroll
+    for (int i = 0; i < NORM_RC; ++i)
+    {
+        const int col = 512 * i + 8 * lane;
+        if (col < n) add_block(col, yk[i]);
+    }
+    for (int col = 512 * NORM_RC + 8 * lane; col < n; col += 512)
+    {
+        u32x4 t;
+        add_block(col, t);
+    }
+    #pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+    const float scale = 1.0f / sqrtf(acc / (float) n + eps);
+    auto norm_block = [&](int col, const u32x4& yv) {
+        const u32x4 wv = *to_global((const u32x4*) (wn + col));
+        const uint32_t yw[4] = { yv.x, yv.y, yv.z, yv.w }, ww[4] = { wv.x, wv.y, wv.z, wv.w };
+        uint32_t o[4];
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const f16x2 y = as_h2(yw[q]);
+            o[q] = as_u32((f16x2) { (f16) ((float) y.x * scale), (f16) ((float) y.y * scale) } * as_h2(ww[q]));
+        }
+        *to_global_w((u32x4*) (rn + col)) = (u32x4) { o[0], o[1], o[2], o[3] };
+    };
+    #pragma unroll
+    for (int i = 0; i < NORM_RC; ++i)
+    {
+        const int col = 512 * i + 8 * lane;
+        if (col < n) norm_block(col, yk[i]);
+    }
+    for (int col = 512 * NORM_RC + 8 * lane; col < n; col += 512)
+    {
+        const u32x4 yv = *to_global((const u32x4*) (h + col));
+        norm_block(col, yv);
+    }
+}
+
+// Row completion for the fused norm: this wave has stored its chunk of C.  Release the stores at
+// device scope (the row's chunks finish on every XCD), count the chunk; the last chunk's wave
+// acquires and normalises the row, then re-arms the counter.  No wave ever waits on another.
+__device__ __forceinline__ void norm_arrive(const GemvArgs& g, const uint16_t* C)
+{
+    const int lane = threadIdx.x & 63;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(g.norm_ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != g.n / 128 - 1) return;
+    if (lane == 0) __hip_atomic_store(to_global_w(g.norm_ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    fused_norm_wave(C, g.norm_h, g.norm_w, g.norm_r, g.n, g.norm_eps);
+}
+
 // One wave's epilogue of an M = 1 chunk (no routing weights): v0, v1 are this workgroup's sums
 // of columns 2 lane, 2 lane + 1 (corrections applied).  One split: rotate and store.  Several:
 // store the partial to this workgroup's slot; in XCD mode count it in the chunk's counter (the
@@ -399,6 +483,7 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
     if (splits == 1)
     {
         store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+        if (g.norm_h) norm_arrive(g, (const uint16_t*) v.C);
         return;
     }
     float* pbase = g.partials + ((size_t) j * (g.n / 128) + chunk) * splits * 128;
@@ -424,6 +509,7 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
             if (p0 + u < splits) { s0 += vv[u].x; s1 += vv[u].y; }
     }
     store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+    if (g.norm_h) norm_arrive(g, (const uint16_t*) v.C);
 }
 
 // Inactive slot (negative index) in weighted XCD mode: still counted once per chunk.

@@ -13,6 +13,13 @@ struct GemvArgs
 {
     const uint16_t* A;          // (bszm_in, m, k) fp16
     const uint16_t* A_up;       // non-null: the input is fp16(silu(A) * A_up) (M = 1 stream kernel only)
+    // non-null norm_h: after the row is complete, norm_h = fp16(norm_h + C) and
+    // norm_r = rmsnorm(norm_h) * norm_w (M = 1 stream kernel, single matrix, fp16 C, one split or XCD hand-off)
+    uint16_t* norm_h;
+    const uint16_t* norm_w;
+    uint16_t* norm_r;
+    int* norm_ctr;              // workspace counter on its own 128-byte line, zero between calls
+    float norm_eps;
     const uint16_t* trellis;    // (k/16, n/16, 16K) uint16 (single matrix)
     void* C;                    // (bszm, m, n) fp16 or fp32
     const uint16_t* suh;        // (k) fp16 or null (single matrix)

@@ -11,7 +11,10 @@ Per layer, on persistent buffers and without host synchronisation:
     d = exl3_gemm(silu(gate) * up)                       one launch: the M = 1 GEMV forms the
                                                          SwiGLU product in its input load
 and finally h, out = rms_norm_res(h, d_last, norm).  `fuse_swiglu=False` runs silu_mul and
-exl3_gemm as two launches, as graphdec.uc does.
+exl3_gemm as two launches, as graphdec.uc does.  `fuse_norm=True` also folds each residual
+norm into the GEMV before it (o_proj with the post-attention norm, down_proj with the next
+layer's input norm or the final norm): the wave that completes the row's last column chunk
+normalises the row, and 4 launches per layer remain.
 """
 from __future__ import annotations
 
@@ -38,12 +41,13 @@ class LayerWeights:
 
 class DecodeStack:
     def __init__(self, layers: List[LayerWeights], final_norm: torch.Tensor, eps: float = 1e-5,
-                 fuse_swiglu: bool = True):
+                 fuse_swiglu: bool = True, fuse_norm: bool = False):
         dev = final_norm.device
         L0 = layers[0]
         self.hidden = L0.q.in_features
         self.inter = L0.gate.out_features
         self.layers, self.final_norm, self.eps, self.fuse = layers, final_norm, eps, fuse_swiglu
+        self.fuse_norm = fuse_norm
         z = lambda *sh: torch.zeros(sh, dtype=torch.half, device=dev)
         H, I = self.hidden, self.inter
         self.x_in = z(1, H)
@@ -73,7 +77,23 @@ class DecodeStack:
         """One decode step over the current contents of x_in; returns the final normed row."""
         h, r, eps = self.h, self.r, self.eps
         h.copy_(self.x_in)
+        nl = len(self.layers)
+        if self.fuse_norm:
+            ops.rms_norm_res(h, self.zero, self.layers[0].input_norm, eps, y=h, n=r)
         for i, Lw in enumerate(self.layers):
+            if self.fuse_norm:
+                self.qkv[i].run(r.view(1, 1, -1))
+                o = Lw.o
+                ops.exl3_gemm_norm(self.qbuf[i].view(1, -1), o.trellis, self.oout[i], o.suh, o.svh, h, Lw.post_norm,
+                                   r, eps, o.mcg, o.mul1, A_had=self.a_had_h)
+                self.gu[i].run(r.view(1, 1, -1))
+                dn = Lw.down
+                last = i == nl - 1
+                ops.exl3_gemm_norm(self.guout[i][0], dn.trellis, self.dout[i], dn.suh, dn.svh, h,
+                                   self.final_norm if last else self.layers[i + 1].input_norm,
+                                   self.out if last else r, eps, dn.mcg, dn.mul1,
+                                   up=self.guout[i][1], act=self.act, A_had=self.a_had_i)
+                continue
             res = self.zero if i == 0 else self.dout[i - 1]
             ops.rms_norm_res(h, res, Lw.input_norm, eps, y=h, n=r)
             self.qkv[i].run(r.view(1, 1, -1))
@@ -88,7 +108,8 @@ class DecodeStack:
             else:
                 ops.silu_mul(g, u, out=self.act)
                 self._linear(dn, self.act, self.dout[i], self.a_had_i)
-        ops.rms_norm_res(h, self.dout[-1], self.final_norm, eps, y=h, n=self.out)
+        if not self.fuse_norm:
+            ops.rms_norm_res(h, self.dout[-1], self.final_norm, eps, y=h, n=self.out)
         return self.out
 
     def capture(self) -> None:

@@ -537,6 +537,39 @@ def exl3_gemm_silu_mul(gate: Tensor, up: Tensor, B: Tensor, C: Tensor, suh: Opti
             _stream(gate)))
 
 
+def exl3_gemm_norm(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], svh: Optional[Tensor],
+                   h: Tensor, weight: Tensor, r: Tensor, eps: float, mcg: bool = False, mul1: bool = False,
+                   up: Optional[Tensor] = None, act: Optional[Tensor] = None, A_had: Optional[Tensor] = None) -> int:
+    """C = exl3_gemm(A) (of silu(A) * up when up is given), then [h, r] = rms_norm_res(h, C,
+    weight) with h updated in place: one launch at one row (the GEMV's last chunk normalises)."""
+    _need(B.dim() == 3, "B must be 3-dimensional")
+    _dtype(A, torch.half, "A")
+    _trellis_dtype(B, "B")
+    _dtype(C, torch.half, "C")
+    for t, nm in ((h, "h"), (weight, "weight"), (r, "r")):
+        _dtype(t, torch.half, nm)
+    k, n = B.size(0) * 16, B.size(1) * 16
+    _need(A.size(-1) == k and C.size(-1) == n and h.numel() == C.numel() and r.numel() == C.numel()
+          and weight.numel() == n, "exl3_gemm_norm: incompatible shapes")
+    if up is not None:
+        _dtype(up, torch.half, "up")
+        _need(up.shape == A.shape, "silu_mul: gate/up size mismatch")
+    tile = B.size(2)
+    half_k = tile % 16 != 0
+    _need(not half_k or (tile % 16 == 8 and mul1), "exl3_gemm: half-integer bitrates require the mul1 codebook")
+    K = tile // 16 + (0.5 if half_k else 0.0)
+    mcg_i, mul1_i = _codebook_flags(mcg, mul1)
+    act = torch.empty_like(A) if (act is None and up is not None) else act
+    A_had = torch.empty_like(A) if A_had is None else A_had
+    m = A.numel() // k
+    _cuda(A, B, C, suh, svh, h, weight, r, up, act, A_had)
+    with torch.cuda.device(A.device):
+        return check(_lib.lib().exl3_amd_gemm_norm(
+            A.data_ptr(), _ptr(up), _ptr(act), B.data_ptr(), C.data_ptr(), _ptr(suh), A_had.data_ptr(), _ptr(svh),
+            m, k, n, float(K), mcg_i, mul1_i, h.data_ptr(), weight.data_ptr(), r.data_ptr(), float(eps),
+            _stream(A)))
+
+
 def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
     """out = a @ b on the dense GEMM library, with TunableOp scoped to this call (the caller's
     process-wide setting is restored)."""

@@ -208,7 +208,8 @@ def decode_step_bench(torch, layers, steps=20):
     """The linear part of the Llama-3-8B decode step with its neighbours (graphdec.uc:151-230:
     rms_norm_res, q/k/v sliced mgemm, o gemm, rms_norm_res, gate/up stacked mgemm, SwiGLU + down,
     final norm) captured into one graph over the same 32 layers; attention is outside the path
-    (the q projection feeds o).  Fused: the down GEMV forms silu(gate) * up in its input load."""
+    (the q projection feeds o).  fused_swiglu: the down GEMV forms silu(gate) * up in its input
+    load; fused_norm_swiglu: o and down also run the residual norm in their last column chunk."""
     from ampstein_amd.decode import DecodeStack, LayerWeights
     H = 4096
     ones = torch.ones(H, dtype=torch.half, device="cuda")
@@ -217,8 +218,9 @@ def decode_step_bench(torch, layers, steps=20):
     nbytes = sum(r[n].trellis.numel() * 2 for r in layers for n in ("q", "k", "v", "o", "gate", "up", "down"))
     x = torch.randn((1, H), device="cuda").half()
     res = {}
-    for name, fuse in (("fused_swiglu", True), ("separate_silu_mul", False)):
-        st = DecodeStack(lw, ones, fuse_swiglu=fuse)
+    for name, fuse, fnorm, launches in (("fused_norm_swiglu", True, True, 4), ("fused_swiglu", True, False, 6),
+                                        ("separate_silu_mul", False, False, 7)):
+        st = DecodeStack(lw, ones, fuse_swiglu=fuse, fuse_norm=fnorm)
         st.capture()
         for _ in range(3):
             st(x)
@@ -232,7 +234,7 @@ def decode_step_bench(torch, layers, steps=20):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / steps
         res[name] = {"us_per_step": round(us, 1), "us_per_layer": round(us / len(layers), 2),
-                     "launches_per_layer": 6 if fuse else 7, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+                     "launches_per_layer": launches, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
         del st
     return {"what": "32-layer decode step without attention: norms + linears + SwiGLU, one graph",
             "packed_bytes": nbytes, **res}

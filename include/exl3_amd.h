@@ -244,6 +244,19 @@ int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* a
                            const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
                            int m, int k, int n, float K, int mcg, int mul1, void* stream);
 
+/* The decode step's linear + residual norm in one call (graphdec.uc:184-189 and :223 then the
+ * next norm): C = exl3_gemm(A) (or of fp16(silu(A) * up) when up is given, with act as the
+ * fallback's scratch), then h = fp16(h + C) in place and r = fp16(fp16(h * rsqrt(mean(h^2) +
+ * eps)) * w), like exl3_amd_rms_norm_res.  With one row, the M = 1 stream GEMV does the norm in
+ * the wave that completes the row's last column chunk: one launch.  Otherwise (or without the
+ * XCD hand-off) the GEMM and exl3_amd_rms_norm_res run as two launches.  C fp16; C, h, w, r
+ * 16-byte aligned.  No counterpart in the reference (a fusion of two of its calls).  Returns the
+ * exl3_gemm tag. */
+int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, const uint16_t* trellis, uint16_t* C,
+                       const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                       int m, int k, int n, float K, int mcg, int mul1,
+                       uint16_t* h, const uint16_t* w, uint16_t* r, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -150,3 +150,54 @@ def test_decode_stack_graph_and_model(orc):
         err = np.abs(got - ref).max() / np.abs(ref).max()
         print(f"decode stack rel err {err:.2e}", flush=True)
         assert err < 5e-3
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (1024, 5120), (512, 640), (14336, 1024)])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_gemm_norm_matches_two_calls(k, n, swiglu):
+    """Fused residual norm in the GEMV's last chunk: C and the updated residual bit-identical to
+    exl3_gemm + rms_norm_res, the normed row within one fp16 ulp (the sum of squares is
+    reduced in another order)."""
+    L = synth.layer(k, n, 4, 0, seed=k + n)
+    L.svh = (L.svh.astype(np.float32) / 16).astype(np.float16)
+    t, s, v = L.torch("cuda")
+    rng = np.random.default_rng(n)
+    a = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float16)).cuda()
+    up = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float16)).cuda() if swiglu else None
+    h0 = torch.from_numpy((rng.standard_normal((1, n)) * 4).astype(np.float16)).cuda()
+    w = torch.from_numpy((rng.standard_normal(n) * 0.2 + 1).astype(np.float16)).cuda()
+    C1, r1, h1 = torch.empty((1, n), dtype=torch.half, device="cuda"), torch.empty((1, n), dtype=torch.half, device="cuda"), h0.clone()
+    for rep in range(2):                  # the row counter must re-arm: a second call behaves the same
+        h1.copy_(h0)
+        ops.exl3_gemm_norm(a, t, C1, s, v, h1, w, r1, 1e-5, up=up)
+        torch.cuda.synchronize()
+        C2 = torch.empty_like(C1)
+        if swiglu:
+            ops.exl3_gemm_silu_mul(a, up, t, C2, s, v)
+        else:
+            ops.exl3_gemm(a, t, C2, s, torch.empty_like(a), v)
+        h2, r2 = ops.rms_norm_res(h0, C2, w, 1e-5)
+        assert torch.equal(C1, C2)
+        assert torch.equal(h1, h2)
+        assert ulp_diff(r1.cpu().numpy(), r2.cpu().numpy()).max() <= 1
+
+
+def test_decode_stack_fused_norm(orc):
+    H, Q, KV, I = 512, 512, 128, 1024
+    st, host, wf = _stack(H, Q, KV, I, 2)
+    st.fuse_norm = True
+    rng = np.random.default_rng(13)
+    xs = [rng.standard_normal(H).astype(np.float16) for _ in range(2)]
+    eager = [st(torch.from_numpy(x).cuda()).clone() for x in xs]
+    st.capture()
+    for rep in range(2):
+        for x, e in zip(xs, eager):
+            y = st(torch.from_numpy(x).cuda())
+            torch.cuda.synchronize()
+            assert torch.equal(y, e), f"graph replay {rep} differs from the eager step"
+    for x, e in zip(xs, eager):
+        ref = _model(host, wf, x, 4, 0).astype(np.float64)
+        got = e.cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        print(f"decode stack (fused norm) rel err {err:.2e}", flush=True)
+        assert err < 5e-3
