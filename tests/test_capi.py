@@ -248,3 +248,36 @@ def test_moe_gather_rejects_bad_arguments():
     rc, msg = call_err(L.exl3_amd_moe_gather, 1, 1, 256, 1, 256, 1, 33, 1, 1, 4, 1, 4, 1, 4, 1, None)
     assert rc == _lib.EINVAL and "top-k" in msg
     assert L.exl3_amd_moe_gather(1, 0, 256, 1, 256, 1, 0, 1, 1, 4, 1, 4, 1, 4, 1, None) == 0
+
+
+def test_decode_neighbours_reject_bad_arguments():
+    """rms_norm_res's checks (amp_torch.cpp:10106-10131: last dim a multiple of 4, 8-byte
+    aligned operands), silu_mul's null check, and exl3_gemm's shape checks in the fused entry
+    points, all before any device access."""
+    L = _lib.lib()
+    f = ctypes.c_float
+    rc, msg = call_err(L.exl3_amd_rms_norm_res, 8, 8, 8, 8, 8, 1, 130, f(1e-5), None)
+    assert rc == _lib.EINVAL and "multiple of 4" in msg
+    rc, msg = call_err(L.exl3_amd_rms_norm_res, 8, 12, 8, 8, 8, 1, 128, f(1e-5), None)
+    assert rc == _lib.EINVAL and "8-byte aligned" in msg
+    rc, msg = call_err(L.exl3_amd_rms_norm_res, None, 8, 8, 8, 8, 1, 128, f(1e-5), None)
+    assert rc == _lib.EINVAL and "null" in msg
+    assert L.exl3_amd_rms_norm_res(None, None, None, None, None, 0, 128, f(1e-5), None) == 0
+    rc, msg = call_err(L.exl3_amd_silu_mul, None, 8, 8, 16, None)
+    assert rc == _lib.EINVAL and "null" in msg
+    assert L.exl3_amd_silu_mul(None, None, None, 0, None) == 0
+    rc, msg = call_err(L.exl3_amd_gemm_silu_mul, 8, 8, 8, 8, 8, 0, None, None, None, 1, 128, 100, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "n must" in msg
+    rc, msg = call_err(L.exl3_amd_gemm_silu_mul, 8, 8, 8, 8, 8, 0, None, None, None, 1, 136, 128, f(4.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "k must" in msg
+    rc, msg = call_err(L.exl3_amd_gemm_silu_mul, 8, 8, 8, 8, 8, 0, None, None, None, 1, 128, 128, f(9.0), 0, 0, None)
+    assert rc == _lib.EINVAL and "bitrate" in msg
+    rc, msg = call_err(L.exl3_amd_gemm_norm, 16, None, None, 16, 16, None, None, None, 1, 128, 128, f(4.0), 0, 0,
+                       16, 16, 8, f(1e-5), None)
+    assert rc == _lib.EINVAL and "16-byte aligned" in msg
+    rc, msg = call_err(L.exl3_amd_gemm_norm, 16, 16, None, 16, 16, None, None, None, 1, 128, 128, f(4.0), 0, 0,
+                       16, 16, 16, f(1e-5), None)
+    assert rc == _lib.EINVAL and "null" in msg
+    rc, msg = call_err(L.exl3_amd_gemm_norm, 16, None, None, 16, 16, None, None, None, 1, 128, 120, f(4.0), 0, 0,
+                       16, 16, 16, f(1e-5), None)
+    assert rc == _lib.EINVAL and "n must" in msg
