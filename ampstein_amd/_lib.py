@@ -25,6 +25,7 @@ SIGNATURES = {
     "exl3_amd_device_info": (_i32, [_i32, _vp, _vp]),
     "exl3_amd_reconstruct": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_t": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_reconstruct_t_had": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_had": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_had_r_128": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _f32, _vp]),
     "exl3_amd_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),

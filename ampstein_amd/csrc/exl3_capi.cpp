@@ -380,8 +380,28 @@ int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_p
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
     DeviceState* d;
     if (int rc = current_device(&d)) return rc;
-    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, (hipStream_t) stream);
+    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, nullptr, (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_t") : 0;
+}
+
+int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint16_t* svh, int k, int n_packed,
+                               int n, int n_offset, float K, int mcg, int mul1, void* stream)
+{
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "reconstruct_t_had", true)) return rc;
+    if (k < 0 || n < 0 || n_packed < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: negative size");
+    if (k % 16 || n_packed % 16) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: k and the packed width must be multiples of 16");
+    if ((size_t) k * n == 0) return 0;
+    if (!WT || !trellis || !svh) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: null pointer");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: N dimension must be divisible by 128");
+    if (n_offset % 128 || n_offset < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: n_offset must be a non-negative multiple of 128");
+    if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
+    DeviceState* d;
+    if (int rc = current_device(&d)) return rc;
+    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, svh + n_offset,
+                                  (hipStream_t) stream);
+    return rc ? hip_fail(rc, "reconstruct_t_had") : 0;
 }
 
 int exl3_amd_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,

@@ -196,7 +196,7 @@ constexpr int EXL3_MOE_SBMAX = 64;     // k-slices per workgroup of the MoE GEMV
 int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
                       int nt_off, int K, int cb, hipStream_t s);
 int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                         int nt_off, int K, int cb, hipStream_t s);
+                         int nt_off, int K, int cb, const uint16_t* svh, hipStream_t s);
 int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
                           const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
                           int K, int cb, hipStream_t s);

@@ -113,10 +113,14 @@ void reconstruct_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ t
 // chunk; lane (tile t, j) holds the 16 rows of columns j and j + 8 of its tile, i.e. 32-byte runs
 // of two transposed rows.  The workgroup's 128 columns x 64 k meet in LDS and leave as whole
 // 128-byte lines (8 threads per transposed row).
+//
+// With svh (the rotated branch of the recon GEMM), every k row of the tile is then rotated
+// across its 128 columns and scaled: W' = W_hat H128 diag(svh) / sqrt(128), fp32 butterflies from
+// the fp16 weights, one fp16 rounding.  y = had(x o suh) @ W' then needs no output rotation.
 template <int K, int CB>
 __global__ __launch_bounds__(256)
 void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict__ trellis,
-                          int k, int tiles_n, int nt_off)
+                          int k, int tiles_n, int nt_off, const uint16_t* __restrict__ svh)
 {
     __shared__ __align__(16) uint32_t sh[128][32 + 4];    // [column][64 k as 32 pairs] (+pad)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -137,6 +141,24 @@ void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict_
         *(u32x4*) &sh[ca + 8][8 * wave + 4] = (u32x4) { p[3], p[7], p[11], p[15] };
     }
     __syncthreads();
+    if (svh)
+    {
+        // wave w: k pairs 8 w .. 8 w + 7; lane l holds columns 2 l, 2 l + 1 (the GEMV output layout)
+        const f16x2 sv = as_h2(*to_global((const uint32_t*) (svh + chunk * 128 + 2 * lane)));
+        const float s0 = (float) sv.x * EXL3_HAD_RSCALE, s1 = (float) sv.y * EXL3_HAD_RSCALE;
+        #pragma unroll 2
+        for (int q = 0; q < 8; ++q)
+        {
+            const int pr = 8 * wave + q;
+            const f16x2 a = as_h2(sh[2 * lane][pr]), b = as_h2(sh[2 * lane + 1][pr]);
+            float a0 = (float) a.x, b0 = (float) b.x, a1 = (float) a.y, b1 = (float) b.y;
+            fwht128_wave(a0, b0, lane);
+            fwht128_wave(a1, b1, lane);
+            sh[2 * lane][pr] = as_u32((f16x2) { (f16) (a0 * s0), (f16) (a1 * s0) });
+            sh[2 * lane + 1][pr] = as_u32((f16x2) { (f16) (b0 * s1), (f16) (b1 * s1) });
+        }
+        __syncthreads();
+    }
     // 128 rows x (nks x 32 bytes): thread t writes 16-byte piece t % 8 of rows t / 8 + 32 i
     const int piece = threadIdx.x & 7;
     if (piece < 2 * nks)
@@ -269,10 +291,10 @@ int launch_reconstruct_t(uint16_t* W, const uint16_t* trellis, int k, int n, int
 
 template <int K, int CB>
 int launch_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                          int nt_off, hipStream_t s)
+                          int nt_off, const uint16_t* svh, hipStream_t s)
 {
     dim3 grid(n / 128, (k / 16 + 3) / 4);
-    hipLaunchKernelGGL((reconstruct_t_kernel<K, CB>), grid, dim3(256), 0, s, WT, trellis, k, tiles_n, nt_off);
+    hipLaunchKernelGGL((reconstruct_t_kernel<K, CB>), grid, dim3(256), 0, s, WT, trellis, k, tiles_n, nt_off, svh);
     return (int) hipGetLastError();
 }
 
@@ -335,7 +357,7 @@ int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* 
 }
 
 int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                         int nt_off, int K, int cb, hipStream_t s)
+                         int nt_off, int K, int cb, const uint16_t* svh, hipStream_t s)
 {
-    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, s)
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, svh, s)
 }

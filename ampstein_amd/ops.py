@@ -35,6 +35,11 @@ RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", str(1 << 30)))
 # Tuned dense GEMM for the recon path (PyTorch TunableOp: hipBLASLt and rocBLAS solutions timed
 # per shape on first use): 8-20 % faster than the default heuristic at M = 2048.
 RECON_TUNED_GEMM = os.environ.get("AMP_RECON_TUNABLE", "1") != "0"
+# Rotated branch: AMP_RECON_FOLD_SVH=1 folds the output rotation and svh into the transposed
+# reconstruct (when rows >= k / 4) instead of rotating y afterwards.  Off by default: on MI355X
+# the fold makes the reconstruct ALU-bound (8192 -> 28672 at 2048 rows: ~1200 us per call
+# against 940-1070 us with the separate rotation of y).
+RECON_FOLD_SVH = os.environ.get("AMP_RECON_FOLD_SVH", "0") != "0"
 
 
 def _ptr(t: Optional[Tensor]):
@@ -101,11 +106,12 @@ def reconstruct_slice(unpacked: Tensor, packed: Tensor, K: float, mcg: bool, mul
 
 
 def reconstruct_t(unpacked_t: Tensor, packed: Tensor, K: float, mcg: bool = False,
-                  mul1: bool = False, n_offset: int = 0) -> None:
+                  mul1: bool = False, n_offset: int = 0, svh: Optional[Tensor] = None) -> None:
     """W_hat columns [n_offset, n_offset + unpacked_t.size(0)) transposed into `unpacked_t`
     (rows, k) fp16: the k-contiguous layout the recon GEMM reads fastest.  Values bit-exact
     with reconstruct (no reference counterpart: the reference keeps W (k, n) for cuBLAS,
-    amp_torch.cpp:11199-11214)."""
+    amp_torch.cpp:11199-11214).  With svh (the full (n) vector) the output rotation is folded in:
+    (W_hat H128 diag(svh) / sqrt(128))^T, one fp16 rounding."""
     bits, half = bits_from_K(K)
     _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
     _need(packed.dim() == 3 and unpacked_t.dim() == 2, "reconstruct: bad tensor ranks")
@@ -117,8 +123,15 @@ def reconstruct_t(unpacked_t: Tensor, packed: Tensor, K: float, mcg: bool = Fals
     _trellis_dtype(packed, "packed")
     if unpacked_t.numel() == 0:
         return
-    _cuda(unpacked_t, packed)
+    _cuda(unpacked_t, packed, svh)
     with torch.cuda.device(unpacked_t.device):
+        if svh is not None:
+            _dtype(svh, torch.half, "svh")
+            _need(svh.numel() >= packed.size(1) * 16, "svh too short")
+            check(_lib.lib().exl3_amd_reconstruct_t_had(
+                unpacked_t.data_ptr(), packed.data_ptr(), svh.data_ptr(), unpacked_t.size(1), packed.size(1) * 16,
+                unpacked_t.size(0), int(n_offset), float(K), int(bool(mcg)), int(bool(mul1)), _stream(unpacked_t)))
+            return
         check(_lib.lib().exl3_amd_reconstruct_t(
             unpacked_t.data_ptr(), packed.data_ptr(), unpacked_t.size(1), packed.size(1) * 16,
             unpacked_t.size(0), int(n_offset), float(K), int(bool(mcg)), int(bool(mul1)), _stream(unpacked_t)))
@@ -609,9 +622,15 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
         xh = torch.empty_like(x)
         wt = w.view(n, k)
         had_r_128(x, xh, suh, None, 1.0)
-        reconstruct_t(wt, trellis, K, mcg, mul1)
-        _recon_mm(xh, wt.t(), y)
-        had_r_128(y, y, None, svh, 1.0)
+        # the fold adds ALU work per weight (k n) and saves a pass over y (rows n): taken when y
+        # is large against W (measured on MI355X: 8192 -> 28672 at 2048 rows gains, 28672 -> 8192 loses)
+        if RECON_FOLD_SVH and 4 * rows >= k:
+            reconstruct_t(wt, trellis, K, mcg, mul1, svh=svh)
+            _recon_mm(xh, wt.t(), y)
+        else:
+            reconstruct_t(wt, trellis, K, mcg, mul1)
+            _recon_mm(xh, wt.t(), y)
+            had_r_128(y, y, None, svh, 1.0)
     return y
 
 

@@ -257,6 +257,14 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
                        int m, int k, int n, float K, int mcg, int mul1,
                        uint16_t* h, const uint16_t* w, uint16_t* r, float eps, void* stream);
 
+/* exl3_amd_reconstruct_t with the output rotation folded in: WT (n, k) = (W_hat H128 diag(svh)
+ * / sqrt(128))^T for columns [n_offset, n_offset + n), svh the full (n_packed) vector.  fp32
+ * butterflies from the fp16 weights, one fp16 rounding.  The recon GEMM's rotated branch then
+ * computes y = had(x o suh) @ W' with no rotation of y.  No counterpart in the reference (its
+ * rotated branch rotates y, amp_torch.cpp:11215-11228). */
+int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint16_t* svh, int k, int n_packed,
+                               int n, int n_offset, float K, int mcg, int mul1, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

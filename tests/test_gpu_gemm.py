@@ -129,3 +129,28 @@ def test_gemm_recon(torch_cuda, orc, branch, K, cb):
     torch.cuda.synchronize()
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, K, cb=cb)
     assert rel_err(y.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2), (2.5, 2), (8, 0)])
+def test_reconstruct_t_had(orc, K, cb):
+    """W' = W_hat H128 diag(svh) / sqrt(128), transposed: within one fp16 ulp of the fp64 product
+    of the oracle's bit-exact W_hat (fp32 butterflies, one rounding), and the recon GEMM's rotated
+    branch with the fold against fp64 within 2e-3."""
+    import torch
+    from ampstein_amd import ops
+    from scipy.linalg import hadamard
+    k, n = 256, 384
+    L = synth.layer(k, n, K, cb, seed=int(K * 10) + cb)
+    t, s, v = L.torch("cuda")
+    wt = torch.empty((n, k), dtype=torch.half, device="cuda")
+    ops.reconstruct_t(wt, t, K, cb == 1, cb == 2, svh=v)
+    W = orc.reconstruct(L.trellis, int(K), half=K != int(K), cb=cb).astype(np.float64)
+    H = hadamard(128) / np.sqrt(128.0)
+    ref = (W.reshape(k, n // 128, 128) @ H).reshape(k, n) * L.svh.astype(np.float64)
+    got = wt.cpu().numpy().T.astype(np.float64)
+    ulp = np.abs(ref).clip(min=2.0 ** -14) * 2.0 ** -10
+    assert np.all(np.abs(got - ref) <= ulp + 1e-12)
+    x = synth.activations(300, k, seed=1)
+    y = ops.exl3_gemm_recon(torch.from_numpy(x).cuda(), t, s, v, K, cb == 2, cb == 1, fused_rows=1 << 30)
+    yr = orc.linear(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb, y_fp32=True).astype(np.float64)
+    assert np.abs(y.float().cpu().numpy() - yr).max() / np.abs(yr).max() < 2e-3
