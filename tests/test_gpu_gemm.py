@@ -132,7 +132,7 @@ def test_gemm_recon(torch_cuda, orc, branch, K, cb):
 
 
 @pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2), (2.5, 2), (8, 0)])
-def test_reconstruct_t_had(orc, K, cb):
+def test_reconstruct_t_had(orc, K, cb, monkeypatch):
     """W' = W_hat H128 diag(svh) / sqrt(128), transposed: within one fp16 ulp of the fp64 product
     of the oracle's bit-exact W_hat (fp32 butterflies, one rounding), and the recon GEMM's rotated
     branch with the fold against fp64 within 2e-3."""
@@ -151,6 +151,7 @@ def test_reconstruct_t_had(orc, K, cb):
     ulp = np.abs(ref).clip(min=2.0 ** -14) * 2.0 ** -10
     assert np.all(np.abs(got - ref) <= ulp + 1e-12)
     x = synth.activations(300, k, seed=1)
+    monkeypatch.setattr(ops, "RECON_FOLD_SVH", True)         # 300 rows >= k / 4: the folded branch
     y = ops.exl3_gemm_recon(torch.from_numpy(x).cuda(), t, s, v, K, cb == 2, cb == 1, fused_rows=1 << 30)
     yr = orc.linear(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb, y_fp32=True).astype(np.float64)
     assert np.abs(y.float().cpu().numpy() - yr).max() / np.abs(yr).max() < 2e-3
