@@ -61,6 +61,9 @@ int parse_K(float K, int mcg, int mul1, int* bits, int* half, int* cb, const cha
 constexpr int MAX_DEVICES = 16;
 constexpr size_t WS_PARTIAL_BYTES = 64ull << 20;     // split-k fp32 partials
 constexpr size_t WS_COUNTERS = 1u << 20;             // column-chunk completion counters
+// the fused norm's row counter: its own 128-byte line after every other counter range
+constexpr size_t WS_NORM_CTR = WS_COUNTERS;
+constexpr size_t WS_COUNTER_INTS = WS_COUNTERS + 32;
 
 struct DeviceState
 {
@@ -97,12 +100,12 @@ int init_device(int device, DeviceState** out)
             void* p = nullptr;
             void* c = nullptr;
             if (hipMalloc(&p, WS_PARTIAL_BYTES) != hipSuccess) return fail(EXL3_AMD_ENOMEM, "workspace allocation failed");
-            if (hipMalloc(&c, WS_COUNTERS * sizeof(int)) != hipSuccess)
+            if (hipMalloc(&c, WS_COUNTER_INTS * sizeof(int)) != hipSuccess)
             {
                 (void) hipFree(p);
                 return fail(EXL3_AMD_ENOMEM, "counter allocation failed");
             }
-            if (hipMemset(c, 0, WS_COUNTERS * sizeof(int)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            if (hipMemset(c, 0, WS_COUNTER_INTS * sizeof(int)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
                 return fail(EXL3_AMD_EHIP, "counter initialisation failed");
             void* f = nullptr;
             if (hipMalloc(&f, MGEMM_MAX_FILTER * (sizeof(int64_t) + sizeof(uint16_t))) != hipSuccess)
@@ -163,11 +166,24 @@ int init_device(int device, DeviceState** out)
 // Every entry point that launches comes through here.  The launchers report their launch
 // status with hipGetLastError, so a stale error left by other code in the process is dropped
 // first: it would otherwise be reported as this call's failure.
-int current_device(DeviceState** out)
+// The first call on a device allocates and clears the workspace, which a stream capture cannot
+// record: such a call is refused (no allocation, no synchronisation) and the capture stays
+// intact.  exl3_amd_init(device) before the capture avoids it.
+int current_device(DeviceState** out, void* stream)
 {
     (void) hipGetLastError();
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(EXL3_AMD_EHIP, "hipGetDevice failed");
+    if (dev >= 0 && dev < MAX_DEVICES && !g_dev[dev].ready)
+    {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t) stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+        {
+            (void) hipGetLastError();
+            return fail(EXL3_AMD_EINVAL, "first call on device %d during stream capture: the workspace is allocated "
+                        "on first use; call exl3_amd_init(%d) before capturing", dev, dev);
+        }
+    }
     return init_device(dev, out);
 }
 
@@ -251,36 +267,6 @@ int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, co
     g.xcd = 0;
     if (d->num_xcd > 0 && chunks % d->num_xcd == 0 && pairs * 32 <= WS_COUNTERS / 2)
         g.xcd = d->num_xcd;
-    // M = 1 balanced stream: one wave per SIMD slot at 4 waves per SIMD, equal runs of slices
-    // (exl3_gemv.hip gemv1p_kernel).  Needs the XCD-local hand-off and per-slot tables of at
-    // most 16 slots without indices or routing weights.
-    // Opt-in (EXL3_AMD_GEMV_P1=1) until its GPU run is cleared.
-    bool p1 = g.m == 1 && g.stream_m1 && !g.A_up && !g.norm_h && d->num_xcd > 0 && !g.indices && !g.weights && g.bszm <= 16 &&
-              g.row0 == 0 && g.slab_m <= 1;
-    {
-        const char* e = getenv("EXL3_AMD_GEMV_P1");
-        p1 = p1 && e && atoi(e) != 0;
-    }
-    if (p1)
-    {
-        const int xg = d->num_xcd;
-        const long units = (long) g.bszm * chunks;                       // upper bound (widths <= n)
-        const long slices = units * (g.k / 16);
-        int lmin = 2;
-        if (const char* e = getenv("EXL3_AMD_P1_LMIN")) { int v = atoi(e); if (v > 0) lmin = v; }
-        long waves = (slices + lmin - 1) / lmin;
-        const long max_waves = (long) d->num_cus * 4 * 4;
-        if (const char* e = getenv("EXL3_AMD_P1_WAVES")) { long v = atol(e); if (v > 0) waves = v; }
-        waves = std::min(std::max(waves, (long) 4 * xg), max_waves);
-        const long per_group = (waves / 4 + xg - 1) / xg;
-        // unit counters: [0, units); partial slots: at most waves + 2 units pieces of 128 floats
-        if (units * 32 <= (long) (WS_COUNTERS / 2) && (size_t) (per_group * xg * 4 + 2 * units) * 512 <= WS_PARTIAL_BYTES)
-        {
-            g.xcd = xg;
-            g.stream_m1 = 2;
-            g.p1_blocks = (int) (per_group * xg);
-        }
-    }
     int rc = dispatch_gemv(bits, cb, g, s);
     return rc ? hip_fail(rc, what) : 0;
 }
@@ -379,7 +365,7 @@ int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_p
     if (n_offset % 128 || n_offset < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t: n_offset must be a non-negative multiple of 128");
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, nullptr, (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_t") : 0;
 }
@@ -398,7 +384,7 @@ int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint
     if (n_offset % 128 || n_offset < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t_had: n_offset must be a non-negative multiple of 128");
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, svh + n_offset,
                                   (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_t_had") : 0;
@@ -457,7 +443,7 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     if (force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "exl3_gemm: bad force_shape_idx %d", force_shape_idx);
 
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     hipStream_t s = (hipStream_t) stream;
 
     if ((m <= 8 && force_shape_idx != 2) || force_shape_idx == 1)
@@ -568,7 +554,7 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: m > 8 with routing weights is not implemented in this build");
 
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     hipStream_t s = (hipStream_t) stream;
 
     GemvArgs g;
@@ -659,7 +645,7 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     if (bsz == 0) return 0;
 
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
 
     MoeArgs a;
     memset(&a, 0, sizeof(a));
@@ -771,7 +757,7 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     if (num_ptrs != num_experts) return fail(EXL3_AMD_EINVAL, "Number of gate tensors doesn't match num_experts");
 
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     if (concurrency * 8 > d->num_cus) return fail(EXL3_AMD_EINVAL, "Concurrency too high for device num_sms");
     if (m_tile > 16)
     {
@@ -900,7 +886,7 @@ int exl3_amd_moe_gather(float* output_state, int tokens, int hidden_dim,
     const int topk = num_assign / tokens;
     if (topk > 32) return fail(EXL3_AMD_EINVAL, "exl3_moe_gather: top-k too large");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     MoesGatherArgs g;
     g.out = output_state; g.scratch = output_scratch; g.flat_expert = flat_expert; g.inv_order = inv_order;
     g.expert_start = expert_start; g.slot_base = slot_base; g.slot_kind = slot_kind; g.weight_sorted = weight_sorted;
@@ -923,7 +909,7 @@ int exl3_amd_rms_norm_res(const uint16_t* x, const uint16_t* r, const uint16_t* 
         return fail(EXL3_AMD_EINVAL, "rms_norm_res: tensors must be 8-byte aligned");
     if (rows > 0x7fffffff) return fail(EXL3_AMD_EINVAL, "rms_norm_res: too many rows");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     int rc = exl3k_rms_norm_res(x, r, w, y, n, (long) rows, dim, eps, (hipStream_t) stream);
     return rc ? hip_fail(rc, "rms_norm_res") : 0;
 }
@@ -934,7 +920,7 @@ int exl3_amd_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64
     if (numel <= 0) return 0;
     if (!g || !u || !out) return fail(EXL3_AMD_EINVAL, "silu_mul: null pointer");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     int rc = exl3k_silu_mul(g, u, out, (long) numel, (hipStream_t) stream);
     return rc ? hip_fail(rc, "silu_mul") : 0;
 }
@@ -955,7 +941,7 @@ int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* a
     if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be positive");
     if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     hipStream_t s = (hipStream_t) stream;
     if (m == 1)
     {
@@ -989,7 +975,7 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
     if (((uintptr_t) C | (uintptr_t) h | (uintptr_t) w | (uintptr_t) r) & 15)
         return fail(EXL3_AMD_EINVAL, "exl3_gemm_norm: C, h, w and r must be 16-byte aligned");
     DeviceState* d;
-    if (int rc = current_device(&d)) return rc;
+    if (int rc = current_device(&d, stream)) return rc;
     hipStream_t s = (hipStream_t) stream;
     if (m == 1)
     {
@@ -1002,7 +988,7 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
         {
             g.A_up = up;
             g.norm_h = h; g.norm_w = w; g.norm_r = r; g.norm_eps = eps;
-            g.norm_ctr = d->counters + WS_COUNTERS - 32;
+            g.norm_ctr = d->counters + WS_NORM_CTR;
             int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm_norm");
             return rc ? rc : EXL3_AMD_TAG_GEMV;
         }

@@ -242,8 +242,17 @@ __device__ __forceinline__ uint32_t load_l2_u32(const void* p)
 }
 
 // All threads: release this workgroup's stores, count it in *ctr; true in the last arrival of
-// `total` (which then re-arms the counter).  Workgroup scope suffices: every workgroup that
-// counts in one counter runs on the same XCD and meets in its L2, where global atomics execute.
+// `total` (which then re-arms the counter).
+//
+// Hardware assumption (outside the HIP memory model, which calls this a race between
+// workgroups): every workgroup that counts in one counter runs on the same XCD, so its
+// partial stores, the workgroup-scope atomic and the last arrival's L1-bypassing loads all
+// meet in that XCD's L2, where gfx950 executes global atomics.  The host enables this mode
+// only after exl3_device.hip's dispatch probe has shown, on this device, that workgroups b and
+// b + xcd land on one XCD (round-robin dispatch); otherwise, and with EXL3_AMD_XCD=0, the
+// partials are summed by the separate gemv_finish kernel.  Agent-scope atomics would not need
+// the assumption but write back through the whole-device coherence point: 2.5-11 us per
+// launch measured on MI355X.
 __device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag)
 {
     // the workgroup-scope release waits for LDS only: wait for this thread's global stores to be
@@ -962,317 +971,6 @@ void gemv1_kernel(const GemvArgs g)
     GEMV_STAMP(g, 3, flag);
 }
 
-// ---------------------------------------------------------------------------------------------
-// M = 1 balanced stream (no indices, no routing weights).  The launch is sized to the chip
-// (gridDim.x workgroups of 4 waves, a multiple of the XCD count), so every SIMD gets the same
-// number of k-slices instead of whole workgroups of unequal count per CU.
-//
-// Work list.  A unit is one 128-column output chunk of one slot (slot-major, each slot's width
-// from its table).  Units are dealt to XCD groups round-robin (unit u to group u % xcd, where
-// workgroups b and b + xcd share an XCD); a group's units form one list of k-slices,
-// unit-major, and its waves take equal consecutive runs of L slices.  A run crosses at most a
-// few unit boundaries; each (wave, unit) overlap is a piece.  The waves of one unit hand off
-// through that unit's counter in the XCD's L2: each piece stores its fp32 partial to slot p of
-// the unit (p = wave index minus the unit's first wave), and the last arrival sums the slots in
-// order (deterministic), rotates, scales and stores.  A unit held by one wave finishes in place.
-//
-// Stream.  One software pipeline per wave across its whole run: PF slices of trellis words in
-// flight, the input chunk after the current one prefetched, units and chunks switched by
-// scalar bookkeeping between slices.
-// ---------------------------------------------------------------------------------------------
-constexpr int P1_MAX_SLOTS = 16;
-
-struct SlotLds
-{
-    uint64_t trellis, suh, svh, C, A;
-    int n, stride;
-};
-
-// Slot j's pointers and widths from the tables (per-lane loads), exl3_gemm_kernel.cuh:169-238.
-__device__ __forceinline__ void resolve_slot(const GemvArgs& g, int j, SlotLds& s)
-{
-    const size_t elt = g.c_fp32 ? 4 : 2;
-    if (g.B_list)
-    {
-        const int src = g.had_src ? *to_global(g.had_src + j) : j;
-        s.trellis = *to_global(g.B_list + j);
-        s.svh = *to_global(g.svh_list + j);
-        s.suh = *to_global(g.suh_list + src);
-        s.n = g.size_n ? *to_global(g.size_n + j) : g.n;
-        s.stride = g.n_stride ? *to_global(g.n_stride + j) : s.n;
-        s.C = g.c_list ? *to_global(g.c_list + j) : (uint64_t) ((char*) g.C + (size_t) j * g.n * elt);
-    }
-    else
-    {
-        s.trellis = (uint64_t) g.trellis;
-        s.suh = (uint64_t) g.suh;
-        s.svh = (uint64_t) g.svh;
-        s.n = g.n;
-        s.stride = g.n;
-        s.C = (uint64_t) g.C;
-    }
-    s.A = (uint64_t) (g.A + (g.bszm_in == 1 ? (size_t) 0 : (size_t) j * g.k));
-}
-
-// Position in a group's slice list: unit q (global unit grp + xcd * q), k-slice ks, and the
-// unit's slot j and column chunk c.
-struct P1Pos
-{
-    int q, ks, j, c;
-};
-
-__device__ __forceinline__ int p1_slot_of(const int* uprefix, int bszm, int u)
-{
-    int j = 0;
-    for (int t = 1; t < bszm; ++t) j = uprefix[t] <= u ? t : j;
-    return j;
-}
-
-__device__ __forceinline__ void p1_set_unit(P1Pos& p, const int* uprefix, int bszm, int grp, int xg)
-{
-    const int u = grp + xg * p.q;
-    p.j = __builtin_amdgcn_readfirstlane(p1_slot_of(uprefix, bszm, u));
-    p.c = u - __builtin_amdgcn_readfirstlane(uprefix[p.j]);
-}
-
-__device__ __forceinline__ void p1_advance(P1Pos& p, int steps, int KS, const int* uprefix, int bszm, int grp, int xg)
-{
-    p.ks += steps;
-    if (p.ks >= KS)
-    {
-        p.ks -= KS;
-        p.q += 1;
-        p1_set_unit(p, uprefix, bszm, grp, xg);
-    }
-}
-
-template <int K, int CB>
-__global__ __launch_bounds__(GEMV_THREADS, 4)
-void gemv1p_kernel(const GemvArgs g)
-{
-    __shared__ SlotLds slots[P1_MAX_SLOTS];
-    __shared__ int uprefix[P1_MAX_SLOTS + 1];
-    __shared__ __align__(16) uint32_t xdup[GEMV_WAVES][2][128];
-    __shared__ float red[GEMV_WAVES][128];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
-    const int bszm = g.bszm;
-    if ((int) threadIdx.x < bszm) resolve_slot(g, threadIdx.x, slots[threadIdx.x]);
-    __syncthreads();
-    if (threadIdx.x == 0)
-    {
-        int u = 0;
-        for (int t = 0; t < bszm; ++t) { uprefix[t] = u; u += slots[t].n / 128; }
-        uprefix[bszm] = u;
-    }
-    __syncthreads();
-
-    // this wave's run [s0, s0 + n) of its group's slice list
-    const int KS = g.k / 16;
-    const int xg = g.xcd;
-    const int grp = blockIdx.x % xg;
-    const int Wg = (gridDim.x / xg) * GEMV_WAVES;
-    const int wig = (blockIdx.x / xg) * GEMV_WAVES + wave;
-    const int U = __builtin_amdgcn_readfirstlane(uprefix[bszm]);
-    const int Ug = U > grp ? (U - grp + xg - 1) / xg : 0;
-    const int Tg = Ug * KS;
-    const int Tmax = ((U + xg - 1) / xg) * KS;                     // the largest group's slices
-    const int L = (Tmax + Wg - 1) / Wg;                            // slices per wave (every group)
-    const int s0 = wig * L;
-    const int n = min(s0 + L, Tg) - s0;
-    if (n <= 0) return;
-
-    P1Pos pr = { s0 / KS, s0 % KS, 0, 0 };
-    p1_set_unit(pr, uprefix, bszm, grp, xg);
-
-    // trellis address of the position's slice for this lane
-    auto slice_ptr = [&](const P1Pos& p) -> const uint32_t* {
-        const int st = __builtin_amdgcn_readfirstlane(slots[p.j].stride);
-        const uint64_t tb = __builtin_amdgcn_readfirstlane((uint32_t) slots[p.j].trellis)
-                          | ((uint64_t) __builtin_amdgcn_readfirstlane((uint32_t) (slots[p.j].trellis >> 32)) << 32);
-        return (const uint32_t*) tb + ((size_t) p.ks * (st / 16) + p.c * 8) * (8 * K) + (size_t) lane * K;
-    };
-    auto slot_u64 = [&](uint64_t v) -> uint64_t {
-        return __builtin_amdgcn_readfirstlane((uint32_t) v) | ((uint64_t) __builtin_amdgcn_readfirstlane((uint32_t) (v >> 32)) << 32);
-    };
-    // input chunk of a position: this lane's pair of A and of suh (A again when suh is absent)
-    auto load_x = [&](const P1Pos& p, uint32_t& xv, uint32_t& sv) {
-        const uint32_t* A = (const uint32_t*) slot_u64(slots[p.j].A);
-        const uint64_t su = slot_u64(slots[p.j].suh);
-        const uint32_t* S = su ? (const uint32_t*) su : A;
-        const size_t o = (size_t) (p.ks / 8) * 64 + lane;
-        xv = __builtin_nontemporal_load(to_global(A) + o);
-        sv = __builtin_nontemporal_load(to_global(S) + o);
-    };
-
-    // input chunks: the current one (x0) and the next (x1), both loaded ahead of the weights
-    P1Pos px = pr;                          // start of the next chunk to load
-    uint32_t xv0, sv0, xv1 = 0, sv1 = 0;
-    load_x(px, xv0, sv0);
-    int xpos = 8 - (px.ks & 7);             // run offset of the next chunk start
-    if (xpos < n)
-    {
-        p1_advance(px, 8 - (px.ks & 7), KS, uprefix, bszm, grp, xg);
-        load_x(px, xv1, sv1);
-    }
-
-    constexpr int PF = EXL3_GEMV_PF;
-    const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
-    uint32_t ring[PF][K + 1];
-    P1Pos pl = pr;                          // next slice to load (clamped to the run's last)
-    int lpos = 0;
-    #pragma unroll
-    for (int d = 0; d < PF; ++d)
-    {
-        load_slot<K>(slice_ptr(pl), prev_off, ring[d]);
-        if (lpos < n - 1) { p1_advance(pl, 1, KS, uprefix, bszm, grp, xg); ++lpos; }
-    }
-
-    f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
-    float sx = 0.0f;
-    int buf = 0;
-    const int c0 = (lane >> 3) * 16 + (lane & 7);
-
-    for (int i0 = 0; i0 < n; i0 += PF)
-    {
-        #pragma unroll
-        for (int d = 0; d < PF; ++d)
-        {
-            const int i = i0 + d;
-            if (i >= n) break;
-            if (i == 0 || (pr.ks & 7) == 0)
-            {
-                // rotate the chunk that starts here; queue the one after it
-                const bool has_suh = slot_u64(slots[pr.j].suh) != 0;
-                const uint32_t xr = rotate_pair(xv0, sv0, has_suh, lane);
-                uint32_t* xd = xdup[wave][buf];
-                const f16x2 pp = as_h2(xr);
-                const f16x2 d0 = { pp.x, pp.x }, d1 = { pp.y, pp.y };
-                *(u32x2*) (xd + 2 * lane) = (u32x2) { as_u32(d0), as_u32(d1) };
-                __builtin_amdgcn_wave_barrier();
-                if (CB == 2)
-                {
-                    const int r0 = pr.ks & 7, cnt = min(8 - r0, n - i);
-                    const bool mine = lane >= r0 * 8 && lane < (r0 + cnt) * 8;
-                    sx += wave_sum(mine ? (float) pp.x + (float) pp.y : 0.0f, lane);
-                }
-                xv0 = xv1; sv0 = sv1;
-                xpos += 8;                  // chunks after the first start on multiples of 8
-                if (xpos < n)
-                {
-                    p1_advance(px, 8, KS, uprefix, bszm, grp, xg);
-                    load_x(px, xv1, sv1);
-                }
-                buf ^= 1;
-            }
-            uint32_t wv[K + 1];
-            #pragma unroll
-            for (int w = 0; w <= K; ++w) wv[w] = ring[d][w];
-            load_slot<K>(slice_ptr(pl), prev_off, ring[d]);
-            if (lpos < n - 1) { p1_advance(pl, 1, KS, uprefix, bszm, grp, xg); ++lpos; }
-
-            // per group of 8 windows (rows 2gq, 2gq + 1, 2gq + 8, 2gq + 9): decode, 4 MFMAs
-            const uint32_t* xs = xdup[wave][buf ^ 1] + (pr.ks & 7) * 16;
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            #pragma unroll
-            for (int gq = 0; gq < 4; ++gq)
-            {
-                uint32_t raw[32];
-                if (gq == 0) raw8<K, CB, 0>(wv, raw, a3, b3);
-                else if (gq == 1) raw8<K, CB, 8>(wv, raw, a3, b3);
-                else if (gq == 2) raw8<K, CB, 16>(wv, raw, a3, b3);
-                else raw8<K, CB, 24>(wv, raw, a3, b3);
-                #pragma unroll
-                for (int h = 0; h < 2; ++h)
-                {
-                    const u32x2 xb = *(const u32x2*) (xs + 2 * gq + 8 * h);
-                    const h4 bx = __builtin_bit_cast(h4, xb);
-                    const int w = 8 * gq + 2 * h;
-                    const h4 wa = __builtin_bit_cast(h4, (u32x2) { raw[w], raw[w + 1] });
-                    const h4 wb = __builtin_bit_cast(h4, (u32x2) { raw[w + 4], raw[w + 5] });
-                    accv[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wa, bx, accv[h], 0, 0, 0);
-                    accv[2 + h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wb, bx, accv[2 + h], 0, 0, 0);
-                }
-            }
-
-            const P1Pos pu = pr;            // unit of this slice
-            p1_advance(pr, 1, KS, uprefix, bszm, grp, xg);
-            if (i == n - 1 || pr.ks == 0)
-            {
-                // piece done: unit pu.q, slices [.., pu.ks] of it
-                const int e = lane & 3;
-                auto pick = [&](const f32x4& v) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; };
-                float a0 = pick(accv[0]) + pick(accv[1]);
-                float a1 = pick(accv[2]) + pick(accv[3]);
-                #pragma unroll
-                for (int t = 0; t < 4; ++t) accv[t] = (f32x4) { 0, 0, 0, 0 };
-                if (CB == 2)
-                {
-                    const float kinv = (float) as_h(0x1eee), bias = sx * (float) as_h(0xc931);
-                    a0 = a0 * kinv + bias;
-                    a1 = a1 * kinv + bias;
-                    sx = 0.0f;
-                }
-                const int qs = pu.q * KS;
-                const int i_first = qs / L;
-                const int i_last = min(qs + KS - 1, Tg - 1) / L;
-                const int np = i_last - i_first + 1;
-                const int u = grp + xg * pu.q;
-                const int col = pu.c * 128 + 2 * lane;
-                const uint64_t svh = slot_u64(slots[pu.j].svh);
-                void* C = (void*) slot_u64(slots[pu.j].C);
-                float v0, v1;
-                bool fin = true;
-                if (np == 1)
-                {
-                    red[wave][c0] = a0;
-                    red[wave][c0 + 8] = a1;
-                    __builtin_amdgcn_wave_barrier();
-                    v0 = red[wave][2 * lane];
-                    v1 = red[wave][2 * lane + 1];
-                    __builtin_amdgcn_wave_barrier();
-                }
-                else
-                {
-                    const int pmax = (KS + L - 1) / L + 1;
-                    float* pb = g.partials + (size_t) u * pmax * 128;
-                    float* mine = pb + (size_t) (wig - i_first) * 128;
-                    *to_global_w(mine + c0) = a0;
-                    *to_global_w(mine + c0 + 8) = a1;
-                    // stores acknowledged by the L2 before the counter moves
-                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                    int* ctr = g.counters + (size_t) u * 32;
-                    int prev = 0;
-                    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    prev = __builtin_amdgcn_readfirstlane(prev);
-                    fin = prev == np - 1;
-                    if (fin)
-                    {
-                        if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                        v0 = 0.0f; v1 = 0.0f;
-                        for (int p0 = 0; p0 < np; p0 += 8)
-                        {
-                            f32x2 vv[8];
-                            #pragma unroll
-                            for (int t = 0; t < 8; ++t)
-                                vv[t] = load_l2_f32x2(pb + (size_t) min(p0 + t, np - 1) * 128 + 2 * lane);
-                            #pragma unroll
-                            for (int t = 0; t < 8; ++t)
-                                if (p0 + t < np) { v0 += vv[t].x; v1 += vv[t].y; }
-                        }
-                    }
-                }
-                if (fin)
-                {
-                    const uint32_t svp = svh ? *to_global((const uint32_t*) svh + col / 2) : 0u;
-                    store_output(v0, v1, C, g.c_fp32, svh != 0, svp, (size_t) col, lane, EXL3_HAD_RSCALE);
-                }
-            }
-        }
-    }
-}
-
 template <typename KernelLaunch>
 int launch_common(const GemvArgs& g, hipStream_t s, KernelLaunch main)
 {
@@ -1322,12 +1020,6 @@ int launch_gemv1(const GemvArgs& g, hipStream_t s)
 template <int K, int CB>
 int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 {
-    if constexpr (!khalf(K))
-        if (g.m == 1 && g.stream_m1 == 2)
-        {
-            hipLaunchKernelGGL((gemv1p_kernel<K, CB>), dim3(g.p1_blocks), dim3(GEMV_THREADS), 0, s, g);
-            return (int) hipGetLastError();
-        }
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
     if (g.A_up) return -1;             // the fused SwiGLU input exists in the M = 1 stream kernel only
     if (g.m == 1) return launch_gemv_t<K, CB, 1>(g, s);

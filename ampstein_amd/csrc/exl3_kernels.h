@@ -42,8 +42,7 @@ struct GemvArgs
     int slab_m;                 // rows per A / C slab (0: m); a launch may cover rows [row0, row0 + m)
     int row0;
     // work split (host planner)
-    int stream_m1;              // 2: M = 1 balanced stream, 1: M = 1 streaming kernel, 0: LDS kernel
-    int p1_blocks;              // balanced stream: workgroups (a multiple of xcd)
+    int stream_m1;              // 1: M = 1 streaming kernel, 0: LDS kernel
     int slices_per_block;       // SB: k-slices (16 rows x 128 columns) per workgroup, divides k/16
     int slots;                  // split partials per column chunk: k/16 / SB
     int xs_chunks;              // rotated 128-row input chunks held in LDS (LDS kernel)

@@ -27,11 +27,12 @@ from ._lib import check
 Tensor = torch.Tensor
 
 # Row count from which exl3_gemm_recon reconstructs the weight in the original basis (one fused
-# W, y = x @ W) instead of rotating x and y around W_hat.  The reference switches at 2048 rows
-# (amp_torch.cpp:11203-11209, models.uc:36-37); on MI355X the rotated form is faster at every
-# measured size (reconstruct_had is ALU-bound, the activation rotations are HBM-bound and short),
-# so by default it is always taken.  AMP_RECON_FUSED_ROWS=2048 restores the reference's routing.
-RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", str(1 << 30)))
+# W, y = x @ W) instead of rotating x and y around W_hat: 2048, the reference's switch
+# (amp_torch.cpp:11203-11209, models.uc:36-37), so the two branches round where the reference's
+# do.  On MI355X the rotated form is faster at every measured size (reconstruct_had is ALU-bound,
+# the activation rotations are HBM-bound and short): AMP_RECON_FUSED_ROWS=0 never takes the fused
+# branch (the opt-in MI355X routing).
+RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", "2048")) or (1 << 30)
 # Tuned dense GEMM for the recon path (PyTorch TunableOp: hipBLASLt and rocBLAS solutions timed
 # per shape on first use): 8-20 % faster than the default heuristic at M = 2048.
 RECON_TUNED_GEMM = os.environ.get("AMP_RECON_TUNABLE", "1") != "0"

@@ -51,27 +51,45 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the M = 2048 prefill GEMM line")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE expert GEMV line")
-    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-qwen", action="store_true", help="skip the configs[2] Qwen-27B-class line")
+    ap.add_argument("--pmc-child", nargs="?", const="gateup", default=None,
+                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe")
+    ap.add_argument("--summarize-pmc", metavar="PMC_DIR",
+                    help="print per-kernel averages of a rocprofv3 --pmc output directory and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
     return ap.parse_args()
 
 
 # ------------------------------------------------------------------ workload
+def host_trellis(torch, k, n, K, seed):
+    """Seeded host generation (one numpy PCG64 generator per tensor, the scheme of
+    ampstein_amd/synth.py), then one copy to the device, so the CPU and GPU legs can see
+    identical bytes.  Uniform uint16 trellis words, +-1 fp16 suh / svh."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    t = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * K), dtype=np.uint16).view(np.int16)
+    s = np.where(rng.integers(0, 2, k) > 0, 1.0, -1.0).astype(np.float16)
+    v = np.where(rng.integers(0, 2, n) > 0, 1.0, -1.0).astype(np.float16)
+    return torch.from_numpy(t).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(v).cuda()
+
+
+def host_normal(torch, shape, seed):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32).astype(np.float16)).cuda()
+
+
 def make_stack(torch, n_layers, K=4):
-    """Per layer: name -> bundles.Linear with GPU-generated random trellis words and signs."""
+    """Per layer: name -> bundles.Linear with host-generated random trellis words and signs
+    (seed = 1000 * config + 7 * layer + linear)."""
     from ampstein_amd.synth import LLAMA3_8B_SHAPES
     from ampstein_amd.bundles import Linear
-    g = torch.Generator(device="cuda")
     layers = []
     for li in range(n_layers):
         row = {}
         for si, (name, k, n) in enumerate(LLAMA3_8B_SHAPES):
-            g.manual_seed(2000 + 7 * li + si)
-            t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16,
-                              device="cuda", generator=g)
-            s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
-            v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
+            t, s, v = host_trellis(torch, k, n, K, 2000 + 7 * li + si)
             row[name] = Linear(t, s, v, float(K))
         layers.append(row)
     return layers
@@ -85,8 +103,8 @@ class Sweep:
         from ampstein_amd import bundles, _lib
         self.L = _lib.lib()
         dev = "cuda"
-        self.x = torch.randn((1, 1, 4096), generator=torch.Generator(device=dev).manual_seed(1), device=dev).half()
-        self.x14 = torch.randn((1, 1, 14336), generator=torch.Generator(device=dev).manual_seed(2), device=dev).half()
+        self.x = host_normal(torch, (1, 1, 4096), 2001)
+        self.x14 = host_normal(torch, (1, 1, 14336), 2002)
         self.outs = {nm: torch.empty((1, 1, n), dtype=torch.half, device=dev)
                      for nm, n in (("q", 4096), ("k", 1024), ("v", 1024), ("o", 4096), ("down", 4096))}
         self.gu = torch.empty((2, 1, 14336), dtype=torch.half, device=dev)
@@ -130,6 +148,19 @@ class Sweep:
                 fn(st)
 
 
+class Launches:
+    """A launch sequence: entries of (label, launch(stream_ptr), packed bytes)."""
+
+    def __init__(self, entries):
+        self.entries = entries
+        self.bytes = sum(e[2] for e in entries)
+
+    def run(self, torch, stream):
+        with torch.cuda.stream(stream):
+            for _, fn, _ in self.entries:
+                fn(stream.cuda_stream)
+
+
 def event_times(torch, sweep, reps=3):
     """Per-launch HIP-event durations (ms) on the launch stream; the first pass is dropped."""
     stream = torch.cuda.Stream()
@@ -154,7 +185,7 @@ def dominant_region(torch, layers, reps=3):
     bytes per launch, launches timed)."""
     from ampstein_amd import bundles
     gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
-    x = torch.randn((1, 1, 4096), device="cuda").half()
+    x = host_normal(torch, (1, 1, 4096), 2003)
     bs = [bundles.Multi([row["gate"], row["up"]], gu_out) for row in layers]
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
@@ -216,7 +247,7 @@ def decode_step_bench(torch, layers, steps=20):
     lw = [LayerWeights(q=r["q"], k=r["k"], v=r["v"], o=r["o"], gate=r["gate"], up=r["up"], down=r["down"],
                        input_norm=ones, post_norm=ones) for r in layers]
     nbytes = sum(r[n].trellis.numel() * 2 for r in layers for n in ("q", "k", "v", "o", "gate", "up", "down"))
-    x = torch.randn((1, H), device="cuda").half()
+    x = host_normal(torch, (1, H), 2004)
     res = {}
     for name, fuse, fnorm, launches in (("fused_norm_swiglu", True, True, 4), ("fused_swiglu", True, False, 6),
                                         ("separate_silu_mul", False, False, 7)):
@@ -265,13 +296,9 @@ def prefill_bench(torch):
     from ampstein_amd import ops
     M = 2048
     res = {}
-    g = torch.Generator(device="cuda")
     for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
-        g.manual_seed(4000 + si)
-        t = torch.randint(-32768, 32768, (k // 16, n // 16, 64), dtype=torch.int16, device="cuda", generator=g)
-        s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
-        v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
-        x = torch.randn((M, k), device="cuda", generator=g).half()
+        t, s, v = host_trellis(torch, k, n, 4, 4000 + si)
+        x = host_normal(torch, (M, k), 4010 + si)
         ah = torch.empty_like(x)
         C = torch.empty((M, n), dtype=torch.half, device="cuda")
         flops = 2.0 * M * k * n
@@ -287,15 +314,67 @@ def prefill_bench(torch):
         torch.cuda.empty_cache()
     best = {name: sum(2.0 * M * int(sh.split("x")[0]) * int(sh.split("x")[1]) for sh in res) /
             sum(res[sh][name]["us"] for sh in res) / 1e6 for name in ("recon", "recon_rotated", "fused")}
-    path = max(best, key=best.get)
+    # the credited line is this build's own kernel; the recon paths run their dense GEMM on
+    # hipBLASLt / rocBLAS and are reported beside it as labelled comparisons
     return {"metric": "prefill GEMM TFLOPS at M=2048 (configs[3], 4 bpw 3INST)", "m": M,
-            "value": round(best[path], 1), "unit": "TFLOPS", "path": path,
-            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best[path] / MFMA_F16_PEAK_TFLOPS, 4),
-            "paths_TFLOPS": {k2: round(v2, 1) for k2, v2 in best.items()}, "per_shape": res}
+            "value": round(best["fused"], 1), "unit": "TFLOPS",
+            "path": "fused: exl3_gemm m > 8, hand-written MFMA kernel (gemm_kernel)",
+            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best["fused"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "comparison_paths_TFLOPS": {"recon (reconstruct_had + hipBLASLt, reference routing)": round(best["recon"], 1),
+                                        "recon_rotated (reconstruct_t + hipBLASLt + had128)": round(best["recon_rotated"], 1)},
+            "per_shape": res}
+
+
+# ------------------------------------------------------------------ Qwen-27B-class shapes
+QWEN_SHAPES = ((5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120))
+
+
+def qwen_bench(torch, min_bytes=1 << 30):
+    """the four Qwen-27B-class shapes as one layer, swept over enough distinct layers
+    (>= 1 GB of packed weights, beyond the 256 MB MALL) in one graph, for K in {2, 3, 5, 8} x
+    {3INST, MCG} x M in {1, 4, 8}.  The same random words serve both codebooks.  GB/s = packed
+    bytes of the sweep / graph time; per-shape us from HIP events around single launches."""
+    from ampstein_amd import _lib
+    from ampstein_amd.bundles import Linear
+    res = {}
+    for K in (2, 3, 5, 8):
+        per_layer = sum(k * n * K // 8 for k, n in QWEN_SHAPES)
+        n_layers = max(2, -(-min_bytes // per_layer))
+        layers = [[Linear(*host_trellis(torch, k, n, K, 7000 + 100 * K + 4 * li + si), float(K))
+                   for si, (k, n) in enumerate(QWEN_SHAPES)] for li in range(n_layers)]
+        for cb in (0, 1):
+            for M in (1, 4, 8):
+                xs = {k: host_normal(torch, (M, k), 7500 + k + M) for k in (5120, 17408)}
+                ys = {n: torch.empty((M, n), dtype=torch.half, device="cuda") for n in (5120, 1024, 17408)}
+                hads = {k: torch.empty((M, k), dtype=torch.half, device="cuda") for k in (5120, 17408)}
+                L = _lib.lib()
+
+                def launch(lin, st):
+                    k, n = lin.in_features, lin.out_features
+                    rc = L.exl3_amd_gemm(xs[k].data_ptr(), lin.trellis.data_ptr(), ys[n].data_ptr(), 0,
+                                         lin.suh.data_ptr(), hads[k].data_ptr(), lin.svh.data_ptr(), M, k, n,
+                                         float(K), cb == 1, 0, 0, st)
+                    if rc < 0:
+                        raise RuntimeError(L.exl3_amd_last_error().decode())
+
+                sw = Launches([(f"{lin.in_features}x{lin.out_features}", (lambda st, lin=lin: launch(lin, st)),
+                                 lin.trellis.numel() * 2) for row in layers for lin in row])
+                ms, _ = graph_time(torch, sw, 10, 2)
+                ev = {}
+                for label, nbytes, t_ms in event_times(torch, sw, reps=2):
+                    ev.setdefault(label, []).append(t_ms)
+                res[f"K{K}_{'mcg' if cb else '3inst'}_M{M}"] = {
+                    "sweep_GB_s": round(per_layer * n_layers / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(per_layer * n_layers / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "per_shape_us": {lab: round(sum(v) / len(v) * 1e3, 2) for lab, v in ev.items()}}
+                del xs, ys, hads
+        del layers
+        torch.cuda.empty_cache()
+    return {"metric": "EXL3 GEMV GB/s on Qwen-27B-class shapes (configs[2])", "per_case": res}
 
 
 # ------------------------------------------------------------------ MoE expert GEMV (configs[4])
-def moe_bench(torch, reps=8):
+def moe_bench(torch, reps=8, ms=(1, 8, 16), token_sorted=True, graph=True):
     """256 experts, gate/up 4096->2048, down 2048->4096, K per expert from {2,3,4} (seeded), mul1;
     router logits N(0,1), softmax top-8; M in {1, 8, 16}.  Algorithmic bytes = packed bytes of the
     distinct routed experts.  `reps` different routings rotate through one graph so the routed
@@ -305,24 +384,18 @@ def moe_bench(torch, reps=8):
     E, Hi, I, Ho, topk = 256, 4096, 2048, 4096, 8
     rng = np.random.default_rng(5000)
     Ks = rng.choice([2, 3, 4], E)
-    g = torch.Generator(device="cuda")
     mats = []
     for e in range(E):
         trio = []
         for pi, (k, n) in enumerate(((Hi, I), (Hi, I), (I, Ho))):
-            g.manual_seed(6000 + 3 * e + pi)
-            t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * int(Ks[e])), dtype=torch.int16, device="cuda",
-                              generator=g)
-            s = (torch.randint(0, 2, (k,), device="cuda", generator=g) * 2 - 1).half()
-            v = (torch.randint(0, 2, (n,), device="cuda", generator=g) * 2 - 1).half()
-            trio.append((t, s, v))
+            trio.append(host_trellis(torch, k, n, int(Ks[e]), 6000 + 3 * e + pi))
         mats.append(trio)
     P = lambda vals: torch.tensor(vals, dtype=torch.long, device="cuda")
     tabs = [P([mats[e][pi][j].data_ptr() for e in range(E)]) for pi in range(3) for j in range(3)]
     bits = torch.tensor(Ks, dtype=torch.uint8, device="cuda")
     per_expert = {e: int(Ks[e]) * (2 * Hi * I + I * Ho) // 8 for e in range(E)}
     res = {}
-    for M in (1, 8, 16):
+    for M in ms:
         slots = M * topk
         routs = []
         for r in range(reps):
@@ -333,7 +406,7 @@ def moe_bench(torch, reps=8):
             rw = np.take_along_axis(p, sel, 1).astype(np.float16)
             routs.append((torch.from_numpy(sel.astype(np.int64)).cuda(), torch.from_numpy(rw).cuda(),
                           sum(per_expert[int(e)] for e in set(sel.reshape(-1).tolist()))))
-        x = torch.randn((M, Hi), device="cuda", generator=g).half()
+        x = host_normal(torch, (M, Hi), 5100 + M)
         z = lambda *sh, dt=torch.half: torch.zeros(sh, dtype=dt, device="cuda")
         had_g, had_u, act_out = z(slots, Hi), z(slots, Hi), z(slots, I)
         gu = z(slots, I, dt=torch.float)
@@ -349,17 +422,19 @@ def moe_bench(torch, reps=8):
             for sel, rw, _ in routs:
                 call(sel, rw)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
+        if not graph:
+            continue
+        cg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(cg, stream=stream):
             for sel, rw, _ in routs:
                 call(sel, rw)
-        graph.replay()
+        cg.replay()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(4):
-            graph.replay()
+            cg.replay()
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (4 * reps)
@@ -369,7 +444,7 @@ def moe_bench(torch, reps=8):
     # token-sorted prefill MoE (exl3_moe) on the same experts: T tokens, pool = every assignment
     pre = {}
     conc = ops.exl3_moe_max_concurrency(torch.cuda.current_device())
-    for T in (512, 2048):
+    for T in ((512, 2048) if token_sorted else ()):
         logits = rng.standard_normal((T, E))
         sel = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
         p = np.exp(logits - logits.max(1, keepdims=True))
@@ -381,7 +456,7 @@ def moe_bench(torch, reps=8):
         max_tok = -(-T * topk // conc)
         dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
         cnt, tok, ws = dv(count), dv((order // topk).astype(np.int64)), dv(rw.reshape(-1)[order])
-        x = torch.randn((T, Hi), device="cuda", generator=g).half()
+        x = host_normal(torch, (T, Hi), 5200 + T)
         out = torch.zeros((T, Ho), dtype=torch.float, device="cuda")
         tsg, tsu = (torch.empty((conc, max_tok, Hi), dtype=torch.half, device="cuda") for _ in range(2))
         tig, tiu = (torch.empty((conc, max_tok, I), dtype=torch.half, device="cuda") for _ in range(2))
@@ -460,24 +535,67 @@ def cpu_baseline(seconds: float):
 GEMV_KERNEL = "gemv1_kernel"
 
 
-def pmc_child():
-    """Profiled child: a device copy of known size, then two eager bundled sweeps (4 layers)."""
+def pmc_child(workload="decode"):
+    """Profiled child (rocprofv3 --pmc runs): a device copy of known size (the calibration
+    dispatch), then a short eager run of one workload:
+      decode  -- two passes of the bundled decode sweep over 4 layers (qkv sliced mgemm, o gemm,
+                 gate/up stacked mgemm, down gemm: four GEMV grids);
+      gateup  -- the stacked gate/up mgemm alone, 2 x 4 launches (the traffic passes);
+      prefill -- the MFMA GEMM at 2048 rows on 8192 -> 28672 and 28672 -> 8192;
+      moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice."""
     import torch
-    from ampstein_amd import ops
+    from ampstein_amd import ops, bundles
     torch.cuda.set_device(0)
     ops.init(0)
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    from ampstein_amd import bundles
-    layers = make_stack(torch, 4)
-    gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
-    x = torch.randn((1, 1, 4096), device="cuda").half()
-    for _ in range(2):
-        for row in layers:
-            bundles.Multi([row["gate"], row["up"]], gu_out).run(x)
+    if workload in ("decode", "gateup"):
+        layers = make_stack(torch, 4)
+        if workload == "gateup":
+            gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
+            x = host_normal(torch, (1, 1, 4096), 2005)
+            for _ in range(2):
+                for row in layers:
+                    bundles.Multi([row["gate"], row["up"]], gu_out).run(x)
+        else:
+            sw = Sweep(torch, layers, bundled=True)
+            stream = torch.cuda.Stream()
+            for _ in range(2):
+                sw.run(torch, stream)
+    elif workload == "prefill":
+        for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
+            t, s, v = host_trellis(torch, k, n, 4, 4000 + si)
+            x = host_normal(torch, (2048, k), 4010 + si)
+            C = torch.empty((2048, n), dtype=torch.half, device="cuda")
+            for _ in range(2):
+                ops.exl3_gemm(x, t, C, s, torch.empty_like(x), v)
+    elif workload == "moe":
+        moe_bench(torch, reps=1, ms=(16,), token_sorted=False, graph=False)
     torch.cuda.synchronize()
+    return 0
+
+
+def summarize_pmc(outdir):
+    """Per (kernel, grid) average of every counter per dispatch in a rocprofv3 --pmc output
+    directory (this library's kernels and the calibration copy)."""
+    acc = {}
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"]
+                if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "reconstruct", "had128", "copy", "Copy")):
+                    continue
+                key = (name.split("(")[0][:70], r.get("Grid_Size", ""))
+                d = acc.setdefault(key, {})
+                d.setdefault(r["Counter_Name"], {}).setdefault(r.get("Dispatch_Id", r.get("Correlation_Id")), 0.0)
+                d[r["Counter_Name"]][r.get("Dispatch_Id", r.get("Correlation_Id"))] += float(r["Counter_Value"])
+    for (name, grid), ctrs in sorted(acc.items()):
+        print(f"{name}  grid {grid}")
+        for cname, per_disp in sorted(ctrs.items()):
+            vals = list(per_disp.values())
+            print(f"    {cname:32s} dispatches {len(vals):3d}  avg {sum(vals) / len(vals):16.1f}")
     return 0
 
 
@@ -502,7 +620,7 @@ def measure_traffic(gemv_alg_bytes_per_launch):
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         outdir = tempfile.mkdtemp(prefix=f"exl3_{counter}_", dir="/tmp")
         cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", counter, "--output-format", "csv", "-d", outdir,
-               "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
+               "--", sys.executable, os.path.abspath(__file__), "--pmc-child", "gateup"]
         p = subprocess.run(cmd, capture_output=True, text=True, env=env, cwd="/tmp")
         if p.returncode != 0:
             return {"error": f"rocprofv3 {counter} pass failed (rc {p.returncode})"}
@@ -546,8 +664,10 @@ def main():
     args = parse()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace)
+    if args.summarize_pmc:
+        return summarize_pmc(args.summarize_pmc)
     if args.pmc_child:
-        return pmc_child()
+        return pmc_child(args.pmc_child)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the EXL3 path runs on a single MI355X; a multi-GPU split is design-only in this build)")
@@ -629,6 +749,8 @@ def main():
         out["prefill"] = prefill_bench(torch)
     if not args.no_moe:
         out["moe"] = moe_bench(torch)
+    if not args.no_qwen:
+        out["qwen27b"] = qwen_bench(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
