@@ -192,6 +192,47 @@ int current_device(DeviceState** out, void* stream)
 // budget (rotated input + reduction buffer) and the split-partial workspace.
 int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
 {
+    // Row-batched matrix-core kernel (exl3_gemv.hip gemvm_kernel) for 2..16 rows:
+    // EXL3_AMD_GEMV_MFMA_ROWS=0 keeps the LDS kernel, =2 also takes single rows there.
+    {
+        int mode = 1;
+        if (const char* e = getenv("EXL3_AMD_GEMV_MFMA_ROWS")) mode = atoi(e);
+        const bool use = m <= 16 && (m >= 2 ? mode != 0 : mode >= 2);
+        if (use)
+        {
+            const int KS = k / 16, chunks = n / 128;
+            const int mt = m == 1 ? 1 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16));
+            int per_cu = 4;
+            if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
+            const long target = (long) per_cu * num_cus;
+            // SB: k-tiles per workgroup, a multiple of 8 dividing k/16; the largest whose grid still
+            // reaches the target (else the smallest), within 48 KB of staged input and the workspace
+            int best = -1;
+            for (int d = 8; d <= KS; d += 8)
+            {
+                if (KS % d) continue;
+                if ((size_t) mt * (d * 16 + 4) * 4 > 48 * 1024) break;
+                if ((size_t) (KS / d) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
+                if ((long) bszm * chunks * (KS / d) >= target || best < 0) best = d;
+                if ((long) bszm * chunks * (KS / d) < target) break;
+            }
+            if (const char* e = getenv("EXL3_AMD_GEMV_SB"))
+            {
+                int v = atoi(e);
+                if (v > 0 && v % 8 == 0 && KS % v == 0 && (size_t) mt * (v * 16 + 4) * 4 <= 64 * 1024) best = v;
+            }
+            if (best > 0)
+            {
+                g.stream_m1 = 0;
+                g.mfma_rows = 1;
+                g.slices_per_block = best;
+                g.slots = KS / best;
+                g.xs_chunks = 0;
+                return 0;
+            }
+        }
+    }
+    g.mfma_rows = 0;
     const int mt = m == 1 ? 1 : (m <= 4 ? 4 : 8);
     const int KS = k / 16, chunks = n / 128;
     int per_cu = 4;

@@ -971,6 +971,178 @@ void gemv1_kernel(const GemvArgs g)
     GEMV_STAMP(g, 3, flag);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Row-batched GEMV on the matrix cores (m = 1..16 rows per launch; the decode path uses it for
+// m >= 2).  v_mfma_f32_16x16x32_f16 with
+//   A (16 x 32): 16 output columns x 16 k-rows of the weight, each weight as its two fp16
+//                halves (lo, hi) -- the 3INST / MCG word before the fp16 add, or MUL1's
+//                (1024 + byte sum, 0);
+//   B (32 x 16): the rotated input rows as duplicated pairs (x, x), activation row = B column;
+//   D (16 x 16): 16 output columns x 16 activation rows, fp32.
+// So the dot product of a decoded weight against every row costs the same matrix-core issue,
+// whatever m is: the work per weight is the decode, as at m = 1.
+//
+// Lane mapping.  A unit of work is 2 column tiles x 4 k-tiles (8 tiles, 256 K bytes).  Lane l
+// decodes tile (k-tile 4u + l / 16, column tile l % 16 / 8) of the wave's column pair as the
+// M = 1 kernels do (lane j = l % 8 of its tile: columns j, j + 8, all 16 rows).  MFMA operand
+// A's lane l must hold output column l % 16 and k-block l / 16: exactly this lane's column j
+// (or j + 8) of its own k-tile.  The 8 MFMAs of a unit are (row group gq, column half c):
+// A = the lane's decoded words 8 gq + 4 c .. + 3 (rows 2 gq, 2 gq + 1, 2 gq + 8, 2 gq + 9 of
+// column j + 8 c), B = the input at those rows of the lane's k-tile, read as one 16-byte LDS
+// load from the input staged in that row order (xperm).
+//
+// Workgroup: one 128-column chunk (4 waves = 4 column pairs) over SB k-tiles (SB % 8 == 0, so
+// the input rotation covers whole 128-row chunks); split-k partials and their hand-off are the
+// LDS kernel's (block_epilogue).
+// ---------------------------------------------------------------------------------------------
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+// position of row rho (0..15) of a 16-row group in the staged input
+__device__ __forceinline__ constexpr int xperm(int rho) { return 4 * ((rho & 7) >> 1) + (rho & 1) + 2 * (rho >> 3); }
+
+template <int K>
+__device__ __forceinline__ void load_tile_lane(const uint32_t* __restrict__ tile, int j, int prev_off, uint32_t* w)
+{
+    if constexpr (khalf(K)) load_frame_half<K>(tile, j, w);
+    else load_slot<K>(tile + j * K, prev_off, w);
+}
+
+template <int K, int CB, int MT>
+__global__ __launch_bounds__(GEMV_THREADS)
+void gemvm_kernel(const GemvArgs g)
+{
+    extern __shared__ uint32_t smem[];
+    __shared__ int flag;
+    __shared__ float sumx[MT];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);       // 3INST multiplier, addend
+    const int m = g.m, k = g.k;
+    const int KS = k / 16;
+    const int SB = g.slices_per_block;                    // k-tiles per workgroup, multiple of 8
+    const int splits = KS / SB;
+    const int j = blockIdx.y;
+    int chunk, slot;
+    block_coords(g, splits, chunk, slot);
+    MatView v;
+    if (!resolve(g, j, v)) { inactive_arrive(g, chunk, slot, &flag); return; }
+    if (chunk * 128 >= v.n) return;
+    const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
+    const int ks0 = slot * SB;
+    const int xs_stride = SB * 16 + 4;                    // u32 per row; +4: rows 16 bytes apart in the banks
+    uint32_t* xs = smem;                                  // [MT][xs_stride] dup pairs, xperm order
+    float* res = (float*) (smem + MT * xs_stride);        // [MT][128]
+    float* tmp = res + MT * 128;                          // epilogue scratch: 2 x (m x 64 column pairs), >= 512
+
+    // this lane's tile: k-tile ks0 + lane / 16 (+ 4 per unit), column tile 2 wave + lane % 16 / 8
+    const int tiles_n = v.stride / 16;
+    constexpr int KB = kbits(K);
+    const int jt = lane & 7;
+    const uint32_t* tile0 = (const uint32_t*) v.trellis
+                          + ((size_t) (ks0 + (lane >> 4)) * tiles_n + chunk * 8 + 2 * wave + ((lane >> 3) & 1)) * tile_words(K);
+    const size_t ustride = (size_t) 4 * tiles_n * tile_words(K);
+    const int nunits = SB / 4;
+    const int prev_off = jt == 0 ? 8 * K - 1 : -1;
+    constexpr int PF = EXL3_GEMV_PF;
+    uint32_t ring[PF][KB + 1];
+    #pragma unroll
+    for (int d = 0; d < PF; ++d) load_tile_lane<K>(tile0 + (size_t) min(d, nunits - 1) * ustride, jt, prev_off, ring[d]);
+
+    // input rotation of the workgroup's SB / 8 chunks, every row, into xs (dup pairs, xperm order)
+    {
+        const int nkc = SB / 8;
+        for (int job = wave; job < m * nkc; job += GEMV_WAVES)
+        {
+            const int row = job / nkc, c = job % nkc;
+            const int col = ks0 * 16 + c * 128 + 2 * lane;
+            f16x2 xv = as_h2(*to_global((const uint32_t*) (v.A + (size_t) row * k + col)));
+            f16x2 o;
+            if (v.suh)
+            {
+                xv = xv * as_h2(*to_global((const uint32_t*) (v.suh + col)));
+                float v0 = (float) xv.x, v1 = (float) xv.y;
+                fwht128_wave(v0, v1, lane);
+                o.x = (f16) (v0 * EXL3_HAD_RSCALE);
+                o.y = (f16) (v1 * EXL3_HAD_RSCALE);
+            }
+            else o = xv;
+            const int e = 2 * lane;                       // even row of its 16-group: xperm(e+1) = xperm(e) + 1
+            const int pos = c * 128 + (e & ~15) + xperm(e & 15);
+            f16x2 d0 = { o.x, o.x }, d1 = { o.y, o.y };
+            *(u32x2*) (xs + row * xs_stride + pos) = (u32x2) { as_u32(d0), as_u32(d1) };
+        }
+    }
+    __syncthreads();
+
+    const int nrow = min(lane & 15, m - 1);               // B column = activation row (clamped)
+    const uint32_t* xb = xs + nrow * xs_stride + (lane >> 4) * 16;
+    f32x4 acc[2] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
+    for (int u0 = 0; u0 < nunits; u0 += PF)
+    {
+        #pragma unroll
+        for (int d = 0; d < PF; ++d)
+        {
+            const int u = u0 + d;
+            if (u >= nunits) break;
+            uint32_t wv[KB + 1];
+            #pragma unroll
+            for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+            uint32_t raw[32];
+            raw32<K, CB>(wv, raw, a3, b3);
+            load_tile_lane<K>(tile0 + (size_t) min(u + PF, nunits - 1) * ustride, jt, prev_off, ring[d]);
+            #pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+            {
+                const u32x4 bx = *(const u32x4*) (xb + u * 64 + 4 * gq);
+                const f16x8v b = __builtin_bit_cast(f16x8v, bx);
+                #pragma unroll
+                for (int c = 0; c < 2; ++c)
+                {
+                    const u32x4 aw = { raw[8 * gq + 4 * c], raw[8 * gq + 4 * c + 1], raw[8 * gq + 4 * c + 2], raw[8 * gq + 4 * c + 3] };
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, aw), b, acc[c], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // D[i][n]: lane holds output columns i = 4 (lane / 16) + e of the wave's half c, row n = lane % 16
+    const int n = lane & 15;
+    if (n < m)
+    {
+        #pragma unroll
+        for (int c = 0; c < 2; ++c)
+        {
+            const float dv[4] = { acc[c].x, acc[c].y, acc[c].z, acc[c].w };
+            #pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const int i = 4 * (lane >> 4) + e;
+                res[n * 128 + 32 * wave + 16 * (i >> 3) + (i & 7) + 8 * c] = dv[e];
+            }
+        }
+    }
+    if (CB == 2)
+    {
+        // MUL1 bias term: sum of the rotated input over this workgroup's k range, per row
+        for (int r = wave; r < m; r += GEMV_WAVES)
+        {
+            float sv = 0.0f;
+            for (int e = lane; e < SB * 16; e += 64) sv += (float) as_h2(xs[r * xs_stride + e]).x;
+            sv = wave_sum(sv, lane);
+            if (lane == 0) sumx[r] = sv;
+        }
+    }
+    __syncthreads();
+    if (CB == 2)
+    {
+        const float kinv = (float) as_h(0x1eee);
+        for (int e = threadIdx.x; e < m * 128; e += GEMV_THREADS)
+            res[e] = res[e] * kinv + sumx[e / 128] * (float) as_h(0xc931);
+        __syncthreads();
+    }
+    block_epilogue(g, v, j, chunk, slot, splits, res, tmp, &flag, svp);
+}
+
 template <typename KernelLaunch>
 int launch_common(const GemvArgs& g, hipStream_t s, KernelLaunch main)
 {
@@ -1017,11 +1189,27 @@ int launch_gemv1(const GemvArgs& g, hipStream_t s)
     });
 }
 
+template <int K, int CB, int MT>
+int launch_gemvm_t(const GemvArgs& g, hipStream_t s)
+{
+    const size_t lds = ((size_t) MT * (g.slices_per_block * 16 + 4) + (size_t) MT * 128 + (MT * 128 > 512 ? MT * 128 : 512)) * 4;
+    return launch_common(g, s, [&](dim3 grid) {
+        hipLaunchKernelGGL((gemvm_kernel<K, CB, MT>), grid, dim3(GEMV_THREADS), lds, s, g);
+    });
+}
+
 template <int K, int CB>
 int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 {
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
     if (g.A_up) return -1;             // the fused SwiGLU input exists in the M = 1 stream kernel only
+    if (g.mfma_rows)
+    {
+        if (g.m == 1) return launch_gemvm_t<K, CB, 1>(g, s);
+        if (g.m <= 4) return launch_gemvm_t<K, CB, 4>(g, s);
+        if (g.m <= 8) return launch_gemvm_t<K, CB, 8>(g, s);
+        return launch_gemvm_t<K, CB, 16>(g, s);
+    }
     if (g.m == 1) return launch_gemv_t<K, CB, 1>(g, s);
     if (g.m <= 4) return launch_gemv_t<K, CB, 4>(g, s);
     return launch_gemv_t<K, CB, 8>(g, s);

@@ -43,6 +43,7 @@ struct GemvArgs
     int row0;
     // work split (host planner)
     int stream_m1;              // 1: M = 1 streaming kernel, 0: LDS kernel
+    int mfma_rows;              // 1: row-batched matrix-core kernel (gemvm_kernel, m <= 16)
     int slices_per_block;       // SB: k-slices (16 rows x 128 columns) per workgroup, divides k/16
     int slots;                  // split partials per column chunk: k/16 / SB
     int xs_chunks;              // rotated 128-row input chunks held in LDS (LDS kernel)
