@@ -158,7 +158,8 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
     }
 }
 
-// Swizzled LDS offsets (u32 units).  A: row stride 16 u32 (4 chunks of 16 B), chunk ^= (row >> 2) & 3.
+// Swizzled LDS offsets (u32 units).  A: row stride 16 u32 (4 chunks of 16 B), chunk ^= (row >> 2) & 3
+// (gfx950 LDS: 64 banks; the 16 lanes of a ds_read_b128 phase touch 16 distinct 16-byte groups).
 // B: per slice, column stride 8 u32 (2 chunks), chunk ^= (col >> 3) & 1.
 __device__ __forceinline__ int a_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
 __device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ ((col >> 3) & 1)); }
@@ -262,8 +263,10 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     u32x4 apf[PF][2], tpf[PF];
     auto load_stage = [&](int s, u32x4* a, u32x4& tw) {
         const int sc = min(s, NST - 1);
-        a[0] = __builtin_nontemporal_load(a_src[0] + 4 * sc);
-        if constexpr (AJ == 2) a[1] = __builtin_nontemporal_load(a_src[1] + 4 * sc);
+        // the activation tile is re-read by every column block: cached loads (it stays in L2 /
+        // the MALL between blocks); the trellis words are read once per row block: nontemporal
+        a[0] = *(a_src[0] + 4 * sc);
+        if constexpr (AJ == 2) a[1] = *(a_src[1] + 4 * sc);
         tw = __builtin_nontemporal_load((const u32x4*) (t_src + sc * t_stage));
     };
     auto store_stage = [&](int buf, const u32x4* a, const u32x4& tw) {

@@ -41,6 +41,9 @@
 #ifndef EXL3_GEMV_MFMA
 #define EXL3_GEMV_MFMA 1
 #endif
+#ifndef EXL3_GEMV_PRIO
+#define EXL3_GEMV_PRIO 3
+#endif
 #ifndef EXL3_GEMV_PF
 #define EXL3_GEMV_PF (EXL3_INST_K <= 4 ? 4 : 2)
 #endif
@@ -789,6 +792,10 @@ void gemv1_kernel(const GemvArgs g)
     MatView v;
     if (!resolve(g, j, v)) { inactive_arrive(g, chunk, slot, &flag); return; }
     if (chunk * 128 >= v.n) return;
+    // Wave priority: a wave that starts (input load and rotation) or ends (hand-off) outranks
+    // the waves in their decode loops, so that no wave of the SIMD is starved at either end of
+    // its stream while older waves keep the VALU busy
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
 #ifdef EXL3_GEMV_TRACE
     {
         uint32_t hw, xcc;
@@ -820,11 +827,17 @@ void gemv1_kernel(const GemvArgs g)
     constexpr int PF = EXL3_GEMV_PF;
     static_assert(8 % PF == 0, "prefetch depth must divide 8");
     const int last = W - 1;
-    // x of the first chunk first (its wait then leaves the weight loads in flight)
-    uint32_t xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8) * 64);
-    uint32_t sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8) * 64);
+    // x of the first chunk first (its wait then leaves the weight loads in flight).  The input,
+    // suh and up vectors are read by every wave: cached loads, so that they stay in the XCD's
+    // L2 after the first miss (nontemporal loads made every wave's read queue behind the weight
+    // stream in HBM: 3-12 us before the first dot, measured with per-wave timestamps)
+    uint32_t xv = *(to_global(xg) + (size_t) (a / 8) * 64);
+    uint32_t sv = *(to_global(sg) + (size_t) (a / 8) * 64);
     uint32_t uv = 0u;
-    if constexpr (ACT) uv = __builtin_nontemporal_load(to_global(ug) + (size_t) (a / 8) * 64);
+    if constexpr (ACT) uv = *(to_global(ug) + (size_t) (a / 8) * 64);
+    // keep them ahead of the weight loads: loads return in issue order, so an input load the
+    // scheduler moved behind the ring would wait for the ring's slices
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t ring[PF][KB + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_slot_k<K>(base + (size_t) min(d, last) * rstride, prev_off, lane, ring[d]);
@@ -845,6 +858,7 @@ void gemv1_kernel(const GemvArgs g)
     {
         const uint32_t xr = rotate_pair(ACT ? silu_mul_pair(xv, uv) : xv, sv, has_suh, lane);
         if (c == 0) GEMV_STAMP(g, 1, __builtin_amdgcn_readfirstlane(xr));
+        if (c == 0) __builtin_amdgcn_s_setprio(0);
         if (CB == 2)
         {
             const f16x2 p = as_h2(xr);
@@ -862,9 +876,9 @@ void gemv1_kernel(const GemvArgs g)
 #endif
         // prefetch the next chunk's x (clamped: stays inside this wave's range)
         const int cn = min(c + 1, nchunks - 1);
-        xv = __builtin_nontemporal_load(to_global(xg) + (size_t) (a / 8 + cn) * 64);
-        sv = __builtin_nontemporal_load(to_global(sg) + (size_t) (a / 8 + cn) * 64);
-        if constexpr (ACT) uv = __builtin_nontemporal_load(to_global(ug) + (size_t) (a / 8 + cn) * 64);
+        xv = *(to_global(xg) + (size_t) (a / 8 + cn) * 64);
+        sv = *(to_global(sg) + (size_t) (a / 8 + cn) * 64);
+        if constexpr (ACT) uv = *(to_global(ug) + (size_t) (a / 8 + cn) * 64);
         #pragma unroll
         for (int s8 = 0; s8 < per; ++s8)
         {
@@ -873,8 +887,10 @@ void gemv1_kernel(const GemvArgs g)
             uint32_t wv[KB + 1];
             #pragma unroll
             for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+#if !EXL3_GEMV_MFMA
             uint32_t raw[32];
             raw32<K, CB>(wv, raw, a3, b3);
+#endif
             // refill with slice i + PF; past the last slice it reads the 8 KiB sink, which every
             // wave's tail reads and nothing writes (L2-resident: no HBM traffic, and the hand-off's
             // wait for the partial stores does not wait on HBM).  Unconditional, so the wait
@@ -884,9 +900,16 @@ void gemv1_kernel(const GemvArgs g)
             // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
             const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            // decode per group of 8 windows, right before its 4 MFMAs: 8 live words instead of 32
+            // (the registers that keep the kernel at 4 waves per SIMD)
             #pragma unroll
             for (int gq = 0; gq < 4; ++gq)
             {
+                uint32_t raw[32];
+                if (gq == 0) raw8<K, CB, 0>(wv, raw, a3, b3);
+                else if (gq == 1) raw8<K, CB, 8>(wv, raw, a3, b3);
+                else if (gq == 2) raw8<K, CB, 16>(wv, raw, a3, b3);
+                else raw8<K, CB, 24>(wv, raw, a3, b3);
                 #pragma unroll
                 for (int h = 0; h < 2; ++h)
                 {
@@ -931,6 +954,7 @@ void gemv1_kernel(const GemvArgs g)
 #endif
 
     GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(acc0 + acc1)));
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
     const int c0 = (lane >> 3) * 16 + (lane & 7);
     red[wave][c0] = acc0;
     red[wave][c0 + 8] = acc1;

@@ -587,7 +587,7 @@ def summarize_pmc(outdir):
                 name = r["Kernel_Name"]
                 if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "reconstruct", "had128", "copy", "Copy")):
                     continue
-                key = (name.split("(")[0][:70], r.get("Grid_Size", ""))
+                key = (name.replace("(anonymous namespace)::", "").split("(")[0][:80], r.get("Grid_Size", ""))
                 d = acc.setdefault(key, {})
                 d.setdefault(r["Counter_Name"], {}).setdefault(r.get("Dispatch_Id", r.get("Correlation_Id")), 0.0)
                 d[r["Counter_Name"]][r.get("Dispatch_Id", r.get("Correlation_Id"))] += float(r["Counter_Value"])
