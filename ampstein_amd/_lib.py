@@ -29,6 +29,7 @@ SIGNATURES = {
     "exl3_amd_reconstruct_had": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_had_r_128": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _f32, _vp]),
     "exl3_amd_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
+    "exl3_amd_gemm_noalloc": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
     "exl3_amd_mgemm": (_i32, [_vp, _i32, _i32, _i32,             # A, bszm_in, m, k
                               _vp, _i32,                         # B table, num_B
                               _vp, _i32, _i32, _i32,             # C, bszm_out, n, c_fp32

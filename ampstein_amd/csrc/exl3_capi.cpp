@@ -81,6 +81,52 @@ constexpr int MGEMM_MAX_FILTER = 128;   // exl3_gemm_kernel.cuh:82 (index-compac
 DeviceState g_dev[MAX_DEVICES];
 std::mutex g_mutex;
 
+// ------------------------------------------------------------------ allocation-free scratch
+// exl3_amd_gemm_noalloc's device memory: one file-scope array, present on every GPU the library
+// runs on until the process ends.  Layout: split-k partials | completion counters | prefetch sink.
+// The counters and the sink start at zero (static initialisation); every kernel that counts
+// re-arms its counter before it ends, and nothing writes the sink, so both are zero again after
+// each call.  Calls on one GPU share the array: calls that overlap on one GPU race.
+constexpr size_t NOALLOC_PARTIAL_BYTES = 16u << 20;
+constexpr size_t NOALLOC_COUNTER_INTS = 64u << 10;
+constexpr size_t NOALLOC_SINK_BYTES = 8192;
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_PARTIAL_BYTES + NOALLOC_COUNTER_INTS * sizeof(int) + NOALLOC_SINK_BYTES;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+struct NoAllocState
+{
+    bool ready = false;
+    unsigned char* ptr = nullptr;       // this device's copy of scratch (hipGetSymbolAddress)
+    int num_cus = 0;
+};
+NoAllocState g_noalloc[MAX_DEVICES];
+
+// Once per device, with that device current: the device address of its scratch copy.  The
+// array's name in host code is only a host-side handle; kernels receive this address.
+int noalloc_setup(int device)
+{
+    if (device < 0 || device >= MAX_DEVICES) return fail(EXL3_AMD_EINVAL, "device %d out of range", device);
+    NoAllocState& st = g_noalloc[device];
+    if (st.ready) return 0;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (st.ready) return 0;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+    {
+        (void) hipGetLastError();
+        return fail(EXL3_AMD_EHIP, "scratch symbol address on device %d: HIP error %d (%s)", device, (int) e,
+                    hipGetErrorString(e));
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        return fail(EXL3_AMD_EHIP, "device attribute query failed");
+    st.ptr = (unsigned char*) ptr;
+    st.num_cus = cus;
+    st.ready = true;
+    return 0;
+}
+
 int init_device(int device, DeviceState** out)
 {
     if (device < 0 || device >= MAX_DEVICES) return fail(EXL3_AMD_EINVAL, "device %d out of range", device);
@@ -190,7 +236,7 @@ int current_device(DeviceState** out, void* stream)
 // GEMV work split (exl3_gemv.hip): SB slices per workgroup, a divisor of k/16 (so no
 // workgroup straddles two column chunks), sized for ~TARGET workgroups per CU within the LDS
 // budget (rotated input + reduction buffer) and the split-partial workspace.
-int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
+int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t partial_bytes = WS_PARTIAL_BYTES)
 {
     // Row-batched matrix-core kernel (exl3_gemv.hip gemvm_kernel) for 2..16 rows:
     // EXL3_AMD_GEMV_MFMA_ROWS=0 keeps the LDS kernel, =2 also takes single rows there.
@@ -212,7 +258,7 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
             {
                 if (KS % d) continue;
                 if ((size_t) mt * (d * 16 + 4) * 4 > 48 * 1024) break;
-                if ((size_t) (KS / d) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
+                if ((size_t) (KS / d) * bszm * m * n * 4 > partial_bytes && KS / d > 1) continue;
                 if ((long) bszm * chunks * (KS / d) >= target || best < 0) best = d;
                 if ((long) bszm * chunks * (KS / d) < target) break;
             }
@@ -249,7 +295,7 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
     {
         if (!ok_sb(d)) continue;
         if (!stream && d / 8 + 2 > max_chunks) break;
-        if ((size_t) (KS / d) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / d > 1) continue;
+        if ((size_t) (KS / d) * bszm * m * n * 4 > partial_bytes && KS / d > 1) continue;
         if (best < 0 || (long) bszm * chunks * (KS / best) > target) best = d;   // fewest blocks >= target
         if ((long) bszm * chunks * (KS / d) <= target) break;
     }
@@ -262,11 +308,11 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g)
         // while the count exceeds that round (measured: gate/up 26.7 -> 25.8 us at 896)
         while (ok_sb(2 * pref) && (long) bszm * chunks * (KS / pref) > 4L * num_cus) pref *= 2;
         for (int d = pref; d >= 4; d /= 2)
-            if (ok_sb(d) && ((size_t) (KS / d) * bszm * m * n * 4 <= WS_PARTIAL_BYTES || KS / d == 1)) { best = d; break; }
+            if (ok_sb(d) && ((size_t) (KS / d) * bszm * m * n * 4 <= partial_bytes || KS / d == 1)) { best = d; break; }
     }
     if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && ok_sb(v)) best = v; }
     if (best < 0) return -1;
-    if ((size_t) (KS / best) * bszm * m * n * 4 > WS_PARTIAL_BYTES && KS / best > 1) return -1;
+    if ((size_t) (KS / best) * bszm * m * n * 4 > partial_bytes && KS / best > 1) return -1;
     g.stream_m1 = stream;
     g.slices_per_block = best;
     g.slots = KS / best;
@@ -291,23 +337,42 @@ int dispatch_gemv(int bits, int cb, const GemvArgs& g, hipStream_t s);
 uint64_t* g_trace = nullptr;
 #endif
 
+// Device memory the GEMV kernels use beyond inputs and outputs: split-k partials, completion
+// counters (zero between calls: every kernel that counts re-arms its counter), the prefetch sink.
+struct Workspace
+{
+    float* partials;
+    size_t partial_bytes;
+    int* counters;
+    size_t counter_ints;
+    const uint32_t* sink;
+    int num_cus;
+    int num_xcd;
+};
+
+Workspace ws_of(const DeviceState* d)
+{
+    return Workspace { d->partials, WS_PARTIAL_BYTES, d->counters, WS_COUNTERS, d->sink, d->num_cus, d->num_xcd };
+}
+
 // Plan the work split, pick the XCD hand-off when the device and shape allow it, launch.
-int launch_gemv(DeviceState* d, int bits, int cb, GemvArgs& g, hipStream_t s, const char* what)
+int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s, const char* what)
 {
     const int chunks = g.n / 128;
-    if (gemv_plan(g.m, g.k, g.n, g.bszm, d->num_cus, g))
-        return fail(EXL3_AMD_EUNSUPPORTED, "%s: shape exceeds the GEMV workspace", what);
-    g.partials = d->partials;
-    g.counters = d->counters;
-    g.counters_half = (int) (WS_COUNTERS / 2);
-    g.sink = d->sink;
+    if (gemv_plan(g.m, g.k, g.n, g.bszm, w.num_cus, g, w.partial_bytes))
+        return fail(EXL3_AMD_EUNSUPPORTED, "%s: shape exceeds the GEMV workspace (%zu bytes of split partials)", what,
+                    w.partial_bytes);
+    g.partials = w.partials;
+    g.counters = w.counters;
+    g.counters_half = (int) (w.counter_ints / 2);
+    g.sink = w.sink;
 #ifdef EXL3_GEMV_TRACE
     g.trace = g_trace;
 #endif
     const size_t pairs = (size_t) g.bszm * chunks;
     g.xcd = 0;
-    if (d->num_xcd > 0 && chunks % d->num_xcd == 0 && pairs * 32 <= WS_COUNTERS / 2)
-        g.xcd = d->num_xcd;
+    if (w.num_xcd > 0 && chunks % w.num_xcd == 0 && pairs * 32 <= w.counter_ints / 2)
+        g.xcd = w.num_xcd;
     int rc = dispatch_gemv(bits, cb, g, s);
     return rc ? hip_fail(rc, what) : 0;
 }
@@ -362,7 +427,13 @@ int exl3_amd_version(void) { return 100; }
 int exl3_amd_init(int device)
 {
     DeviceState* d;
-    return init_device(device, &d);
+    if (int rc = init_device(device, &d)) return rc;
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return fail(EXL3_AMD_EHIP, "hipGetDevice failed");
+    if (prev != device && hipSetDevice(device) != hipSuccess) return fail(EXL3_AMD_EHIP, "hipSetDevice(%d) failed", device);
+    const int rc = noalloc_setup(device);
+    if (prev != device) (void) hipSetDevice(prev);
+    return rc;
 }
 
 int exl3_amd_device_info(int device, int* num_cus, int* num_xcd)
@@ -465,42 +536,54 @@ int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
     return rc ? hip_fail(rc, "had_r_128") : 0;
 }
 
-int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
-                  const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
-                  int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
-                  void* stream)
+}  // extern "C"
+
+namespace {
+
+// exl3_gemm on a given workspace (the library's per-device one, or the no-alloc scratch).
+// ws == nullptr: the library's, set up on first use.
+int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+              const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+              int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
+              void* stream, const char* name)
 {
-    (void) A_had;
     g_last_error.clear();
     int bits, half, cb;
-    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
-    if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: negative size");
-    if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
-    if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, name)) return rc;
+    if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "%s: negative size", name);
+    if (k % 16) return fail(EXL3_AMD_EINVAL, "%s: k must be a multiple of 16", name);
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "%s: n must be a multiple of 128", name);
     if (m == 0 || n == 0) return EXL3_AMD_TAG_GEMV;
-    if (!A || !trellis || !C) return fail(EXL3_AMD_EINVAL, "exl3_gemm: null pointer");
-    if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be positive");
-    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
-    if (force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "exl3_gemm: bad force_shape_idx %d", force_shape_idx);
+    if (!A || !trellis || !C) return fail(EXL3_AMD_EINVAL, "%s: null pointer", name);
+    if (k == 0) return fail(EXL3_AMD_EINVAL, "%s: k must be positive", name);
+    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "%s: k %% 128 != 0 is not implemented in this build", name);
+    if (force_shape_idx > 2) return fail(EXL3_AMD_EINVAL, "%s: bad force_shape_idx %d", name, force_shape_idx);
 
-    DeviceState* d;
-    if (int rc = current_device(&d, stream)) return rc;
+    Workspace lw;
+    if (!ws)
+    {
+        DeviceState* d;
+        if (int rc = current_device(&d, stream)) return rc;
+        lw = ws_of(d);
+        ws = &lw;
+    }
+    else (void) hipGetLastError();
     hipStream_t s = (hipStream_t) stream;
 
     if ((m <= 8 && force_shape_idx != 2) || force_shape_idx == 1)
     {
-        if (m > 8) return fail(EXL3_AMD_EINVAL, "exl3_gemm: the GEMV kernel takes at most 8 rows");
+        if (m > 8) return fail(EXL3_AMD_EINVAL, "%s: the GEMV kernel takes at most 8 rows", name);
         GemvArgs g = gemv_args_single(A, trellis, C, c_fp32, suh, svh, m, k, n);
-        int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm");
+        int rc = launch_gemv(*ws, bits, cb, g, s, name);
         return rc ? rc : EXL3_AMD_TAG_GEMV;
     }
     // MFMA GEMM: input rotation into the caller's A_had (exl3_gemm_kernel.cuh writes it there
     // too), then the tiled kernel
-    if (suh && !A_had) return fail(EXL3_AMD_EINVAL, "exl3_gemm: must supply A_had with suh");
+    if (suh && !A_had) return fail(EXL3_AMD_EINVAL, "%s: must supply A_had with suh", name);
     if (suh)
     {
         int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
-        if (rc) return hip_fail(rc, "exl3_gemm");
+        if (rc) return hip_fail(rc, name);
     }
     if (half)
     {
@@ -511,7 +594,7 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
         {
             GemvArgs g = gemv_args_single(A + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt, c_fp32,
                                           suh, svh, std::min(8, m - r0), k, n);
-            if (int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm")) return rc;
+            if (int rc = launch_gemv(*ws, bits, cb, g, s, name)) return rc;
         }
         return EXL3_AMD_TAG_GEMV;
     }
@@ -520,7 +603,44 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
     gg.trellis = trellis; gg.C = C; gg.svh = svh;
     gg.m = m; gg.k = k; gg.n = n; gg.c_fp32 = c_fp32 ? 1 : 0;
     int rc = dispatch_gemm(bits, cb, gg, s);
-    return rc ? hip_fail(rc, "exl3_gemm") : EXL3_AMD_TAG_GEMM;
+    return rc ? hip_fail(rc, name) : EXL3_AMD_TAG_GEMM;
+}
+
+}  // namespace
+
+extern "C" {
+
+int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+                  const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                  int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
+                  void* stream)
+{
+    return gemm_impl(nullptr, A, trellis, C, c_fp32, suh, A_had, svh, m, k, n, K, mcg, mul1, force_shape_idx, stream,
+                     "exl3_gemm");
+}
+
+int exl3_amd_gemm_noalloc(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+                          const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                          int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
+                          void* stream)
+{
+    g_last_error.clear();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(EXL3_AMD_EHIP, "hipGetDevice failed");
+    if (int rc = noalloc_setup(dev)) return rc;
+    const NoAllocState& st = g_noalloc[dev];
+    Workspace w;
+    w.partials = (float*) st.ptr;
+    w.partial_bytes = NOALLOC_PARTIAL_BYTES;
+    w.counters = (int*) (st.ptr + NOALLOC_PARTIAL_BYTES);
+    w.counter_ints = NOALLOC_COUNTER_INTS;
+    w.sink = (const uint32_t*) (st.ptr + NOALLOC_PARTIAL_BYTES + NOALLOC_COUNTER_INTS * sizeof(int));
+    w.num_cus = st.num_cus;
+    // the XCD-local hand-off only where exl3_amd_init (or an earlier call of another entry point)
+    // has already verified the dispatch order; otherwise the finish kernel sums the partials
+    w.num_xcd = (dev < MAX_DEVICES && g_dev[dev].ready) ? g_dev[dev].num_xcd : 0;
+    return gemm_impl(&w, A, trellis, C, c_fp32, suh, A_had, svh, m, k, n, K, mcg, mul1, force_shape_idx, stream,
+                     "exl3_gemm_noalloc");
 }
 
 int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
@@ -619,7 +739,7 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         GemvArgs gr = g;
         gr.m = std::min(8, m - r0);
         gr.row0 = r0;
-        if (int rc = launch_gemv(d, bits, cb, gr, s, "exl3_mgemm")) return rc;
+        if (int rc = launch_gemv(ws_of(d), bits, cb, gr, s, "exl3_mgemm")) return rc;
     }
     return EXL3_AMD_TAG_GEMV;
 }
@@ -988,10 +1108,10 @@ int exl3_amd_gemm_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* a
     {
         GemvArgs g = gemv_args_single(gate, trellis, C, c_fp32, suh, svh, m, k, n);
         GemvArgs probe = g;
-        if (!gemv_plan(m, k, n, 1, d->num_cus, probe) && probe.stream_m1 == 1)
+        if (!gemv_plan(m, k, n, 1, d->num_cus, probe, WS_PARTIAL_BYTES) && probe.stream_m1 == 1)
         {
             g.A_up = up;                             // silu(gate) * up formed in the input load
-            int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm_silu_mul");
+            int rc = launch_gemv(ws_of(d), bits, cb, g, s, "exl3_gemm_silu_mul");
             return rc ? rc : EXL3_AMD_TAG_GEMV;
         }
     }
@@ -1022,7 +1142,7 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
     {
         GemvArgs g = gemv_args_single(A, trellis, C, 0, suh, svh, m, k, n);
         GemvArgs probe = g;
-        const bool plan_ok = !gemv_plan(m, k, n, 1, d->num_cus, probe) && probe.stream_m1 == 1;
+        const bool plan_ok = !gemv_plan(m, k, n, 1, d->num_cus, probe, WS_PARTIAL_BYTES) && probe.stream_m1 == 1;
         const int chunks = n / 128;
         const bool handoff = probe.slots == 1 || (d->num_xcd > 0 && chunks % d->num_xcd == 0 && chunks * 32 <= (int) (WS_COUNTERS / 2));
         if (plan_ok && handoff)
@@ -1030,7 +1150,7 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
             g.A_up = up;
             g.norm_h = h; g.norm_w = w; g.norm_r = r; g.norm_eps = eps;
             g.norm_ctr = d->counters + WS_NORM_CTR;
-            int rc = launch_gemv(d, bits, cb, g, s, "exl3_gemm_norm");
+            int rc = launch_gemv(ws_of(d), bits, cb, g, s, "exl3_gemm_norm");
             return rc ? rc : EXL3_AMD_TAG_GEMV;
         }
     }

@@ -101,6 +101,23 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
                   int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
                   void* stream);
 
+/* exl3_amd_gemm without any allocation: the same operation, arguments, kernels and error codes,
+ * but the GEMV's split-k partials, completion counters and prefetch sink live in a file-scope
+ * device array of the library (16 MiB of partials, 256 KiB of counters, 8 KiB sink) instead of
+ * the workspace exl3_amd_gemm allocates on first use.  It calls no hipMalloc / hipFree and no
+ * allocating library routine, so it serves callers that cannot allocate (code under stream
+ * capture, serving loops, harnesses that forbid allocation).  A shape whose split partials
+ * exceed the array returns EXL3_AMD_EUNSUPPORTED with a message.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (concurrent streams) race.  Call
+ * exl3_amd_init(device) first to take the XCD-local hand-off; without it the partials are
+ * summed by a second kernel.
+ * No counterpart in the reference (the reference's exl3_gemm takes its lock buffer from a
+ * per-device context that allocates on first use, quant/exl3_devctx.cu:81-93). */
+int exl3_amd_gemm_noalloc(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
+                          const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                          int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
+                          void* stream);
+
 /* Multi-matrix GEMV over device pointer tables: slot j (0 <= j < max(bszm_in, bszm_out))
  * computes C[j] = had(had(A[j or 0] o suh[q]) @ W_hat[q]) o svh[q] with q = indices[j] (or j;
  * negative = slot skipped).  Tables B, suh, svh hold num_B device addresses (uint64) of
