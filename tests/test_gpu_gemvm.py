@@ -81,3 +81,4 @@ def test_gemvm_mgemm_row_groups(torch_cuda, orc, m):
     got = C.cpu().numpy()
     for q, L in enumerate(layers):
         assert_close(got[q], orc.linear_f64(x, L.trellis, L.suh, L.svh, 3, cb=1), what=f"slot {q}")
+
