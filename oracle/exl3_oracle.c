@@ -437,9 +437,57 @@ static void had128_h16_lane_stages(h16* v)
             }
 }
 
+/* The two-pass Hadamard of one 128 x 128 block, in place in blk (row-major, stride 128), then
+   out[R * out_stride + C] = result * su[R] * sv[C] (reconstruct.cu:290-357). */
+static void had_block_h16(h16* blk, const h16* su, const h16* sv, h16* out, size_t out_stride)
+{
+    const h16 rs = exl3o_h_from_f32(0.08838834764831845f);   /* __float2half2_rn(r_scale) */
+    h16 v[128];
+    /* column pass (reconstruct.cu:290-318): per column, over the 128 rows; fp16 4-point
+       stage, each result times rs, then fp16 lane stages */
+    for (int col = 0; col < 128; ++col)
+    {
+        for (int R = 0; R < 128; ++R) v[R] = blk[R * 128 + col];
+        for (int t = 0; t < 32; ++t)
+        {
+            h16* q = v + 4 * t;
+            h16 s0 = exl3o_hadd(q[0], q[1]), d0 = exl3o_hsub(q[0], q[1]);
+            h16 s1 = exl3o_hadd(q[2], q[3]), d1 = exl3o_hsub(q[2], q[3]);
+            q[0] = exl3o_hmul(exl3o_hadd(s0, s1), rs);
+            q[1] = exl3o_hmul(exl3o_hadd(d0, d1), rs);
+            q[2] = exl3o_hmul(exl3o_hsub(s0, s1), rs);
+            q[3] = exl3o_hmul(exl3o_hsub(d0, d1), rs);
+        }
+        had128_h16_lane_stages(v);
+        for (int R = 0; R < 128; ++R) blk[R * 128 + col] = v[R];
+    }
+    /* row pass fused with the store (reconstruct.cu:331-357): fp32 4-point stage,
+       round to half, times rs in fp16, fp16 lane stages, then * su[row] * sv[col] */
+    for (int R = 0; R < 128; ++R)
+    {
+        h16* row = blk + R * 128;
+        for (int t = 0; t < 32; ++t)
+        {
+            float v0 = half_to_float_bits(row[4 * t + 0]);
+            float v1 = half_to_float_bits(row[4 * t + 1]);
+            float v2 = half_to_float_bits(row[4 * t + 2]);
+            float v3 = half_to_float_bits(row[4 * t + 3]);
+            float s0 = v0 + v1, d0 = v0 - v1, s1 = v2 + v3, d1 = v2 - v3;
+            v[4 * t + 0] = exl3o_hmul(exl3o_h_from_f32(s0 + s1), rs);
+            v[4 * t + 1] = exl3o_hmul(exl3o_h_from_f32(d0 + d1), rs);
+            v[4 * t + 2] = exl3o_hmul(exl3o_h_from_f32(s0 - s1), rs);
+            v[4 * t + 3] = exl3o_hmul(exl3o_h_from_f32(d0 - d1), rs);
+        }
+        had128_h16_lane_stages(v);
+        h16* o = out + (size_t) R * out_stride;
+        for (int i = 0; i < 128; ++i)
+            o[i] = exl3o_hmul(exl3o_hmul(v[i], su[R]), sv[i]);
+    }
+}
+
 struct rh_ctx
 {
-    h16* W; const uint16_t* trellis; const h16* suh; const h16* svh;
+    h16* W; const uint16_t* trellis; const h16* W_hat; const h16* suh; const h16* svh;
     int k, n, n_packed, n_offset, bits, half, cb;
     uint16_t perm[256];
 };
@@ -447,67 +495,35 @@ struct rh_ctx
 static void rh_blocks(void* vctx, int b0, int b1)
 {
     struct rh_ctx* c = (struct rh_ctx*) vctx;
-    const int tu16 = exl3o_tile_u16(c->bits, c->half);
+    const int tu16 = c->W_hat ? 0 : exl3o_tile_u16(c->bits, c->half);
     const int tiles_n = c->n_packed / 16;
     const int nblk = c->n / 128;
-    const h16 rs = exl3o_h_from_f32(0.08838834764831845f);   /* __float2half2_rn(r_scale) */
     h16* blk = (h16*) malloc(128 * 128 * sizeof(h16));
     h16 tile[256];
-    h16 v[128];
     for (int b = b0; b < b1; ++b)
     {
         int kb = b / nblk, nb = b % nblk;
-        /* decode 8x8 tiles into the 128x128 block (rows = k, cols = n) */
-        for (int j = 0; j < 8; ++j)
-            for (int wn = 0; wn < 8; ++wn)
-            {
-                int nt = c->n_offset / 16 + nb * 8 + wn;
-                const uint16_t* tp = c->trellis + ((size_t)(kb * 8 + j) * tiles_n + nt) * tu16;
-                decode_tile(tile, tp, c->bits, c->half, c->cb, c->perm);
-                for (int r = 0; r < 16; ++r)
-                    memcpy(blk + (j * 16 + r) * 128 + wn * 16, tile + r * 16, 32);
-            }
-        /* column pass (reconstruct.cu:290-318): per column, over the 128 rows; fp16 4-point
-           stage, each result times rs, then fp16 lane stages */
-        for (int col = 0; col < 128; ++col)
+        if (c->W_hat)
         {
-            for (int R = 0; R < 128; ++R) v[R] = blk[R * 128 + col];
-            for (int t = 0; t < 32; ++t)
-            {
-                h16* q = v + 4 * t;
-                h16 s0 = exl3o_hadd(q[0], q[1]), d0 = exl3o_hsub(q[0], q[1]);
-                h16 s1 = exl3o_hadd(q[2], q[3]), d1 = exl3o_hsub(q[2], q[3]);
-                q[0] = exl3o_hmul(exl3o_hadd(s0, s1), rs);
-                q[1] = exl3o_hmul(exl3o_hadd(d0, d1), rs);
-                q[2] = exl3o_hmul(exl3o_hsub(s0, s1), rs);
-                q[3] = exl3o_hmul(exl3o_hsub(d0, d1), rs);
-            }
-            had128_h16_lane_stages(v);
-            for (int R = 0; R < 128; ++R) blk[R * 128 + col] = v[R];
+            /* caller-supplied W_hat (k x n, row-major) */
+            for (int R = 0; R < 128; ++R)
+                memcpy(blk + R * 128, c->W_hat + (size_t)(kb * 128 + R) * c->n + nb * 128, 256);
         }
-        /* row pass fused with the store (reconstruct.cu:331-357): fp32 4-point stage,
-           round to half, times rs in fp16, fp16 lane stages, then * suh[row] * svh[col] */
-        for (int R = 0; R < 128; ++R)
+        else
         {
-            h16* row = blk + R * 128;
-            for (int t = 0; t < 32; ++t)
-            {
-                float v0 = half_to_float_bits(row[4 * t + 0]);
-                float v1 = half_to_float_bits(row[4 * t + 1]);
-                float v2 = half_to_float_bits(row[4 * t + 2]);
-                float v3 = half_to_float_bits(row[4 * t + 3]);
-                float s0 = v0 + v1, d0 = v0 - v1, s1 = v2 + v3, d1 = v2 - v3;
-                v[4 * t + 0] = exl3o_hmul(exl3o_h_from_f32(s0 + s1), rs);
-                v[4 * t + 1] = exl3o_hmul(exl3o_h_from_f32(d0 + d1), rs);
-                v[4 * t + 2] = exl3o_hmul(exl3o_h_from_f32(s0 - s1), rs);
-                v[4 * t + 3] = exl3o_hmul(exl3o_h_from_f32(d0 - d1), rs);
-            }
-            had128_h16_lane_stages(v);
-            h16 su = c->suh[kb * 128 + R];
-            h16* out = c->W + (size_t)(kb * 128 + R) * c->n + nb * 128;
-            for (int i = 0; i < 128; ++i)
-                out[i] = exl3o_hmul(exl3o_hmul(v[i], su), c->svh[nb * 128 + i]);
+            /* decode 8x8 tiles into the 128x128 block (rows = k, cols = n) */
+            for (int j = 0; j < 8; ++j)
+                for (int wn = 0; wn < 8; ++wn)
+                {
+                    int nt = c->n_offset / 16 + nb * 8 + wn;
+                    const uint16_t* tp = c->trellis + ((size_t)(kb * 8 + j) * tiles_n + nt) * tu16;
+                    decode_tile(tile, tp, c->bits, c->half, c->cb, c->perm);
+                    for (int r = 0; r < 16; ++r)
+                        memcpy(blk + (j * 16 + r) * 128 + wn * 16, tile + r * 16, 32);
+                }
         }
+        had_block_h16(blk, c->suh + kb * 128, c->svh + nb * 128,
+                      c->W + (size_t)(kb * 128) * c->n + nb * 128, (size_t) c->n);
     }
     free(blk);
 }
@@ -518,8 +534,17 @@ int exl3o_reconstruct_had(h16* W, const uint16_t* trellis, const h16* suh, const
 {
     if (k % 128 || n % 128 || n_offset % 128 || n_offset < 0 || n_offset + n > n_packed) return -1;
     if (bits < 1 || bits > 8 || (half && (bits > 3 || cb != 2)) || cb < 0 || cb > 2) return -1;
-    struct rh_ctx c = { W, trellis, suh, svh, k, n, n_packed, n_offset, bits, half, cb, {0} };
+    struct rh_ctx c = { W, trellis, NULL, suh, svh, k, n, n_packed, n_offset, bits, half, cb, {0} };
     exl3o_tile_perm(c.perm);
+    parallel_for(rh_blocks, &c, (k / 128) * (n / 128), nthreads);
+    return 0;
+}
+
+int exl3o_had_transform(h16* W, const h16* W_hat, const h16* suh, const h16* svh,
+                        int k, int n, int nthreads)
+{
+    if (k % 128 || n % 128 || k <= 0 || n <= 0) return -1;
+    struct rh_ctx c = { W, NULL, W_hat, suh, svh, k, n, n, 0, 0, 0, 0, {0} };
     parallel_for(rh_blocks, &c, (k / 128) * (n / 128), nthreads);
     return 0;
 }

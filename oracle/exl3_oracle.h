@@ -61,6 +61,12 @@ int exl3o_reconstruct_had(h16* W, const uint16_t* trellis, const h16* suh, const
                           int k, int n, int n_packed, int n_offset,
                           int bits, int half, int cb, int nthreads);
 
+/* The transform step of exl3o_reconstruct_had on a caller-supplied fp16 W_hat (k, n),
+ * row-major: the same per-block sequence, without the trellis decode.  It exists so that
+ * tests can feed the rounding sequence inputs whose results have closed forms. */
+int exl3o_had_transform(h16* W, const h16* W_hat, const h16* suh, const h16* svh,
+                        int k, int n, int nthreads);
+
 /* ---- a6/a7: Hadamard-128 (quant/hadamard_inner.cuh:93-281, hadamard.cu:125-210) ----
  * y[r, 128j..] = H128(x[r, 128j..] (*pre)) * scale/sqrt(128) (*post), cols % 128 == 0.
  * pre/post are fp16 vectors of length cols (or NULL).  In place allowed. */

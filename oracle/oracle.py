@@ -53,6 +53,7 @@ def lib():
         L.exl3o_bits_from_K.argtypes = [f32, vp, vp]
         L.exl3o_reconstruct.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]
         L.exl3o_reconstruct_had.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]
+        L.exl3o_had_transform.argtypes = [vp, vp, vp, vp, i32, i32, i32]
         L.exl3o_had128_hf.argtypes = [vp, vp, i32, i32, vp, vp, f32]
         L.exl3o_had128_ff.argtypes = [vp, vp, i32, i32, vp, vp, f32]
         L.exl3o_had128_fh.argtypes = [vp, vp, i32, i32, vp, f32]
@@ -132,6 +133,18 @@ def reconstruct_had(trellis, suh, svh, bits, half=False, cb=0, n=None, n_offset=
                                      n_offset, bits, int(half), cb, _threads(nthreads))
     if rc:
         raise ValueError("reconstruct_had: bad arguments")
+    return W
+
+
+def had_transform(W_hat, suh, svh, nthreads=0):
+    """reconstruct_had's per-block transform on a given fp16 W_hat (k, n)."""
+    W_hat = np.ascontiguousarray(W_hat, np.float16)
+    k, n = W_hat.shape
+    W = np.empty((k, n), np.float16)
+    rc = lib().exl3o_had_transform(_p(W), _p(W_hat), _p(np.ascontiguousarray(suh, np.float16)),
+                                   _p(np.ascontiguousarray(svh, np.float16)), k, n, _threads(nthreads))
+    if rc:
+        raise ValueError("had_transform: bad arguments")
     return W
 
 
