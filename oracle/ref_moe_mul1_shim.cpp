@@ -54,4 +54,43 @@ void ref_hadamard_128_scalar(float* v) { hadamard_128_scalar(v); }
 // moe_mul1.cpp:202-207 (fp32 form of the mul1 value)
 float ref_decode_mul1_scalar(uint16_t s) { return decode_mul1_scalar(s); }
 
+
+// moe_mul1.cpp:2418-2474 (exl3_moe_cpu_make_layer) and :2529-2654 (exl3_moe_cpu_forward_raw):
+// the reference's CPU MoE forward on E mul1 experts.  mats[3 * e + p] for p = gate, up, down
+// (gate entries ignored when !gated); biases may be NULL.  Returns 0, or -1 when the reference
+// rejects the arguments.
+int ref_moe_forward(int E, int H, int I, const int* bits, int gated,
+                    const uint16_t* const* trellis, const uint16_t* const* suh,
+                    const uint16_t* const* svh, const uint16_t* const* bias,
+                    int activation, float limit, const uint16_t* x, const int* sel,
+                    const uint16_t* w, float* out, int rows, int topk)
+{
+    try
+    {
+        auto i16 = torch::TensorOptions().dtype(torch::kInt16);
+        auto f16 = torch::TensorOptions().dtype(torch::kHalf);
+        std::vector<at::Tensor> tr[3], su[3], sv[3], bi[3];
+        for (int e = 0; e < E; ++e)
+            for (int p = 0; p < 3; ++p)
+            {
+                if (p == 0 && !gated) continue;
+                const int k = p == 2 ? I : H, n = p == 2 ? H : I;
+                const int q = 3 * e + p;
+                tr[p].push_back(torch::from_blob((void*) trellis[q], {k / 16, n / 16, 16 * bits[e]}, i16));
+                su[p].push_back(torch::from_blob((void*) suh[q], {k}, f16));
+                sv[p].push_back(torch::from_blob((void*) svh[q], {n}, f16));
+                if (bias) bi[p].push_back(torch::from_blob((void*) bias[q], {n}, f16));
+            }
+        int64_t hd = exl3_moe_cpu_make_layer(tr[0], su[0], sv[0], tr[1], su[1], sv[1], tr[2], su[2],
+                                             sv[2], bi[0], bi[1], bi[2], activation, limit, 0);
+        exl3_moe_cpu_forward_raw(hd, (const at::Half*) x, sel, (const at::Half*) w, out, rows, topk, 1);
+        exl3_moe_cpu_free_layer(hd);
+        return 0;
+    }
+    catch (const std::exception&)
+    {
+        return -1;
+    }
+}
+
 }

@@ -3,6 +3,7 @@ arithmetic on the oracle's bit-exact W_hat, with the kernel's fp16 rounding poin
 / up input, rotated activation).  Also the host statement of the run table and a synthetic expert
 set with its device pointer tables."""
 import numpy as np
+import scipy.special
 from scipy.linalg import hadamard
 
 from ampstein_amd import synth
@@ -20,7 +21,9 @@ def f16(v):
     return np.asarray(v, np.float64).astype(np.float16).astype(np.float64)
 
 
-def act_fn(act, gated, g, u, limit):
+def act_fn(act, gated, g, u, limit, gelu_erf=False):
+    """act_gate of exl3_moe_coop_kernel.cuh:115-129 (GELU as its tanh form, or with gelu_erf the
+    erf form of the reference's CPU forward, cpu/moe_mul1.cpp:2196-2201)."""
     if act == 3:
         if limit != 0.0:
             g = np.minimum(g, limit)
@@ -30,6 +33,8 @@ def act_fn(act, gated, g, u, limit):
         x = np.maximum(0.0, u)
     elif act == 0:
         x = g / (1.0 + np.exp(-g))
+    elif act == 1 and gelu_erf:
+        x = 0.5 * g * (1.0 + scipy.special.erf(g / np.sqrt(2.0)))
     elif act == 1:
         x = 0.5 * g * (1.0 + np.tanh(0.797884560803 * (g + 0.044715 * g ** 3)))
     else:
@@ -38,6 +43,25 @@ def act_fn(act, gated, g, u, limit):
         u = np.clip(u, -limit, limit)
         x = np.minimum(x, limit)
     return x * u
+
+
+def project(xp, W, suh, svh, bias, round16):
+    """One expert projection: had(xp * suh) (rounded to fp16 when round16) @ W_hat, had, * svh,
+    + bias."""
+    hx = had(xp * suh)
+    if round16:
+        hx = f16(hx)
+    y = had(hx @ W) * svh
+    return y + bias if bias is not None else y
+
+
+def expert_out(xp, W, sv, bias, act, gated, limit, round16=True, gelu_erf=False):
+    """gate / up projections, activation, down projection of one expert for one row.
+    W = (Wg, Wu, Wd) W_hat matrices, sv = ((suh, svh) per projection), bias per projection or
+    None.  round16 applies the fp16 rounding points of the fused kernels (rotated inputs)."""
+    uu = project(xp, W[1], *sv[1], bias[1], round16)
+    gg = project(xp, W[0], *sv[0], bias[0], round16) if gated else uu
+    return project(act_fn(act, gated, gg, uu, limit, gelu_erf), W[2], *sv[2], bias[2], round16)
 
 
 class ExpertSet:
@@ -72,20 +96,13 @@ class ExpertSet:
 
     def slot_out(self, x_row, e, act, gated, limit, use_bias=False):
         """One slot's down output (before the routing weight), fp64 with fp16 rounding points."""
-        (g, u, d), (Wg, Wu, Wd) = self.layers[e], self.W[e]
         xp = np.zeros(self.Hi)
         xp[: x_row.shape[0]] = x_row
-        def proj(L, W, bias):
-            hx = f16(had(xp * L.suh.astype(np.float64)))
-            y = had(hx @ W) * L.svh.astype(np.float64)
-            return y + (bias.astype(np.float64) if bias is not None else 0.0)
-        bg, bu, bd = self.bias_np[e] if (use_bias and self.bias_np is not None) else (None, None, None)
-        uu = proj(u, Wu, bu)
-        gg = proj(g, Wg, bg) if gated else uu
-        a = act_fn(act, gated, gg, uu, limit)
-        ad = f16(had(a * d.suh.astype(np.float64)))
-        v = had(ad @ Wd) * d.svh.astype(np.float64)
-        return v + (bd.astype(np.float64) if bd is not None else 0.0)
+        sv = [(L.suh.astype(np.float64), L.svh.astype(np.float64)) for L in self.layers[e]]
+        bias = [None] * 3
+        if use_bias and self.bias_np is not None:
+            bias = [b.astype(np.float64) for b in self.bias_np[e]]
+        return expert_out(xp, self.W[e], sv, bias, act, gated, limit)
 
 
 def active(sel, rw, mn, mx):
