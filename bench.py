@@ -53,9 +53,10 @@ def parse():
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE expert GEMV line")
     ap.add_argument("--no-qwen", action="store_true", help="skip the configs[2] Qwen-27B-class line")
     ap.add_argument("--pmc-child", nargs="?", const="gateup", default=None,
-                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe")
-    ap.add_argument("--summarize-pmc", metavar="PMC_DIR",
-                    help="print per-kernel averages of a rocprofv3 --pmc output directory and exit")
+                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe | moes")
+    ap.add_argument("--summarize-pmc", metavar="PMC_DIR", nargs="+",
+                    help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
+                         "directories (one per counter pass) and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
     return ap.parse_args()
@@ -542,7 +543,8 @@ def pmc_child(workload="decode"):
                  gate/up stacked mgemm, down gemm: four GEMV grids);
       gateup  -- the stacked gate/up mgemm alone, 2 x 4 launches (the traffic passes);
       prefill -- the MFMA GEMM at 2048 rows on 8192 -> 28672 and 28672 -> 8192;
-      moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice."""
+      moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice;
+      moes    -- the token-sorted exl3_moe on the same experts, T = 512 and 2048."""
     import torch
     from ampstein_amd import ops, bundles
     torch.cuda.set_device(0)
@@ -573,29 +575,72 @@ def pmc_child(workload="decode"):
                 ops.exl3_gemm(x, t, C, s, torch.empty_like(x), v)
     elif workload == "moe":
         moe_bench(torch, reps=1, ms=(16,), token_sorted=False, graph=False)
+    elif workload == "moes":
+        moe_bench(torch, reps=1, ms=(), token_sorted=True, graph=False)
     torch.cuda.synchronize()
     return 0
 
 
-def summarize_pmc(outdir):
-    """Per (kernel, grid) average of every counter per dispatch in a rocprofv3 --pmc output
-    directory (this library's kernels and the calibration copy)."""
+# MI355X: 32 shader engines (SQ_BUSY_CYCLES is summed over them), 1024 SIMDs, and a wave64 VALU
+# instruction holds its SIMD for 4 cycles
+N_SE, N_SIMD, VALU_CYCLES = 32, 1024, 4
+
+
+def summarize_pmc(outdirs):
+    """Per (kernel, grid) average of every counter per dispatch over one or more rocprofv3 --pmc
+    output directories (one per counter pass; this library's kernels and the calibration copy),
+    then derived figures:
+      cycles      SQ_BUSY_CYCLES / 32 (per shader engine: the dispatch's busy cycles)
+      valu_busy   4 * SQ_INSTS_VALU / (1024 SIMDs * cycles)
+      mfma_busy   SQ_VALU_MFMA_BUSY_CYCLES / (1024 * cycles)
+      wait_share  SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (share of wave time waiting on a dependency)
+      lds_conflict  SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS
+      fetch/write MiB  FETCH_SIZE and WRITE_SIZE scaled by the copy calibration (the copy of
+                  COPY_BYTES in the same run reads FETCH = COPY_BYTES / 2, WRITE = COPY_BYTES)."""
     acc = {}
-    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
-        with open(path) as f:
-            for r in csv.DictReader(f):
-                name = r["Kernel_Name"]
-                if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "reconstruct", "had128", "copy", "Copy")):
-                    continue
-                key = (name.replace("(anonymous namespace)::", "").split("(")[0][:80], r.get("Grid_Size", ""))
-                d = acc.setdefault(key, {})
-                d.setdefault(r["Counter_Name"], {}).setdefault(r.get("Dispatch_Id", r.get("Correlation_Id")), 0.0)
-                d[r["Counter_Name"]][r.get("Dispatch_Id", r.get("Correlation_Id"))] += float(r["Counter_Value"])
-    for (name, grid), ctrs in sorted(acc.items()):
-        print(f"{name}  grid {grid}")
-        for cname, per_disp in sorted(ctrs.items()):
-            vals = list(per_disp.values())
-            print(f"    {cname:32s} dispatches {len(vals):3d}  avg {sum(vals) / len(vals):16.1f}")
+    for outdir in outdirs:
+        for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    name = r["Kernel_Name"]
+                    if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "reconstruct", "had128", "copy", "Copy")):
+                        continue
+                    key = (name.replace("(anonymous namespace)::", "").split("(")[0][:80], r.get("Grid_Size", ""))
+                    d = acc.setdefault(key, {}).setdefault(r["Counter_Name"], {})
+                    disp = (outdir, r.get("Dispatch_Id", r.get("Correlation_Id")))
+                    d[disp] = d.get(disp, 0.0) + float(r["Counter_Value"])
+    avg = {k: {c: sum(v.values()) / len(v) for c, v in ctrs.items()} for k, ctrs in acc.items()}
+    ndisp = {k: max(len(v) for v in ctrs.values()) for k, ctrs in acc.items()}
+    copies = [(int(g or 0), a) for (n, g), a in avg.items() if "copy" in n.lower()]
+    cal = max(copies)[1] if copies else {}
+    fscale = COPY_BYTES / (cal["FETCH_SIZE"] * 1024.0) if cal.get("FETCH_SIZE") else None
+    wscale = COPY_BYTES / (cal["WRITE_SIZE"] * 1024.0) if cal.get("WRITE_SIZE") else None
+    for (name, grid), a in sorted(avg.items()):
+        if "copy" in name.lower() and a is not cal:
+            continue
+        print(f"{name}  grid {grid}  ({ndisp[(name, grid)]} dispatches)")
+        for cname in sorted(a):
+            print(f"    {cname:32s} avg {a[cname]:16.1f}")
+        out = []
+        cyc = a.get("SQ_BUSY_CYCLES", 0.0) / N_SE
+        if cyc:
+            out.append(f"cycles {cyc:.0f}")
+            if "SQ_INSTS_VALU" in a:
+                out.append(f"valu_busy {VALU_CYCLES * a['SQ_INSTS_VALU'] / (N_SIMD * cyc):.3f}")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in a:
+                out.append(f"mfma_busy {a['SQ_VALU_MFMA_BUSY_CYCLES'] / (N_SIMD * cyc):.3f}")
+        if a.get("SQ_WAVE_CYCLES"):
+            out.append(f"wait_share {a.get('SQ_WAIT_INST_ANY', 0.0) / a['SQ_WAVE_CYCLES']:.3f}")
+        if a.get("SQ_ACTIVE_INST_LDS"):
+            out.append(f"lds_conflict {a.get('SQ_LDS_BANK_CONFLICT', 0.0) / a['SQ_ACTIVE_INST_LDS']:.3f}")
+        if fscale and "FETCH_SIZE" in a:
+            out.append(f"fetch_MiB {a['FETCH_SIZE'] * 1024.0 * fscale / 2**20:.2f}")
+        if wscale and "WRITE_SIZE" in a:
+            out.append(f"write_MiB {a['WRITE_SIZE'] * 1024.0 * wscale / 2**20:.2f}")
+        if out:
+            print("    derived: " + ", ".join(out))
+    if fscale or wscale:
+        print(f"copy calibration: FETCH_SIZE x {fscale}, WRITE_SIZE x {wscale} (copy of {COPY_BYTES} bytes)")
     return 0
 
 
