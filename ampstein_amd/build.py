@@ -50,6 +50,7 @@ def units():
         u.append(("exl3_gemm.hip", f"exl3_gemm_k{k}.o", [f"-DEXL3_INST_K={k}"]))
     for k in (17, 18, 19):       # half rates 1.5 / 2.5 / 3.5 (rate code 16 + b, mul1 only)
         u.append(("exl3_gemv.hip", f"exl3_gemv_k{k}.o", [f"-DEXL3_INST_K={k}"]))
+        u.append(("exl3_gemm.hip", f"exl3_gemm_k{k}.o", [f"-DEXL3_INST_K={k}"]))
     return u
 
 

@@ -389,6 +389,9 @@ int dispatch_gemm(int bits, int cb, const GemmArgs& g, hipStream_t s)
         case 6: return exl3k_gemm_k6(g, cb, s);
         case 7: return exl3k_gemm_k7(g, cb, s);
         case 8: return exl3k_gemm_k8(g, cb, s);
+        case 17: return exl3k_gemm_k17(g, cb, s);
+        case 18: return exl3k_gemm_k18(g, cb, s);
+        case 19: return exl3k_gemm_k19(g, cb, s);
     }
     return -1;
 }
@@ -584,19 +587,6 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     {
         int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
         if (rc) return hip_fail(rc, name);
-    }
-    if (half)
-    {
-        // half rates: the tiled kernel decodes integer rates only; the GEMV takes the rows in
-        // groups of 8 (callers route large row counts to the reconstruct + dense GEMM path)
-        const size_t elt = c_fp32 ? 4 : 2;
-        for (int r0 = 0; r0 < m; r0 += 8)
-        {
-            GemvArgs g = gemv_args_single(A + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt, c_fp32,
-                                          suh, svh, std::min(8, m - r0), k, n);
-            if (int rc = launch_gemv(*ws, bits, cb, g, s, name)) return rc;
-        }
-        return EXL3_AMD_TAG_GEMV;
     }
     GemmArgs gg;
     gg.A_rot = suh ? A_had : A;
@@ -925,14 +915,14 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
         if (!gate_mul1) return fail(EXL3_AMD_EINVAL, "exl3_moe: row tiles above 16 are instantiated for the mul1 codebook only");
         if (max_tokens_per_expert < m_tile) return fail(EXL3_AMD_EINVAL, "exl3_moe: temp buffers hold fewer rows than the tile");
     }
-    // this build's limits: 128-multiples (every row is rotated in 128-chunks), integer rates in
-    // the MFMA tiles, the plan's expert count
+    // this build's limits: 128-multiples (every row is rotated in 128-chunks), the plan's expert count
     if (hidden_dim % 128 || intermediate_dim % 128)
         return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: hidden and intermediate sizes must be multiples of 128");
-    if (K2g % 2 || K2u % 2 || K2d % 2)
-        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: half-integer bitrates are not implemented in the MFMA tiles");
-    if (!bits_g && !(K2g >= 2 && K2g <= 16 && K2u >= 2 && K2u <= 16 && K2d >= 2 && K2d <= 16))
+    // bits_k.cuh:12-27: integer 1..8, or 1.5 / 2.5 / 3.5
+    auto k2_ok = [](int K2) { return (K2 % 2 == 0 && K2 >= 2 && K2 <= 16) || K2 == 3 || K2 == 5 || K2 == 7; };
+    if (!bits_g && !(k2_ok(K2g) && k2_ok(K2u) && k2_ok(K2d)))
         return fail(EXL3_AMD_EINVAL, "exl3_moe: bitrate out of range");
+    auto rate = [](int K2) { return K2 % 2 ? 16 + K2 / 2 : K2 / 2; };     // the kernels' rate code
     if (num_experts > 4096) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: more than 4096 experts");
 
     const int64_t pool64 = (int64_t) concurrency * max_tokens_per_expert;
@@ -948,7 +938,7 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
         if (v == 64 || v == 128 || v == 256) tile_rows = v;
     }
     const int rt_cap = pool / tile_rows + std::min(num_experts, pool) + 1;
-    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 24 * (size_t) rt_cap + 24;
+    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1);
     if (ws_ints * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: pool exceeds the library workspace");
 
     MoesArgs a;
@@ -963,26 +953,29 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     a.u_trellis = up_ptrs_trellis; a.u_suh = up_ptrs_suh; a.u_svh = up_ptrs_svh;
     a.d_trellis = down_ptrs_trellis; a.d_suh = down_ptrs_suh; a.d_svh = down_ptrs_svh;
     a.bits_g = bits_g; a.bits_u = bits_u; a.bits_d = bits_d;
-    a.K_g = K2g / 2; a.K_u = K2u / 2; a.K_d = K2d / 2;
+    a.K_g = rate(K2g); a.K_u = rate(K2u); a.K_d = rate(K2d);
     a.act = act_function; a.gated = act_function != 2;      // MOE_ACT_RELU2_NOGATE skips the gate
     a.act_limit = act_limit;
     int* ws = (int*) d->partials;
     a.rowinfo = ws;
     a.rt = ws + 3 * (size_t) pool;
     a.lists = a.rt + 3 * (size_t) rt_cap;
-    a.counts = a.lists + 24 * (size_t) rt_cap;
+    a.counts = a.lists + 3 * MOES_RATES * (size_t) rt_cap;
     a.rt_cap = rt_cap;
     a.tile_rows = tile_rows;
 
     typedef int (*group_fn)(const GemmGroupArgs&, int, hipStream_t);
-    static const group_fn gfn[8] = { exl3k_gemm_group_k1, exl3k_gemm_group_k2, exl3k_gemm_group_k3, exl3k_gemm_group_k4,
-                                     exl3k_gemm_group_k5, exl3k_gemm_group_k6, exl3k_gemm_group_k7, exl3k_gemm_group_k8 };
+    static const group_fn gfn[MOES_RATES] = {
+        exl3k_gemm_group_k1, exl3k_gemm_group_k2, exl3k_gemm_group_k3, exl3k_gemm_group_k4, exl3k_gemm_group_k5,
+        exl3k_gemm_group_k6, exl3k_gemm_group_k7, exl3k_gemm_group_k8, exl3k_gemm_group_k17, exl3k_gemm_group_k18,
+        exl3k_gemm_group_k19 };
     const int cb = gate_mul1 ? 2 : 1;
     hipStream_t s = (hipStream_t) stream;
     // one grouped launch per (phase, bitrate) that can occur: the list counts sit on the device
     auto gemm_phase = [&](int phase) -> int {
-        for (int K = 1; K <= 8; ++K)
+        for (int slot = 0; slot < MOES_RATES; ++slot)
         {
+            const int K = moes_slot_rate(slot);
             GemmGroupArgs g;
             memset(&g, 0, sizeof(g));
             g.rt = a.rt;
@@ -990,10 +983,10 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
             g.tile_rows = tile_rows;
             int mats = 0;
             auto add = [&](int m, const uint16_t* A, uint16_t* C, const uint64_t* tab, int Km) {
-                if (!bits_g && Km != K) return;
+                if (bits_g ? K > 8 : Km != K) return;          // the tables hold integer widths
                 g.A[mats] = A; g.C[mats] = C; g.tab[mats] = tab;
-                g.list[mats] = a.lists + (size_t) (m * 8 + K - 1) * rt_cap;
-                g.count[mats] = a.counts + m * 8 + K - 1;
+                g.list[mats] = a.lists + (size_t) (m * MOES_RATES + slot) * rt_cap;
+                g.count[mats] = a.counts + m * MOES_RATES + slot;
                 ++mats;
             };
             if (phase == 0)
@@ -1009,7 +1002,7 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
             }
             if (!mats) continue;
             g.mats = mats;
-            if (int rc = gfn[K - 1](g, cb, s)) return rc;
+            if (int rc = gfn[slot](g, cb, s)) return rc;
         }
         return 0;
     };

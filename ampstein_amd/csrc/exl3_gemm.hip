@@ -44,9 +44,24 @@ constexpr int BM = 256;          // rows per workgroup
 constexpr int BN = 256;          // columns per workgroup
 constexpr int PF = 3;            // register prefetch depth, stages (32 k each)
 
+// Rate code K (exl3_common.cuh kbits / khalf): 1..8, or 16 + b for b + 1/2 (mul1).  The window of
+// tile position t ends at ring bit tile_end(t): (t + 1) K for integer rates; for b + 1/2 the
+// positions alternate b and b + 1 bits (exl3_dq.cuh:254-285, cpu/moe_mul1.cpp:78-83).
+template <int K>
+__host__ __device__ constexpr int tile_end(int t)
+{
+    return khalf(K) ? (t >> 1) * (2 * kbits(K) + 1) + ((t & 1) ? 2 * kbits(K) + 1 : kbits(K)) : (t + 1) * K;
+}
+// Offset of position t0 + d's window from position t0's (t0 even: the decode runs start there).
+template <int K>
+__host__ __device__ constexpr int run_rel(int d) { return tile_end<K>(d) - tile_end<K>(0); }
+// Words of a normalised run: the 26 positions t0 .. t0 + 25 plus the 16-bit window of t0.
+template <int K>
+__host__ __device__ constexpr int run_words() { return (run_rel<K>(25) + 16 + 31) / 32; }
+
 template <int K, int RB> struct GemmLds
 {
-    static constexpr int TW = 8 * K + 1;                 // words per staged tile: ring word -1, then 8K
+    static constexpr int TW = tile_words(K) + 1;         // words per staged tile: ring word -1, then the tile
     static constexpr int A_U32 = RB * 16;                // A block: RB rows x 32 fp16
     static constexpr int B_U32 = 2 * BN * 8;             // B block: 2 slices x 256 columns x 16 fp16
     static constexpr int T_U32 = 2 * 16 * TW;            // 2 slices x 16 tiles
@@ -106,7 +121,7 @@ __device__ __forceinline__ uint32_t weight_pair(uint32_t r0, uint32_t r1)
 template <int K, int CB>
 __device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, int sh)
 {
-    constexpr int NW = (25 * K + 16 + 31) / 32;
+    constexpr int NW = run_words<K>();
     uint32_t rw[NW + 1], nw[NW + 1];
     #pragma unroll
     for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
@@ -114,14 +129,14 @@ __device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, int
     for (int i = 0; i < NW; ++i) nw[i] = __builtin_amdgcn_alignbit(rw[i], rw[i + 1], 32 - sh);
     nw[NW] = 0u;
     uint32_t r[8];
-    r[0] = cb_raw<CB>(win16<0 * K>(nw));
-    r[1] = cb_raw<CB>(win16<1 * K>(nw));
-    r[2] = cb_raw<CB>(win16<8 * K>(nw));
-    r[3] = cb_raw<CB>(win16<9 * K>(nw));
-    r[4] = cb_raw<CB>(win16<16 * K>(nw));
-    r[5] = cb_raw<CB>(win16<17 * K>(nw));
-    r[6] = cb_raw<CB>(win16<24 * K>(nw));
-    r[7] = cb_raw<CB>(win16<25 * K>(nw));
+    r[0] = cb_raw<CB>(win16<run_rel<K>(0)>(nw));
+    r[1] = cb_raw<CB>(win16<run_rel<K>(1)>(nw));
+    r[2] = cb_raw<CB>(win16<run_rel<K>(8)>(nw));
+    r[3] = cb_raw<CB>(win16<run_rel<K>(9)>(nw));
+    r[4] = cb_raw<CB>(win16<run_rel<K>(16)>(nw));
+    r[5] = cb_raw<CB>(win16<run_rel<K>(17)>(nw));
+    r[6] = cb_raw<CB>(win16<run_rel<K>(24)>(nw));
+    r[7] = cb_raw<CB>(win16<run_rel<K>(25)>(nw));
     return (u32x4) { weight_pair<CB>(r[0], r[1]), weight_pair<CB>(r[2], r[3]),
                      weight_pair<CB>(r[4], r[5]), weight_pair<CB>(r[6], r[7]) };
 }
@@ -226,31 +241,32 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         a_src[j] = (const u32x4*) (Ain + (size_t) min(mb * RB + row, M - 1) * k + 8 * ch);
     }
     // ---- trellis staging: words 4t..4t+3 of the stage's 2 slices x 16 tiles (t < 64K)
-    const bool tload = t < 64 * K;
+    constexpr int TWD = tile_words(K);                   // u32 per tile
+    const bool tload = t < 8 * TWD;
     int t_lds[4], t_ring = LD::DUMMY + 4;
     const uint32_t* t_src;
     {
         const int wi = 4 * (tload ? t : 0);
-        const int s2 = wi / (128 * K), wj = wi - s2 * (128 * K);
-        const int tile = wj / (8 * K), wk = wj - tile * (8 * K);
+        const int s2 = wi / (16 * TWD), wj = wi - s2 * (16 * TWD);
+        const int tile = wj / TWD, wk = wj - tile * TWD;
         #pragma unroll
         for (int e = 0; e < 4; ++e) t_lds[e] = LD::T0 + (s2 * 16 + tile) * LD::TW + 1 + wk + e;
-        if (wk + 3 == 8 * K - 1) t_ring = LD::T0 + (s2 * 16 + tile) * LD::TW;
+        if (wk + 3 == TWD - 1) t_ring = LD::T0 + (s2 * 16 + tile) * LD::TW;
         if (!tload)
         {
             #pragma unroll
             for (int e = 0; e < 4; ++e) t_lds[e] = LD::DUMMY + e;
         }
         const int gtile = min(nb * 16 + tile, n / 16 - 1);   // columns past n: a valid tile, results dropped
-        t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * (8 * K) + wk;
+        t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * TWD + wk;
     }
-    const size_t t_stage = (size_t) 2 * (n / 16) * (8 * K);    // u32 per stage (two tile rows)
+    const size_t t_stage = (size_t) 2 * (n / 16) * TWD;        // u32 per stage (two tile rows)
 
     // ---- decode assignment: column dc of the block, half dh; both slices of a stage
     const int dc = t & 255, dh = t >> 8;
     const int dtile = dc >> 4, dcc = dc & 15;
     const int dbase = 32 * (dcc & 7) + 4 * (dcc >> 3) + 2 * dh;
-    const int dB0 = (dbase + 1) * K - 16;                // first window's first bit (< 0: ring)
+    const int dB0 = tile_end<K>(dbase) - 16;             // first window's first bit (< 0: ring)
     const int df = dB0 - 1 >= 0 ? (dB0 - 1) / 32 : -1;
     const int dsh = dB0 - 32 * df;                       // 1..32
     const int d_src = LD::T0 + dtile * LD::TW + 1 + df;  // + slice * 16 * TW
@@ -331,7 +347,7 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
                     av[mt] = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off((RB / 2) * wm + 32 * mt + l32, 2 * sl + lh)));
                 // the decode of this slice of B(s + 1), cut into 8 pieces that ride in the shadow
                 // of the 8 MFMAs (each 32 cycles on the matrix pipe); sched_barrier keeps the cuts
-                constexpr int NW = (25 * K + 16 + 31) / 32;
+                constexpr int NW = run_words<K>();
                 const uint32_t* tl = lds + nxt * LD::T_U32 + d_src + sl * 16 * LD::TW;
                 uint32_t rw[NW + 1], nw[NW + 1], r[8], wp[4];
                 #pragma unroll
@@ -346,20 +362,20 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
                 for (int i = 0; i < NW; ++i) nw[i] = __builtin_amdgcn_alignbit(rw[i], rw[i + 1], 32 - dsh);
                 nw[NW] = 0u;
                 EXL3_MFMA_STEP(0, 1)
-                r[0] = cb_raw<CB>(win16<0 * K>(nw));
-                r[1] = cb_raw<CB>(win16<1 * K>(nw));
+                r[0] = cb_raw<CB>(win16<run_rel<K>(0)>(nw));
+                r[1] = cb_raw<CB>(win16<run_rel<K>(1)>(nw));
                 EXL3_MFMA_STEP(1, 0)
-                r[2] = cb_raw<CB>(win16<8 * K>(nw));
-                r[3] = cb_raw<CB>(win16<9 * K>(nw));
+                r[2] = cb_raw<CB>(win16<run_rel<K>(8)>(nw));
+                r[3] = cb_raw<CB>(win16<run_rel<K>(9)>(nw));
                 EXL3_MFMA_STEP(1, 1)
                 wp[0] = weight_pair<CB>(r[0], r[1]);
                 wp[1] = weight_pair<CB>(r[2], r[3]);
                 EXL3_MFMA_STEP(2, 0)
-                r[4] = cb_raw<CB>(win16<16 * K>(nw));
-                r[5] = cb_raw<CB>(win16<17 * K>(nw));
+                r[4] = cb_raw<CB>(win16<run_rel<K>(16)>(nw));
+                r[5] = cb_raw<CB>(win16<run_rel<K>(17)>(nw));
                 EXL3_MFMA_STEP(2, 1)
-                r[6] = cb_raw<CB>(win16<24 * K>(nw));
-                r[7] = cb_raw<CB>(win16<25 * K>(nw));
+                r[6] = cb_raw<CB>(win16<run_rel<K>(24)>(nw));
+                r[7] = cb_raw<CB>(win16<run_rel<K>(25)>(nw));
                 EXL3_MFMA_STEP(3, 0)
                 wp[2] = weight_pair<CB>(r[4], r[5]);
                 wp[3] = weight_pair<CB>(r[6], r[7]);
@@ -448,6 +464,9 @@ int launch_gemm_group(const GemmGroupArgs& g, hipStream_t s)
 
 int EXL3_CAT(exl3k_gemm_k, EXL3_INST_K)(const GemmArgs& g, int cb, hipStream_t s)
 {
+#if EXL3_INST_K >= 16
+    return cb == 2 ? launch_gemm<EXL3_INST_K, 2>(g, s) : -1;       // half rates: mul1 only
+#endif
     switch (cb)
     {
         case 0: return launch_gemm<EXL3_INST_K, 0>(g, s);
@@ -460,6 +479,9 @@ int EXL3_CAT(exl3k_gemm_k, EXL3_INST_K)(const GemmArgs& g, int cb, hipStream_t s
 int EXL3_CAT(exl3k_gemm_group_k, EXL3_INST_K)(const GemmGroupArgs& g, int cb, hipStream_t s)
 {
     // the token-sorted MoE takes the mcg and mul1 codebooks only (exl3_moe.cu:242)
+#if EXL3_INST_K >= 16
+    return cb == 2 ? launch_gemm_group<EXL3_INST_K, 2>(g, s) : -1;
+#endif
     switch (cb)
     {
         case 1: return launch_gemm_group<EXL3_INST_K, 1>(g, s);

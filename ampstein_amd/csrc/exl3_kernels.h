@@ -74,6 +74,9 @@ int exl3k_gemm_k5(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k6(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k7(const GemmArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_k8(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k17(const GemmArgs& g, int cb, hipStream_t s);   // half rates 1.5 / 2.5 / 3.5: mul1
+int exl3k_gemm_k18(const GemmArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_k19(const GemmArgs& g, int cb, hipStream_t s);
 
 // Grouped GEMM of the token-sorted MoE: one launch runs every row tile of one bitrate.  A row
 // tile is (expert, first row, rows <= 256) of the compacted row pool; workgroup b runs column
@@ -101,9 +104,17 @@ int exl3k_gemm_group_k5(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k6(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k7(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k8(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k17(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k18(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_gemm_group_k19(const GemmGroupArgs& g, int cb, hipStream_t s);
 
 // Token-sorted MoE (exl3_moe_sorted.hip).  Pool rows are the caller's temp buffers; the plan
 // tables live in the library workspace.
+// Rate slots of the token-sorted MoE's per (matrix, bitrate) lists: K 1..8, then 1.5 / 2.5 / 3.5.
+constexpr int MOES_RATES = 11;
+__host__ __device__ constexpr int moes_rate_slot(int K) { return K >= 1 && K <= 8 ? K - 1 : (K >= 17 && K <= 19 ? K - 9 : -1); }
+__host__ __device__ constexpr int moes_slot_rate(int slot) { return slot < 8 ? slot + 1 : slot + 9; }
+
 struct MoesArgs
 {
     const uint16_t* x;          // (bsz, H) fp16
@@ -120,13 +131,13 @@ struct MoesArgs
     uint16_t *ti_g, *ti_u;      // (pool_rows, I) fp16
     const uint64_t *g_trellis, *g_suh, *g_svh, *u_trellis, *u_suh, *u_svh, *d_trellis, *d_suh, *d_svh;
     const uint8_t *bits_g, *bits_u, *bits_d;
-    int K_g, K_u, K_d;          // integer bitrates when there are no tables
+    int K_g, K_u, K_d;          // rate codes when there are no tables (1..8, 16 + b for b + 1/2)
     int act, gated;
     float act_limit;
     int* rowinfo;               // workspace: (sorted position or -1, expert, row within expert) per pool row
     int* rt;                    // workspace: row tiles (expert, first pool row, rows)
-    int* lists;                 // workspace: 3 x 8 lists of row-tile ids, rt_cap each
-    int* counts;                // workspace: 3 x 8 list lengths
+    int* lists;                 // workspace: 3 x MOES_RATES lists of row-tile ids, rt_cap each
+    int* counts;                // workspace: 3 x MOES_RATES list lengths
     int rt_cap;
     int tile_rows;              // rows per row tile (64, 128 or 256)
 };

@@ -139,9 +139,9 @@ __global__ __launch_bounds__(PLAN_THREADS)
 void moes_plan_kernel(MoesArgs a, int pass_row0)
 {
     __shared__ int s_start[PLAN_EMAX], s_cst[PLAN_EMAX], s_nt[PLAN_EMAX], s_tmp[PLAN_THREADS];
-    __shared__ int s_lc[3 * 8];
+    __shared__ int s_lc[3 * MOES_RATES];
     const int t = threadIdx.x, E = a.num_experts;
-    if (t < 24) s_lc[t] = 0;
+    if (t < 3 * MOES_RATES) s_lc[t] = 0;
     for (int e = t; e < E; e += PLAN_THREADS)
     {
         const int64_t c64 = a.expert_count[e];
@@ -195,15 +195,16 @@ void moes_plan_kernel(MoesArgs a, int pass_row0)
             #pragma unroll
             for (int m = 0; m < 3; ++m)
             {
-                if (kb[m] < 1 || kb[m] > 8) continue;      // no instance: the reference's switch runs no case
-                const int l = m * 8 + kb[m] - 1;
+                const int slot = moes_rate_slot(kb[m]);
+                if (slot < 0) continue;                    // no instance: the reference's switch runs no case
+                const int l = m * MOES_RATES + slot;
                 const int pos = atomicAdd(&s_lc[l], 1);
                 a.lists[(size_t) l * a.rt_cap + pos] = tid;
             }
         }
     }
     __syncthreads();
-    if (t < 24) a.counts[t] = s_lc[t];
+    if (t < 3 * MOES_RATES) a.counts[t] = s_lc[t];
     // pool row -> (sorted position, expert, row within the expert); -1 past the pass's rows
     for (int r = t; r < a.pool_rows; r += PLAN_THREADS)
     {

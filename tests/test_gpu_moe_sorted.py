@@ -130,6 +130,10 @@ CASES = [
     ("mul1-k4-relu2-limit", 6, 384, 256, 30, 2, 2, [4] * 6, 2, 4.0, 64, 1, 0, 1 << 30, 0),
     ("mcg-k2-range", 8, 256, 256, 64, 2, 1, [2] * 8, 0, 6.0, 20, 2, 12, 18, 0),
     ("mul1-k5-many-rows", 2, 256, 256, 300, 2, 2, [5, 5], 0, 0.0, 320, 2, 0, 1 << 30, 0),
+    # half rates (mul1): the MFMA tiles' 1.5 / 2.5 / 3.5 decode, 64- and 256-row tiles
+    ("mul1-k1.5-silu", 8, 256, 256, 48, 2, 2, [1.5] * 8, 0, 0.0, 64, 2, 0, 1 << 30, 0),
+    ("mul1-k2.5-gelu", 8, 256, 384, 48, 3, 2, [2.5] * 8, 1, 0.0, 64, 2, 0, 1 << 30, 2),
+    ("mul1-k3.5-many-rows", 2, 256, 256, 300, 2, 2, [3.5, 3.5], 0, 0.0, 320, 2, 0, 1 << 30, 0),
 ]
 
 
