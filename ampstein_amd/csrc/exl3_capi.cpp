@@ -233,16 +233,21 @@ int current_device(DeviceState** out, void* stream)
     return init_device(dev, out);
 }
 
+// Row-batched matrix-core GEMV (exl3_gemv.hip gemvm_kernel) for 2..16 rows:
+// EXL3_AMD_GEMV_MFMA_ROWS=0 keeps the LDS kernel (up to 8 rows), =2 also takes single rows there.
+int gemv_mfma_mode()
+{
+    const char* e = getenv("EXL3_AMD_GEMV_MFMA_ROWS");
+    return e ? atoi(e) : 1;
+}
+
 // GEMV work split (exl3_gemv.hip): SB slices per workgroup, a divisor of k/16 (so no
 // workgroup straddles two column chunks), sized for ~TARGET workgroups per CU within the LDS
 // budget (rotated input + reduction buffer) and the split-partial workspace.
 int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t partial_bytes = WS_PARTIAL_BYTES)
 {
-    // Row-batched matrix-core kernel (exl3_gemv.hip gemvm_kernel) for 2..16 rows:
-    // EXL3_AMD_GEMV_MFMA_ROWS=0 keeps the LDS kernel, =2 also takes single rows there.
     {
-        int mode = 1;
-        if (const char* e = getenv("EXL3_AMD_GEMV_MFMA_ROWS")) mode = atoi(e);
+        const int mode = gemv_mfma_mode();
         const bool use = m <= 16 && (m >= 2 ? mode != 0 : mode >= 2);
         if (use)
         {
@@ -701,8 +706,6 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
     if (m == 0 || n == 0 || bszm == 0) return EXL3_AMD_TAG_GEMV;
     if (k == 0) return fail(EXL3_AMD_EINVAL, "exl3_mgemm: k must be positive");
     if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: k %% 128 != 0 is not implemented in this build");
-    if (m > 8 && weights)
-        return fail(EXL3_AMD_EUNSUPPORTED, "exl3_mgemm: m > 8 with routing weights is not implemented in this build");
 
     DeviceState* d;
     if (int rc = current_device(&d, stream)) return rc;
@@ -722,12 +725,14 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         g.indices = d->filt_idx;
         if (weights) g.weights = d->filt_w;
     }
-    // more than 8 rows: the GEMV in row groups of 8 (slab strides stay those of all m rows)
+    // more than 8 rows: the GEMV in row groups (slab strides stay those of all m rows): 16 rows
+    // per group on the row-batched matrix-core kernel, 8 on the LDS kernel
     g.slab_m = m;
-    for (int r0 = 0; r0 < m; r0 += 8)
+    const int group = gemv_mfma_mode() != 0 ? 16 : 8;
+    for (int r0 = 0; r0 < m; r0 += group)
     {
         GemvArgs gr = g;
-        gr.m = std::min(8, m - r0);
+        gr.m = std::min(group, m - r0);
         gr.row0 = r0;
         if (int rc = launch_gemv(ws_of(d), bits, cb, gr, s, "exl3_mgemm")) return rc;
     }

@@ -283,12 +283,13 @@ __device__ void weighted_reduce(const GemvArgs& g, int chunk, bool via_l2)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int stride = g.bszm / g.num_tokens;
-    const size_t slab = (size_t) g.m * g.n;
+    // slabs hold all rows of the call; this launch owns rows [row0, row0 + m) of each
+    const size_t slab = (size_t) (g.slab_m ? g.slab_m : g.m) * g.n;
     for (int t = 0; t < g.num_tokens; ++t)
     {
         for (int r = wave; r < g.m; r += GEMV_WAVES)
         {
-            const size_t e = (size_t) r * g.n + chunk * 128 + 2 * lane;
+            const size_t e = (size_t) (g.row0 + r) * g.n + chunk * 128 + 2 * lane;
             if (g.c_fp32)
             {
                 float* C = (float*) g.C;

@@ -142,7 +142,6 @@ def test_mgemm_rejects_bad_arguments():
         (dict(tokens=0), "num_tokens"),
         (dict(w=1, idx=1, num_idx=2, tokens=3), "token groups"),
         (dict(K=f(2.5), mul1=0), "mul1"),
-        (dict(m=9, w=1, idx=1, num_idx=2), "routing weights"),
     ]
     for kw, text in cases:
         rc, msg = call_err(L.exl3_amd_mgemm, *mgemm_args(**kw))

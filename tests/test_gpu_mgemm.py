@@ -200,6 +200,29 @@ def test_mgemm_weighted_tokens(torch_cuda, orc, n, y_fp32, bszm_in):
         assert rel_err(got[t], ref[t]) < TOL, t
 
 
+@pytest.mark.parametrize("m", [12, 20])
+@pytest.mark.parametrize("num_tokens", [1, 2])
+@pytest.mark.parametrize("y_fp32", [False, True])
+def test_mgemm_weighted_many_rows(torch_cuda, orc, m, num_tokens, y_fp32):
+    """Weighted reduction with more than 8 rows per slot: the rows run in groups (16 on the
+    matrix-core GEMV) and each group reduces its own rows of every slot."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    bd = Bundle(torch, 256, [1024] * 6, 3, 2, seed=140)
+    xs = synth.activations(4 * m, 256, seed=14).reshape(4, m, 256)
+    sel = [4, 1, -1, 5]
+    w = np.array([0.75, 0.25, 0.5, 0.625], np.float16)
+    C = torch.full((4, m, 1024), 3.0, dtype=torch.float if y_fp32 else torch.half, device="cuda")
+    A_had = torch.empty((4, m, 256), dtype=torch.half, device="cuda")
+    idx = torch.tensor([sel], dtype=torch.long, device="cuda")
+    wt = torch.from_numpy(w[None]).cuda()
+    ops.exl3_mgemm(cuda_x(torch, xs), bd.B, C, bd.suh, A_had, bd.svh, idx, wt, 3, mul1=1, num_tokens=num_tokens)
+    got = C.cpu().numpy()
+    ref = weighted_ref(bd, orc, [xs[j] for j in range(4)], sel, w.astype(np.float64), num_tokens, y_fp32)
+    for t in range(num_tokens):
+        assert rel_err(got[t], ref[t]) < TOL, t
+
+
 @pytest.mark.parametrize("num_tokens", [1, 2])
 def test_mgemm_range_filter(torch_cuda, orc, num_tokens):
     """Expert-range filtering: selections outside [2, 6) dropped, kept ones rebased (the local
