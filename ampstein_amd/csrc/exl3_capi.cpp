@@ -936,14 +936,22 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     // little padding (the weights are decoded once per tile).  Measured on MI355X, 256 experts
     // 4096 -> 2048 -> 4096, top-8: best tile 64 up to a mean of 32 rows, 128 at 64, 256 at 128
     const int mean_rows = num_assign / std::max(num_experts, 1);
-    int tile_rows = mean_rows <= 40 ? 64 : (mean_rows <= 96 ? 128 : 256);
+    // GEMM kernel: the register-decode moeg_kernel (default) or the LDS-tiled gemm_kernel
+    // (EXL3_AMD_MOE_GEMM=lds).  moeg rows per tile: one tile per expert for most experts
+    const char* gsel = getenv("EXL3_AMD_MOE_GEMM");
+    const bool reg_gemm = !(gsel && !strcmp(gsel, "lds"));
+    int tile_rows = reg_gemm ? (mean_rows <= 20 ? 32 : (mean_rows <= 80 ? 64 : 128))
+                             : (mean_rows <= 40 ? 64 : (mean_rows <= 96 ? 128 : 256));
     if (const char* e = getenv("EXL3_AMD_MOE_TILE_ROWS"))
     {
         const int v = atoi(e);
-        if (v == 64 || v == 128 || v == 256) tile_rows = v;
+        if (reg_gemm ? (v == 32 || v == 64 || v == 128) : (v == 64 || v == 128 || v == 256)) tile_rows = v;
     }
+    int grid_wgs = d->num_cus * 4;
+    if (const char* e = getenv("EXL3_AMD_MOEG_WGS")) { const int v = atoi(e); if (v > 0) grid_wgs = v; }
     const int rt_cap = pool / tile_rows + std::min(num_experts, pool) + 1;
-    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1);
+    const size_t ps_floats = (size_t) pool * (2 * (hidden_dim / 128) + intermediate_dim / 128);
+    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1) + ps_floats;
     if (ws_ints * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: pool exceeds the library workspace");
 
     MoesArgs a;
@@ -966,14 +974,21 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     a.rt = ws + 3 * (size_t) pool;
     a.lists = a.rt + 3 * (size_t) rt_cap;
     a.counts = a.lists + 3 * MOES_RATES * (size_t) rt_cap;
+    a.ps_g = (float*) (a.counts + 3 * MOES_RATES);
+    a.ps_u = a.ps_g + (size_t) pool * (hidden_dim / 128);
+    a.ps_d = a.ps_u + (size_t) pool * (hidden_dim / 128);
     a.rt_cap = rt_cap;
     a.tile_rows = tile_rows;
 
     typedef int (*group_fn)(const GemmGroupArgs&, int, hipStream_t);
-    static const group_fn gfn[MOES_RATES] = {
+    static const group_fn gfn_lds[MOES_RATES] = {
         exl3k_gemm_group_k1, exl3k_gemm_group_k2, exl3k_gemm_group_k3, exl3k_gemm_group_k4, exl3k_gemm_group_k5,
         exl3k_gemm_group_k6, exl3k_gemm_group_k7, exl3k_gemm_group_k8, exl3k_gemm_group_k17, exl3k_gemm_group_k18,
         exl3k_gemm_group_k19 };
+    static const group_fn gfn_reg[MOES_RATES] = {
+        exl3k_moeg_k1, exl3k_moeg_k2, exl3k_moeg_k3, exl3k_moeg_k4, exl3k_moeg_k5, exl3k_moeg_k6, exl3k_moeg_k7,
+        exl3k_moeg_k8, exl3k_moeg_k17, exl3k_moeg_k18, exl3k_moeg_k19 };
+    const group_fn* gfn = reg_gemm ? gfn_reg : gfn_lds;
     const int cb = gate_mul1 ? 2 : 1;
     hipStream_t s = (hipStream_t) stream;
     // one grouped launch per (phase, bitrate) that can occur: the list counts sit on the device
@@ -986,23 +1001,24 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
             g.rt = a.rt;
             g.nrt = rt_cap;
             g.tile_rows = tile_rows;
+            g.grid_wgs = grid_wgs;
             int mats = 0;
-            auto add = [&](int m, const uint16_t* A, uint16_t* C, const uint64_t* tab, int Km) {
+            auto add = [&](int m, const uint16_t* A, uint16_t* C, const uint64_t* tab, int Km, const float* ps) {
                 if (bits_g ? K > 8 : Km != K) return;          // the tables hold integer widths
-                g.A[mats] = A; g.C[mats] = C; g.tab[mats] = tab;
+                g.A[mats] = A; g.C[mats] = C; g.tab[mats] = tab; g.psum[mats] = ps;
                 g.list[mats] = a.lists + (size_t) (m * MOES_RATES + slot) * rt_cap;
                 g.count[mats] = a.counts + m * MOES_RATES + slot;
                 ++mats;
             };
             if (phase == 0)
             {
-                if (a.gated) add(0, a.ts_g, a.ti_g, a.g_trellis, a.K_g);
-                add(1, a.ts_u, a.ti_u, a.u_trellis, a.K_u);
+                if (a.gated) add(0, a.ts_g, a.ti_g, a.g_trellis, a.K_g, a.ps_g);
+                add(1, a.ts_u, a.ti_u, a.u_trellis, a.K_u, a.ps_u);
                 g.k = hidden_dim; g.n = intermediate_dim;
             }
             else
             {
-                add(2, a.ti_g, a.ts_g, a.d_trellis, a.K_d);
+                add(2, a.ti_g, a.ts_g, a.d_trellis, a.K_d, a.ps_d);
                 g.k = intermediate_dim; g.n = hidden_dim;
             }
             if (!mats) continue;

@@ -26,6 +26,7 @@
 #include <cstring>
 
 #include "exl3_common.cuh"
+#include "exl3_gemv_core.cuh"
 #include "exl3_kernels.h"
 
 #ifndef EXL3_INST_K
@@ -457,6 +458,235 @@ int launch_gemm_group(const GemmGroupArgs& g, hipStream_t s)
     return (int) hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Register-decode grouped GEMM of the token-sorted MoE (moeg_kernel).
+//
+// The token-sorted MoE's row tiles hold few rows (T * topk / experts: 16 at T = 512, 64 at
+// T = 2048), so the weight decode, not the matrix pipe, bounds its GEMMs.  Here every weight is
+// decoded once per row tile straight into MFMA operand registers (no LDS round trip and no
+// barrier for the weights), and each decoded fragment feeds one v_mfma_f32_16x16x32_f16 per
+// 16-row group of the tile.
+//
+// Work item = (row tile, matrix, 128-column chunk); a workgroup of 4 waves owns the chunk, wave w
+// the column tiles 2w, 2w+1.  Per unit of 4 k-tiles (64 k) lane l decodes tile (k-tile l/16,
+// column tile 2w + (l%16)/8) at position j = l%8 -- columns j and j+8, all 16 rows -- into 16
+// packed fp16 pairs (pair q: rows 2(q>>2) + 8(q&1) + {0,1}, column half (q>>1)&1).  Operand A
+// (16 columns x 32 k) for column half c and row half h is lane l's rows 8h..8h+7 of its column,
+// pairs {h+2c, 4+h+2c, 8+h+2c, 12+h+2c}, in natural k order; operand B (32 k x 16 rows) is, for
+// lane l, row l%16 of the group at k = 64u + 16(l/16) + 8h .. +7: 16 contiguous bytes in LDS.
+//
+// MUL1 weights enter as h = 1024 + byte sum, the decode's exact fp16 value, and the codebook's
+// affine map is applied to the sums: y = kinv sum(h x) + bias sum(x) (codebook.cuh:78-84), with
+// sum(x) from the 128-chunk sums the staging kernels write beside the rows (psum, added in a
+// fixed order).  MCG weights are the reference's fp16 lo + hi (one rounding).
+//
+// The rows are staged one unit at a time into LDS, double-buffered through registers, one
+// barrier per unit.  Items run persistently and XCD-aware: the workgroups of XCD x (blockIdx % 8)
+// take the (row tile, matrix) entries e with e % 8 == x, so all chunks of an entry share one L2.
+// Tuning, measured on MI355X (256 experts 4096 -> 2048 -> 4096, T = 512 / 2048): a trellis ring of
+// 2 units, X loaded 2 units ahead, one unit per barrier, B operands read before the decode, and
+// 4 waves per SIMD for 32- and 64-row tiles; barrier count, prefetch depth and occupancy moved
+// the time by under 3 %: the decode VALU and the MFMAs, which issue mostly serially on a SIMD,
+// bound the kernel.
+constexpr int MG_PF = 2, MG_XD = 2, MG_XU = 1;
+constexpr int MG_THREADS = 256;
+constexpr int MG_OW = 68;        // u32 per epilogue row: 128 fp16 + 16 bytes
+
+template <int R> struct MgLds
+{
+    static constexpr int RT = 16 * R;                   // rows per tile
+    static constexpr int XBUF = RT * (32 * MG_XU + 4);  // staged rows of one phase (+ 16 bytes per row)
+    static constexpr int OUT = RT * MG_OW;
+    static constexpr int MAIN = 2 * XBUF > OUT ? 2 * XBUF : OUT;
+    static constexpr int TOTAL = MAIN;
+};
+
+
+template <int K, int CB, int R>
+__global__ __launch_bounds__(MG_THREADS)
+__attribute__((amdgpu_waves_per_eu(R <= 4 ? 4 : 2, R <= 4 ? 4 : 2)))
+void moeg_kernel(const GemmGroupArgs g)
+{
+    using LD = MgLds<R>;
+    static_assert(R >= 2, "a tile stages at least 32 rows (two 16-byte loads per 8 threads)");
+    constexpr int TWD = tile_words(K), KB = kbits(K), XC = R / 2;
+    constexpr int PF = MG_PF, XD = MG_XD;                 // trellis ring depth, X prefetch distance (phases)
+    static_assert(PF % (XD * MG_XU) == 0, "the X ring slot must be a compile-time function of the unroll index");
+    __shared__ __align__(16) uint32_t lds[LD::TOTAL];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = threadIdx.x;
+    const int k = g.k, n = g.n;
+    const int nch = n / 128, units = k / 64, tiles_n = n / 16;   // units is even (k % 128 == 0)
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);
+    const int cnt0 = *to_global(g.count[0]);
+    const int cnt1 = g.mats > 1 ? *to_global(g.count[1]) : 0;
+    const int ents = (cnt0 > cnt1 ? cnt0 : cnt1) * g.mats;
+    const int xcd = blockIdx.x & 7, lb = blockIdx.x >> 3, nlb = gridDim.x >> 3;
+    const int per_xcd = ents > xcd ? (ents - xcd + 7) / 8 : 0;
+    uint16_t* ot = (uint16_t*) lds;                       // epilogue [RT][2 MG_OW] fp16
+
+    for (int it = lb; it < per_xcd * nch; it += nlb)
+    {
+        const int ent = xcd + 8 * (it / nch), chunk = it % nch;
+        const int mat = ent % g.mats, li = ent / g.mats;
+        if (li >= (mat ? cnt1 : cnt0)) continue;
+        const int tid = *to_global((mat ? g.list[1] : g.list[0]) + li);
+        const int e = *to_global(g.rt + 3 * tid), row0 = *to_global(g.rt + 3 * tid + 1);
+        const int M = *to_global(g.rt + 3 * tid + 2);
+        const uint16_t* A = (mat ? g.A[1] : g.A[0]) + (size_t) row0 * k;
+        uint16_t* C = (mat ? g.C[1] : g.C[0]) + (size_t) row0 * n + chunk * 128;
+        const uint32_t* trellis = (const uint32_t*) *to_global((mat ? g.tab[1] : g.tab[0]) + e);
+        const int rg = (M + 15) >> 4;                     // live 16-row groups (1..R)
+
+        const int jt = lane & 7;
+        const uint32_t* tile0 = trellis + ((size_t) (lane >> 4) * tiles_n + chunk * 8 + 2 * wave + ((lane >> 3) & 1)) * TWD;
+        const size_t ustride = (size_t) 4 * tiles_n * TWD;
+        const int prev_off = jt == 0 ? 8 * KB - 1 : -1;
+        uint32_t ring[PF][KB + 1];
+        #pragma unroll
+        for (int d = 0; d < PF; ++d) load_tile_lane<K>(tile0 + (size_t) min(d, units - 1) * ustride, jt, prev_off, ring[d]);
+
+        // X: one phase of XU units (64 XU k per row) at a time into LDS, double-buffered; phase
+        // p + XD is loaded while phase p computes, phase p + 1 stored after it (one barrier per
+        // phase)
+        constexpr int XU = MG_XU, XWD = 32 * XU + 4;      // row stride (u32): + 16 bytes, conflict-free B reads
+        constexpr int PCH = 8 * XU;                       // 16-byte chunks per row and phase
+        constexpr int XCP = R * XU / 2;                   // chunk loads per thread and phase
+        const int phases = units / XU;
+        u32x4 xr[XD][XCP];
+        auto xload = [&](u32x4* x, int ph) {
+            #pragma unroll
+            for (int i = 0; i < XCP; ++i)
+            {
+                const int c = t + MG_THREADS * i, row = c / PCH;
+                x[i] = *to_global((const u32x4*) (A + (size_t) min(row, M - 1) * k + min(ph, phases - 1) * 64 * XU + (c % PCH) * 8));
+            }
+        };
+        auto xstore = [&](const u32x4* x, int buf) {
+            #pragma unroll
+            for (int i = 0; i < XCP; ++i)
+            {
+                const int c = t + MG_THREADS * i;
+                *(u32x4*) (lds + buf * (LD::RT * XWD) + (c / PCH) * XWD + (c % PCH) * 4) = x[i];
+            }
+        };
+        #pragma unroll
+        for (int d = 0; d < XD; ++d) xload(xr[d], d);
+        xstore(xr[0], 0);
+        xload(xr[0], XD);                                 // slot p % XD holds phase p
+        f32x4 acc[2][R];
+        #pragma unroll
+        for (int r = 0; r < R; ++r) { acc[0][r] = (f32x4) { }; acc[1][r] = (f32x4) { }; }
+        __syncthreads();
+
+        for (int u0 = 0; u0 < units; u0 += PF)
+        {
+            #pragma unroll
+            for (int d = 0; d < PF; ++d)
+            {
+                const int u = u0 + d;                     // (PF divides units: no tail)
+                const int ph = u / XU;
+                // this unit's B operands first: their LDS latency hides behind the decode
+                const uint32_t* xb = lds + (ph & 1) * (LD::RT * XWD) + (lane & 15) * XWD + (u % XU) * 32 + (lane >> 4) * 8;
+                h8v bx[2][R];
+                #pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    #pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        bx[h][r] = __builtin_bit_cast(h8v, *(const u32x4*) (xb + 16 * r * XWD + 4 * h));
+                }
+                uint32_t wv[KB + 1], pk[16];
+                #pragma unroll
+                for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+                if constexpr (CB == 2) mul1_pairs<K>(wv, pk);
+                else
+                {
+                    uint32_t raw[32];
+                    raw32<K, CB>(wv, raw, a3, b3);
+                    #pragma unroll
+                    for (int q = 0; q < 16; ++q) pk[q] = weight_pair<CB>(raw[2 * q], raw[2 * q + 1]);
+                }
+                load_tile_lane<K>(tile0 + (size_t) min(u + PF, units - 1) * ustride, jt, prev_off, ring[d]);
+                #pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    const u32x4 a0 = { pk[h], pk[4 + h], pk[8 + h], pk[12 + h] };
+                    const u32x4 a1 = { pk[2 + h], pk[6 + h], pk[10 + h], pk[14 + h] };
+                    #pragma unroll
+                    for (int r = 0; r < R; ++r)
+                    {
+                        if (r >= rg) break;
+                        const h8v b = bx[h][r];
+                        acc[0][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a0), b, acc[0][r], 0, 0, 0);
+                        acc[1][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a1), b, acc[1][r], 0, 0, 0);
+                    }
+                }
+                if ((d + 1) % XU == 0)
+                {
+                    const int slot = ((d + 1) / XU) % XD;     // phase ph + 1's slot
+                    xstore(xr[slot], (ph + 1) & 1);           // (past the last phase: an unread buffer)
+                    xload(xr[slot], ph + 1 + XD);             // (clamped past the end)
+                    __syncthreads();
+                }
+            }
+        }
+
+        // epilogue: D[i][nn] of acc[c][r] (lane l: i = 4 (l/16) + e, nn = l%16) is column
+        // 32 w + 16 (i/8) + i%8 + 8 c, row 16 r + nn; rows meet in LDS for coalesced stores
+        const int kc = k / 128;
+        const float* ps = (mat ? g.psum[1] : g.psum[0]) + (size_t) row0 * kc;
+        #pragma unroll
+        for (int r = 0; r < R; ++r)
+        {
+            if (r >= rg) break;
+            const int row = 16 * r + (lane & 15);
+            float sx = 0.0f;
+            if (CB == 2)
+            {
+                const float* pr = ps + (size_t) min(row, M - 1) * kc;
+                for (int c = 0; c < kc; ++c) sx += *to_global(pr + c);
+                sx *= (float) as_h(0xc931);
+            }
+            #pragma unroll
+            for (int c = 0; c < 2; ++c)
+            {
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    const int i = 4 * (lane >> 4) + q;
+                    const int col = 32 * wave + 16 * (i >> 3) + (i & 7) + 8 * c;
+                    float v = acc[c][r][q];
+                    if (CB == 2) v = v * (float) as_h(0x1eee) + sx;
+                    ot[row * (2 * MG_OW) + col] = h_bits((f16) v);
+                }
+            }
+        }
+        __syncthreads();
+        for (int q = t; q < M * 16; q += MG_THREADS)
+        {
+            const int row = q >> 4, part = q & 15;
+            *to_global_w((u32x4*) (C + (size_t) row * n + part * 8)) = *(const u32x4*) (ot + row * (2 * MG_OW) + part * 8);
+        }
+        __syncthreads();
+    }
+}
+
+template <int K, int CB>
+int launch_moeg(const GemmGroupArgs& g, hipStream_t s)
+{
+    const long items = (long) g.nrt * g.mats * (g.n / 128);
+    long grid = g.grid_wgs > 0 && g.grid_wgs < items ? g.grid_wgs : items;
+    grid = (grid + 7) / 8 * 8;
+    if (items <= 0) return 0;
+    const dim3 gr((unsigned) grid), block(MG_THREADS);
+    if (g.tile_rows <= 32) hipLaunchKernelGGL((moeg_kernel<K, CB, 2>), gr, block, 0, s, g);
+    else if (g.tile_rows <= 64) hipLaunchKernelGGL((moeg_kernel<K, CB, 4>), gr, block, 0, s, g);
+    else hipLaunchKernelGGL((moeg_kernel<K, CB, 8>), gr, block, 0, s, g);
+    return (int) hipGetLastError();
+}
 }  // namespace
 
 #define EXL3_CAT2(a, b) a##b
@@ -472,6 +702,19 @@ int EXL3_CAT(exl3k_gemm_k, EXL3_INST_K)(const GemmArgs& g, int cb, hipStream_t s
         case 0: return launch_gemm<EXL3_INST_K, 0>(g, s);
         case 1: return launch_gemm<EXL3_INST_K, 1>(g, s);
         case 2: return launch_gemm<EXL3_INST_K, 2>(g, s);
+    }
+    return -1;
+}
+
+int EXL3_CAT(exl3k_moeg_k, EXL3_INST_K)(const GemmGroupArgs& g, int cb, hipStream_t s)
+{
+#if EXL3_INST_K >= 16
+    return cb == 2 ? launch_moeg<EXL3_INST_K, 2>(g, s) : -1;
+#endif
+    switch (cb)
+    {
+        case 1: return launch_moeg<EXL3_INST_K, 1>(g, s);
+        case 2: return launch_moeg<EXL3_INST_K, 2>(g, s);
     }
     return -1;
 }

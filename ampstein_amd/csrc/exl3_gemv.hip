@@ -1025,13 +1025,6 @@ typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 // position of row rho (0..15) of a 16-row group in the staged input
 __device__ __forceinline__ constexpr int xperm(int rho) { return 4 * ((rho & 7) >> 1) + (rho & 1) + 2 * (rho >> 3); }
 
-template <int K>
-__device__ __forceinline__ void load_tile_lane(const uint32_t* __restrict__ tile, int j, int prev_off, uint32_t* w)
-{
-    if constexpr (khalf(K)) load_frame_half<K>(tile, j, w);
-    else load_slot<K>(tile + j * K, prev_off, w);
-}
-
 template <int K, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemvm_kernel(const GemvArgs g)

@@ -61,6 +61,15 @@ __device__ __forceinline__ void load_slot_k(const uint32_t* __restrict__ p, int 
     else load_slot<K>(p, prev_off, w);
 }
 
+// Load lane j's frame of one tile (tile = the tile's first word): integer K, words jK..jK+K-1
+// and the ring predecessor (prev_off, relative to word jK); half rates, load_frame_half.
+template <int K>
+__device__ __forceinline__ void load_tile_lane(const uint32_t* __restrict__ tile, int j, int prev_off, uint32_t* w)
+{
+    if constexpr (khalf(K)) load_frame_half<K>(tile, j, w);
+    else load_slot<K>(tile + j * K, prev_off, w);
+}
+
 // Clean 16-bit state of window I (exl3_common.cuh: Win): one bfe, from word hi when the window
 // sits inside it, else from the half-word-shifted word alignbit(wv[hi-1], wv[hi], 16) (one per
 // word, shared by the windows that straddle that word boundary).

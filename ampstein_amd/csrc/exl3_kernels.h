@@ -93,7 +93,9 @@ struct GemmGroupArgs
     int mats;                   // 1 or 2
     int k, n;
     int nrt;                    // row-tile capacity of the launch
-    int tile_rows;              // rows per tile: 64, 128 or 256
+    int tile_rows;              // rows per tile: 64, 128 or 256 (moeg: 32, 64 or 128)
+    int grid_wgs;               // moeg: persistent workgroups (0: one per item)
+    const float* psum[2];       // moeg, mul1: (pool rows, k / 128) chunk sums of A, per matrix set
 };
 
 int exl3k_gemm_group_k1(const GemmGroupArgs& g, int cb, hipStream_t s);
@@ -104,6 +106,18 @@ int exl3k_gemm_group_k5(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k6(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k7(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k8(const GemmGroupArgs& g, int cb, hipStream_t s);
+// Register-decode grouped GEMM (exl3_gemm.hip moeg_kernel), same arguments.
+int exl3k_moeg_k1(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k2(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k3(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k4(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k5(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k6(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k7(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k8(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k17(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k18(const GemmGroupArgs& g, int cb, hipStream_t s);
+int exl3k_moeg_k19(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k17(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k18(const GemmGroupArgs& g, int cb, hipStream_t s);
 int exl3k_gemm_group_k19(const GemmGroupArgs& g, int cb, hipStream_t s);
@@ -139,7 +153,9 @@ struct MoesArgs
     int* lists;                 // workspace: 3 x MOES_RATES lists of row-tile ids, rt_cap each
     int* counts;                // workspace: 3 x MOES_RATES list lengths
     int rt_cap;
-    int tile_rows;              // rows per row tile (64, 128 or 256)
+    int tile_rows;              // rows per row tile
+    float *ps_g, *ps_u;         // workspace: (pool_rows, H / 128) sums of each staged 128-chunk
+    float* ps_d;                // workspace: (pool_rows, I / 128) the same for the down input
 };
 
 struct MoesGatherArgs

@@ -100,6 +100,22 @@ __device__ __forceinline__ void hmul4(uint32_t* w, const uint32_t* s)
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *to_global((const u32x4*) p); }
 
+// Sum of the 16-lane group's 128 fp16 values (lane g holds 8), in a fixed order: the row-chunk
+// sums the mul1 GEMM needs for its affine map (exl3_gemm.hip moeg_kernel).
+__device__ __forceinline__ float group_sum16(const uint32_t* w)
+{
+    float v = 0.0f;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q)
+    {
+        const f16x2 h = as_h2(w[q]);
+        v += (float) h.x + (float) h.y;
+    }
+    #pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
 // ------------------------------------------------------------------------------- plan
 // In-place exclusive scan of n <= PLAN_EMAX ints in LDS by PLAN_THREADS threads (4 per thread).
 __device__ int scan_excl(int* a, int n, int* tmp)
@@ -264,8 +280,12 @@ void moes_gather_kernel(MoesArgs a)
             #pragma unroll
             for (int i = 0; i < 8; ++i) f[i] *= R128;
             to_h(f, w);
+            const float cs = group_sum16(w);
             if (valid)
+            {
                 *(u32x4*) ((m ? a.ts_u : a.ts_g) + (size_t) r * a.H + col) = (u32x4) { w[0], w[1], w[2], w[3] };
+                if (g == 0) (m ? a.ps_u : a.ps_g)[(size_t) r * chunks + c] = cs;
+            }
         }
     }
 }
@@ -342,7 +362,12 @@ void moes_act_kernel(MoesArgs a)
         #pragma unroll
         for (int i = 0; i < 8; ++i) f[i] *= R128;
         to_h(f, gg);
-        if (valid) *(u32x4*) (a.ti_g + idx) = (u32x4) { gg[0], gg[1], gg[2], gg[3] };
+        const float cs = group_sum16(gg);
+        if (valid)
+        {
+            *(u32x4*) (a.ti_g + idx) = (u32x4) { gg[0], gg[1], gg[2], gg[3] };
+            if (g == 0) a.ps_d[(size_t) r * chunks + c] = cs;
+        }
     }
 }
 

@@ -603,7 +603,7 @@ def summarize_pmc(outdirs):
             with open(path) as f:
                 for r in csv.DictReader(f):
                     name = r["Kernel_Name"]
-                    if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "reconstruct", "had128", "copy", "Copy")):
+                    if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "moeg", "reconstruct", "had128", "copy", "Copy")):
                         continue
                     key = (name.replace("(anonymous namespace)::", "").split("(")[0][:80], r.get("Grid_Size", ""))
                     d = acc.setdefault(key, {}).setdefault(r["Counter_Name"], {})
@@ -693,7 +693,7 @@ def summarize_trace(path):
     with open(path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "rms_norm", "silu_mul")):
+            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "moeg", "rms_norm", "silu_mul")):
                 continue
             grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
             d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
