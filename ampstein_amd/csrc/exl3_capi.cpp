@@ -585,16 +585,36 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
         int rc = launch_gemv(*ws, bits, cb, g, s, name);
         return rc ? rc : EXL3_AMD_TAG_GEMV;
     }
-    // MFMA GEMM: input rotation into the caller's A_had (exl3_gemm_kernel.cuh writes it there
-    // too), then the tiled kernel
+    // m > 8: input rotation into the caller's A_had (exl3_gemm_kernel.cuh writes it there too)
     if (suh && !A_had) return fail(EXL3_AMD_EINVAL, "%s: must supply A_had with suh", name);
     if (suh)
     {
         int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
         if (rc) return hip_fail(rc, name);
     }
+    const uint16_t* A_rot = suh ? A_had : A;
+    // Medium batches: the row-batched matrix-core GEMV in 16-row groups when it beats the tiled
+    // GEMM, whose 256 x 256 tiles leave most CUs idle at small m.  Measured on MI355X (K = 2..4):
+    // a 16-row GEMV group decodes ~2.2 G weights per ms; a GEMM round (up to one tile per CU)
+    // takes ~28 ns per k.  Groups win while ceil(m / 16) * n < 61600 * rounds.
+    if (force_shape_idx == 0 && gemv_mfma_mode() != 0)
+    {
+        const long blocks = (long) ((n + 255) / 256) * ((m + 255) / 256);
+        const long rounds = (blocks + ws->num_cus - 1) / ws->num_cus;
+        if ((long) ((m + 15) / 16) * n < 61600L * rounds)
+        {
+            const size_t elt = c_fp32 ? 4 : 2;
+            for (int r0 = 0; r0 < m; r0 += 16)
+            {
+                GemvArgs g = gemv_args_single(A_rot + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt,
+                                              c_fp32, nullptr, svh, std::min(16, m - r0), k, n);
+                if (int rc = launch_gemv(*ws, bits, cb, g, s, name)) return rc;
+            }
+            return EXL3_AMD_TAG_GEMV;
+        }
+    }
     GemmArgs gg;
-    gg.A_rot = suh ? A_had : A;
+    gg.A_rot = A_rot;
     gg.trellis = trellis; gg.C = C; gg.svh = svh;
     gg.m = m; gg.k = k; gg.n = n; gg.c_fp32 = c_fp32 ? 1 : 0;
     int rc = dispatch_gemm(bits, cb, gg, s);

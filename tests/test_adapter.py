@@ -78,7 +78,8 @@ def gpu():
 @pytest.mark.parametrize("m", [1, 5, 32])
 @pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2)])
 def test_adapter_exl3_gemm(ad, orc, m, K, cb):
-    """GEMV (m <= 8, tag 90) and MFMA GEMM (m = 32, tag 91, A_had written) through the adapter."""
+    """GEMV (m <= 8, tag 90), and m = 32 (A_had written) through the adapter: the library routes
+    this small shape to 16-row GEMV groups (tag 90); force_shape_idx 2 takes the MFMA GEMM."""
     gpu()
     L = synth.layer(512, 384, K, cb, seed=300 + 10 * K + cb)
     t, s, v = L.torch("cuda:0")
@@ -86,7 +87,7 @@ def test_adapter_exl3_gemm(ad, orc, m, K, cb):
     A = torch.from_numpy(x).cuda()
     A_had = torch.empty_like(A)
     C = torch.empty((m, 384), dtype=torch.half, device="cuda")
-    tag = ad.exl3_gemm(A, t, C, s, A_had, v, 0, cb == 1, cb == 2, 0)
+    tag = ad.exl3_gemm(A, t, C, s, A_had, v, 0 if m <= 8 else 2, cb == 1, cb == 2, 0)
     torch.cuda.synchronize()
     assert tag == (90 if m <= 8 else 91)
     ref = orc.linear(x, L.trellis, L.suh, L.svh, K, cb=cb)

@@ -32,13 +32,14 @@ def rel_err(y, ref):
     return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
 
 
-def run_gemm(torch, L, x, y_fp32, suh=True, svh=True):
+def run_gemm(torch, L, x, y_fp32, suh=True, svh=True, force=2):
+    """force 2 (default here): the MFMA GEMM whatever m; 0: the library's routing."""
     from ampstein_amd import ops
     t, s, v = L.torch()
     A = torch.from_numpy(x).cuda()
     A_had = torch.empty_like(A)
     C = torch.empty((x.shape[0], L.n), dtype=torch.float if y_fp32 else torch.half, device="cuda")
-    tag = ops.exl3_gemm(A, t, C, s if suh else None, A_had, v if svh else None, 0, L.cb == 1, L.cb == 2)
+    tag = ops.exl3_gemm(A, t, C, s if suh else None, A_had, v if svh else None, force, L.cb == 1, L.cb == 2)
     return tag, C.cpu().numpy(), A_had.cpu().numpy()
 
 
@@ -65,6 +66,24 @@ def test_gemm_shapes(torch_cuda, orc, m, k, n, y_fp32):
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4, cb=0)
     assert rel_err(y, ref) < TOL
     assert np.array_equal(A_had.view(np.uint16), orc.had128(x, pre=L.suh).view(np.uint16))
+
+
+@pytest.mark.parametrize("m,k,n,K,cb", [(9, 5120, 17408, 2, 0), (16, 17408, 5120, 4, 1), (33, 4096, 14336, 3, 2),
+                                          (64, 5120, 5120, 2.5, 2), (100, 4096, 1024, 4, 0)])
+def test_gemm_medium_batch_routing(torch_cuda, orc, m, k, n, K, cb):
+    """m > 8 with few 256-row tiles per CU: 16-row groups of the matrix-core GEMV (tag 90), the
+    rotated input still written into A_had; the same call forced onto the MFMA GEMM agrees."""
+    torch = torch_cuda
+    L = synth.layer(k, n, K, cb, seed=650 + m + n)
+    x = synth.activations(m, k, seed=651 + m)
+    tag, y, A_had = run_gemm(torch, L, x, False, force=0)
+    assert tag == 90
+    assert np.array_equal(A_had.view(np.uint16), orc.had128(x, pre=L.suh).view(np.uint16))
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
+    assert rel_err(y, ref) < TOL
+    tag2, y2, _ = run_gemm(torch, L, x, False, force=2)
+    assert tag2 == 91
+    assert rel_err(y2, ref) < TOL
 
 
 @pytest.mark.parametrize("suh,svh", [(False, False), (True, False), (False, True)])

@@ -44,7 +44,8 @@ def test_gemm_half_rate(torch_cuda, orc, K, m, y_fp32):
     t, s, v = L.torch()
     A = torch.from_numpy(x).cuda()
     C = torch.empty((m, 1024), dtype=torch.float if y_fp32 else torch.half, device="cuda")
-    tag = ops.exl3_gemm(A, t, C, s, torch.empty_like(A), v, 0, False, True)
+    # m > 8: force the MFMA GEMM (the library routes these small shapes to the GEMV)
+    tag = ops.exl3_gemm(A, t, C, s, torch.empty_like(A), v, 0 if m <= 8 else 2, False, True)
     torch.cuda.synchronize()
     assert tag == (90 if m <= 8 else 91)
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=True, cb=2)
