@@ -253,13 +253,17 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
         {
             const int KS = k / 16, chunks = n / 128;
             const int mt = m == 1 ? 1 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16));
-            int per_cu = 4;
-            if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
-            const long target = (long) per_cu * num_cus;
-            // SB: k-tiles per workgroup, a multiple of 8 dividing k/16; the largest whose grid still
-            // reaches the target (else the smallest), within 48 KB of staged input and the workspace
+            // target grid: 1.5 workgroups per CU (EXL3_AMD_GEMV_WG_PER_CU: that many instead)
+            long target = 3L * num_cus / 2;
+            if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) target = (long) v * num_cus; }
+            // SB: k-tiles per workgroup, a multiple of 8 dividing k/16, at most 64 (16 units per
+            // wave; 32 for 16 rows); the largest whose grid still reaches the target (else the smallest), within
+            // 48 KB of staged input and the workspace.  Measured on MI355X over SB (Qwen 5120 x
+            // {5120, 17408}, 17408 x 5120, m = 1..16): the optimum sits at 1.5-2.7 workgroups per
+            // CU with SB 32-64; SB 8 (the most workgroups) is up to 1.5x slower.
             int best = -1;
-            for (int d = 8; d <= KS; d += 8)
+            const int sb_max = mt >= 16 ? 32 : 64;                // 16 rows: SB 32 measured best
+            for (int d = 8; d <= KS && d <= sb_max; d += 8)
             {
                 if (KS % d) continue;
                 if ((size_t) mt * (d * 16 + 4) * 4 > 48 * 1024) break;
@@ -594,14 +598,16 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     }
     const uint16_t* A_rot = suh ? A_had : A;
     // Medium batches: the row-batched matrix-core GEMV in 16-row groups when it beats the tiled
-    // GEMM, whose 256 x 256 tiles leave most CUs idle at small m.  Measured on MI355X (K = 2..4):
-    // a 16-row GEMV group decodes ~2.2 G weights per ms; a GEMM round (up to one tile per CU)
-    // takes ~28 ns per k.  Groups win while ceil(m / 16) * n < 61600 * rounds.
+    // GEMM, whose 256 x 256 tiles leave most CUs idle at small m.  Measured on MI355X (K = 2..4,
+    // k x n from 4096 x 1024 to 17408 x 5120, m = 16..192): a 16-row group takes ~8 us + 0.37 ns
+    // per 1000 weights; a GEMM round (up to one tile per CU) ~28 ns per k.
     if (force_shape_idx == 0 && gemv_mfma_mode() != 0)
     {
         const long blocks = (long) ((n + 255) / 256) * ((m + 255) / 256);
         const long rounds = (blocks + ws->num_cus - 1) / ws->num_cus;
-        if ((long) ((m + 15) / 16) * n < 61600L * rounds)
+        const double t_groups = ((m + 15) / 16) * (8.0 + 3.7e-7 * (double) n * k);
+        const double t_gemm = 0.028 * k * rounds;
+        if (t_groups < t_gemm)
         {
             const size_t elt = c_fp32 ? 4 : 2;
             for (int r0 = 0; r0 < m; r0 += 16)

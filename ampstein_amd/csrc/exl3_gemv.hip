@@ -553,7 +553,7 @@ template <int K, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemv_kernel(const GemvArgs g)
 {
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __align__(16) uint32_t smem[];
     __shared__ int flag;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1029,7 +1029,7 @@ template <int K, int CB, int MT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemvm_kernel(const GemvArgs g)
 {
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __align__(16) uint32_t smem[];
     __shared__ int flag;
     __shared__ float sumx[MT];
     const int lane = threadIdx.x & 63;
@@ -1045,12 +1045,66 @@ void gemvm_kernel(const GemvArgs g)
     MatView v;
     if (!resolve(g, j, v)) { inactive_arrive(g, chunk, slot, &flag); return; }
     if (chunk * 128 >= v.n) return;
-    const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
+    // the wave's start (staging) and end (hand-off) outrank the decode loops of the SIMD's other
+    // waves, as in the M = 1 kernel
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
+#ifdef EXL3_GEMV_TRACE
+    {
+        uint32_t hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n\ts_getreg_b32 %1, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(hw), "=s"(xcc));
+        GEMV_STAMP(g, 0, hw);
+        if ((threadIdx.x & 63) == 0)
+            g.trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + 5] = ((uint64_t) xcc << 32) | hw;
+    }
+#endif
     const int ks0 = slot * SB;
     const int xs_stride = SB * 16 + 4;                    // u32 per row; +4: rows 16 bytes apart in the banks
     uint32_t* xs = smem;                                  // [MT][xs_stride] dup pairs, xperm order
     float* res = (float*) (smem + MT * xs_stride);        // [MT][128]
     float* tmp = res + MT * 128;                          // epilogue scratch: 2 x (m x 64 column pairs), >= 512
+
+    // Input rotation of the workgroup's SB / 8 chunks, every row, into xs (dup pairs, xperm order).
+    // Job q of wave w: row / chunk (w + 4 q) of m x SB / 8.  The first XB jobs' input and suh loads
+    // are issued before the weight ring's: loads return in issue order, so behind the ring they
+    // would wait for its HBM traffic.
+    constexpr int XB = 4;                                 // measured best of 2 / 4 / 8 / 16 (m = 2..8)
+    const int nkc = SB / 8, njobs = m * nkc;
+    uint32_t xr[XB], sr[XB];
+    auto xload = [&](int jb) {
+        #pragma unroll
+        for (int q = 0; q < XB; ++q)
+        {
+            const int job = min(jb + q * GEMV_WAVES, njobs - 1);
+            const int row = job / nkc, c = job % nkc;
+            const int col = ks0 * 16 + c * 128 + 2 * lane;
+            xr[q] = *to_global((const uint32_t*) (v.A + (size_t) row * k + col));
+            sr[q] = *to_global((const uint32_t*) ((v.suh ? v.suh : v.A) + col));   // unused without suh
+        }
+    };
+    auto xstage = [&](int jb) {
+        #pragma unroll
+        for (int q = 0; q < XB; ++q)
+        {
+            const int job = jb + q * GEMV_WAVES;
+            if (job >= njobs) break;
+            const int row = job / nkc, c = job % nkc;
+            f16x2 o = as_h2(xr[q]);
+            if (v.suh)
+            {
+                const f16x2 xv = o * as_h2(sr[q]);
+                float v0 = (float) xv.x, v1 = (float) xv.y;
+                fwht128_wave(v0, v1, lane);
+                o.x = (f16) (v0 * EXL3_HAD_RSCALE);
+                o.y = (f16) (v1 * EXL3_HAD_RSCALE);
+            }
+            const int e = 2 * lane;                       // even row of its 16-group: xperm(e+1) = xperm(e) + 1
+            const int pos = c * 128 + (e & ~15) + xperm(e & 15);
+            f16x2 d0 = { o.x, o.x }, d1 = { o.y, o.y };
+            *(u32x2*) (xs + row * xs_stride + pos) = (u32x2) { as_u32(d0), as_u32(d1) };
+        }
+    };
+    xload(wave);
+    __builtin_amdgcn_sched_barrier(0);
 
     // this lane's tile: k-tile ks0 + lane / 16 (+ 4 per unit), column tile 2 wave + lane % 16 / 8
     const int tiles_n = v.stride / 16;
@@ -1065,32 +1119,18 @@ void gemvm_kernel(const GemvArgs g)
     uint32_t ring[PF][KB + 1];
     #pragma unroll
     for (int d = 0; d < PF; ++d) load_tile_lane<K>(tile0 + (size_t) min(d, nunits - 1) * ustride, jt, prev_off, ring[d]);
+    // svh pair for the epilogue, behind the first weights
+    const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
 
-    // input rotation of the workgroup's SB / 8 chunks, every row, into xs (dup pairs, xperm order)
+    xstage(wave);
+    for (int jb = wave + GEMV_WAVES * XB; jb < njobs; jb += GEMV_WAVES * XB)
     {
-        const int nkc = SB / 8;
-        for (int job = wave; job < m * nkc; job += GEMV_WAVES)
-        {
-            const int row = job / nkc, c = job % nkc;
-            const int col = ks0 * 16 + c * 128 + 2 * lane;
-            f16x2 xv = as_h2(*to_global((const uint32_t*) (v.A + (size_t) row * k + col)));
-            f16x2 o;
-            if (v.suh)
-            {
-                xv = xv * as_h2(*to_global((const uint32_t*) (v.suh + col)));
-                float v0 = (float) xv.x, v1 = (float) xv.y;
-                fwht128_wave(v0, v1, lane);
-                o.x = (f16) (v0 * EXL3_HAD_RSCALE);
-                o.y = (f16) (v1 * EXL3_HAD_RSCALE);
-            }
-            else o = xv;
-            const int e = 2 * lane;                       // even row of its 16-group: xperm(e+1) = xperm(e) + 1
-            const int pos = c * 128 + (e & ~15) + xperm(e & 15);
-            f16x2 d0 = { o.x, o.x }, d1 = { o.y, o.y };
-            *(u32x2*) (xs + row * xs_stride + pos) = (u32x2) { as_u32(d0), as_u32(d1) };
-        }
+        xload(jb);
+        xstage(jb);
     }
     __syncthreads();
+    GEMV_STAMP(g, 1, 0);
+    __builtin_amdgcn_s_setprio(0);
 
     const int nrow = min(lane & 15, m - 1);               // B column = activation row (clamped)
     const uint32_t* xb = xs + nrow * xs_stride + (lane >> 4) * 16;
@@ -1122,7 +1162,8 @@ void gemvm_kernel(const GemvArgs g)
             }
         }
     }
-
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
+    GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(acc[0].x + acc[1].x)));
     // D[i][n]: lane holds output columns i = 4 (lane / 16) + e of the wave's half c, row n = lane % 16
     const int n = lane & 15;
     if (n < m)
@@ -1159,6 +1200,7 @@ void gemvm_kernel(const GemvArgs g)
         __syncthreads();
     }
     block_epilogue(g, v, j, chunk, slot, splits, res, tmp, &flag, svp);
+    GEMV_STAMP(g, 3, flag);
 }
 
 template <typename KernelLaunch>

@@ -571,7 +571,7 @@ template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_a_kernel(const MoeArgs a)
 {
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __align__(16) uint32_t smem[];
     __shared__ int rows[ROWS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nproj = a.gated ? 2 : 1;
@@ -670,7 +670,7 @@ template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_b_kernel(const MoeArgs a)
 {
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __align__(16) uint32_t smem[];
     __shared__ int rows[ROWS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int chunks = a.Ho / 128;
