@@ -776,9 +776,9 @@ template <int K, int CB, int WS, bool ACT>
 __global__ __launch_bounds__(GEMV_THREADS)
 void gemv1_kernel(const GemvArgs g)
 {
-    __shared__ float red[GEMV_WAVES][128];
-    __shared__ float res[128];
-    __shared__ float tmp[2 * GEMV_THREADS];
+    __shared__ __align__(16) float red[GEMV_WAVES][128];
+    __shared__ __align__(16) float res[128];
+    __shared__ __align__(16) float tmp[2 * GEMV_THREADS];
     __shared__ float sumx_w[GEMV_WAVES];
     __shared__ int flag;
     const int lane = threadIdx.x & 63;

@@ -377,7 +377,7 @@ void moes_out_kernel(MoesArgs a)
 {
     // per wave: its 4 chunks (16 lanes x 8 values each) transposed so that atomic i of lane g
     // adds element 16 i + g: 64 contiguous bytes per group and instruction instead of 16 lines
-    __shared__ float tr[4][4 * 128];
+    __shared__ __align__(16) float tr[4][4 * 128];
     const int lane = threadIdx.x & 63, g = lane & 15;
     float* trw = tr[threadIdx.x >> 6] + 128 * (lane >> 4);
     const int chunks = a.H / 128;

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256)
 void reconstruct_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ trellis,
                         int k, int n, int tiles_n, int nt_off)
 {
-    __shared__ uint32_t sh[4][16][64 + 4];     // per wave: 16 rows x 128 halves (+pad)
+    __shared__ __align__(16) uint32_t sh[4][16][64 + 4];     // per wave: 16 rows x 128 halves (+pad)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kt = blockIdx.y * 4 + wave;
     const int chunk = blockIdx.x;
@@ -206,7 +206,7 @@ void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict
                             const uint16_t* __restrict__ suh, const uint16_t* __restrict__ svh,
                             int n, int tiles_n, int nt_off)
 {
-    __shared__ uint32_t blk[128 * 64];
+    __shared__ __align__(16) uint32_t blk[128 * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = blockIdx.x, kb = blockIdx.y;
     const DecodeRegs r = make_decode_regs<CB>();
