@@ -246,45 +246,73 @@ void moes_plan_kernel(MoesArgs a, int pass_row0)
 }
 
 // ------------------------------------------------------------------------------- gather + rotate
+// Row-per-wave elementwise kernels.  Wave w takes pool rows w, w + waves, ...; the row's sorted
+// position, expert, token and routing weight are wave-uniform (scalar loads, once per row), and
+// the row's 128-column chunks go in batches of 4 EW_B chunks (16 lanes per chunk, 8 values per
+// lane) whose loads are all issued before the first butterfly.  The per-chunk arithmetic is the
+// chunk-per-job form's, value for value.
+constexpr int EW_B = 2;                  // 4-chunk groups per batch
+
+__device__ __forceinline__ int wave_id()
+{
+    return __builtin_amdgcn_readfirstlane((int) blockIdx.x * 4 + (int) (threadIdx.x >> 6));
+}
+
 __global__ __launch_bounds__(256)
 void moes_gather_kernel(MoesArgs a)
 {
-    const int lane = threadIdx.x & 63, g = lane & 15;
+    const int lane = threadIdx.x & 63, g = lane & 15, sub = lane >> 4;
     const int chunks = a.H / 128;
-    const long jobs = (long) a.pool_rows * chunks;
-    const long step = (long) gridDim.x * 16;
-    for (long base = ((long) blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; base < jobs; base += step)
+    const int nw = gridDim.x * 4;
+    for (int r = wave_id(); r < a.pool_rows; r += nw)
     {
-        const long job = min(base + (lane >> 4), jobs - 1);
-        const int r = (int) (job / chunks), c = (int) (job - (long) r * chunks);
         const int pos = a.rowinfo[3 * r];
-        const bool valid = base + (lane >> 4) < jobs && pos >= 0;
+        if (pos < 0) continue;                             // (uniform) rows past the pass
         const int e = a.rowinfo[3 * r + 1];
-        const int64_t token = pos >= 0 ? a.token_sorted[pos] : 0;
-        const int col = 128 * c + 8 * g;
-        uint32_t xw[4];
-        unpack8(__builtin_nontemporal_load(to_global((const u32x4*) (a.x + token * a.H + col))), xw);
-        #pragma unroll
-        for (int m = 0; m < 2; ++m)
+        const int64_t token = a.token_sorted[pos];
+        const uint16_t* xrow = a.x + token * a.H;
+        const uint16_t* suh_g = a.gated ? (const uint16_t*) a.g_suh[e] : nullptr;
+        const uint16_t* suh_u = (const uint16_t*) a.u_suh[e];
+        for (int c0 = 0; c0 < chunks; c0 += 4 * EW_B)
         {
-            if (m == 0 && !a.gated) continue;              // non-gated: no gate staging
-            const uint16_t* suh = (const uint16_t*) (m ? a.u_suh : a.g_suh)[e];
-            uint32_t w[4], sw[4];
-            unpack8(ld16(suh + col), sw);
+            u32x4 xv[EW_B], sv[2][EW_B];
             #pragma unroll
-            for (int q = 0; q < 4; ++q) w[q] = xw[q];
-            hmul4(w, sw);                                  // fp16 pre-scale
-            float f[8];
-            to_f32(w, f);
-            fwht128_g16(f, lane);
-            #pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] *= R128;
-            to_h(f, w);
-            const float cs = group_sum16(w);
-            if (valid)
+            for (int bq = 0; bq < EW_B; ++bq)
             {
-                *(u32x4*) ((m ? a.ts_u : a.ts_g) + (size_t) r * a.H + col) = (u32x4) { w[0], w[1], w[2], w[3] };
-                if (g == 0) (m ? a.ps_u : a.ps_g)[(size_t) r * chunks + c] = cs;
+                const int col = 128 * min(c0 + 4 * bq + sub, chunks - 1) + 8 * g;
+                xv[bq] = __builtin_nontemporal_load(to_global((const u32x4*) (xrow + col)));
+                sv[1][bq] = ld16(suh_u + col);
+                if (a.gated) sv[0][bq] = ld16(suh_g + col);
+            }
+            #pragma unroll
+            for (int bq = 0; bq < EW_B; ++bq)
+            {
+                const int c = c0 + 4 * bq + sub;
+                const int col = 128 * min(c, chunks - 1) + 8 * g;
+                uint32_t xw[4];
+                unpack8(xv[bq], xw);
+                #pragma unroll
+                for (int m = 0; m < 2; ++m)
+                {
+                    if (m == 0 && !a.gated) continue;      // non-gated: no gate staging
+                    uint32_t w[4], sw[4];
+                    unpack8(sv[m][bq], sw);
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) w[q] = xw[q];
+                    hmul4(w, sw);                          // fp16 pre-scale
+                    float f[8];
+                    to_f32(w, f);
+                    fwht128_g16(f, lane);
+                    #pragma unroll
+                    for (int i = 0; i < 8; ++i) f[i] *= R128;
+                    to_h(f, w);
+                    const float cs = group_sum16(w);
+                    if (c < chunks)
+                    {
+                        *(u32x4*) ((m ? a.ts_u : a.ts_g) + (size_t) r * a.H + col) = (u32x4) { w[0], w[1], w[2], w[3] };
+                        if (g == 0) (m ? a.ps_u : a.ps_g)[(size_t) r * chunks + c] = cs;
+                    }
+                }
             }
         }
     }
@@ -300,73 +328,96 @@ __device__ __forceinline__ float gelu_f(float x)
 __global__ __launch_bounds__(256)
 void moes_act_kernel(MoesArgs a)
 {
-    const int lane = threadIdx.x & 63, g = lane & 15;
+    const int lane = threadIdx.x & 63, g = lane & 15, sub = lane >> 4;
     const int chunks = a.I / 128;
-    const long jobs = (long) a.pool_rows * chunks;
-    const long step = (long) gridDim.x * 16;
+    const int nw = gridDim.x * 4;
     const f16 lim = (f16) a.act_limit;
-    for (long base = ((long) blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; base < jobs; base += step)
+    for (int r = wave_id(); r < a.pool_rows; r += nw)
     {
-        const long job = min(base + (lane >> 4), jobs - 1);
-        const int r = (int) (job / chunks), c = (int) (job - (long) r * chunks);
-        const bool valid = base + (lane >> 4) < jobs && a.rowinfo[3 * r] >= 0;
+        if (a.rowinfo[3 * r] < 0) continue;                // (uniform) rows past the pass
         const int e = a.rowinfo[3 * r + 1];
-        const int col = 128 * c + 8 * g;
-        const size_t idx = (size_t) r * a.I + col;
-        // had(u) o svh_u
-        uint32_t u[4], gg[4] = { 0u, 0u, 0u, 0u }, s[4];
-        float f[8];
-        unpack8(ld16(a.ti_u + idx), u);
-        to_f32(u, f);
-        fwht128_g16(f, lane);
-        #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] *= R128;
-        to_h(f, u);
-        unpack8(ld16((const uint16_t*) a.u_svh[e] + col), s);
-        hmul4(u, s);
-        if (a.gated)
+        const uint16_t* svh_u = (const uint16_t*) a.u_svh[e];
+        const uint16_t* svh_g = a.gated ? (const uint16_t*) a.g_svh[e] : nullptr;
+        const uint16_t* suh_d = (const uint16_t*) a.d_suh[e];
+        for (int c0 = 0; c0 < chunks; c0 += 4 * EW_B)
         {
-            unpack8(ld16(a.ti_g + idx), gg);
-            to_f32(gg, f);
-            fwht128_g16(f, lane);
+            u32x4 uv[EW_B], gv[EW_B], su[EW_B], sg[EW_B], sd[EW_B];
             #pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] *= R128;
-            to_h(f, gg);
-            unpack8(ld16((const uint16_t*) a.g_svh[e] + col), s);
-            hmul4(gg, s);
-        }
-        // activation of the gate lane, per element in fp32 from the fp16 value, rounded once
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
-        {
-            f16x2 hg = as_h2(gg[q]);
-            const f16x2 hu = as_h2(u[q]);
-            if (a.act == 0) hg = (f16x2) { (f16) silu_f((float) hg.x), (f16) silu_f((float) hg.y) };
-            else if (a.act == 1) hg = (f16x2) { (f16) gelu_f((float) hg.x), (f16) gelu_f((float) hg.y) };
-            else if (a.act == 2)
-                hg = (f16x2) { hu.x > (f16) 0 ? hu.x : (f16) 0, hu.y > (f16) 0 ? hu.y : (f16) 0 };
-            f16x2 uu = hu;
-            if (a.act_limit != 0.0f)
+            for (int bq = 0; bq < EW_B; ++bq)
             {
-                uu.x = uu.x < -lim ? -lim : (uu.x > lim ? lim : uu.x);
-                uu.y = uu.y < -lim ? -lim : (uu.y > lim ? lim : uu.y);
-                hg.x = hg.x > lim ? lim : hg.x;
-                hg.y = hg.y > lim ? lim : hg.y;
+                const int col = 128 * min(c0 + 4 * bq + sub, chunks - 1) + 8 * g;
+                const size_t idx = (size_t) r * a.I + col;
+                uv[bq] = ld16(a.ti_u + idx);
+                su[bq] = ld16(svh_u + col);
+                sd[bq] = ld16(suh_d + col);
+                if (a.gated)
+                {
+                    gv[bq] = ld16(a.ti_g + idx);
+                    sg[bq] = ld16(svh_g + col);
+                }
             }
-            gg[q] = as_u32(hg * uu);                       // fp16 gate product
-        }
-        unpack8(ld16((const uint16_t*) a.d_suh[e] + col), s);
-        hmul4(gg, s);                                      // fp16 down pre-scale
-        to_f32(gg, f);
-        fwht128_g16(f, lane);
-        #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] *= R128;
-        to_h(f, gg);
-        const float cs = group_sum16(gg);
-        if (valid)
-        {
-            *(u32x4*) (a.ti_g + idx) = (u32x4) { gg[0], gg[1], gg[2], gg[3] };
-            if (g == 0) a.ps_d[(size_t) r * chunks + c] = cs;
+            #pragma unroll
+            for (int bq = 0; bq < EW_B; ++bq)
+            {
+                const int c = c0 + 4 * bq + sub;
+                const int col = 128 * min(c, chunks - 1) + 8 * g;
+                const size_t idx = (size_t) r * a.I + col;
+                // had(u) o svh_u
+                uint32_t u[4], gg[4] = { 0u, 0u, 0u, 0u }, s[4];
+                float f[8];
+                unpack8(uv[bq], u);
+                to_f32(u, f);
+                fwht128_g16(f, lane);
+                #pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] *= R128;
+                to_h(f, u);
+                unpack8(su[bq], s);
+                hmul4(u, s);
+                if (a.gated)
+                {
+                    unpack8(gv[bq], gg);
+                    to_f32(gg, f);
+                    fwht128_g16(f, lane);
+                    #pragma unroll
+                    for (int i = 0; i < 8; ++i) f[i] *= R128;
+                    to_h(f, gg);
+                    unpack8(sg[bq], s);
+                    hmul4(gg, s);
+                }
+                // activation of the gate lane, per element in fp32 from the fp16 value, rounded once
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    f16x2 hg = as_h2(gg[q]);
+                    const f16x2 hu = as_h2(u[q]);
+                    if (a.act == 0) hg = (f16x2) { (f16) silu_f((float) hg.x), (f16) silu_f((float) hg.y) };
+                    else if (a.act == 1) hg = (f16x2) { (f16) gelu_f((float) hg.x), (f16) gelu_f((float) hg.y) };
+                    else if (a.act == 2)
+                        hg = (f16x2) { hu.x > (f16) 0 ? hu.x : (f16) 0, hu.y > (f16) 0 ? hu.y : (f16) 0 };
+                    f16x2 uu = hu;
+                    if (a.act_limit != 0.0f)
+                    {
+                        uu.x = uu.x < -lim ? -lim : (uu.x > lim ? lim : uu.x);
+                        uu.y = uu.y < -lim ? -lim : (uu.y > lim ? lim : uu.y);
+                        hg.x = hg.x > lim ? lim : hg.x;
+                        hg.y = hg.y > lim ? lim : hg.y;
+                    }
+                    gg[q] = as_u32(hg * uu);               // fp16 gate product
+                }
+                unpack8(sd[bq], s);
+                hmul4(gg, s);                              // fp16 down pre-scale
+                to_f32(gg, f);
+                fwht128_g16(f, lane);
+                #pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] *= R128;
+                to_h(f, gg);
+                const float cs = group_sum16(gg);
+                if (c < chunks)
+                {
+                    *(u32x4*) (a.ti_g + idx) = (u32x4) { gg[0], gg[1], gg[2], gg[3] };
+                    if (g == 0) a.ps_d[(size_t) r * chunks + c] = cs;
+                }
+            }
         }
     }
 }
@@ -378,52 +429,72 @@ void moes_out_kernel(MoesArgs a)
     // per wave: its 4 chunks (16 lanes x 8 values each) transposed so that atomic i of lane g
     // adds element 16 i + g: 64 contiguous bytes per group and instruction instead of 16 lines
     __shared__ __align__(16) float tr[4][4 * 128];
-    const int lane = threadIdx.x & 63, g = lane & 15;
-    float* trw = tr[threadIdx.x >> 6] + 128 * (lane >> 4);
+    const int lane = threadIdx.x & 63, g = lane & 15, sub = lane >> 4;
+    float* trw = tr[threadIdx.x >> 6] + 128 * sub;
     const int chunks = a.H / 128;
-    const long jobs = (long) a.pool_rows * chunks;
-    const long step = (long) gridDim.x * 16;
-    for (long base = ((long) blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; base < jobs; base += step)
+    const int nw = gridDim.x * 4;
+    for (int r = wave_id(); r < a.pool_rows; r += nw)
     {
-        const long job = min(base + (lane >> 4), jobs - 1);
-        const int r = (int) (job / chunks), c = (int) (job - (long) r * chunks);
         const int pos = a.rowinfo[3 * r];
-        const bool valid = base + (lane >> 4) < jobs && pos >= 0;
+        if (pos < 0) continue;                             // (uniform) rows past the pass
         const int e = a.rowinfo[3 * r + 1], j = a.rowinfo[3 * r + 2];
-        const int col = 128 * c + 8 * g;
-        uint32_t w[4], s[4];
-        float f[8];
-        unpack8(ld16(a.ts_g + (size_t) r * a.H + col), w);
-        to_f32(w, f);
-        fwht128_g16(f, lane);
-        const float rs = R128 * (float) as_h(pos >= 0 ? a.weight_sorted[pos] : (uint16_t) 0);
-        unpack8(ld16((const uint16_t*) a.d_svh[e] + col), s);
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        const float rs = R128 * (float) as_h(a.weight_sorted[pos]);
+        const uint16_t* svh_d = (const uint16_t*) a.d_svh[e];
+        const int64_t token = a.token_sorted[pos];
+        for (int c0 = 0; c0 < chunks; c0 += 4 * EW_B)
         {
-            const f16x2 sv = as_h2(s[q]);
-            f[2 * q] = (f[2 * q] * rs) * (float) sv.x;
-            f[2 * q + 1] = (f[2 * q + 1] * rs) * (float) sv.y;
-        }
-        if (!valid) continue;
-        if (a.scratch)
-        {
-            float* dst = a.scratch + (size_t) (a.fused_base[e] + j) * a.H + col;
-            *(f32x4*) dst = (f32x4) { f[0], f[1], f[2], f[3] };
-            *(f32x4*) (dst + 4) = (f32x4) { f[4], f[5], f[6], f[7] };
-        }
-        else
-        {
+            u32x4 yv[EW_B], sv[EW_B];
             #pragma unroll
-            for (int i = 0; i < 8; ++i) trw[8 * g + i] = f[i];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            float* dst = a.out + (size_t) a.token_sorted[pos] * a.H + 128 * c + g;
+            for (int bq = 0; bq < EW_B; ++bq)
+            {
+                const int col = 128 * min(c0 + 4 * bq + sub, chunks - 1) + 8 * g;
+                yv[bq] = ld16(a.ts_g + (size_t) r * a.H + col);
+                sv[bq] = ld16(svh_d + col);
+            }
             #pragma unroll
-            for (int i = 0; i < 8; ++i) atomicAdd(dst + 16 * i, trw[16 * i + g]);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
+            for (int bq = 0; bq < EW_B; ++bq)
+            {
+                const int c = c0 + 4 * bq + sub;
+                const int col = 128 * min(c, chunks - 1) + 8 * g;
+                uint32_t w[4], s[4];
+                float f[8];
+                unpack8(yv[bq], w);
+                to_f32(w, f);
+                fwht128_g16(f, lane);
+                unpack8(sv[bq], s);
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                {
+                    const f16x2 svv = as_h2(s[q]);
+                    f[2 * q] = (f[2 * q] * rs) * (float) svv.x;
+                    f[2 * q + 1] = (f[2 * q + 1] * rs) * (float) svv.y;
+                }
+                if (a.scratch)
+                {
+                    if (c < chunks)
+                    {
+                        float* dst = a.scratch + (size_t) (a.fused_base[e] + j) * a.H + col;
+                        *(f32x4*) dst = (f32x4) { f[0], f[1], f[2], f[3] };
+                        *(f32x4*) (dst + 4) = (f32x4) { f[4], f[5], f[6], f[7] };
+                    }
+                }
+                else
+                {
+                    #pragma unroll
+                    for (int i = 0; i < 8; ++i) trw[8 * g + i] = f[i];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    if (c < chunks)
+                    {
+                        float* dst = a.out + (size_t) token * a.H + 128 * c + g;
+                        #pragma unroll
+                        for (int i = 0; i < 8; ++i) atomicAdd(dst + 16 * i, trw[16 * i + g]);
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
         }
     }
 }
@@ -492,21 +563,26 @@ int exl3k_moes_plan(const MoesArgs& a, int pass_row0, hipStream_t s)
     return (int) hipGetLastError();
 }
 
+static int rows_grid(int rows, int cus)
+{
+    return (int) std::max(1L, std::min((long) (rows + 3) / 4, 8L * cus));
+}
+
 int exl3k_moes_gather(const MoesArgs& a, int cus, hipStream_t s)
 {
-    hipLaunchKernelGGL(moes_gather_kernel, dim3(grid_for((long) a.pool_rows * (a.H / 128), cus)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(moes_gather_kernel, dim3(rows_grid(a.pool_rows, cus)), dim3(256), 0, s, a);
     return (int) hipGetLastError();
 }
 
 int exl3k_moes_act(const MoesArgs& a, int cus, hipStream_t s)
 {
-    hipLaunchKernelGGL(moes_act_kernel, dim3(grid_for((long) a.pool_rows * (a.I / 128), cus)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(moes_act_kernel, dim3(rows_grid(a.pool_rows, cus)), dim3(256), 0, s, a);
     return (int) hipGetLastError();
 }
 
 int exl3k_moes_out(const MoesArgs& a, int cus, hipStream_t s)
 {
-    hipLaunchKernelGGL(moes_out_kernel, dim3(grid_for((long) a.pool_rows * (a.H / 128), cus)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(moes_out_kernel, dim3(rows_grid(a.pool_rows, cus)), dim3(256), 0, s, a);
     return (int) hipGetLastError();
 }
 
