@@ -561,7 +561,11 @@ void moeg_kernel(const GemmGroupArgs g)
             for (int i = 0; i < XCP; ++i)
             {
                 const int c = t + MG_THREADS * i, row = c / PCH;
+#ifdef EXL3_MG_NOX
+                x[i] = *to_global((const u32x4*) (A + (c % PCH) * 8));
+#else
                 x[i] = *to_global((const u32x4*) (A + (size_t) min(row, M - 1) * k + min(ph, phases - 1) * 64 * XU + (c % PCH) * 8));
+#endif
             }
         };
         auto xstore = [&](const u32x4* x, int buf) {
@@ -601,8 +605,14 @@ void moeg_kernel(const GemmGroupArgs g)
                 uint32_t wv[KB + 1], pk[16];
                 #pragma unroll
                 for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+#ifdef EXL3_MG_NODEC
+                #pragma unroll
+                for (int q = 0; q < 16; ++q) pk[q] = wv[q % (KB + 1)] ^ (0x3c003c00u + q);
+                if constexpr (false)
+#else
                 if constexpr (CB == 2) mul1_pairs<K>(wv, pk);
                 else
+#endif
                 {
                     uint32_t raw[32];
                     raw32<K, CB>(wv, raw, a3, b3);
@@ -620,8 +630,13 @@ void moeg_kernel(const GemmGroupArgs g)
                     {
                         if (r >= rg) break;
                         const h8v b = bx[h][r];
+#ifdef EXL3_MG_NOMFMA
+                        acc[0][r][0] += __uint_as_float(a0.x ^ a0.y ^ a0.z ^ a0.w) + (float) b[0];
+                        acc[1][r][0] += __uint_as_float(a1.x ^ a1.y ^ a1.z ^ a1.w) + (float) b[1];
+#else
                         acc[0][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a0), b, acc[0][r], 0, 0, 0);
                         acc[1][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a1), b, acc[1][r], 0, 0, 0);
+#endif
                     }
                 }
                 if ((d + 1) % XU == 0)
@@ -638,18 +653,52 @@ void moeg_kernel(const GemmGroupArgs g)
         // 32 w + 16 (i/8) + i%8 + 8 c, row 16 r + nn; rows meet in LDS for coalesced stores
         const int kc = k / 128;
         const float* ps = (mat ? g.psum[1] : g.psum[0]) + (size_t) row0 * kc;
+        // MUL1 row sums sum(x) from the 128-chunk sums: lane quarter q4 = lane / 16 adds chunks
+        // q4, q4 + 4, ... of its row, all groups' loads issued together, then the quarters
+        // combine in a fixed order (q4 0 + 1, 2 + 3, then the pairs)
+        float sxr[R];
+        if (CB == 2)
+        {
+            constexpr int PQ = 8;                             // loads in flight per lane and group
+            #pragma unroll
+            for (int r = 0; r < R; ++r) sxr[r] = 0.0f;
+            const int q4 = lane >> 4;
+            for (int c0 = 0; c0 < kc; c0 += 4 * PQ)
+            {
+                float v[R][PQ];
+                #pragma unroll
+                for (int r = 0; r < R; ++r)
+                {
+                    const float* pr = ps + (size_t) min(16 * r + (lane & 15), M - 1) * kc;
+                    #pragma unroll
+                    for (int i = 0; i < PQ; ++i)
+                    {
+                        const int c = c0 + 4 * i + q4;
+                        v[r][i] = *to_global(pr + min(c, kc - 1));
+                    }
+                }
+                #pragma unroll
+                for (int r = 0; r < R; ++r)
+                {
+                    #pragma unroll
+                    for (int i = 0; i < PQ; ++i)
+                        if (c0 + 4 * i + q4 < kc) sxr[r] += v[r][i];
+                }
+            }
+            #pragma unroll
+            for (int r = 0; r < R; ++r)
+            {
+                float t = sxr[r] + __shfl_xor(sxr[r], 16, 64);
+                t += __shfl_xor(t, 32, 64);
+                sxr[r] = t * (float) as_h(0xc931);
+            }
+        }
         #pragma unroll
         for (int r = 0; r < R; ++r)
         {
             if (r >= rg) break;
             const int row = 16 * r + (lane & 15);
-            float sx = 0.0f;
-            if (CB == 2)
-            {
-                const float* pr = ps + (size_t) min(row, M - 1) * kc;
-                for (int c = 0; c < kc; ++c) sx += *to_global(pr + c);
-                sx *= (float) as_h(0xc931);
-            }
+            const float sx = CB == 2 ? sxr[r] : 0.0f;
             #pragma unroll
             for (int c = 0; c < 2; ++c)
             {
