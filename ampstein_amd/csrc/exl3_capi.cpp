@@ -959,19 +959,25 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     const int64_t pool64 = (int64_t) concurrency * max_tokens_per_expert;
     const int pool = (int) std::min<int64_t>(pool64, (int64_t) num_assign);   // rows a pass can hold
     // rows per MFMA tile from the mean rows per expert: one tile covers most experts, with
-    // little padding (the weights are decoded once per tile).  Measured on MI355X, 256 experts
-    // 4096 -> 2048 -> 4096, top-8: best tile 64 up to a mean of 32 rows, 128 at 64, 256 at 128
+    // little padding (the weights are decoded once per tile).  LDS-tiled kernel, measured on
+    // MI355X, 256 experts 4096 -> 2048 -> 4096, top-8: best tile 64 up to a mean of 32 rows,
+    // 128 at 64, 256 at 128
     const int mean_rows = num_assign / std::max(num_experts, 1);
     // GEMM kernel: the register-decode moeg_kernel (default) or the LDS-tiled gemm_kernel
     // (EXL3_AMD_MOE_GEMM=lds).  moeg rows per tile: one tile per expert for most experts
     const char* gsel = getenv("EXL3_AMD_MOE_GEMM");
     const bool reg_gemm = !(gsel && !strcmp(gsel, "lds"));
-    int tile_rows = reg_gemm ? (mean_rows <= 20 ? 32 : (mean_rows <= 80 ? 64 : 128))
+    // moeg: the smallest tile holding ~1.5x the mean rows (the largest expert, for top-k routing
+    // of random tokens).  Measured, 256 experts 4096 -> 2048 -> 4096, top-8: T = 512 (mean 16,
+    // max 27) best at 32; T = 2048 (mean 64, max 91) best at 96: 2.32 ms against 2.49 at 64 and
+    // 2.54 at 128 (fewer tiles read each expert's weights fewer times; 96 keeps 3 waves per SIMD)
+    const int want = mean_rows * 3 / 2;
+    int tile_rows = reg_gemm ? (want <= 32 ? 32 : (want <= 64 ? 64 : (want <= 96 ? 96 : 128)))
                              : (mean_rows <= 40 ? 64 : (mean_rows <= 96 ? 128 : 256));
     if (const char* e = getenv("EXL3_AMD_MOE_TILE_ROWS"))
     {
         const int v = atoi(e);
-        if (reg_gemm ? (v == 32 || v == 64 || v == 128) : (v == 64 || v == 128 || v == 256)) tile_rows = v;
+        if (reg_gemm ? (v == 32 || v == 64 || v == 96 || v == 128) : (v == 64 || v == 128 || v == 256)) tile_rows = v;
     }
     int grid_wgs = d->num_cus * 4;
     if (const char* e = getenv("EXL3_AMD_MOEG_WGS")) { const int v = atoi(e); if (v > 0) grid_wgs = v; }

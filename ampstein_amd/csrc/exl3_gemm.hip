@@ -486,7 +486,7 @@ int launch_gemm_group(const GemmGroupArgs& g, hipStream_t s)
 // take the (row tile, matrix) entries e with e % 8 == x, so all chunks of an entry share one L2.
 // Tuning, measured on MI355X (256 experts 4096 -> 2048 -> 4096, T = 512 / 2048): a trellis ring of
 // 2 units, X loaded 2 units ahead, one unit per barrier, B operands read before the decode, and
-// 4 waves per SIMD for 32- and 64-row tiles; barrier count, prefetch depth and occupancy moved
+// 4 waves per SIMD for 32- and 64-row tiles (3 for 96, 2 for 128); barrier count, prefetch depth and occupancy moved
 // the time by under 3 %: the decode VALU and the MFMAs, which issue mostly serially on a SIMD,
 // bound the kernel.
 constexpr int MG_PF = 2, MG_XD = 2, MG_XU = 1;
@@ -505,7 +505,7 @@ template <int R> struct MgLds
 
 template <int K, int CB, int R>
 __global__ __launch_bounds__(MG_THREADS)
-__attribute__((amdgpu_waves_per_eu(R <= 4 ? 4 : 2, R <= 4 ? 4 : 2)))
+__attribute__((amdgpu_waves_per_eu(R <= 4 ? 4 : (R <= 6 ? 3 : 2), R <= 4 ? 4 : (R <= 6 ? 3 : 2))))
 void moeg_kernel(const GemmGroupArgs g)
 {
     using LD = MgLds<R>;
@@ -561,11 +561,7 @@ void moeg_kernel(const GemmGroupArgs g)
             for (int i = 0; i < XCP; ++i)
             {
                 const int c = t + MG_THREADS * i, row = c / PCH;
-#ifdef EXL3_MG_NOX
-                x[i] = *to_global((const u32x4*) (A + (c % PCH) * 8));
-#else
                 x[i] = *to_global((const u32x4*) (A + (size_t) min(row, M - 1) * k + min(ph, phases - 1) * 64 * XU + (c % PCH) * 8));
-#endif
             }
         };
         auto xstore = [&](const u32x4* x, int buf) {
@@ -605,14 +601,8 @@ void moeg_kernel(const GemmGroupArgs g)
                 uint32_t wv[KB + 1], pk[16];
                 #pragma unroll
                 for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
-#ifdef EXL3_MG_NODEC
-                #pragma unroll
-                for (int q = 0; q < 16; ++q) pk[q] = wv[q % (KB + 1)] ^ (0x3c003c00u + q);
-                if constexpr (false)
-#else
                 if constexpr (CB == 2) mul1_pairs<K>(wv, pk);
                 else
-#endif
                 {
                     uint32_t raw[32];
                     raw32<K, CB>(wv, raw, a3, b3);
@@ -630,13 +620,8 @@ void moeg_kernel(const GemmGroupArgs g)
                     {
                         if (r >= rg) break;
                         const h8v b = bx[h][r];
-#ifdef EXL3_MG_NOMFMA
-                        acc[0][r][0] += __uint_as_float(a0.x ^ a0.y ^ a0.z ^ a0.w) + (float) b[0];
-                        acc[1][r][0] += __uint_as_float(a1.x ^ a1.y ^ a1.z ^ a1.w) + (float) b[1];
-#else
                         acc[0][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a0), b, acc[0][r], 0, 0, 0);
                         acc[1][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a1), b, acc[1][r], 0, 0, 0);
-#endif
                     }
                 }
                 if ((d + 1) % XU == 0)
@@ -733,6 +718,7 @@ int launch_moeg(const GemmGroupArgs& g, hipStream_t s)
     const dim3 gr((unsigned) grid), block(MG_THREADS);
     if (g.tile_rows <= 32) hipLaunchKernelGGL((moeg_kernel<K, CB, 2>), gr, block, 0, s, g);
     else if (g.tile_rows <= 64) hipLaunchKernelGGL((moeg_kernel<K, CB, 4>), gr, block, 0, s, g);
+    else if (g.tile_rows <= 96) hipLaunchKernelGGL((moeg_kernel<K, CB, 6>), gr, block, 0, s, g);
     else hipLaunchKernelGGL((moeg_kernel<K, CB, 8>), gr, block, 0, s, g);
     return (int) hipGetLastError();
 }

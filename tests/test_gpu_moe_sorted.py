@@ -157,6 +157,32 @@ def test_exl3_moe(orc, case):
     assert err < 2e-3
 
 
+TILE_CASES = [
+    # ~80 rows per expert: 32- and 64-row tiles split every expert, 96 and 128 hold most whole
+    ("mul1-mixed-80rows", 4, 256, 256, 160, 2, 2, [2, 3, 4, 2], 0, 0.0, 256, 1, 0, 1 << 30, 0),
+    ("mul1-k2.5-80rows", 4, 256, 384, 160, 2, 2, [2.5] * 4, 1, 0.0, 256, 1, 0, 1 << 30, 0),
+]
+
+
+@pytest.mark.parametrize("tile_rows", [32, 64, 96, 128])
+@pytest.mark.parametrize("case", TILE_CASES, ids=[c[0] for c in TILE_CASES])
+def test_exl3_moe_tile_rows(orc, monkeypatch, case, tile_rows):
+    """Every row-tile size of the grouped GEMM (16-row groups R = 2, 4, 6, 8) against the model."""
+    monkeypatch.setenv("EXL3_AMD_MOE_TILE_ROWS", str(tile_rows))
+    name, E, H, I, T, topk, cb, Ks, act, limit, max_tok, conc, lo, hi, sentinel = case
+    es = ExpertSet(torch, orc, E, H, I, H, Ks, cb, seed=TILE_CASES.index(case) + 71)
+    x = np.random.default_rng(7).standard_normal((T, H)).astype(np.float16)
+    rt = routing(T, E, topk, seed=len(name) + 1, sentinel=sentinel)
+    flat, order, inv, token_sorted, weight_sorted, count, start = rt
+    out, _, _, elig = run_moe(es, x, rt, max_tok, conc, lo, hi, act, limit, Ks)
+    ref, _ = model(es, x, flat, token_sorted, weight_sorted, count, start, max_tok, lo, hi, act, limit)
+    y = out.cpu().numpy().astype(np.float64)
+    assert count.max() > 64, "the case must put more than 64 rows on some expert"
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    print(f"  {name} tile {tile_rows}: max rows {count.max()}, rel err {err:.2e}", flush=True)
+    assert err < 2e-3
+
+
 def test_exl3_moe_slots_and_gather(orc):
     """Deterministic mode: slot outputs against the model per (expert, row); then the fixed-order
     gather sums them into the token rows; two runs are bit-identical."""
