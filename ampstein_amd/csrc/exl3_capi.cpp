@@ -983,7 +983,15 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     if (const char* e = getenv("EXL3_AMD_MOEG_WGS")) { const int v = atoi(e); if (v > 0) grid_wgs = v; }
     const int rt_cap = pool / tile_rows + std::min(num_experts, pool) + 1;
     const size_t ps_floats = (size_t) pool * (2 * (hidden_dim / 128) + intermediate_dim / 128);
-    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1) + ps_floats;
+    // token-major output lists (atomic mode): starts, positions, build space, position -> row
+    // (used when the per-call list build fits one workgroup's LDS; else the atomic output kernel)
+    // (EXL3_AMD_MOE_OUT=atomic forces the atomic output kernel)
+    const char* omode = getenv("EXL3_AMD_MOE_OUT");
+    const bool tok_mode = !output_scratch && exl3k_moes_tokens_lds(bsz, num_assign) <= 150 * 1024
+                          && !(omode && !strcmp(omode, "atomic"));
+    const size_t tok_ints = tok_mode ? (size_t) (bsz + 1) + 2 * (size_t) num_assign : 0;
+    const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1) + ps_floats
+                         + tok_ints;
     if (ws_ints * 4 > WS_PARTIAL_BYTES) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe: pool exceeds the library workspace");
 
     MoesArgs a;
@@ -1011,6 +1019,13 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     a.ps_d = a.ps_u + (size_t) pool * (hidden_dim / 128);
     a.rt_cap = rt_cap;
     a.tile_rows = tile_rows;
+    a.bsz = bsz;
+    if (tok_mode)
+    {
+        a.tok_start = (int*) (a.ps_d + (size_t) pool * (intermediate_dim / 128));
+        a.tok_pos = a.tok_start + (bsz + 1);
+        a.inv_row = a.tok_pos + num_assign;
+    }
 
     typedef int (*group_fn)(const GemmGroupArgs&, int, hipStream_t);
     static const group_fn gfn_lds[MOES_RATES] = {
@@ -1060,6 +1075,8 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
         return 0;
     };
     const int cus = d->num_cus;
+    if (a.tok_start)
+        if (int rc = exl3k_moes_tokens(a, s)) return hip_fail(rc, "exl3_moe");
     for (int row0 = 0; row0 < num_assign; row0 += pool)
     {
         int rc = exl3k_moes_plan(a, row0, s);

@@ -156,6 +156,12 @@ struct MoesArgs
     int tile_rows;              // rows per row tile
     float *ps_g, *ps_u;         // workspace: (pool_rows, H / 128) sums of each staged 128-chunk
     float* ps_d;                // workspace: (pool_rows, I / 128) the same for the down input
+    // token-major output (atomic mode): per-token lists of sorted positions and, per pass, the
+    // pool row of each position
+    int bsz;                    // tokens (rows of x and out)
+    int* tok_start;             // workspace: (bsz + 1) list starts
+    int* tok_pos;               // workspace: (num_assign) sorted positions, ascending per token
+    int* inv_row;               // workspace: (num_assign) pool row of a position in the current pass
 };
 
 struct MoesGatherArgs
@@ -175,6 +181,8 @@ int exl3k_moes_plan(const MoesArgs& a, int pass_row0, hipStream_t s);
 int exl3k_moes_gather(const MoesArgs& a, int cus, hipStream_t s);
 int exl3k_moes_act(const MoesArgs& a, int cus, hipStream_t s);
 int exl3k_moes_out(const MoesArgs& a, int cus, hipStream_t s);
+int exl3k_moes_tokens(const MoesArgs& a, hipStream_t s);
+size_t exl3k_moes_tokens_lds(int bsz, int num_assign);       // bytes; at most 160 KiB
 int exl3k_moes_sum(const MoesGatherArgs& a, hipStream_t s);
 
 // Fused decode-shaped MoE (exl3_moe_coop): route/rotate, gate/up GEMV + activation, down GEMV +

@@ -240,9 +240,78 @@ void moes_plan_kernel(MoesArgs a, int pass_row0)
             if (info0 >= a.num_assign) info0 = -1;
         }
         a.rowinfo[3 * r] = info0;
+        if (info0 >= 0 && a.inv_row) a.inv_row[info0] = r;
         a.rowinfo[3 * r + 1] = e;
         a.rowinfo[3 * r + 2] = j;
     }
+}
+
+// ------------------------------------------------------------------------------- token lists
+// Sorted positions of every token, ascending (one workgroup, once per call), all in LDS:
+// count per token (LDS atomics), exclusive scan, scatter through the running offsets, an
+// insertion sort of each (top-k long) list -- so that the output kernel sums a token's rows in a
+// fixed order -- then coalesced copies out.  LDS: bsz + num_assign + PLAN_THREADS ints (the host
+// checks the size).
+__global__ __launch_bounds__(PLAN_THREADS)
+void moes_tokens_kernel(MoesArgs a)
+{
+    extern __shared__ __align__(16) int sm[];
+    const int t = threadIdx.x, T = a.bsz, N = a.num_assign;
+    int* s_cnt = sm;                  // counts, then start offsets, then end offsets
+    int* s_pos = sm + T;
+    int* s_tmp = sm + T + N;
+    for (int i = t; i < T; i += PLAN_THREADS) s_cnt[i] = 0;
+    __syncthreads();
+    for (int p = t; p < N; p += PLAN_THREADS)
+    {
+        const int64_t tk = a.token_sorted[p];
+        if (tk >= 0 && tk < T) atomicAdd(&s_cnt[tk], 1);
+    }
+    __syncthreads();
+    // blocked exclusive scan: thread t owns tokens [t seg, (t + 1) seg)
+    const int seg = (T + PLAN_THREADS - 1) / PLAN_THREADS;
+    const int lo = min(T, t * seg), hi = min(T, lo + seg);
+    int sum = 0;
+    for (int i = lo; i < hi; ++i) sum += s_cnt[i];
+    s_tmp[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < PLAN_THREADS; off <<= 1)
+    {
+        const int v = t >= off ? s_tmp[t - off] : 0;
+        __syncthreads();
+        s_tmp[t] += v;
+        __syncthreads();
+    }
+    int run = s_tmp[t] - sum;
+    for (int i = lo; i < hi; ++i)
+    {
+        const int c = s_cnt[i];
+        s_cnt[i] = run;
+        a.tok_start[i] = run;
+        run += c;
+    }
+    if (t == PLAN_THREADS - 1) a.tok_start[T] = s_tmp[t];
+    __syncthreads();
+    for (int p = t; p < N; p += PLAN_THREADS)
+    {
+        const int64_t tk = a.token_sorted[p];
+        if (tk >= 0 && tk < T) s_pos[atomicAdd(&s_cnt[tk], 1)] = p;     // s_cnt ends at the list ends
+    }
+    __syncthreads();
+    for (int i = t; i < T; i += PLAN_THREADS)
+    {
+        const int e1 = s_cnt[i], e0 = i ? s_cnt[i - 1] : 0;
+        for (int x = e0 + 1; x < e1; ++x)
+        {
+            const int v = s_pos[x];
+            int y = x - 1;
+            while (y >= e0 && s_pos[y] > v) { s_pos[y + 1] = s_pos[y]; --y; }
+            s_pos[y + 1] = v;
+        }
+    }
+    __syncthreads();
+    const int total = T ? s_cnt[T - 1] : 0;
+    for (int i = t; i < total; i += PLAN_THREADS) a.tok_pos[i] = s_pos[i];
 }
 
 // ------------------------------------------------------------------------------- gather + rotate
@@ -499,6 +568,81 @@ void moes_out_kernel(MoesArgs a)
     }
 }
 
+// Token-major output (atomic-free): wave w takes tokens w, w + waves, ...; for each of the
+// token's sorted positions whose row is in this pass (inv_row, confirmed by rowinfo) it adds
+// that row's down output -- rotated, times the routing weight and svh, as the slot form computes
+// it -- into fp32 registers, 8 four-chunk groups at a time, then adds the sum into out once.
+// One writer per token and pass, and a fixed summation order.
+constexpr int OUTT_G = 8;                 // 4-chunk groups held in registers per sweep
+
+__global__ __launch_bounds__(256)
+void moes_outt_kernel(MoesArgs a)
+{
+    const int lane = threadIdx.x & 63, g = lane & 15, sub = lane >> 4;
+    const int chunks = a.H / 128, groups = (chunks + 3) / 4;
+    const int nw = gridDim.x * 4;
+    for (int tok = wave_id(); tok < a.bsz; tok += nw)
+    {
+        const int p0 = a.tok_start[tok], p1 = a.tok_start[tok + 1];
+        if (p0 == p1) continue;
+        for (int g0 = 0; g0 < groups; g0 += OUTT_G)
+        {
+            float acc[OUTT_G][8];
+            #pragma unroll
+            for (int q = 0; q < OUTT_G; ++q)
+                #pragma unroll
+                for (int i = 0; i < 8; ++i) acc[q][i] = 0.0f;
+            bool any = false;
+            for (int pi = p0; pi < p1; ++pi)
+            {
+                const int pos = a.tok_pos[pi];
+                const int r = a.inv_row[pos];
+                if (r < 0 || r >= a.pool_rows || a.rowinfo[3 * r] != pos) continue;   // (uniform) not in this pass
+                any = true;
+                const int e = a.rowinfo[3 * r + 1];
+                const float rs = R128 * (float) as_h(a.weight_sorted[pos]);
+                const uint16_t* svh_d = (const uint16_t*) a.d_svh[e];
+                u32x4 yv[OUTT_G], sv[OUTT_G];
+                #pragma unroll
+                for (int q = 0; q < OUTT_G; ++q)
+                {
+                    const int col = 128 * min(4 * (g0 + q) + sub, chunks - 1) + 8 * g;
+                    yv[q] = ld16(a.ts_g + (size_t) r * a.H + col);
+                    sv[q] = ld16(svh_d + col);
+                }
+                #pragma unroll
+                for (int q = 0; q < OUTT_G; ++q)
+                {
+                    uint32_t w[4], s[4];
+                    float f[8];
+                    unpack8(yv[q], w);
+                    to_f32(w, f);
+                    fwht128_g16(f, lane);
+                    unpack8(sv[q], s);
+                    #pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        const f16x2 svv = as_h2(s[j]);
+                        acc[q][2 * j] += (f[2 * j] * rs) * (float) svv.x;
+                        acc[q][2 * j + 1] += (f[2 * j + 1] * rs) * (float) svv.y;
+                    }
+                }
+            }
+            if (!any) continue;
+            #pragma unroll
+            for (int q = 0; q < OUTT_G; ++q)
+            {
+                const int c = 4 * (g0 + q) + sub;
+                if (c >= chunks) continue;
+                float* dst = a.out + (size_t) tok * a.H + 128 * c + 8 * g;
+                const f32x4 o0 = *(const f32x4*) dst, o1 = *(const f32x4*) (dst + 4);
+                *(f32x4*) dst = (f32x4) { o0.x + acc[q][0], o0.y + acc[q][1], o0.z + acc[q][2], o0.w + acc[q][3] };
+                *(f32x4*) (dst + 4) = (f32x4) { o1.x + acc[q][4], o1.y + acc[q][5], o1.z + acc[q][6], o1.w + acc[q][7] };
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------- fixed-order gather
 constexpr int GATHER_MAX_TOPK = 32;      // exl3_moe.cu:408 MOE_GATHER_MAX_TOPK
 
@@ -580,8 +724,31 @@ int exl3k_moes_act(const MoesArgs& a, int cus, hipStream_t s)
     return (int) hipGetLastError();
 }
 
+size_t exl3k_moes_tokens_lds(int bsz, int num_assign)
+{
+    return ((size_t) bsz + (size_t) num_assign + PLAN_THREADS) * 4;
+}
+
+int exl3k_moes_tokens(const MoesArgs& a, hipStream_t s)
+{
+    const size_t lds = exl3k_moes_tokens_lds(a.bsz, a.num_assign);
+    static bool attr = false;
+    if (!attr)
+    {
+        (void) hipFuncSetAttribute((const void*) moes_tokens_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    hipLaunchKernelGGL(moes_tokens_kernel, dim3(1), dim3(PLAN_THREADS), lds, s, a);
+    return (int) hipGetLastError();
+}
+
 int exl3k_moes_out(const MoesArgs& a, int cus, hipStream_t s)
 {
+    if (!a.scratch && a.tok_start)
+    {
+        hipLaunchKernelGGL(moes_outt_kernel, dim3(rows_grid(a.bsz, cus)), dim3(256), 0, s, a);
+        return (int) hipGetLastError();
+    }
     hipLaunchKernelGGL(moes_out_kernel, dim3(rows_grid(a.pool_rows, cus)), dim3(256), 0, s, a);
     return (int) hipGetLastError();
 }

@@ -157,6 +157,14 @@ def test_exl3_moe(orc, case):
     assert err < 2e-3
 
 
+@pytest.mark.parametrize("case", CASES[:3], ids=[c[0] for c in CASES[:3]])
+def test_exl3_moe_atomic_output(orc, monkeypatch, case):
+    """The atomic output kernel (used when the per-token lists do not fit one workgroup's LDS),
+    forced: the same cases, the same bar."""
+    monkeypatch.setenv("EXL3_AMD_MOE_OUT", "atomic")
+    test_exl3_moe(orc, case)
+
+
 TILE_CASES = [
     # ~80 rows per expert: 32- and 64-row tiles split every expert, 96 and 128 hold most whole
     ("mul1-mixed-80rows", 4, 256, 256, 160, 2, 2, [2, 3, 4, 2], 0, 0.0, 256, 1, 0, 1 << 30, 0),
