@@ -329,7 +329,7 @@ __device__ void weighted_reduce(const GemvArgs& g, int chunk, bool via_l2)
 // the partials -- in a fixed order -- rotates and stores.  Weighted mode adds a second hand-off
 // per chunk over all slots, whose last arrival runs the token-group reduction.
 __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int chunk, int slot, int splits,
-                               const float* res, float* tmp, int* flag, uint32_t svp)
+                               const float* res, float* tmp, int* flag, uint32_t svp, int rs = 128)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = g.m;
@@ -338,7 +338,7 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
     {
         float* pbase = g.partials + ((size_t) j * chunks + chunk) * splits * m * 128;
         for (int e = threadIdx.x; e < m * 32; e += GEMV_THREADS)
-            *to_global_w((f32x4*) (pbase + (size_t) slot * m * 128 + 4 * e)) = *(const f32x4*) (res + 4 * e);
+            *to_global_w((f32x4*) (pbase + (size_t) slot * m * 128 + 4 * e)) = *(const f32x4*) (res + (e >> 5) * rs + 4 * (e & 31));
         if (!g.xcd) return;
         GEMV_STAMP(g, 4, 0);
         if (!arrive_last(g.counters + ((size_t) j * chunks + chunk) * 32, splits, flag)) return;
@@ -387,7 +387,7 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
         for (int r = wave; r < m; r += GEMV_WAVES)
         {
             const int col = chunk * 128 + 2 * lane;
-            store_output(res[r * 128 + 2 * lane], res[r * 128 + 2 * lane + 1], v.C, g.c_fp32, v.svh != nullptr,
+            store_output(res[r * rs + 2 * lane], res[r * rs + 2 * lane + 1], v.C, g.c_fp32, v.svh != nullptr,
                          svp, (size_t) r * v.stride + col, lane, v.scale);
         }
     }
@@ -1060,8 +1060,9 @@ void gemvm_kernel(const GemvArgs g)
     const int ks0 = slot * SB;
     const int xs_stride = SB * 16 + 4;                    // u32 per row; +4: rows 16 bytes apart in the banks
     uint32_t* xs = smem;                                  // [MT][xs_stride] dup pairs, xperm order
-    float* res = (float*) (smem + MT * xs_stride);        // [MT][128]
-    float* tmp = res + MT * 128;                          // epilogue scratch: 2 x (m x 64 column pairs), >= 512
+    constexpr int RS = 132;                               // res row stride: 16-byte column groups of 16 rows in distinct banks
+    float* res = (float*) (smem + MT * xs_stride);        // [MT][RS]
+    float* tmp = res + MT * RS;                           // epilogue scratch: 2 x (m x 64 column pairs), >= 512
 
     // Input rotation of the workgroup's SB / 8 chunks, every row, into xs (dup pairs, xperm order).
     // Job q of wave w: row / chunk (w + 4 q) of m x SB / 8.  The first XB jobs' input and suh loads
@@ -1168,17 +1169,11 @@ void gemvm_kernel(const GemvArgs g)
     const int n = lane & 15;
     if (n < m)
     {
+        // the lane's 4 values are columns 32 wave + 16 (q >> 1) + 4 (q & 1) + 8 c + 0..3, q = lane / 16
+        const int q = lane >> 4;
         #pragma unroll
         for (int c = 0; c < 2; ++c)
-        {
-            const float dv[4] = { acc[c].x, acc[c].y, acc[c].z, acc[c].w };
-            #pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                const int i = 4 * (lane >> 4) + e;
-                res[n * 128 + 32 * wave + 16 * (i >> 3) + (i & 7) + 8 * c] = dv[e];
-            }
-        }
+            *(f32x4*) (res + n * RS + 32 * wave + 16 * (q >> 1) + 4 * (q & 1) + 8 * c) = acc[c];
     }
     if (CB == 2)
     {
@@ -1196,10 +1191,13 @@ void gemvm_kernel(const GemvArgs g)
     {
         const float kinv = (float) as_h(0x1eee);
         for (int e = threadIdx.x; e < m * 128; e += GEMV_THREADS)
-            res[e] = res[e] * kinv + sumx[e / 128] * (float) as_h(0xc931);
+        {
+            float& rv = res[(e >> 7) * RS + (e & 127)];
+            rv = rv * kinv + sumx[e >> 7] * (float) as_h(0xc931);
+        }
         __syncthreads();
     }
-    block_epilogue(g, v, j, chunk, slot, splits, res, tmp, &flag, svp);
+    block_epilogue(g, v, j, chunk, slot, splits, res, tmp, &flag, svp, RS);
     GEMV_STAMP(g, 3, flag);
 }
 
@@ -1252,7 +1250,7 @@ int launch_gemv1(const GemvArgs& g, hipStream_t s)
 template <int K, int CB, int MT>
 int launch_gemvm_t(const GemvArgs& g, hipStream_t s)
 {
-    const size_t lds = ((size_t) MT * (g.slices_per_block * 16 + 4) + (size_t) MT * 128 + (MT * 128 > 512 ? MT * 128 : 512)) * 4;
+    const size_t lds = ((size_t) MT * (g.slices_per_block * 16 + 4) + (size_t) MT * 132 + (MT * 128 > 512 ? MT * 128 : 512)) * 4;
     return launch_common(g, s, [&](dim3 grid) {
         hipLaunchKernelGGL((gemvm_kernel<K, CB, MT>), grid, dim3(GEMV_THREADS), lds, s, g);
     });

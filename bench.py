@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE expert GEMV line")
     ap.add_argument("--no-qwen", action="store_true", help="skip the configs[2] Qwen-27B-class line")
     ap.add_argument("--pmc-child", nargs="?", const="gateup", default=None,
-                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe | moes")
+                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe | moes | qwenm")
     ap.add_argument("--summarize-pmc", metavar="PMC_DIR", nargs="+",
                     help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
                          "directories (one per counter pass) and exit")
@@ -544,7 +544,9 @@ def pmc_child(workload="decode"):
       gateup  -- the stacked gate/up mgemm alone, 2 x 4 launches (the traffic passes);
       prefill -- the MFMA GEMM at 2048 rows on 8192 -> 28672 and 28672 -> 8192;
       moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice;
-      moes    -- the token-sorted exl3_moe on the same experts, T = 512 and 2048."""
+      moes    -- the token-sorted exl3_moe on the same experts, T = 512 and 2048;
+      qwenm   -- the row-batched matrix-core GEMV (gemvm_kernel) on the configs[2] shapes 5120 -> 17408
+                 and 17408 -> 5120, K = 4 3INST, M = 4 and 8, twice each."""
     import torch
     from ampstein_amd import ops, bundles
     torch.cuda.set_device(0)
@@ -577,6 +579,14 @@ def pmc_child(workload="decode"):
         moe_bench(torch, reps=1, ms=(16,), token_sorted=False, graph=False)
     elif workload == "moes":
         moe_bench(torch, reps=1, ms=(), token_sorted=True, graph=False)
+    elif workload == "qwenm":
+        for si, (k, n) in enumerate(((5120, 17408), (17408, 5120))):
+            t, s, v = host_trellis(torch, k, n, 4, 5000 + si)
+            for m in (4, 8):
+                x = host_normal(torch, (m, k), 5010 + m)
+                C = torch.empty((m, n), dtype=torch.half, device="cuda")
+                for _ in range(2):
+                    ops.exl3_gemm(x, t, C, s, torch.empty_like(x), v)
     torch.cuda.synchronize()
     return 0
 
