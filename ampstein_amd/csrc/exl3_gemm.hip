@@ -19,8 +19,9 @@
 // compile-time offsets.  Weights are the reference's fp16 values exactly: 3INST / MCG lo + hi
 // rounded by one v_pk_add_f16 per pair, MUL1 by one v_pk_fma_f16 (codebook.cuh:57-90).
 //
-// LDS layouts are XOR-swizzled so that 16 lanes of every ds_read_b128 / ds_write_b128 touch
-// 16 distinct 16-byte bank groups.
+// LDS layouts are XOR-swizzled for the bank rules measured on MI355X: a ds_read_b128 serves 16
+// lanes at a time over 64 banks, a ds_write_b128 8 lanes at a time over 32 banks.  The trellis
+// words are staged with one 16-byte store per staging thread.
 //
 // Compiled once per K (EXL3_INST_K).
 #include <cstring>
@@ -62,7 +63,11 @@ __host__ __device__ constexpr int run_words() { return (run_rel<K>(25) + 16 + 31
 
 template <int K, int RB> struct GemmLds
 {
-    static constexpr int TW = tile_words(K) + 1;         // words per staged tile: ring word -1, then the tile
+    // words per staged tile: the tile's words, padded to a multiple of 4 so that each staging
+    // thread writes its 4 words with one ds_write_b128 (a tile always holds a multiple of 4 words).
+    // The padding at 8 and 2.5 bits spreads the decode's word reads over more LDS banks (the
+    // fewest bank conflicts among multiple-of-4 strides, measured on MI355X).
+    static constexpr int TW = tile_words(K) + ((K == 8 || K == 18) ? 4 : 0);
     static constexpr int A_U32 = RB * 16;                // A block: RB rows x 32 fp16
     static constexpr int B_U32 = 2 * BN * 8;             // B block: 2 slices x 256 columns x 16 fp16
     static constexpr int T_U32 = 2 * 16 * TW;            // 2 slices x 16 tiles
@@ -70,8 +75,8 @@ template <int K, int RB> struct GemmLds
     static constexpr int B0 = 2 * A_U32;
     static constexpr int T0 = B0 + 2 * B_U32;
     static constexpr int DUMMY = T0 + 2 * T_U32 + 4;     // (+4: a run may read one word past the last tile)
-    // (+8: sink for the stores of threads without trellis words; at least the epilogue's 64 x 256 fp32)
-    static constexpr int TOTAL = DUMMY + 8 > 64 * BN ? DUMMY + 8 : 64 * BN;
+    // (at least the epilogue's 64 x 256 fp32)
+    static constexpr int TOTAL = DUMMY > 64 * BN ? DUMMY : 64 * BN;
 };
 
 // 16-bit window at MSB-first bit offset REL of a normalised word run.
@@ -118,14 +123,16 @@ __device__ __forceinline__ uint32_t weight_pair(uint32_t r0, uint32_t r1)
     }
 }
 
-// Weights of rows 8h..8h+7 of one column from its normalised 26-position run.
+// Weights of rows 8h..8h+7 of one column from its normalised 26-position run: words tl[0..NW],
+// with tl[0] read from t0 instead (the tile's last word when the run starts in the ring word -1).
 template <int K, int CB>
-__device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, int sh)
+__device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, const uint32_t* __restrict__ t0, int sh)
 {
     constexpr int NW = run_words<K>();
     uint32_t rw[NW + 1], nw[NW + 1];
+    rw[0] = *t0;
     #pragma unroll
-    for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
+    for (int i = 1; i <= NW; ++i) rw[i] = tl[i];
     #pragma unroll
     for (int i = 0; i < NW; ++i) nw[i] = __builtin_amdgcn_alignbit(rw[i], rw[i + 1], 32 - sh);
     nw[NW] = 0u;
@@ -176,9 +183,12 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
 
 // Swizzled LDS offsets (u32 units).  A: row stride 16 u32 (4 chunks of 16 B), chunk ^= (row >> 2) & 3
 // (gfx950 LDS: 64 banks; the 16 lanes of a ds_read_b128 phase touch 16 distinct 16-byte groups).
-// B: per slice, column stride 8 u32 (2 chunks), chunk ^= (col >> 3) & 1.
+// B: per slice, column stride 8 u32 (2 chunks), chunk ^= ((col >> 2) ^ (col >> 3)) & 1.  The
+// decode's ds_write_b128 is served 8 lanes (8 consecutive columns) at a time over 32 banks, so
+// columns c and c + 4 must take different chunks; the MFMA reads (16 lanes over 64 banks) need
+// columns c and c + 8 to differ, which the (col >> 3) term keeps.
 __device__ __forceinline__ int a_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
-__device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ ((col >> 3) & 1)); }
+__device__ __forceinline__ int b_off(int slice, int col, int h) { return slice * (BN * 8) + col * 8 + 4 * (h ^ (((col >> 2) ^ (col >> 3)) & 1)); }
 
 template <int K, int CB, bool GROUP, int RB>
 __global__ __launch_bounds__(GT, 1)
@@ -244,20 +254,13 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     // ---- trellis staging: words 4t..4t+3 of the stage's 2 slices x 16 tiles (t < 64K)
     constexpr int TWD = tile_words(K);                   // u32 per tile
     const bool tload = t < 8 * TWD;
-    int t_lds[4], t_ring = LD::DUMMY + 4;
+    int t_lds;
     const uint32_t* t_src;
     {
         const int wi = 4 * (tload ? t : 0);
         const int s2 = wi / (16 * TWD), wj = wi - s2 * (16 * TWD);
         const int tile = wj / TWD, wk = wj - tile * TWD;
-        #pragma unroll
-        for (int e = 0; e < 4; ++e) t_lds[e] = LD::T0 + (s2 * 16 + tile) * LD::TW + 1 + wk + e;
-        if (wk + 3 == TWD - 1) t_ring = LD::T0 + (s2 * 16 + tile) * LD::TW;
-        if (!tload)
-        {
-            #pragma unroll
-            for (int e = 0; e < 4; ++e) t_lds[e] = LD::DUMMY + e;
-        }
+        t_lds = LD::T0 + (s2 * 16 + tile) * LD::TW + wk;    // 16-byte aligned: TW, wk and T0 are multiples of 4
         const int gtile = min(nb * 16 + tile, n / 16 - 1);   // columns past n: a valid tile, results dropped
         t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * TWD + wk;
     }
@@ -270,7 +273,8 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     const int dB0 = tile_end<K>(dbase) - 16;             // first window's first bit (< 0: ring)
     const int df = dB0 - 1 >= 0 ? (dB0 - 1) / 32 : -1;
     const int dsh = dB0 - 32 * df;                       // 1..32
-    const int d_src = LD::T0 + dtile * LD::TW + 1 + df;  // + slice * 16 * TW
+    const int d_src = LD::T0 + dtile * LD::TW + df;      // + slice * 16 * TW; word df + i, i >= 1
+    const int d_ring = LD::T0 + dtile * LD::TW + (df < 0 ? TWD - 1 : df);   // word df (-1: the tile's last)
     const int d_dst0 = LD::B0 + b_off(0, dc, dh), d_dst1 = LD::B0 + b_off(1, dc, dh);
 
     // ---- MFMA operand assignment
@@ -290,19 +294,13 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
         *(u32x4*) (lds + buf * LD::A_U32 + a_lds[0]) = a[0];
         if constexpr (AJ == 2) *(u32x4*) (lds + buf * LD::A_U32 + a_lds[1]) = a[1];
     };
-    // branch-free: threads without trellis words (and the ring copy of non-final words) write
-    // into a sink past the buffers (stage-relative offsets: buf 1 sinks land in the other sink)
-    const int sink_fix = LD::T_U32;
     auto store_trellis = [&](int buf, const u32x4& tw) {
-        uint32_t* T = lds + buf * LD::T_U32;
-        const int fix = (tload ? 0 : buf * sink_fix);
-        T[t_lds[0] - fix] = tw.x; T[t_lds[1] - fix] = tw.y; T[t_lds[2] - fix] = tw.z; T[t_lds[3] - fix] = tw.w;
-        T[t_ring - (t_ring >= LD::DUMMY ? buf * sink_fix : 0)] = tw.w;
+        if (tload) *(u32x4*) (lds + buf * LD::T_U32 + t_lds) = tw;
     };
     auto decode_slice = [&](int buf, int sl) {
         const uint32_t* T = lds + buf * LD::T_U32;
         uint32_t* B = lds + buf * LD::B_U32;
-        *(u32x4*) (B + (sl ? d_dst1 : d_dst0)) = decode_run<K, CB>(T + d_src + sl * 16 * LD::TW, dsh);
+        *(u32x4*) (B + (sl ? d_dst1 : d_dst0)) = decode_run<K, CB>(T + d_src + sl * 16 * LD::TW, T + d_ring + sl * 16 * LD::TW, dsh);
     };
     auto decode_stage = [&](int buf) { decode_slice(buf, 0); decode_slice(buf, 1); };
 
@@ -351,8 +349,9 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
                 constexpr int NW = run_words<K>();
                 const uint32_t* tl = lds + nxt * LD::T_U32 + d_src + sl * 16 * LD::TW;
                 uint32_t rw[NW + 1], nw[NW + 1], r[8], wp[4];
+                rw[0] = lds[nxt * LD::T_U32 + d_ring + sl * 16 * LD::TW];
                 #pragma unroll
-                for (int i = 0; i <= NW; ++i) rw[i] = tl[i];
+                for (int i = 1; i <= NW; ++i) rw[i] = tl[i];
 #define EXL3_MFMA_STEP(mt, nt) \
                 __builtin_amdgcn_sched_barrier(0); \
                 if constexpr ((mt) < MT) \
