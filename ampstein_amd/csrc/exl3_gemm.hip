@@ -24,6 +24,7 @@
 // words are staged with one 16-byte store per staging thread.
 //
 // Compiled once per K (EXL3_INST_K).
+#include <cstdlib>
 #include <cstring>
 
 #include "exl3_common.cuh"
@@ -430,14 +431,241 @@ void gemm_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// LDS-DMA form of gemm_kernel for dense launches (256-row tiles, same tiling, decode schedule and
+// epilogue).  The A tile and the stage's trellis words go from global memory straight into LDS
+// with global_load_lds_dwordx4: no register staging and no ds_write for them.  Each has 4 LDS
+// buffers; the DMA for stage s + 3 (A) and s + 4 (trellis) is issued at the start of stage s, and
+// each wave waits for its own DMAs of the next stage (vmcnt, counted per wave) before the stage
+// barrier.  A lane's 16 bytes land at the wave's LDS block + 16 * lane, so the A swizzle is
+// applied by choosing which global chunk each lane loads.
+constexpr int DMA_D = 3;                                 // stages of DMA in flight
+constexpr int DMA_NB = DMA_D + 1;                         // LDS buffers for A and for trellis
+
+template <int K> struct DmaLds
+{
+    static constexpr int TWD = tile_words(K);
+    static constexpr int A_U32 = 256 * 16;                // A block: 256 rows x 32 fp16
+    static constexpr int B_U32 = 2 * BN * 8;              // decoded B block: 2 slices x 256 columns x 16 fp16
+    static constexpr int T_U32 = 2 * 16 * TWD;            // 2 slices x 16 tiles, unpadded
+    static constexpr int A0 = 0;
+    static constexpr int B0 = DMA_NB * A_U32;
+    static constexpr int T0 = B0 + 2 * B_U32;
+    static constexpr int END = T0 + DMA_NB * T_U32 + 4;    // (+4: a run may read one word past the last tile)
+    static constexpr int TOTAL = END > 64 * BN ? END : 64 * BN;
+};
+
+// s_waitcnt with vmcnt(n) and lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+#define EXL3_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int K, int CB>
+__global__ __launch_bounds__(GT, 1)
+void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ trellis, void* __restrict__ C,
+                     const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+{
+    using LD = DmaLds<K>;
+    constexpr int RB = 256, MT = 4, TWD = tile_words(K), D = DMA_D, NB = DMA_NB;
+    __shared__ __align__(16) uint32_t lds[LD::TOTAL];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = threadIdx.x;
+    const int NST = k / 32;
+    const int nbn = (n + BN - 1) / BN;
+    const int nmb = (M + RB - 1) / RB;
+    int nb, mb;
+    if (nbn % 8 == 0)
+    {
+        const int x = blockIdx.x % 8, r = blockIdx.x / 8;
+        nb = x + 8 * (r / nmb);
+        mb = r % nmb;
+    }
+    else
+    {
+        nb = blockIdx.x / nmb;
+        mb = blockIdx.x % nmb;
+    }
+
+    // A: wave w's DMAs j = 0, 1 fill the 1 KB blocks q = w + 8 j (rows 16 q .. 16 q + 15); lane L
+    // fills slot L, i.e. row 16 q + L / 4 and the chunk that a_off puts in slot L % 4
+    const u32x4* a_src[2];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j)
+    {
+        const int q = wave + 8 * j, row = 16 * q + (lane >> 2), ch = (lane & 3) ^ ((row >> 2) & 3);
+        a_src[j] = (const u32x4*) (Ain + (size_t) min(mb * RB + row, M - 1) * k + 8 * ch);
+    }
+    // trellis: thread t < 8 TWD copies words 4t .. 4t + 3 of the stage's 2 slices x 16 tiles
+    const bool tload = t < 8 * TWD;
+    const bool t_wave = 64 * wave < 8 * TWD;              // the wave issues a trellis DMA
+    const uint32_t* t_src;
+    {
+        const int wi = 4 * (tload ? t : 0);
+        const int s2 = wi / (16 * TWD), wj = wi - s2 * (16 * TWD);
+        const int tile = wj / TWD, wk = wj - tile * TWD;
+        const int gtile = min(nb * 16 + tile, n / 16 - 1);   // columns past n: a valid tile, results dropped
+        t_src = (const uint32_t*) trellis + ((size_t) s2 * (n / 16) + gtile) * TWD + wk;
+    }
+    const size_t t_stage = (size_t) 2 * (n / 16) * TWD;
+
+    auto issue_a = [&](int sa) {
+        const int c = min(sa, NST - 1);
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+            __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + LD::A0 + (sa % NB) * LD::A_U32 + 256 * (wave + 8 * j)), 16, 0, 0);
+    };
+    auto issue_t = [&](int st) {
+        const int c = min(st, NST - 1);
+        if (tload)
+            __builtin_amdgcn_global_load_lds((const void*) (t_src + c * t_stage),
+                                             (lds_ptr_t) (lds + LD::T0 + (st % NB) * LD::T_U32 + 256 * wave), 16, 0, 0);
+    };
+
+    // ---- decode assignment (as gemm_kernel, unpadded tiles)
+    const int dc = t & 255, dh = t >> 8;
+    const int dtile = dc >> 4, dcc = dc & 15;
+    const int dbase = 32 * (dcc & 7) + 4 * (dcc >> 3) + 2 * dh;
+    const int dB0 = tile_end<K>(dbase) - 16;
+    const int df = dB0 - 1 >= 0 ? (dB0 - 1) / 32 : -1;
+    const int dsh = dB0 - 32 * df;
+    const int d_src = LD::T0 + dtile * TWD + df;
+    const int d_ring = LD::T0 + dtile * TWD + (df < 0 ? TWD - 1 : df);
+    const int d_dst0 = LD::B0 + b_off(0, dc, dh), d_dst1 = LD::B0 + b_off(1, dc, dh);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    // prologue: T(0), then groups g = 0 .. D - 1 of (A(g), T(g + 1)); B(0) decoded from T(0)
+    issue_t(0);
+    #pragma unroll
+    for (int g = 0; g < D; ++g) { issue_a(g); issue_t(g + 1); }
+    if (t_wave) EXL3_VM_LGKM0(3 * D); else EXL3_VM_LGKM0(2 * D);
+    __builtin_amdgcn_s_barrier();
+    #pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+    {
+        const uint32_t* T = lds + sl * 16 * TWD;
+        *(u32x4*) (lds + (sl ? d_dst1 : d_dst0)) = decode_run<K, CB>(T + d_src, T + d_ring, dsh);
+    }
+    if (t_wave) EXL3_VM_LGKM0(3 * (D - 1)); else EXL3_VM_LGKM0(2 * (D - 1));
+    __builtin_amdgcn_s_barrier();
+
+    acc16 acc[MT][2];
+    #pragma unroll
+    for (int i = 0; i < MT; ++i) { acc[i][0] = (acc16) { }; acc[i][1] = (acc16) { }; }
+
+    for (int s = 0; s < NST; ++s)
+    {
+        // stage s + D's A and s + D + 1's trellis: their buffers were last read in stage s - 1
+        issue_a(s + D);
+        issue_t(s + D + 1);
+        const uint32_t* A = lds + LD::A0 + (s % NB) * LD::A_U32;
+        const uint32_t* B = lds + LD::B0 + (s & 1) * LD::B_U32;
+        const uint32_t* Tn = lds + ((s + 1) % NB) * LD::T_U32;
+        uint32_t* Bn = lds + ((s + 1) & 1) * LD::B_U32;
+        #pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+        {
+            h8v bv[2], av[MT];
+            #pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+                bv[nt] = __builtin_bit_cast(h8v, *(const u32x4*) (B + b_off(sl, 64 * wn + 32 * nt + l32, lh)));
+            #pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                av[mt] = __builtin_bit_cast(h8v, *(const u32x4*) (A + a_off((RB / 2) * wm + 32 * mt + l32, 2 * sl + lh)));
+            constexpr int NW = run_words<K>();
+            const uint32_t* tl = Tn + d_src + sl * 16 * TWD;
+            uint32_t rw[NW + 1], nw[NW + 1], r[8], wp[4];
+            rw[0] = Tn[d_ring + sl * 16 * TWD];
+            #pragma unroll
+            for (int i = 1; i <= NW; ++i) rw[i] = tl[i];
+#define EXL3_MFMA_STEP(mt, nt) \
+            __builtin_amdgcn_sched_barrier(0); \
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0); \
+            __builtin_amdgcn_sched_barrier(0);
+            EXL3_MFMA_STEP(0, 0)
+            #pragma unroll
+            for (int i = 0; i < NW; ++i) nw[i] = __builtin_amdgcn_alignbit(rw[i], rw[i + 1], 32 - dsh);
+            nw[NW] = 0u;
+            EXL3_MFMA_STEP(0, 1)
+            r[0] = cb_raw<CB>(win16<run_rel<K>(0)>(nw));
+            r[1] = cb_raw<CB>(win16<run_rel<K>(1)>(nw));
+            EXL3_MFMA_STEP(1, 0)
+            r[2] = cb_raw<CB>(win16<run_rel<K>(8)>(nw));
+            r[3] = cb_raw<CB>(win16<run_rel<K>(9)>(nw));
+            EXL3_MFMA_STEP(1, 1)
+            wp[0] = weight_pair<CB>(r[0], r[1]);
+            wp[1] = weight_pair<CB>(r[2], r[3]);
+            EXL3_MFMA_STEP(2, 0)
+            r[4] = cb_raw<CB>(win16<run_rel<K>(16)>(nw));
+            r[5] = cb_raw<CB>(win16<run_rel<K>(17)>(nw));
+            EXL3_MFMA_STEP(2, 1)
+            r[6] = cb_raw<CB>(win16<run_rel<K>(24)>(nw));
+            r[7] = cb_raw<CB>(win16<run_rel<K>(25)>(nw));
+            EXL3_MFMA_STEP(3, 0)
+            wp[2] = weight_pair<CB>(r[4], r[5]);
+            wp[3] = weight_pair<CB>(r[6], r[7]);
+            EXL3_MFMA_STEP(3, 1)
+#undef EXL3_MFMA_STEP
+            *(u32x4*) (Bn + (sl ? d_dst1 : d_dst0)) = (u32x4) { wp[0], wp[1], wp[2], wp[3] };
+        }
+        // the next stage's A and trellis (issued D stages ago) have landed, this stage's B stores
+        // are done: then the barrier
+        if (t_wave) EXL3_VM_LGKM0(3 * (D - 1)); else EXL3_VM_LGKM0(2 * (D - 1));
+        __builtin_amdgcn_s_barrier();
+    }
+    // no DMA may still write LDS when the epilogue reuses it
+    EXL3_VM_LGKM0(0);
+    __builtin_amdgcn_s_barrier();
+
+    // ---- epilogue (as gemm_kernel)
+    float* E = (float*) lds;                              // [64][256] fp32
+    const bool has_svh = svh != nullptr;
+    #pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+    {
+        #pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+        {
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    E[(32 * wm + 8 * j + 4 * lh + i) * BN + 64 * wn + 32 * nt + l32] = acc[mt][nt][4 * j + i];
+            }
+        }
+        __syncthreads();
+        #pragma unroll 2
+        for (int q = 0; q < 16; ++q)
+        {
+            const int rc = wave * 16 + q;
+            const int er = rc >> 1, ch = rc & 1;
+            const int row = mb * RB + (RB / 2) * (er >> 5) + 32 * mt + (er & 31);
+            const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
+            const int col = nb * BN + 128 * ch + 2 * lane;
+            if (nb * BN + 128 * ch >= n) continue;
+            const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
+        }
+        __syncthreads();
+    }
+}
+
 template <int K, int CB>
 int launch_gemm(const GemmArgs& g, hipStream_t s)
 {
     const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     GemmGroupArgs none;
     memset(&none, 0, sizeof(none));
-    hipLaunchKernelGGL((gemm_kernel<K, CB, false, BM>), dim3(blocks), dim3(GT), 0, s,
-                       g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, none);
+    static const int dma = [] { const char* e = getenv("EXL3_AMD_GEMM_DMA"); return e ? atoi(e) : 1; }();
+    if (dma)
+        hipLaunchKernelGGL((gemm_dma_kernel<K, CB>), dim3(blocks), dim3(GT), 0, s,
+                           g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32);
+    else
+        hipLaunchKernelGGL((gemm_kernel<K, CB, false, BM>), dim3(blocks), dim3(GT), 0, s,
+                           g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, none);
     return (int) hipGetLastError();
 }
 
