@@ -55,6 +55,25 @@ def test_gemm_parity_all_bitrates(torch_cuda, orc, K, cb):
     assert rel_err(y, ref) < TOL
 
 
+@pytest.mark.parametrize("K,cb,m,k,n", [(4, 0, 300, 512, 2048), (2, 1, 513, 1024, 384), (8, 2, 256, 256, 1024),
+                                         (2.5, 2, 40, 384, 256), (3, 0, 9, 128, 128)])
+def test_gemm_dma_and_register_staging(torch_cuda, orc, monkeypatch, K, cb, m, k, n):
+    """The LDS-DMA kernel (default) and the register-staged kernel (EXL3_AMD_GEMM_DMA=0) do the
+    same arithmetic in the same order: bit-identical outputs, both within the bar."""
+    torch = torch_cuda
+    L = synth.layer(k, n, K, cb, seed=900 + int(10 * K) + cb)
+    x = synth.activations(m, k, seed=901 + int(10 * K))
+    ys = []
+    for dma in ("1", "0"):
+        monkeypatch.setenv("EXL3_AMD_GEMM_DMA", dma)
+        tag, y, _ = run_gemm(torch, L, x, False)
+        assert tag == 91
+        ys.append(y)
+    assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
+    assert rel_err(ys[0], ref) < TOL
+
+
 @pytest.mark.parametrize("m,k,n", [(9, 128, 128), (256, 512, 1024), (300, 256, 384), (513, 1024, 1024)])
 @pytest.mark.parametrize("y_fp32", [False, True])
 def test_gemm_shapes(torch_cuda, orc, m, k, n, y_fp32):
