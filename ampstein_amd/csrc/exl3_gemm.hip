@@ -724,7 +724,7 @@ constexpr int MG_OW = 68;        // u32 per epilogue row: 128 fp16 + 16 bytes
 template <int R> struct MgLds
 {
     static constexpr int RT = 16 * R;                   // rows per tile
-    static constexpr int XBUF = RT * (32 * MG_XU + 4);  // staged rows of one phase (+ 16 bytes per row)
+    static constexpr int XBUF = RT * 32 * MG_XU;        // staged rows of one phase
     static constexpr int OUT = RT * MG_OW;
     static constexpr int MAIN = 2 * XBUF > OUT ? 2 * XBUF : OUT;
     static constexpr int TOTAL = MAIN;
@@ -779,7 +779,14 @@ void moeg_kernel(const GemmGroupArgs g)
         // X: one phase of XU units (64 XU k per row) at a time into LDS, double-buffered; phase
         // p + XD is loaded while phase p computes, phase p + 1 stored after it (one barrier per
         // phase)
-        constexpr int XU = MG_XU, XWD = 32 * XU + 4;      // row stride (u32): + 16 bytes, conflict-free B reads
+        constexpr int XU = MG_XU, XWD = 32 * XU;          // row stride (u32)
+        static_assert(XU == 1, "the X swizzle below covers one unit (8 chunks of 16 bytes) per row");
+        // 16-byte chunk c of staged row r sits at chunk c ^ s(r % 16), s(q) = (q ^ (q >> 3)) & 7: no
+        // LDS bank conflicts for the B-operand reads (16 rows x 4 chunks per instruction) nor for
+        // the row stores (measured on MI355X; a 16-byte row padding left 4 conflict cycles per
+        // read).  Depending on r % 16 only, the offsets of the other 16-row groups are constants.
+        auto xoff = [](int r, int c) { const int q = r & 15; return r * XWD + 4 * (c ^ ((q ^ (q >> 3)) & 7)); };
+        const int xb0 = xoff(lane & 15, 2 * (lane >> 4));     // h = 0; h = 1 is the next chunk: ^ 4
         constexpr int PCH = 8 * XU;                       // 16-byte chunks per row and phase
         constexpr int XCP = R * XU / 2;                   // chunk loads per thread and phase
         const int phases = units / XU;
@@ -797,7 +804,7 @@ void moeg_kernel(const GemmGroupArgs g)
             for (int i = 0; i < XCP; ++i)
             {
                 const int c = t + MG_THREADS * i;
-                *(u32x4*) (lds + buf * (LD::RT * XWD) + (c / PCH) * XWD + (c % PCH) * 4) = x[i];
+                *(u32x4*) (lds + buf * (LD::RT * XWD) + xoff(c / PCH, c % PCH)) = x[i];
             }
         };
         #pragma unroll
@@ -817,14 +824,14 @@ void moeg_kernel(const GemmGroupArgs g)
                 const int u = u0 + d;                     // (PF divides units: no tail)
                 const int ph = u / XU;
                 // this unit's B operands first: their LDS latency hides behind the decode
-                const uint32_t* xb = lds + (ph & 1) * (LD::RT * XWD) + (lane & 15) * XWD + (u % XU) * 32 + (lane >> 4) * 8;
+                const uint32_t* xb = lds + (ph & 1) * (LD::RT * XWD);
                 h8v bx[2][R];
                 #pragma unroll
                 for (int h = 0; h < 2; ++h)
                 {
                     #pragma unroll
                     for (int r = 0; r < R; ++r)
-                        bx[h][r] = __builtin_bit_cast(h8v, *(const u32x4*) (xb + 16 * r * XWD + 4 * h));
+                        bx[h][r] = __builtin_bit_cast(h8v, *(const u32x4*) (xb + 16 * r * XWD + (xb0 ^ (4 * h))));
                 }
                 uint32_t wv[KB + 1], pk[16];
                 #pragma unroll
