@@ -319,7 +319,7 @@ def prefill_bench(torch):
     # hipBLASLt / rocBLAS and are reported beside it as labelled comparisons
     return {"metric": "prefill GEMM TFLOPS at M=2048 (configs[3], 4 bpw 3INST)", "m": M,
             "value": round(best["fused"], 1), "unit": "TFLOPS",
-            "path": "fused: exl3_gemm m > 8, hand-written MFMA kernel (gemm_kernel)",
+            "path": "fused: exl3_gemm m > 8, hand-written MFMA kernel (gemm_dma_kernel)",
             "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best["fused"] / MFMA_F16_PEAK_TFLOPS, 4),
             "comparison_paths_TFLOPS": {"recon (reconstruct_had + hipBLASLt, reference routing)": round(best["recon"], 1),
                                         "recon_rotated (reconstruct_t + hipBLASLt + had128)": round(best["recon_rotated"], 1)},
