@@ -308,11 +308,12 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
         if (best < 0 || (long) bszm * chunks * (KS / best) > target) best = d;   // fewest blocks >= target
         if ((long) bszm * chunks * (KS / d) <= target) break;
     }
-    // M = 1 stream: 8 k-slices per wave (16 from k = 8192), the best split measured on MI355X for
-    // the Llama-3-8B shapes (4096 x {1024, 4096, 14336}, 14336 x 4096) at 1-3.5 waves per SIMD
+    // M = 1 stream: 4 k-slices per wave below k = 8192, 16 from there: the best splits measured
+    // on MI355X for the Llama-3-8B shapes in a captured sweep (4096 x 4096: 6.85 -> 6.45 us, the
+    // sliced q/k/v bundle 9.1 -> 7.9 us against 8 per wave; 14336 x 4096 best at 16)
     if (stream)
     {
-        int pref = k >= 8192 ? 64 : 32;
+        int pref = k >= 8192 ? 64 : 16;
         // more workgroups than one round of 4 per CU (stacked gate/up: 1792): double the split
         // while the count exceeds that round (measured: gate/up 26.7 -> 25.8 us at 896)
         while (ok_sb(2 * pref) && (long) bszm * chunks * (KS / pref) > 4L * num_cus) pref *= 2;
