@@ -283,14 +283,16 @@ __device__ __forceinline__ float xor_partner(float v, int lane)
 {
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
     uint32_t p;
-    if constexpr (M == 1) p = __builtin_amdgcn_update_dpp(0u, u, 0xB1, 0xf, 0xf, false);       // quad_perm [1,0,3,2]
-    else if constexpr (M == 2) p = __builtin_amdgcn_update_dpp(0u, u, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    // (full row and bank masks with a permutation inside each row: every lane is written, so
+    // v_mov_b32_dpp needs no old value, and none is materialised)
+    if constexpr (M == 1) p = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xf, 0xf, false);               // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) p = __builtin_amdgcn_mov_dpp(u, 0x4E, 0xf, 0xf, false);          // quad_perm [2,3,0,1]
     else if constexpr (M == 4)
     {
         p = __builtin_amdgcn_update_dpp(0u, u, 0x104, 0xf, 0x5, false);   // row_shl:4 into banks 0, 2
         p = __builtin_amdgcn_update_dpp(p, u, 0x114, 0xf, 0xa, false);    // row_shr:4 into banks 1, 3
     }
-    else if constexpr (M == 8) p = __builtin_amdgcn_update_dpp(0u, u, 0x128, 0xf, 0xf, false); // row_ror:8
+    else if constexpr (M == 8) p = __builtin_amdgcn_mov_dpp(u, 0x128, 0xf, 0xf, false);         // row_ror:8
     else if constexpr (M == 16)
     {
         const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);

@@ -187,8 +187,28 @@ __device__ __forceinline__ int rh_dw(int R, int cp) { return R * 64 + (cp ^ (((R
 template <int M>
 __device__ __forceinline__ f16x2 had_h2_stage(f16x2 v, int lane)
 {
+    // one v_pk_fma_f16 with a +-1 factor: exactly v + p (lower lane) or p - v (upper), one rounding
     const f16x2 p = as_h2(__builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, as_u32(v)), lane)));
-    return (lane & M) ? (p + (-v)) : (v + p);
+    const f16 sg = (lane & M) ? (f16) -1.0f : (f16) 1.0f;
+    const f16x2 sg2 = { sg, sg };
+    return __builtin_elementwise_fma(v, sg2, p);
+}
+
+// Stage-major over N independent values, so each DPP read has other values' work in front of it
+// instead of the read-after-write wait states of one chain.
+template <int N>
+__device__ __forceinline__ void had_h2x32_n(f16x2 (&v)[N], int lane)
+{
+    #pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = had_h2_stage<1>(v[i], lane);
+    #pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = had_h2_stage<2>(v[i], lane);
+    #pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = had_h2_stage<4>(v[i], lane);
+    #pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = had_h2_stage<8>(v[i], lane);
+    #pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = had_h2_stage<16>(v[i], lane);
 }
 
 __device__ __forceinline__ f16x2 had_h2x32(f16x2 v, int lane)
@@ -247,8 +267,7 @@ void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict
         v[1] = (d0 + d1) * rs2;
         v[2] = (s0 - s1) * rs2;
         v[3] = (d0 - d1) * rs2;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = had_h2x32(v[i], lane);
+        had_h2x32_n<4>(v, lane);
         #pragma unroll
         for (int i = 0; i < 4; ++i) blk[rh_dw(4 * t + i, cp)] = as_u32(v[i]);
     }
@@ -269,8 +288,10 @@ void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict
         f16x2 h23 = { (f16) (s0 - s1), (f16) (d0 - d1) };
         h01 = h01 * rs2;
         h23 = h23 * rs2;
-        h01 = had_h2x32(h01, lane);
-        h23 = had_h2x32(h23, lane);
+        f16x2 hh[2] = { h01, h23 };
+        had_h2x32_n<2>(hh, lane);
+        h01 = hh[0];
+        h23 = hh[1];
         const f16 su = as_h(suh[kb * 128 + R]);
         const f16x2 su2 = { su, su };
         h01 = (h01 * su2) * as_h2(sv01);
