@@ -306,6 +306,16 @@ __device__ __forceinline__ float xor_partner(float v, int lane)
     return __builtin_bit_cast(float, p);
 }
 
+// The same partner through the LDS crossbar (ds_swizzle_b32, bit mode: lane ^ M within each
+// 32-lane half; no LDS memory is touched), for M <= 16.  One instruction on the LDS pipe instead
+// of one or two VALU ops: for kernels whose VALU, not latency, is the limit.
+template <int M>
+__device__ __forceinline__ float xor_partner_sw(float v)
+{
+    static_assert(M >= 1 && M <= 16, "ds_swizzle xor reaches within 32 lanes");
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (M << 10)));
+}
+
 // One butterfly stage: lower lane a + b, upper lane a - b (a = lower element), one rounding each
 // (fma with a +-1 factor is exactly the sum or the difference).
 template <int M>

@@ -48,26 +48,30 @@ __device__ __forceinline__ void fwht8_inlane(float* e)
     }
 }
 
-template <int M>
+// SW: the partner through the LDS crossbar (ds_swizzle) instead of DPP: one LDS-pipe op instead
+// of one or two VALU ops, for the VALU-bound gather and activation kernels (activation 92 -> 80
+// us at T = 2048); the output kernel is latency-bound and keeps DPP.
+template <int M, bool SW>
 __device__ __forceinline__ void fwht8_stage(float* e, int lane)
 {
     const float sg = (lane & M) ? -1.0f : 1.0f;
     #pragma unroll
     for (int i = 0; i < 8; ++i)
     {
-        const float p = xor_partner<M>(e[i], lane);
+        const float p = SW ? xor_partner_sw<M>(e[i]) : xor_partner<M>(e[i], lane);
         e[i] = __builtin_fmaf(sg, e[i], p);
     }
 }
 
 // H128 of the 16-lane group's chunk (lane g holds elements 8g .. 8g+7), unscaled.
+template <bool SW = false>
 __device__ __forceinline__ void fwht128_g16(float* e, int lane)
 {
     fwht8_inlane(e);
-    fwht8_stage<1>(e, lane);
-    fwht8_stage<2>(e, lane);
-    fwht8_stage<4>(e, lane);
-    fwht8_stage<8>(e, lane);
+    fwht8_stage<1, SW>(e, lane);
+    fwht8_stage<2, SW>(e, lane);
+    fwht8_stage<4, SW>(e, lane);
+    fwht8_stage<8, SW>(e, lane);
 }
 
 __device__ __forceinline__ void unpack8(const u32x4& v, uint32_t* w)
@@ -371,7 +375,7 @@ void moes_gather_kernel(MoesArgs a)
                     hmul4(w, sw);                          // fp16 pre-scale
                     float f[8];
                     to_f32(w, f);
-                    fwht128_g16(f, lane);
+                    fwht128_g16<true>(f, lane);
                     #pragma unroll
                     for (int i = 0; i < 8; ++i) f[i] *= R128;
                     to_h(f, w);
@@ -436,7 +440,7 @@ void moes_act_kernel(MoesArgs a)
                 float f[8];
                 unpack8(uv[bq], u);
                 to_f32(u, f);
-                fwht128_g16(f, lane);
+                fwht128_g16<true>(f, lane);
                 #pragma unroll
                 for (int i = 0; i < 8; ++i) f[i] *= R128;
                 to_h(f, u);
@@ -446,7 +450,7 @@ void moes_act_kernel(MoesArgs a)
                 {
                     unpack8(gv[bq], gg);
                     to_f32(gg, f);
-                    fwht128_g16(f, lane);
+                    fwht128_g16<true>(f, lane);
                     #pragma unroll
                     for (int i = 0; i < 8; ++i) f[i] *= R128;
                     to_h(f, gg);
@@ -476,7 +480,7 @@ void moes_act_kernel(MoesArgs a)
                 unpack8(sd[bq], s);
                 hmul4(gg, s);                              // fp16 down pre-scale
                 to_f32(gg, f);
-                fwht128_g16(f, lane);
+                fwht128_g16<true>(f, lane);
                 #pragma unroll
                 for (int i = 0; i < 8; ++i) f[i] *= R128;
                 to_h(f, gg);
