@@ -38,7 +38,9 @@ __device__ __forceinline__ void fwht8_stage(float* e, int lane)
     #pragma unroll
     for (int i = 0; i < 8; ++i)
     {
-        const float p = xor_partner<M>(e[i], lane);
+        // partner through the LDS crossbar (ds_swizzle): fewer VALU ops than DPP, measured 4-13 %
+        // faster on 2048 x {8192, 28672} and 16384 x 4096 rotations
+        const float p = xor_partner_sw<M>(e[i]);
         e[i] = __builtin_fmaf(sg, e[i], p);
     }
 }
