@@ -274,7 +274,10 @@ __device__ __forceinline__ float xor_shfl(float v, int mask, int lane)
 }
 
 // silu(x) = x / (1 + exp(-x)) in fp32 (amp_silu_mul_kernel, src/torch/amp_kernels.cu:235-251).
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+// SiLU in fp32 from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each),
+// a few ops instead of the IEEE expf and division sequences; the fp16 result it feeds stays
+// within one ulp of the exact value (the reference's own SiLU is an fp16 h2exp / h2rcp form)
+__device__ __forceinline__ float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Value of lane (lane ^ M) without LDS: DPP quad permutes (M = 1, 2), two bank-masked row
 // shifts (M = 4), a row rotate (M = 8), gfx950 permlane swaps (M = 16, 32).

@@ -392,7 +392,7 @@ void moes_gather_kernel(MoesArgs a)
 }
 
 // ------------------------------------------------------------------------------- activation
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return silu_f32(x); }
 __device__ __forceinline__ float gelu_f(float x)
 {
     return 0.5f * x * (1.0f + tanhf(0.797884560803f * (x + 0.044715f * x * x * x)));
