@@ -21,6 +21,8 @@ _vp, _i32, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "exl3_amd_last_error": (ctypes.c_char_p, []),
     "exl3_amd_version": (_i32, []),
+    "exl3_amd_set_policy": (_i32, [_i32, _i32]),
+    "exl3_amd_get_policy": (_i32, [_i32]),
     "exl3_amd_init": (_i32, [_i32]),
     "exl3_amd_device_info": (_i32, [_i32, _vp, _vp]),
     "exl3_amd_reconstruct": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
@@ -107,6 +109,33 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+# Kernel-path policy keys and values (include/exl3_amd.h EXL3_AMD_POLICY_*): 0 = the library's
+# own choice; the other values select alternative paths with the same results.
+POLICY_GEMV_ROWS, GEMV_ROWS_LDS, GEMV_ROWS_MFMA_ALL = 0, 1, 2
+POLICY_GEMM_STAGING, GEMM_STAGING_REGS = 1, 1
+POLICY_MOE_GEMM, MOE_GEMM_LDS = 2, 1
+POLICY_MOE_TILE_ROWS = 3
+POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1
+POLICY_RECON_GEMM = 5
+
+
+class policy:
+    """Context manager: `with policy(POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC): ...` sets a kernel-path
+    policy for the block and restores the previous value afterwards."""
+
+    def __init__(self, key: int, value: int):
+        self.key, self.value = key, value
+
+    def __enter__(self):
+        self.prev = check(lib().exl3_amd_get_policy(self.key))
+        check(lib().exl3_amd_set_policy(self.key, self.value))
+        return self
+
+    def __exit__(self, *exc):
+        check(lib().exl3_amd_set_policy(self.key, self.prev))
+        return False
 
 
 def check(rc: int) -> int:

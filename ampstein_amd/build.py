@@ -63,12 +63,25 @@ def _compile(src, obj, extra):
     return obj, time.time() - t0
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """True when the object is missing or older than its source or any shared header."""
+    o = os.path.join(OBJ, obj)
+    if not os.path.exists(o):
+        return True
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                                        if f.endswith((".h", ".cuh"))]
+    deps.append(os.path.join(ROOT, "include", "exl3_amd.h"))
+    return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(o)
+
+
+def build(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every unit (incremental: only units whose object is stale) and link."""
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
+    todo = [u for u in units() if not incremental or _stale(u[0], u[1])]
     with cf.ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_compile, *u) for u in units()]
+        futs = [ex.submit(_compile, *u) for u in todo]
         for f in cf.as_completed(futs):
             obj, dt = f.result()
             if verbose:
@@ -124,10 +137,12 @@ def build_adapter(verbose: bool = False) -> str:
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true", help="recompile stale units only; keep the adapter")
     args = ap.parse_args(argv)
     t0 = time.time()
-    path = build(args.j, verbose=True)
-    build_adapter(verbose=True)
+    path = build(args.j, verbose=True, incremental=args.incremental)
+    if not args.incremental or not os.path.exists(adapter_path()):
+        build_adapter(verbose=True)
     print(f"built {path} in {time.time() - t0:.1f}s")
 
 

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -80,6 +81,12 @@ constexpr int MGEMM_MAX_FILTER = 128;   // exl3_gemm_kernel.cuh:82 (index-compac
 
 DeviceState g_dev[MAX_DEVICES];
 std::mutex g_mutex;
+
+// Kernel-path policy (exl3_amd_set_policy): the library's defaults unless a test or benchmark
+// selects an alternative path explicitly.  Read once per call.
+std::atomic<int> g_policy[EXL3_AMD_POLICY_COUNT];
+
+int policy(int key) { return g_policy[key].load(std::memory_order_relaxed); }
 
 // ------------------------------------------------------------------ allocation-free scratch
 // exl3_amd_gemm_noalloc's device memory: one file-scope array, present on every GPU the library
@@ -233,13 +240,24 @@ int current_device(DeviceState** out, void* stream)
     return init_device(dev, out);
 }
 
-// Row-batched matrix-core GEMV (exl3_gemv.hip gemvm_kernel) for 2..16 rows:
-// EXL3_AMD_GEMV_MFMA_ROWS=0 keeps the LDS kernel (up to 8 rows), =2 also takes single rows there.
+// Row-batched matrix-core GEMV (exl3_gemv.hip gemvm_kernel) for 2..16 rows (policy
+// EXL3_AMD_POLICY_GEMV_ROWS: 0 = default; EXL3_AMD_GEMV_ROWS_LDS keeps the LDS kernel for up to
+// 8 rows, EXL3_AMD_GEMV_ROWS_MFMA_ALL also takes single rows there).  Returns 0 (LDS kernel),
+// 1 (matrix cores from 2 rows) or 2 (matrix cores from 1 row).
 int gemv_mfma_mode()
 {
-    const char* e = getenv("EXL3_AMD_GEMV_MFMA_ROWS");
-    return e ? atoi(e) : 1;
+    switch (policy(EXL3_AMD_POLICY_GEMV_ROWS))
+    {
+        case EXL3_AMD_GEMV_ROWS_LDS: return 0;
+        case EXL3_AMD_GEMV_ROWS_MFMA_ALL: return 2;
+    }
+    return 1;
 }
+
+// Work-split constants of the GEMV planner (measured on MI355X; see the comments at their uses).
+constexpr int GEMVM_TARGET_WG_PER_CU_X2 = 3;     // matrix-core GEMV: 1.5 workgroups per CU
+constexpr int GEMVM_STAGED_X_BYTES = 48 * 1024;  // its staged input rows, per workgroup
+constexpr int GEMV_LDS_WG_PER_CU = 4;            // LDS / stream kernels: 4 workgroups per CU
 
 // GEMV work split (exl3_gemv.hip): SB slices per workgroup, a divisor of k/16 (so no
 // workgroup straddles two column chunks), sized for ~TARGET workgroups per CU within the LDS
@@ -253,9 +271,8 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
         {
             const int KS = k / 16, chunks = n / 128;
             const int mt = m == 1 ? 1 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16));
-            // target grid: 1.5 workgroups per CU (EXL3_AMD_GEMV_WG_PER_CU: that many instead)
-            long target = 3L * num_cus / 2;
-            if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) target = (long) v * num_cus; }
+            // target grid: 1.5 workgroups per CU
+            const long target = (long) GEMVM_TARGET_WG_PER_CU_X2 * num_cus / 2;
             // SB: k-tiles per workgroup, a multiple of 8 dividing k/16, at most 64 (16 units per
             // wave; 32 for 16 rows); the largest whose grid still reaches the target (else the smallest), within
             // 48 KB of staged input and the workspace.  Measured on MI355X over SB (Qwen 5120 x
@@ -266,15 +283,10 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
             for (int d = 8; d <= KS && d <= sb_max; d += 8)
             {
                 if (KS % d) continue;
-                if ((size_t) mt * (d * 16 + 4) * 4 > 48 * 1024) break;
+                if ((size_t) mt * (d * 16 + 4) * 4 > (size_t) GEMVM_STAGED_X_BYTES) break;
                 if ((size_t) (KS / d) * bszm * m * n * 4 > partial_bytes && KS / d > 1) continue;
                 if ((long) bszm * chunks * (KS / d) >= target || best < 0) best = d;
                 if ((long) bszm * chunks * (KS / d) < target) break;
-            }
-            if (const char* e = getenv("EXL3_AMD_GEMV_SB"))
-            {
-                int v = atoi(e);
-                if (v > 0 && v % 8 == 0 && KS % v == 0 && (size_t) mt * (v * 16 + 4) * 4 <= 64 * 1024) best = v;
             }
             if (best > 0)
             {
@@ -287,15 +299,15 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
             }
         }
     }
+    // the LDS and stream kernels hold at most 8 rows: a group of 9..16 rows whose matrix-core
+    // plan did not fit is split by the caller (launch_gemv)
+    if (m > 8) return -1;
     g.mfma_rows = 0;
     const int mt = m == 1 ? 1 : (m <= 4 ? 4 : 8);
     const int KS = k / 16, chunks = n / 128;
-    int per_cu = 4;
-    if (const char* e = getenv("EXL3_AMD_GEMV_WG_PER_CU")) { int v = atoi(e); if (v > 0) per_cu = v; }
-    const long target = (long) per_cu * num_cus;
+    const long target = (long) GEMV_LDS_WG_PER_CU * num_cus;
     // M = 1 streaming kernel: 1, 2 or 4 slices per wave, or whole 128-row input chunks (SB % 32 == 0)
-    int stream = m == 1;
-    if (const char* e = getenv("EXL3_AMD_GEMV_STREAM")) stream = stream && atoi(e) != 0;
+    const int stream = m == 1;
     auto ok_sb = [&](int d) { return KS % d == 0 && (!stream || d == 4 || d == 8 || d == 16 || d % 32 == 0); };
     const int lds_budget = 64 * 1024 - 4 * mt * 128 * 4;
     const int max_chunks = lds_budget / (mt * 512);           // rotated 128-row chunks in LDS
@@ -320,7 +332,6 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
         for (int d = pref; d >= 4; d /= 2)
             if (ok_sb(d) && ((size_t) (KS / d) * bszm * m * n * 4 <= partial_bytes || KS / d == 1)) { best = d; break; }
     }
-    if (const char* e = getenv("EXL3_AMD_GEMV_SB")) { int v = atoi(e); if (v > 0 && ok_sb(v)) best = v; }
     if (best < 0) return -1;
     if ((size_t) (KS / best) * bszm * m * n * 4 > partial_bytes && KS / best > 1) return -1;
     g.stream_m1 = stream;
@@ -370,8 +381,23 @@ int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s
 {
     const int chunks = g.n / 128;
     if (gemv_plan(g.m, g.k, g.n, g.bszm, w.num_cus, g, w.partial_bytes))
+    {
+        // a 9..16-row group whose matrix-core plan exceeds the split-partial workspace (or with
+        // the matrix-core GEMV off): two launches of at most 8 rows, rows [row0, row0 + 8) and
+        // the rest, on the same slabs
+        if (g.m > 8)
+        {
+            GemvArgs lo = g, hi = g;
+            if (!g.slab_m) lo.slab_m = hi.slab_m = g.m;
+            lo.m = 8;
+            hi.m = g.m - 8;
+            hi.row0 = g.row0 + 8;
+            if (int rc = launch_gemv(w, bits, cb, lo, s, what)) return rc;
+            return launch_gemv(w, bits, cb, hi, s, what);
+        }
         return fail(EXL3_AMD_EUNSUPPORTED, "%s: shape exceeds the GEMV workspace (%zu bytes of split partials)", what,
                     w.partial_bytes);
+    }
     g.partials = w.partials;
     g.counters = w.counters;
     g.counters_half = (int) (w.counter_ints / 2);
@@ -435,7 +461,21 @@ void exl3_amd_debug_set_trace(void* p) { g_trace = (uint64_t*) p; }
 
 const char* exl3_amd_last_error(void) { return g_last_error.c_str(); }
 
-int exl3_amd_version(void) { return 100; }
+int exl3_amd_version(void) { return 10100; }
+
+int exl3_amd_set_policy(int key, int value)
+{
+    g_last_error.clear();
+    if (key < 0 || key >= EXL3_AMD_POLICY_COUNT) return fail(EXL3_AMD_EINVAL, "set_policy: unknown key %d", key);
+    g_policy[key].store(value, std::memory_order_relaxed);
+    return 0;
+}
+
+int exl3_amd_get_policy(int key)
+{
+    if (key < 0 || key >= EXL3_AMD_POLICY_COUNT) return fail(EXL3_AMD_EINVAL, "get_policy: unknown key %d", key);
+    return policy(key);
+}
 
 int exl3_amd_init(int device)
 {
@@ -583,9 +623,8 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     else (void) hipGetLastError();
     hipStream_t s = (hipStream_t) stream;
 
-    if ((m <= 8 && force_shape_idx != 2) || force_shape_idx == 1)
+    if (m <= 8 && force_shape_idx != 2)
     {
-        if (m > 8) return fail(EXL3_AMD_EINVAL, "%s: the GEMV kernel takes at most 8 rows", name);
         GemvArgs g = gemv_args_single(A, trellis, C, c_fp32, suh, svh, m, k, n);
         int rc = launch_gemv(*ws, bits, cb, g, s, name);
         return rc ? rc : EXL3_AMD_TAG_GEMV;
@@ -602,28 +641,33 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     // GEMM, whose 256 x 256 tiles leave most CUs idle at small m.  Measured on MI355X (K = 2..4,
     // k x n from 4096 x 1024 to 17408 x 5120, m = 16..192): a 16-row group takes ~8 us + 0.37 ns
     // per 1000 weights; a GEMM round (up to one tile per CU) ~28 ns per k.
+    // force_shape_idx 1 takes the GEMV for any row count (16-row groups, each split in two
+    // launches of at most 8 rows when the matrix-core GEMV is off or its plan does not fit).
+    bool groups = force_shape_idx == 1;
     if (force_shape_idx == 0 && gemv_mfma_mode() != 0)
     {
         const long blocks = (long) ((n + 255) / 256) * ((m + 255) / 256);
         const long rounds = (blocks + ws->num_cus - 1) / ws->num_cus;
         const double t_groups = ((m + 15) / 16) * (8.0 + 3.7e-7 * (double) n * k);
         const double t_gemm = 0.028 * k * rounds;
-        if (t_groups < t_gemm)
+        groups = t_groups < t_gemm;
+    }
+    if (groups)
+    {
+        const size_t elt = c_fp32 ? 4 : 2;
+        for (int r0 = 0; r0 < m; r0 += 16)
         {
-            const size_t elt = c_fp32 ? 4 : 2;
-            for (int r0 = 0; r0 < m; r0 += 16)
-            {
-                GemvArgs g = gemv_args_single(A_rot + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt,
-                                              c_fp32, nullptr, svh, std::min(16, m - r0), k, n);
-                if (int rc = launch_gemv(*ws, bits, cb, g, s, name)) return rc;
-            }
-            return EXL3_AMD_TAG_GEMV;
+            GemvArgs g = gemv_args_single(A_rot + (size_t) r0 * k, trellis, (char*) C + (size_t) r0 * n * elt,
+                                          c_fp32, nullptr, svh, std::min(16, m - r0), k, n);
+            if (int rc = launch_gemv(*ws, bits, cb, g, s, name)) return rc;
         }
+        return EXL3_AMD_TAG_GEMV;
     }
     GemmArgs gg;
     gg.A_rot = A_rot;
     gg.trellis = trellis; gg.C = C; gg.svh = svh;
     gg.m = m; gg.k = k; gg.n = n; gg.c_fp32 = c_fp32 ? 1 : 0;
+    gg.reg_staging = policy(EXL3_AMD_POLICY_GEMM_STAGING) == EXL3_AMD_GEMM_STAGING_REGS;
     int rc = dispatch_gemm(bits, cb, gg, s);
     return rc ? hip_fail(rc, name) : EXL3_AMD_TAG_GEMM;
 }
@@ -752,10 +796,11 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         g.indices = d->filt_idx;
         if (weights) g.weights = d->filt_w;
     }
-    // more than 8 rows: the GEMV in row groups (slab strides stay those of all m rows): 16 rows
-    // per group on the row-batched matrix-core kernel, 8 on the LDS kernel
+    // more than 8 rows: the GEMV in 16-row groups (slab strides stay those of all m rows); a
+    // group runs on the row-batched matrix-core kernel, or as two launches of at most 8 rows on
+    // the LDS kernel (launch_gemv)
     g.slab_m = m;
-    const int group = gemv_mfma_mode() != 0 ? 16 : 8;
+    const int group = 16;
     for (int r0 = 0; r0 < m; r0 += group)
     {
         GemvArgs gr = g;
@@ -853,8 +898,7 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     const int nproj = gated ? 2 : 1;
     // 2 workgroups per CU: the one-token batch (8 slots) then splits gate/up and down k in 2
     // (measured 1, 2, 4, 8 per CU: 51.9, 51.6, 53.6, 68.4 us)
-    long target = 2L * d->num_cus;
-    if (const char* e = getenv("EXL3_AMD_MOE_WG_PER_CU")) { int v = atoi(e); if (v > 0) target = (long) v * d->num_cus; }
+    const long target = 2L * d->num_cus;
     auto pick = [&](int KS, long base) {
         int S = (KS + EXL3_MOE_SBMAX - 1) / EXL3_MOE_SBMAX;
         while (base * S < target && KS / (S + 1) >= 8) ++S;
@@ -965,9 +1009,9 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     // 128 at 64, 256 at 128
     const int mean_rows = num_assign / std::max(num_experts, 1);
     // GEMM kernel: the register-decode moeg_kernel (default) or the LDS-tiled gemm_kernel
-    // (EXL3_AMD_MOE_GEMM=lds).  moeg rows per tile: one tile per expert for most experts
-    const char* gsel = getenv("EXL3_AMD_MOE_GEMM");
-    const bool reg_gemm = !(gsel && !strcmp(gsel, "lds"));
+    // (policy EXL3_AMD_POLICY_MOE_GEMM = EXL3_AMD_MOE_GEMM_LDS).  moeg rows per tile: one tile per
+    // expert for most experts
+    const bool reg_gemm = policy(EXL3_AMD_POLICY_MOE_GEMM) != EXL3_AMD_MOE_GEMM_LDS;
     // moeg: the smallest tile holding ~1.5x the mean rows (the largest expert, for top-k routing
     // of random tokens).  Measured, 256 experts 4096 -> 2048 -> 4096, top-8: T = 512 (mean 16,
     // max 27) best at 32; T = 2048 (mean 64, max 91) best at 96: 2.32 ms against 2.49 at 64 and
@@ -975,21 +1019,20 @@ int exl3_amd_moe(const uint16_t* hidden_state, int bsz, int hidden_dim, float* o
     const int want = mean_rows * 3 / 2;
     int tile_rows = reg_gemm ? (want <= 32 ? 32 : (want <= 64 ? 64 : (want <= 96 ? 96 : 128)))
                              : (mean_rows <= 40 ? 64 : (mean_rows <= 96 ? 128 : 256));
-    if (const char* e = getenv("EXL3_AMD_MOE_TILE_ROWS"))
+    // policy EXL3_AMD_POLICY_MOE_TILE_ROWS: a forced tile height (tests cover every instance)
     {
-        const int v = atoi(e);
+        const int v = policy(EXL3_AMD_POLICY_MOE_TILE_ROWS);
         if (reg_gemm ? (v == 32 || v == 64 || v == 96 || v == 128) : (v == 64 || v == 128 || v == 256)) tile_rows = v;
     }
-    int grid_wgs = d->num_cus * 4;
-    if (const char* e = getenv("EXL3_AMD_MOEG_WGS")) { const int v = atoi(e); if (v > 0) grid_wgs = v; }
+    // persistent moeg workgroups: 4 per CU
+    const int grid_wgs = d->num_cus * 4;
     const int rt_cap = pool / tile_rows + std::min(num_experts, pool) + 1;
     const size_t ps_floats = (size_t) pool * (2 * (hidden_dim / 128) + intermediate_dim / 128);
     // token-major output lists (atomic mode): starts, positions, build space, position -> row
     // (used when the per-call list build fits one workgroup's LDS; else the atomic output kernel)
-    // (EXL3_AMD_MOE_OUT=atomic forces the atomic output kernel)
-    const char* omode = getenv("EXL3_AMD_MOE_OUT");
+    // (policy EXL3_AMD_POLICY_MOE_OUTPUT = EXL3_AMD_MOE_OUTPUT_ATOMIC forces the atomic output kernel)
     const bool tok_mode = !output_scratch && exl3k_moes_tokens_lds(bsz, num_assign) <= 150 * 1024
-                          && !(omode && !strcmp(omode, "atomic"));
+                          && policy(EXL3_AMD_POLICY_MOE_OUTPUT) != EXL3_AMD_MOE_OUTPUT_ATOMIC;
     const size_t tok_ints = tok_mode ? (size_t) (bsz + 1) + 2 * (size_t) num_assign : 0;
     const size_t ws_ints = (size_t) 3 * pool + 3 * (size_t) rt_cap + 3 * MOES_RATES * ((size_t) rt_cap + 1) + ps_floats
                          + tok_ints;

@@ -659,9 +659,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s)
     const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     GemmGroupArgs none;
     memset(&none, 0, sizeof(none));
-    const char* e = getenv("EXL3_AMD_GEMM_DMA");        // 0: register staging (gemm_kernel)
-    const int dma = e ? atoi(e) : 1;
-    if (dma)
+    if (!g.reg_staging)
         hipLaunchKernelGGL((gemm_dma_kernel<K, CB>), dim3(blocks), dim3(GT), 0, s,
                            g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32);
     else

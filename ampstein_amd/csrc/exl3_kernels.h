@@ -64,6 +64,7 @@ struct GemmArgs
     const uint16_t* svh;        // (n) fp16 or null
     int m, k, n;
     int c_fp32;
+    int reg_staging;            // 1: register-staged operands (gemm_kernel) instead of LDS DMA
 };
 
 int exl3k_gemm_k1(const GemmArgs& g, int cb, hipStream_t s);

@@ -43,6 +43,27 @@ const char* exl3_amd_last_error(void);
 /* Library ABI version (major * 10000 + minor * 100 + patch). */
 int exl3_amd_version(void);
 
+/* Kernel-path policy, process-wide.  Every key defaults to 0, the library's own choice (the
+ * measured fastest path for the shape).  A nonzero value selects an alternative kernel path that
+ * computes the same result, so that tests can cover every instance and benchmarks can compare
+ * paths.  Calls made while another thread changes a policy see either value.  No counterpart in
+ * the reference (its tuning is compiled in); for tests and benchmarks. */
+#define EXL3_AMD_POLICY_GEMV_ROWS       0   /* rows of the GEMV (exl3_gemm / exl3_mgemm, m <= 16)       */
+#define EXL3_AMD_GEMV_ROWS_LDS          1   /*   the LDS kernel for 2..8 rows, no matrix-core GEMV      */
+#define EXL3_AMD_GEMV_ROWS_MFMA_ALL     2   /*   the matrix-core GEMV for single rows as well           */
+#define EXL3_AMD_POLICY_GEMM_STAGING    1   /* operand staging of the fused MFMA GEMM (m > 8)          */
+#define EXL3_AMD_GEMM_STAGING_REGS      1   /*   register-staged instead of LDS DMA                     */
+#define EXL3_AMD_POLICY_MOE_GEMM        2   /* grouped GEMM of exl3_amd_moe                            */
+#define EXL3_AMD_MOE_GEMM_LDS           1   /*   the LDS-tiled kernel instead of the register decode    */
+#define EXL3_AMD_POLICY_MOE_TILE_ROWS   3   /* exl3_amd_moe row-tile height: 0 = by mean rows, else the
+                                             * value (32 / 64 / 96 / 128; LDS-tiled: 64 / 128 / 256)  */
+#define EXL3_AMD_POLICY_MOE_OUTPUT      4   /* exl3_amd_moe output kernel                              */
+#define EXL3_AMD_MOE_OUTPUT_ATOMIC      1   /*   per-row atomics instead of the per-token lists         */
+#define EXL3_AMD_POLICY_RECON_GEMM      5   /* dense GEMM of exl3_amd_recon_mm                         */
+#define EXL3_AMD_POLICY_COUNT           6
+int exl3_amd_set_policy(int key, int value);
+int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */
+
 /* Allocate the per-device workspace (split-k partials and completion counters) of `device`.
  * Optional: the first call on a device does it lazily.  Call it before capturing a graph.
  * Replaces DevCtx::get_locks (vendor/exl3/exllamav3_ext/quant/exl3_devctx.cu:81-93). */

@@ -9,7 +9,7 @@ rotated input afterwards, bit-exact with had_r_128(A, pre=suh).
 import numpy as np
 import pytest
 
-from ampstein_amd import synth
+from ampstein_amd import _lib, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -57,15 +57,15 @@ def test_gemm_parity_all_bitrates(torch_cuda, orc, K, cb):
 
 @pytest.mark.parametrize("K,cb,m,k,n", [(4, 0, 300, 512, 2048), (2, 1, 513, 1024, 384), (8, 2, 256, 256, 1024),
                                          (2.5, 2, 40, 384, 256), (3, 0, 9, 128, 128)])
-def test_gemm_dma_and_register_staging(torch_cuda, orc, monkeypatch, K, cb, m, k, n):
-    """The LDS-DMA kernel (default) and the register-staged kernel (EXL3_AMD_GEMM_DMA=0) do the
+def test_gemm_dma_and_register_staging(torch_cuda, orc, kernel_policy, K, cb, m, k, n):
+    """The LDS-DMA kernel (default) and the register-staged kernel (policy EXL3_AMD_GEMM_STAGING_REGS) do the
     same arithmetic in the same order: bit-identical outputs, both within the bar."""
     torch = torch_cuda
     L = synth.layer(k, n, K, cb, seed=900 + int(10 * K) + cb)
     x = synth.activations(m, k, seed=901 + int(10 * K))
     ys = []
-    for dma in ("1", "0"):
-        monkeypatch.setenv("EXL3_AMD_GEMM_DMA", dma)
+    for staging in (0, _lib.GEMM_STAGING_REGS):
+        kernel_policy(_lib.POLICY_GEMM_STAGING, staging)
         tag, y, _ = run_gemm(torch, L, x, False)
         assert tag == 91
         ys.append(y)

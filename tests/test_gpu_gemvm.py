@@ -1,5 +1,5 @@
 """GPU parity of the row-batched matrix-core GEMV (gemvm_kernel: 2..16 rows, and single rows
-when EXL3_AMD_GEMV_MFMA_ROWS=2 routes them there) against the CPU oracle.
+when the policy EXL3_AMD_GEMV_ROWS_MFMA_ALL routes them there) against the CPU oracle.
 
 Covers every integer K and codebook, the half rates, fp16 / fp32 outputs, column-chunk counts
 that take the XCD hand-off (8 chunks) and the finish kernel (3 chunks), one to sixteen rows
@@ -9,7 +9,7 @@ Bar (tests/tol.py): max relative error 2e-3, norm-wise and element-wise, against
 import numpy as np
 import pytest
 
-from ampstein_amd import synth
+from ampstein_amd import _lib, synth
 from tests.tol import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -37,8 +37,8 @@ def run(torch, L, x, y_fp32):
 
 @pytest.mark.parametrize("K,cb", [(k, c) for k in range(1, 9) for c in range(3)] + [(1.5, 2), (2.5, 2), (3.5, 2)])
 @pytest.mark.parametrize("m", [1, 2, 5, 8])
-def test_gemvm_parity(torch_cuda, orc, monkeypatch, K, cb, m):
-    monkeypatch.setenv("EXL3_AMD_GEMV_MFMA_ROWS", "2")
+def test_gemvm_parity(torch_cuda, orc, kernel_policy, K, cb, m):
+    kernel_policy(_lib.POLICY_GEMV_ROWS, _lib.GEMV_ROWS_MFMA_ALL)
     torch = torch_cuda
     L = synth.layer(1024, 1024, K, cb, seed=900 + int(10 * K) + cb)
     x = synth.activations(m, 1024, seed=m + int(K))
@@ -53,8 +53,8 @@ def test_gemvm_parity(torch_cuda, orc, monkeypatch, K, cb, m):
 @pytest.mark.parametrize("k,n", [(256, 384), (4096, 1024), (14336, 4096), (5120, 17408)])
 @pytest.mark.parametrize("m", [1, 3, 8])
 @pytest.mark.parametrize("y_fp32", [False, True])
-def test_gemvm_shapes(torch_cuda, orc, monkeypatch, k, n, m, y_fp32):
-    monkeypatch.setenv("EXL3_AMD_GEMV_MFMA_ROWS", "2")
+def test_gemvm_shapes(torch_cuda, orc, kernel_policy, k, n, m, y_fp32):
+    kernel_policy(_lib.POLICY_GEMV_ROWS, _lib.GEMV_ROWS_MFMA_ALL)
     torch = torch_cuda
     L = synth.layer(k, n, 4, 0, seed=950 + k + n)
     x = synth.activations(m, k, seed=951)

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from ampstein_amd import _lib
 from tests.moe_ref import ExpertSet, act_fn, f16, had
 
 pytestmark = pytest.mark.gpu
@@ -158,10 +159,10 @@ def test_exl3_moe(orc, case):
 
 
 @pytest.mark.parametrize("case", CASES[:3], ids=[c[0] for c in CASES[:3]])
-def test_exl3_moe_atomic_output(orc, monkeypatch, case):
+def test_exl3_moe_atomic_output(orc, kernel_policy, case):
     """The atomic output kernel (used when the per-token lists do not fit one workgroup's LDS),
     forced: the same cases, the same bar."""
-    monkeypatch.setenv("EXL3_AMD_MOE_OUT", "atomic")
+    kernel_policy(_lib.POLICY_MOE_OUTPUT, _lib.MOE_OUTPUT_ATOMIC)
     test_exl3_moe(orc, case)
 
 
@@ -174,9 +175,9 @@ TILE_CASES = [
 
 @pytest.mark.parametrize("tile_rows", [32, 64, 96, 128])
 @pytest.mark.parametrize("case", TILE_CASES, ids=[c[0] for c in TILE_CASES])
-def test_exl3_moe_tile_rows(orc, monkeypatch, case, tile_rows):
+def test_exl3_moe_tile_rows(orc, kernel_policy, case, tile_rows):
     """Every row-tile size of the grouped GEMM (16-row groups R = 2, 4, 6, 8) against the model."""
-    monkeypatch.setenv("EXL3_AMD_MOE_TILE_ROWS", str(tile_rows))
+    kernel_policy(_lib.POLICY_MOE_TILE_ROWS, tile_rows)
     name, E, H, I, T, topk, cb, Ks, act, limit, max_tok, conc, lo, hi, sentinel = case
     es = ExpertSet(torch, orc, E, H, I, H, Ks, cb, seed=TILE_CASES.index(case) + 71)
     x = np.random.default_rng(7).standard_normal((T, H)).astype(np.float16)
