@@ -24,11 +24,15 @@ SIGNATURES = {
     "exl3_amd_set_policy": (_i32, [_i32, _i32]),
     "exl3_amd_get_policy": (_i32, [_i32]),
     "exl3_amd_init": (_i32, [_i32]),
+    "exl3_amd_debug_read_workspace": (_i32, [_i32, ctypes.c_int64, ctypes.c_int64, _vp]),
+    "exl3_amd_debug_fill_workspace": (_i32, [_i32, _i32]),
     "exl3_amd_device_info": (_i32, [_i32, _vp, _vp]),
     "exl3_amd_reconstruct": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_t": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_t_had": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_had": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_reconstruct_had_t": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+    "exl3_amd_recon_mm": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "exl3_amd_had_r_128": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _f32, _vp]),
     "exl3_amd_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
     "exl3_amd_gemm_noalloc": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp]),
@@ -118,7 +122,7 @@ POLICY_GEMM_STAGING, GEMM_STAGING_REGS = 1, 1
 POLICY_MOE_GEMM, MOE_GEMM_LDS = 2, 1
 POLICY_MOE_TILE_ROWS = 3
 POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1
-POLICY_RECON_GEMM = 5
+POLICY_RECON_MM, RECON_MM_8WAVES = 5, 1
 
 
 class policy:

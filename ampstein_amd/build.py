@@ -42,6 +42,7 @@ def units():
         ("exl3_device.hip", "exl3_device.o", []),
         ("exl3_moe_sorted.hip", "exl3_moe_sorted.o", []),
         ("exl3_decode_ops.hip", "exl3_decode_ops.o", []),
+        ("exl3_dense.hip", "exl3_dense.o", []),
     ]
     for cb in range(3):
         u.append(("exl3_moe.hip", f"exl3_moe_cb{cb}.o", [f"-DEXL3_MOE_CB={cb}"]))
@@ -96,6 +97,25 @@ def build(jobs: int | None = None, verbose: bool = False, incremental: bool = Fa
     return LIB
 
 
+PROBE_LIB = os.path.join(LIB_DIR, "libexl3_probe.so")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """Issue-rate microbenchmarks (csrc/exl3_probe.hip) for `bench.py --rates`: a library of its
+    own, not part of the C ABI."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [HIPCC] + COMMON + ["-shared", "-x", "hip", os.path.join(CSRC, "exl3_probe.hip"), "-o", tmp]
+    t0 = time.time()
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{p.stderr[-6000:]}")
+    shutil.move(tmp, PROBE_LIB)
+    if verbose:
+        print(f"  libexl3_probe.so: {time.time() - t0:.1f}s", flush=True)
+    return PROBE_LIB
+
+
 ADAPTER_DIR = os.path.join(PKG, "adapter")
 
 
@@ -143,6 +163,7 @@ def main(argv=None):
     path = build(args.j, verbose=True, incremental=args.incremental)
     if not args.incremental or not os.path.exists(adapter_path()):
         build_adapter(verbose=True)
+    build_probe(verbose=True)
     print(f"built {path} in {time.time() - t0:.1f}s")
 
 

@@ -489,6 +489,30 @@ int exl3_amd_init(int device)
     return rc;
 }
 
+int exl3_amd_debug_read_workspace(int device, int64_t offset, int64_t bytes, void* host_dst)
+{
+    g_last_error.clear();
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    if (offset < 0 || bytes < 0 || (uint64_t) (offset + bytes) > WS_PARTIAL_BYTES || (bytes && !host_dst))
+        return fail(EXL3_AMD_EINVAL, "debug_read_workspace: range outside the %zu-byte workspace", WS_PARTIAL_BYTES);
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(host_dst, (char*) d->partials + offset, (size_t) bytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(EXL3_AMD_EHIP, "debug_read_workspace: copy failed");
+    return 0;
+}
+
+int exl3_amd_debug_fill_workspace(int device, int byte_value)
+{
+    g_last_error.clear();
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    if (hipDeviceSynchronize() != hipSuccess || hipMemset(d->partials, byte_value & 0xff, WS_PARTIAL_BYTES) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess)
+        return fail(EXL3_AMD_EHIP, "debug_fill_workspace: memset failed");
+    return 0;
+}
+
 int exl3_amd_device_info(int device, int* num_cus, int* num_xcd)
 {
     DeviceState* d;
@@ -574,6 +598,43 @@ int exl3_amd_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_
     int rc = exl3k_reconstruct_had(W, trellis, suh, svh, k, n, n_packed / 16, n_offset / 16, bits, cb,
                                    (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_had") : 0;
+}
+
+int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                               const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                               float K, int mcg, int mul1, void* stream)
+{
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "reconstruct_had_t", true)) return rc;
+    if (k < 0 || n < 0 || n_packed < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: negative size");
+    if ((size_t) k * n == 0) return 0;
+    if (!WT || !trellis || !suh || !svh) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: null pointer");
+    if (k % 128) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: K dimension must be divisible by 128");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: N dimension must be divisible by 128");
+    if (n_packed % 16) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: packed width must be a multiple of 16");
+    if (n_offset % 128) return fail(EXL3_AMD_EINVAL, "n_offset must be divisible by 128");
+    if (n_offset < 0) return fail(EXL3_AMD_EINVAL, "n_offset must be non-negative");
+    if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
+    int rc = exl3k_reconstruct_had_tr(WT, trellis, suh, svh, k, n, n_packed / 16, n_offset / 16, bits, cb,
+                                      (hipStream_t) stream);
+    return rc ? hip_fail(rc, "reconstruct_had_t") : 0;
+}
+
+int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                      int m, int k, int n, void* stream)
+{
+    g_last_error.clear();
+    if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "recon_mm: negative size");
+    if (k % 32) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be a multiple of 32");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "recon_mm: n must be a multiple of 128");
+    if ((size_t) m * n == 0) return 0;
+    if (k == 0) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be positive");
+    if (!A || !WT || !C) return fail(EXL3_AMD_EINVAL, "recon_mm: null pointer");
+    (void) hipGetLastError();
+    int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n,
+                              policy(EXL3_AMD_POLICY_RECON_MM), (hipStream_t) stream);
+    return rc ? hip_fail(rc, "recon_mm") : 0;
 }
 
 int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,

@@ -342,4 +342,36 @@ __device__ __forceinline__ void fwht128_wave(float& v0, float& v1, int lane)
     fwht_stage<32>(v0, v1, lane);
 }
 
+// Output rotation of one fp32 row chunk (elements 2l, 2l+1) and store: had_fh / had_ff.
+__device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp32, bool has_svh, uint32_t svp,
+                                           size_t idx, int lane)
+{
+    if (has_svh)
+    {
+        fwht128_wave(v0, v1, lane);
+        v0 *= EXL3_HAD_RSCALE;
+        v1 *= EXL3_HAD_RSCALE;
+        const f16x2 s = as_h2(svp);
+        if (!c_fp32)
+        {
+            f16x2 h = { (f16) v0, (f16) v1 };
+            h = h * s;
+            *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
+            return;
+        }
+        v0 *= (float) s.x;
+        v1 *= (float) s.y;
+    }
+    if (c_fp32)
+    {
+        f32x2 o = { v0, v1 };
+        *(f32x2*) ((float*) C + idx) = o;
+    }
+    else
+    {
+        f16x2 h = { (f16) v0, (f16) v1 };
+        *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
+    }
+}
+
 }  // namespace exl3

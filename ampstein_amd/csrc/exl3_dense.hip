@@ -1,0 +1,361 @@
+// Dense fp16 GEMM of the recon route (exl3_gemm_recon, src/torch/amp_torch.cpp:11083-11230: the
+// reference reconstructs the weight to fp16 once and runs a dense GEMM on cuBLAS):
+//
+//     C (m, n) = A (m, k) . WT (n, k)^T            fp16 operands, fp32 accumulation
+//     optional epilogue: each 128-column chunk of the fp32 row rotated by H128 / sqrt(128), x svh
+//
+// The weight is stored transposed, (n, k) row-major (exl3_amd_reconstruct_t /
+// exl3_amd_reconstruct_had_t write it so), so both operands are k-contiguous: a lane's MFMA operand
+// (8 consecutive k of one row or column) is one 16-byte LDS read, and both tiles are staged by the
+// same LDS DMA with the same swizzle.
+//
+// Tiling: a workgroup owns a 256 x 256 output tile.  The k loop runs in stages of 32.  Each
+// stage's A and WT blocks (256 x 32 fp16 each) go from global memory straight into LDS with
+// global_load_lds_dwordx4; D + 1 LDS buffers per operand, D stages in flight.  Two forms: four
+// waves of 128 x 128 (default, dense_gemm4_kernel) and eight waves of 128 x 64 (dense_gemm_kernel,
+// policy EXL3_AMD_RECON_MM_8WAVES).  Measured on MI355X, 2048 rows, interleaved runs (median
+// TFLOPS, four-wave / eight-wave): 28672 -> 8192 1072 / 986, 8192 -> 28672 977 / 932,
+// 24576 -> 8192 1043 / 968.  Also measured and not kept: D = 4 (160 KiB of LDS; 1051 / 962 /
+// 1034 for the four-wave form) and register staging (global_load_dwordx4 two stages ahead, then
+// ds_write_b128; 1080 / 894 / 994).  Workgroups b and b + 8 run on one XCD: the row blocks of one column block
+// are consecutive on an XCD, so each 256-column slice of WT is read from HBM once per XCD and
+// served to the other row blocks from its L2.
+#include "exl3_common.cuh"
+#include "exl3_kernels.h"
+
+using namespace exl3;
+
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float acc16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int DENSE_T = 512;              // threads per workgroup (8 waves)
+constexpr int DENSE_BM = 256;             // rows per workgroup
+constexpr int DENSE_BN = 256;             // columns per workgroup
+constexpr int DENSE_TILE_U32 = 256 * 16;  // one operand block: 256 rows x 32 fp16
+constexpr int DENSE_A0 = 0;
+// D stages of DMA in flight, D + 1 LDS buffers per operand: 32 KiB per stage (D = 3: 128 KiB,
+// D = 4: 160 KiB); the epilogue reuses 64 KiB
+template <int D> struct DenseLds
+{
+    static constexpr int NB = D + 1;
+    static constexpr int B0 = NB * DENSE_TILE_U32;
+    static constexpr int U32 = 2 * NB * DENSE_TILE_U32;
+    static_assert(U32 >= 64 * DENSE_BN, "the epilogue's 64 x 256 fp32 rows fit the staging buffers");
+};
+
+// 16-byte chunk c (0..3) of staged row r: chunk c ^ ((r >> 2) & 3) of the row's 64 bytes, so that
+// the 16 lanes of each ds_read_b128 phase (rows r .. r + 15, one chunk) hit 16 distinct 16-byte
+// bank groups of the 64-bank LDS.
+__device__ __forceinline__ int x_off(int row, int chunk) { return row * 16 + 4 * (chunk ^ ((row >> 2) & 3)); }
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+#define DENSE_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+template <int D>
+__global__ __launch_bounds__(DENSE_T, 1)
+void dense_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
+                       const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+{
+    constexpr int MT = 4, NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
+    __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int NST = k / 32;
+    const int nbn = (n + DENSE_BN - 1) / DENSE_BN;       // n % 128 == 0: the last block may be half
+    const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
+    int nb, mb;
+    if (nbn % 8 == 0)
+    {
+        const int x = blockIdx.x % 8, r = blockIdx.x / 8;
+        nb = x + 8 * (r / nmb);
+        mb = r % nmb;
+    }
+    else
+    {
+        nb = blockIdx.x / nmb;
+        mb = blockIdx.x % nmb;
+    }
+
+    // wave w's DMAs j = 0, 1 fill the 1 KiB blocks q = w + 8 j (rows 16 q .. 16 q + 15) of each
+    // operand; lane L fills slot L, i.e. row 16 q + L / 4 and the global chunk that x_off puts in
+    // slot L % 4.  Rows past M and columns past n read a valid row (results dropped).
+    const u32x4* a_src[2];
+    const u32x4* b_src[2];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j)
+    {
+        const int q = wave + 8 * j, row = 16 * q + (lane >> 2), ch = (lane & 3) ^ ((row >> 2) & 3);
+        a_src[j] = (const u32x4*) (A + (size_t) min(mb * DENSE_BM + row, M - 1) * k + 8 * ch);
+        b_src[j] = (const u32x4*) (WT + (size_t) min(nb * DENSE_BN + row, n - 1) * k + 8 * ch);
+    }
+    auto issue = [&](int st) {
+        const int c = min(st, NST - 1);                  // past the end: rewrites a buffer nobody reads
+        const int buf = (st % NB) * DENSE_TILE_U32;
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+        {
+            __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 8 * j)), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*) (b_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 8 * j)), 16, 0, 0);
+        }
+    };
+
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    #pragma unroll
+    for (int g = 0; g < D; ++g) issue(g);
+    DENSE_VM_LGKM0(4 * (D - 1));                          // this wave's stage-0 DMAs have landed
+    __builtin_amdgcn_s_barrier();
+
+    acc16 acc[MT][2];
+    #pragma unroll
+    for (int i = 0; i < MT; ++i) { acc[i][0] = (acc16) { }; acc[i][1] = (acc16) { }; }
+
+    for (int s = 0; s < NST; ++s)
+    {
+        issue(s + D);                                    // its buffers were last read in stage s - 1
+        const uint32_t* As = lds + DENSE_A0 + (s % NB) * DENSE_TILE_U32;
+        const uint32_t* Bs = lds + DENSE_B0 + (s % NB) * DENSE_TILE_U32;
+        h8v av[2][MT], bv[2][2];
+        #pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+        {
+            #pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+                bv[sl][nt] = __builtin_bit_cast(h8v, *(const u32x4*) (Bs + x_off(64 * wn + 32 * nt + l32, 2 * sl + lh)));
+            #pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                av[sl][mt] = __builtin_bit_cast(h8v, *(const u32x4*) (As + x_off(128 * wm + 32 * mt + l32, 2 * sl + lh)));
+        }
+        // all 12 operand reads in flight before the first MFMA (they return in order, so the
+        // MFMAs of slice 0 wait only for theirs)
+        __builtin_amdgcn_sched_barrier(0);
+        #pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+        {
+            #pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+            {
+                #pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[sl][mt], bv[sl][nt], acc[mt][nt], 0, 0, 0);
+            }
+        }
+        // the next stage's DMAs (issued D - 1 stages ago) have landed for this wave, and its LDS
+        // reads of this stage are complete: then the barrier
+        DENSE_VM_LGKM0(4 * (D - 1));
+        __builtin_amdgcn_s_barrier();
+    }
+    DENSE_VM_LGKM0(0);                                    // no DMA may still write LDS under the epilogue
+    __builtin_amdgcn_s_barrier();
+
+    // epilogue: MT rounds of 64 rows; a row's 256 columns meet in LDS, then each wave stores
+    // (rotating, with svh) whole 128-column chunks
+    float* E = (float*) lds;                              // [64][256] fp32
+    const bool has_svh = svh != nullptr;
+    #pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+    {
+        #pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+        {
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    E[(32 * wm + 8 * j + 4 * lh + i) * DENSE_BN + 64 * wn + 32 * nt + l32] = acc[mt][nt][4 * j + i];
+            }
+        }
+        __syncthreads();
+        #pragma unroll 2
+        for (int q = 0; q < 16; ++q)
+        {
+            const int rc = wave * 16 + q;
+            const int er = rc >> 1, ch = rc & 1;
+            const int row = mb * DENSE_BM + 128 * (er >> 5) + 32 * mt + (er & 31);
+            const int col = nb * DENSE_BN + 128 * ch + 2 * lane;
+            if (nb * DENSE_BN + 128 * ch >= n) continue;          // half block: chunk past n (uniform per wave)
+            const f32x2 v = *(const f32x2*) (E + er * DENSE_BN + 128 * ch + 2 * lane);
+            const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Four-wave form (default): one wave per SIMD, each wave a 128 x 128 quarter of the 256 x 256 tile
+// (4 x 4 accumulators of v_mfma_f32_32x32x16_f16, held in AGPRs).  Per 16-k slice a wave reads 8
+// operand blocks for 16 MFMAs (the eight-wave form: 6 for 8), so the LDS serves a third less per
+// flop.  With one wave per SIMD the wave hides its own LDS latency: the operand reads of slice
+// s + 1 are issued between the MFMAs of slice s (two register sets), and the stage barrier sits
+// between the two slices of a stage, so the first slice of stage s + 1 is read while the second
+// slice of stage s computes.
+constexpr int DENSE4_T = 256;
+
+template <int D>
+__global__ __launch_bounds__(DENSE4_T, 1)
+void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
+                        const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+{
+    constexpr int NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
+    __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int NST = k / 32;
+    const int nbn = (n + DENSE_BN - 1) / DENSE_BN;
+    const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
+    int nb, mb;
+    if (nbn % 8 == 0)
+    {
+        const int x = blockIdx.x % 8, r = blockIdx.x / 8;
+        nb = x + 8 * (r / nmb);
+        mb = r % nmb;
+    }
+    else
+    {
+        nb = blockIdx.x / nmb;
+        mb = blockIdx.x % nmb;
+    }
+
+    // wave w's DMAs j = 0..3 fill the 1 KiB blocks q = w + 4 j (rows 16 q .. 16 q + 15) of each operand
+    const u32x4* a_src[4];
+    const u32x4* b_src[4];
+    #pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        const int q = wave + 4 * j, row = 16 * q + (lane >> 2), ch = (lane & 3) ^ ((row >> 2) & 3);
+        a_src[j] = (const u32x4*) (A + (size_t) min(mb * DENSE_BM + row, M - 1) * k + 8 * ch);
+        b_src[j] = (const u32x4*) (WT + (size_t) min(nb * DENSE_BN + row, n - 1) * k + 8 * ch);
+    }
+    auto issue = [&](int st) {
+        const int c = min(st, NST - 1);
+        const int buf = (st % NB) * DENSE_TILE_U32;
+        #pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*) (b_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
+        }
+    };
+
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+    #pragma unroll
+    for (int g = 0; g < D; ++g) issue(g);
+    DENSE_VM_LGKM0(8 * (D - 1));
+    __builtin_amdgcn_s_barrier();
+
+    acc16 acc[4][4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (acc16) { };
+
+    // The loop body is written out in issue order, fenced by sched_barrier: the 16 MFMAs of a slice
+    // alternate with the 8 operand reads of the next slice and (first half) the 8 LDS DMAs of stage
+    // s + D, so that no burst of memory instructions holds up the matrix pipe (a wave whose VMEM
+    // issue stalls cannot issue MFMAs meanwhile).  Reads are issued in the order the MFMAs consume
+    // them (a[0], b[0..3], a[1..3]), so each MFMA waits only for its own operands.
+    h8v a0[4], b0[4], a1[4], b1[4];
+    auto read_one = [&](int st, int sl, int q, h8v* av, h8v* bv) {
+        const uint32_t* As = lds + DENSE_A0 + (st % NB) * DENSE_TILE_U32;
+        const uint32_t* Bs = lds + DENSE_B0 + (st % NB) * DENSE_TILE_U32;
+        constexpr int ord[8] = { 0, 4, 5, 6, 7, 1, 2, 3 };       // a0, b0..b3, a1..a3
+        const int o = ord[q];
+        if (o < 4) av[o] = __builtin_bit_cast(h8v, *(const u32x4*) (As + x_off(128 * wm + 32 * o + l32, 2 * sl + lh)));
+        else bv[o - 4] = __builtin_bit_cast(h8v, *(const u32x4*) (Bs + x_off(128 * wn + 32 * (o - 4) + l32, 2 * sl + lh)));
+    };
+    auto issue_one = [&](int st, int q) {
+        const int c = min(st, NST - 1);
+        const int buf = (st % NB) * DENSE_TILE_U32, j = q >> 1;
+        if (q & 1)
+            __builtin_amdgcn_global_load_lds((const void*) (b_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
+                                             (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
+    };
+    #pragma unroll
+    for (int q = 0; q < 8; ++q) read_one(0, 0, q, a0, b0);
+    for (int s = 0; s < NST; ++s)
+    {
+        #pragma unroll
+        for (int t = 0; t < 16; ++t)
+        {
+            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[t >> 2], b0[t & 3], acc[t >> 2][t & 3], 0, 0, 0);
+            if (t & 1) issue_one(s + D, t >> 1);
+            else read_one(s, 1, t >> 1, a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // stage s + 1 landed for this wave, its own reads of stage s are complete: barrier, after
+        // which every wave's reads of stage s are complete too (its buffer is refilled next stage)
+        DENSE_VM_LGKM0(8 * (D - 1));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // slice 0 of stage s + 1 read under the MFMAs of slice 1 (past the end: an unread buffer)
+        #pragma unroll
+        for (int t = 0; t < 16; ++t)
+        {
+            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[t >> 2], b1[t & 3], acc[t >> 2][t & 3], 0, 0, 0);
+            if (!(t & 1)) read_one(s + 1, 0, t >> 1, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    DENSE_VM_LGKM0(0);
+    __builtin_amdgcn_s_barrier();
+
+    // epilogue: 4 rounds; round r holds rows 128 wm + 32 r + (0..31) of each wave in E[64][256]
+    float* E = (float*) lds;
+    const bool has_svh = svh != nullptr;
+    #pragma unroll
+    for (int r = 0; r < 4; ++r)
+    {
+        #pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            #pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    E[(32 * wm + 8 * jj + 4 * lh + i) * DENSE_BN + 128 * wn + 32 * j + l32] = acc[r][j][4 * jj + i];
+            }
+        }
+        __syncthreads();
+        #pragma unroll 2
+        for (int q = 0; q < 32; ++q)
+        {
+            const int rc = wave * 32 + q;
+            const int er = rc >> 1, ch = rc & 1;
+            const int row = mb * DENSE_BM + 128 * (er >> 5) + 32 * r + (er & 31);
+            const int col = nb * DENSE_BN + 128 * ch + 2 * lane;
+            if (nb * DENSE_BN + 128 * ch >= n) continue;
+            const f32x2 v = *(const f32x2*) (E + er * DENSE_BN + 128 * ch + 2 * lane);
+            const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                     int m, int k, int n, int variant, hipStream_t s)
+{
+    const int blocks = ((n + DENSE_BN - 1) / DENSE_BN) * ((m + DENSE_BM - 1) / DENSE_BM);
+    if (variant == 1)
+        hipLaunchKernelGGL((dense_gemm_kernel<3>), dim3(blocks), dim3(DENSE_T), 0, s, A, WT, C, svh, m, k, n, c_fp32);
+    else
+        hipLaunchKernelGGL((dense_gemm4_kernel<3>), dim3(blocks), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32);
+    return (int) hipGetLastError();
+}

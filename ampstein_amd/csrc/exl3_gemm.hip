@@ -150,38 +150,6 @@ __device__ __forceinline__ u32x4 decode_run(const uint32_t* __restrict__ tl, con
                      weight_pair<CB>(r[4], r[5]), weight_pair<CB>(r[6], r[7]) };
 }
 
-// Output rotation of one fp32 row chunk (elements 2l, 2l+1) and store: had_fh / had_ff.
-__device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp32, bool has_svh, uint32_t svp,
-                                           size_t idx, int lane)
-{
-    if (has_svh)
-    {
-        fwht128_wave(v0, v1, lane);
-        v0 *= EXL3_HAD_RSCALE;
-        v1 *= EXL3_HAD_RSCALE;
-        const f16x2 s = as_h2(svp);
-        if (!c_fp32)
-        {
-            f16x2 h = { (f16) v0, (f16) v1 };
-            h = h * s;
-            *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
-            return;
-        }
-        v0 *= (float) s.x;
-        v1 *= (float) s.y;
-    }
-    if (c_fp32)
-    {
-        f32x2 o = { v0, v1 };
-        *(f32x2*) ((float*) C + idx) = o;
-    }
-    else
-    {
-        f16x2 h = { (f16) v0, (f16) v1 };
-        *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
-    }
-}
-
 // Swizzled LDS offsets (u32 units).  A: row stride 16 u32 (4 chunks of 16 B), chunk ^= (row >> 2) & 3
 // (gfx950 LDS: 64 banks; the 16 lanes of a ds_read_b128 phase touch 16 distinct 16-byte groups).
 // B: per slice, column stride 8 u32 (2 chunks), chunk ^= ((col >> 2) ^ (col >> 3)) & 1.  The

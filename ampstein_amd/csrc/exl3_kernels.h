@@ -241,6 +241,14 @@ int exl3k_xcd_probe(int* out, int blocks_x, int blocks_y, hipStream_t s);
 int exl3k_mgemm_filter(const int64_t* indices, const uint16_t* weights, int bszm, int min_index,
                        int max_index, int num_tokens, int64_t* idx_out, uint16_t* w_out, hipStream_t s);
 
+// reconstruct_had written transposed: WT (n, k)
+int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                             const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                             int K, int cb, hipStream_t s);
+// Dense fp16 GEMM C (m, n) = A (m, k) . WT (n, k)^T, fp32 accumulation; svh non-null: output
+// rotation per 128-column chunk, x svh (exl3_dense.hip)
+int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                     int m, int k, int n, int variant, hipStream_t s);
 int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
                  const uint16_t* pre, const uint16_t* post, float scale, hipStream_t s);
 

@@ -222,11 +222,14 @@ __device__ __forceinline__ f16x2 had_h2x32(f16x2 v, int lane)
     return had_h2_stage<16>(v, lane);
 }
 
-template <int K, int CB>
+// TR: write the block transposed, WT (n, k) row-major (the layout the recon route's dense GEMM
+// reads): the row pass leaves its fp16 results in LDS, then each wave stores whole 128-element
+// columns.  The values are those of the (k, n) form, bit for bit.
+template <int K, int CB, bool TR>
 __global__ __launch_bounds__(256)
 void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ trellis,
                             const uint16_t* __restrict__ suh, const uint16_t* __restrict__ svh,
-                            int n, int tiles_n, int nt_off)
+                            int n, int tiles_n, int nt_off, int k)
 {
     __shared__ __align__(16) uint32_t blk[128 * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -298,8 +301,29 @@ void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict
         const f16x2 su2 = { su, su };
         h01 = (h01 * su2) * as_h2(sv01);
         h23 = (h23 * su2) * as_h2(sv23);
-        u32x2 o = { as_u32(h01), as_u32(h23) };
-        *(u32x2*) (W + (size_t) (kb * 128 + R) * n + nb * 128 + 4 * t) = o;
+        if constexpr (TR)
+        {
+            blk[d] = as_u32(h01);                          // in place: this lane's own words
+            blk[d + 1] = as_u32(h23);
+        }
+        else
+        {
+            u32x2 o = { as_u32(h01), as_u32(h23) };
+            *(u32x2*) (W + (size_t) (kb * 128 + R) * n + nb * 128 + 4 * t) = o;
+        }
+    }
+    if constexpr (TR)
+    {
+        // 4. column c of the block = 128 contiguous k of row nb * 128 + c of WT: lane l stores rows
+        //    R = 2l, 2l + 1 of it as one u32 (wave w: columns w, w + 4, ...)
+        __syncthreads();
+        for (int c = wave; c < 128; c += 4)
+        {
+            const int R = 2 * lane;
+            const uint32_t lo = b16[rh_dw(R, c >> 1) * 2 + (c & 1)];
+            const uint32_t hi = b16[rh_dw(R + 1, c >> 1) * 2 + (c & 1)];
+            *(uint32_t*) (W + (size_t) (nb * 128 + c) * k + kb * 128 + R) = lo | (hi << 16);
+        }
     }
 }
 
@@ -327,7 +351,19 @@ int launch_reconstruct_had_t(uint16_t* W, const uint16_t* trellis, const uint16_
                              hipStream_t s)
 {
     dim3 grid(n / 128, k / 128);
-    hipLaunchKernelGGL((reconstruct_had_kernel<K, CB>), grid, dim3(256), 0, s, W, trellis, suh, svh, n, tiles_n, nt_off);
+    hipLaunchKernelGGL((reconstruct_had_kernel<K, CB, false>), grid, dim3(256), 0, s, W, trellis, suh, svh, n, tiles_n,
+                       nt_off, k);
+    return (int) hipGetLastError();
+}
+
+template <int K, int CB>
+int launch_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                              const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                              hipStream_t s)
+{
+    dim3 grid(n / 128, k / 128);
+    hipLaunchKernelGGL((reconstruct_had_kernel<K, CB, true>), grid, dim3(256), 0, s, WT, trellis, suh, svh, n, tiles_n,
+                       nt_off, k);
     return (int) hipGetLastError();
 }
 
@@ -383,4 +419,11 @@ int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, in
                          int nt_off, int K, int cb, const uint16_t* svh, hipStream_t s)
 {
     EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, svh, s)
+}
+
+int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                             const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
+                             int K, int cb, hipStream_t s)
+{
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_had_tr, WT, trellis, suh, svh, k, n, tiles_n, nt_off, s)
 }

@@ -33,15 +33,6 @@ Tensor = torch.Tensor
 # the activation rotations are HBM-bound and short): AMP_RECON_FUSED_ROWS=0 never takes the fused
 # branch (the opt-in MI355X routing).
 RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", "2048")) or (1 << 30)
-# Tuned dense GEMM for the recon path (PyTorch TunableOp: hipBLASLt and rocBLAS solutions timed
-# per shape on first use): 8-20 % faster than the default heuristic at M = 2048.
-RECON_TUNED_GEMM = os.environ.get("AMP_RECON_TUNABLE", "1") != "0"
-# Rotated branch: AMP_RECON_FOLD_SVH=1 folds the output rotation and svh into the transposed
-# reconstruct (when rows >= k / 4) instead of rotating y afterwards.  Off by default: on MI355X
-# the fold makes the reconstruct ALU-bound (8192 -> 28672 at 2048 rows: ~1200 us per call
-# against 940-1070 us with the separate rotation of y).
-RECON_FOLD_SVH = os.environ.get("AMP_RECON_FOLD_SVH", "0") != "0"
-
 
 def _ptr(t: Optional[Tensor]):
     return None if t is None else t.data_ptr()
@@ -168,6 +159,51 @@ def reconstruct_had_slice(unpacked: Tensor, packed: Tensor, suh: Tensor, svh: Te
             unpacked.data_ptr(), packed.data_ptr(), suh.data_ptr(), svh.data_ptr(),
             unpacked.size(0), packed.size(1) * 16, unpacked.size(1), int(n_offset), float(K),
             mcg_i, mul1_i, _stream(unpacked)))
+
+
+def reconstruct_had_t(unpacked_t: Tensor, packed: Tensor, suh: Tensor, svh: Tensor,
+                      K: float, mcg: bool = False, mul1: bool = False, n_offset: int = 0) -> None:
+    """reconstruct_had_slice written transposed: unpacked_t (n, k) = (diag(suh) H W_hat H
+    diag(svh))^T per 128 x 128 block, bit for bit the values of reconstruct_had_slice.  The
+    layout recon_mm reads (no reference counterpart: the reference keeps W (k, n) for cuBLAS)."""
+    bits, half = bits_from_K(K)
+    _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
+    _need(packed.dim() == 3 and unpacked_t.dim() == 2, "reconstruct_had: bad tensor ranks")
+    _need(unpacked_t.size(1) == packed.size(0) * 16 and n_offset >= 0
+          and n_offset + unpacked_t.size(0) <= packed.size(1) * 16, "unpacked and packed shapes are incompatible")
+    _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
+    for t, nm in ((unpacked_t, "unpacked"), (suh, "suh"), (svh, "svh")):
+        _dtype(t, torch.half, nm)
+    _trellis_dtype(packed, "packed")
+    if unpacked_t.numel() == 0:
+        return
+    _need(suh.numel() >= unpacked_t.size(1), "reconstruct_had: suh size")
+    _need(svh.numel() >= unpacked_t.size(0), "reconstruct_had: svh size")
+    _cuda(unpacked_t, packed, suh, svh)
+    with torch.cuda.device(unpacked_t.device):
+        check(_lib.lib().exl3_amd_reconstruct_had_t(
+            unpacked_t.data_ptr(), packed.data_ptr(), suh.data_ptr(), svh.data_ptr(), unpacked_t.size(1),
+            packed.size(1) * 16, unpacked_t.size(0), int(n_offset), float(K), int(bool(mcg)), int(bool(mul1)),
+            _stream(unpacked_t)))
+
+
+def recon_mm(a: Tensor, wt: Tensor, out: Tensor, svh: Optional[Tensor] = None) -> None:
+    """out (m, n) = a (m, k) @ wt (n, k)^T on the hand-written MFMA kernel (exl3_amd_recon_mm),
+    fp32 accumulation, out fp16 or fp32; with svh each 128-column chunk of the fp32 result is
+    rotated (H128 / sqrt(128)) and scaled by svh before the store."""
+    _dtype(a, torch.half, "a")
+    _dtype(wt, torch.half, "wt")
+    _need(out.dtype in (torch.half, torch.float), "out is incorrect datatype, must be half or float")
+    _need(a.dim() == 2 and wt.dim() == 2 and out.dim() == 2 and a.size(1) == wt.size(1)
+          and out.shape == (a.size(0), wt.size(0)), "recon_mm: incompatible shapes")
+    _need(a.is_contiguous() and wt.is_contiguous() and out.is_contiguous(), "recon_mm: tensors must be contiguous")
+    if svh is not None:
+        _dtype(svh, torch.half, "svh")
+        _need(svh.numel() >= wt.size(0), "svh too short")
+    _cuda(a, wt, out, svh)
+    with torch.cuda.device(a.device):
+        check(_lib.lib().exl3_amd_recon_mm(a.data_ptr(), wt.data_ptr(), out.data_ptr(), int(out.dtype == torch.float),
+                                           _ptr(svh), a.size(0), a.size(1), wt.size(0), _stream(a)))
 
 
 def had_r_128(input: Tensor, output: Tensor, pre_scale: Optional[Tensor] = None,
@@ -584,11 +620,11 @@ def exl3_gemm_norm(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], svh: 
             _stream(A)))
 
 
-def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
-    """out = a @ b on the dense GEMM library, with TunableOp scoped to this call (the caller's
-    process-wide setting is restored)."""
+def _library_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
+    """out = a @ b on the vendor GEMM library (hipBLASLt / rocBLAS through torch.mm, TunableOp
+    scoped to this call): the comparison path of bench.py, never the default route."""
     tun = getattr(torch.cuda, "tunable", None)
-    if not RECON_TUNED_GEMM or tun is None:
+    if tun is None:
         torch.mm(a, b, out=out)
         return
     was = tun.is_enabled()
@@ -602,35 +638,36 @@ def _recon_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
 
 
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
-                    mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None) -> Tensor:
+                    mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None,
+                    gemm: str = "hip") -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to
     fp16 once, then one dense GEMM.  rows >= 2048: original-basis W and y = x @ W; otherwise
-    y = had(had(x o suh) @ W_hat) o svh.  The dense GEMM is torch.mm on hipBLASLt / rocBLAS,
-    tuned per shape (_recon_mm)."""
+    y = had(had(x o suh) @ W_hat) o svh.  The weight is reconstructed transposed, (n, k), and the
+    dense GEMM is this build's MFMA kernel (recon_mm), which in the rotated branch also applies
+    the output rotation and svh in its epilogue.  gemm="library" runs the same reconstructions
+    with the vendor GEMM (torch.mm) instead, for comparison."""
     _need(trellis.dim() == 3, "exl3_gemm_recon: trellis must be 3-D")
+    _need(gemm in ("hip", "library"), "exl3_gemm_recon: gemm must be 'hip' or 'library'")
     k, n = trellis.size(0) * 16, trellis.size(1) * 16
     _need(x.dim() == 2 and x.size(1) == k and suh.numel() == k and svh.numel() == n and n <= 32768,
           f"exl3_gemm_recon: incompatible shapes (x {tuple(x.shape)}, weight {k} x {n})")
     rows = x.size(0)
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device)
-    w = torch.empty((k, n), dtype=x.dtype, device=x.device)
+    wt = torch.empty((n, k), dtype=x.dtype, device=x.device)
     if rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows):
-        reconstruct_had_slice(w, trellis, suh, svh, K, mcg, mul1, 0)
-        _recon_mm(x, w, y)
-    else:
-        # W_hat stored transposed: the GEMM then reads both operands k-contiguous (~15 %
-        # faster in hipBLASLt on MI355X at M = 2048)
-        xh = torch.empty_like(x)
-        wt = w.view(n, k)
-        had_r_128(x, xh, suh, None, 1.0)
-        # the fold adds ALU work per weight (k n) and saves a pass over y (rows n): taken when y
-        # is large against W (measured on MI355X: 8192 -> 28672 at 2048 rows gains, 28672 -> 8192 loses)
-        if RECON_FOLD_SVH and 4 * rows >= k:
-            reconstruct_t(wt, trellis, K, mcg, mul1, svh=svh)
-            _recon_mm(xh, wt.t(), y)
+        reconstruct_had_t(wt, trellis, suh, svh, K, mcg, mul1, 0)
+        if gemm == "hip":
+            recon_mm(x.contiguous(), wt, y)
         else:
-            reconstruct_t(wt, trellis, K, mcg, mul1)
-            _recon_mm(xh, wt.t(), y)
+            _library_mm(x, wt.t(), y)
+    else:
+        xh = torch.empty_like(x)
+        had_r_128(x, xh, suh, None, 1.0)
+        reconstruct_t(wt, trellis, K, mcg, mul1)
+        if gemm == "hip":
+            recon_mm(xh, wt, y, svh)
+        else:
+            _library_mm(xh, wt.t(), y)
             had_r_128(y, y, None, svh, 1.0)
     return y
 

@@ -53,10 +53,12 @@ def parse():
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE expert GEMV line")
     ap.add_argument("--no-qwen", action="store_true", help="skip the configs[2] Qwen-27B-class line")
     ap.add_argument("--pmc-child", nargs="?", const="gateup", default=None,
-                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | moe | moes | qwenm")
+                    help="profiled child for rocprofv3 --pmc: decode | gateup | prefill | dense | moe | moes | qwenm")
     ap.add_argument("--summarize-pmc", metavar="PMC_DIR", nargs="+",
                     help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
                          "directories (one per counter pass) and exit")
+    ap.add_argument("--rates", action="store_true",
+                    help="print the gfx950 issue-rate microbenchmarks (ampstein_amd/csrc/exl3_probe.hip) and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
     return ap.parse_args()
@@ -290,39 +292,51 @@ def timed(torch, fn, reps=5):
 
 
 def prefill_bench(torch):
-    """M = 2048 fp16 x N(0,1) against 8192->28672 and 28672->8192 at 4 bpw (3INST).  Paths:
-    recon = the reference's routing for rows >= 2048 (amp_torch.cpp:11149-11230: our
-    reconstruct_had, then one hipBLASLt fp16 GEMM); recon_rotated = its rows < 2048 branch
-    (input/output Hadamard around W_hat); fused = our MFMA kernel (exl3_gemm, m > 8)."""
+    """M = 2048 fp16 x N(0,1) against 8192->28672 and 28672->8192 at 4 bpw (3INST).  Paths, all on
+    this build's kernels: fused = the MFMA GEMM decoding the trellis in its loop (exl3_gemm, m > 8);
+    recon = the reference's routing for rows >= 2048 (amp_torch.cpp:11149-11230): reconstruct_had_t
+    then the dense MFMA GEMM (recon_mm); recon_rotated = its rows < 2048 branch (had128 on x,
+    reconstruct_t, recon_mm with the output rotation in its epilogue); dense_gemm = recon_mm alone on
+    a reconstructed W_hat^T.  Beside them, labelled comparisons on the vendor library (torch.mm on
+    hipBLASLt / rocBLAS, tuned): the same dense GEMM and the rotated recon route around it."""
     from ampstein_amd import ops
     M = 2048
     res = {}
+    mine = ("fused", "recon", "recon_rotated", "dense_gemm")
+    lib = ("library_dense_gemm", "library_recon_rotated")
     for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
         t, s, v = host_trellis(torch, k, n, 4, 4000 + si)
         x = host_normal(torch, (M, k), 4010 + si)
         ah = torch.empty_like(x)
         C = torch.empty((M, n), dtype=torch.half, device="cuda")
+        wt = torch.empty((n, k), dtype=torch.half, device="cuda")
+        ops.reconstruct_t(wt, t, 4.0)
         flops = 2.0 * M * k * n
         row = {}
-        for name, fn in (("recon", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=2048)),
+        for name, fn in (("fused", lambda: ops.exl3_gemm(x, t, C, s, ah, v)),
+                         ("recon", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=2048)),
                          ("recon_rotated", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30)),
-                         ("fused", lambda: ops.exl3_gemm(x, t, C, s, ah, v))):
+                         ("dense_gemm", lambda: ops.recon_mm(x, wt, C)),
+                         ("library_dense_gemm", lambda: ops._library_mm(x, wt.t(), C)),
+                         ("library_recon_rotated", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30,
+                                                                             gemm="library"))):
             us = timed(torch, fn)
             row[name] = {"us": round(us, 1), "TFLOPS": round(flops / us / 1e6, 1),
                          "frac_mfma_peak": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
         res[f"{k}x{n}"] = row
-        del t, s, v, x, ah, C
+        del t, s, v, x, ah, C, wt
         torch.cuda.empty_cache()
-    best = {name: sum(2.0 * M * int(sh.split("x")[0]) * int(sh.split("x")[1]) for sh in res) /
-            sum(res[sh][name]["us"] for sh in res) / 1e6 for name in ("recon", "recon_rotated", "fused")}
-    # the credited line is this build's own kernel; the recon paths run their dense GEMM on
-    # hipBLASLt / rocBLAS and are reported beside it as labelled comparisons
+    tot = lambda name: sum(2.0 * M * int(sh.split("x")[0]) * int(sh.split("x")[1]) for sh in res) / \
+        sum(res[sh][name]["us"] for sh in res) / 1e6
+    best = {name: tot(name) for name in mine + lib}
+    route = max(("fused", "recon", "recon_rotated"), key=lambda nm: best[nm])
     return {"metric": "prefill GEMM TFLOPS at M=2048 (configs[3], 4 bpw 3INST)", "m": M,
-            "value": round(best["fused"], 1), "unit": "TFLOPS",
-            "path": "fused: exl3_gemm m > 8, hand-written MFMA kernel (gemm_dma_kernel)",
-            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best["fused"] / MFMA_F16_PEAK_TFLOPS, 4),
-            "comparison_paths_TFLOPS": {"recon (reconstruct_had + hipBLASLt, reference routing)": round(best["recon"], 1),
-                                        "recon_rotated (reconstruct_t + hipBLASLt + had128)": round(best["recon_rotated"], 1)},
+            "value": round(best[route], 1), "unit": "TFLOPS",
+            "path": f"{route} (fastest of this build's hand-written routes; no vendor GEMM)",
+            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best[route] / MFMA_F16_PEAK_TFLOPS, 4),
+            "paths_TFLOPS": {nm: round(best[nm], 1) for nm in mine},
+            "dense_gemm_frac_mfma_peak": round(best["dense_gemm"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "comparison_library_TFLOPS": {nm: round(best[nm], 1) for nm in lib},
             "per_shape": res}
 
 
@@ -543,6 +557,8 @@ def pmc_child(workload="decode"):
                  gate/up stacked mgemm, down gemm: four GEMV grids);
       gateup  -- the stacked gate/up mgemm alone, 2 x 4 launches (the traffic passes);
       prefill -- the MFMA GEMM at 2048 rows on 8192 -> 28672 and 28672 -> 8192;
+      dense   -- the recon route's dense GEMM (recon_mm, both kernel forms) and the vendor
+                 library's torch.mm on the same operands, 2048 rows, both shapes;
       moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice;
       moes    -- the token-sorted exl3_moe on the same experts, T = 512 and 2048;
       qwenm   -- the row-batched matrix-core GEMV (gemvm_kernel) on the configs[2] shapes 5120 -> 17408
@@ -573,8 +589,27 @@ def pmc_child(workload="decode"):
             t, s, v = host_trellis(torch, k, n, 4, 4000 + si)
             x = host_normal(torch, (2048, k), 4010 + si)
             C = torch.empty((2048, n), dtype=torch.half, device="cuda")
+            wt = torch.empty((n, k), dtype=torch.half, device="cuda")
             for _ in range(2):
                 ops.exl3_gemm(x, t, C, s, torch.empty_like(x), v)
+            for _ in range(2):
+                ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30)
+                ops.reconstruct_t(wt, t, 4.0)
+                ops.recon_mm(x, wt, C)
+            del t, s, v, x, C, wt
+    elif workload == "dense":
+        from ampstein_amd import _lib
+        for k, n in ((28672, 8192), (8192, 28672)):
+            x = host_normal(torch, (2048, k), 4020)
+            wt = host_normal(torch, (n, k), 4021)
+            C = torch.empty((2048, n), dtype=torch.half, device="cuda")
+            for var in (0, _lib.RECON_MM_8WAVES):
+                with _lib.policy(_lib.POLICY_RECON_MM, var):
+                    for _ in range(2):
+                        ops.recon_mm(x, wt, C)
+            for _ in range(2):
+                torch.mm(x, wt.t(), out=C)            # the vendor library's default solution
+            del x, wt, C
     elif workload == "moe":
         moe_bench(torch, reps=1, ms=(16,), token_sorted=False, graph=False)
     elif workload == "moes":
@@ -613,7 +648,7 @@ def summarize_pmc(outdirs):
             with open(path) as f:
                 for r in csv.DictReader(f):
                     name = r["Kernel_Name"]
-                    if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "moeg", "reconstruct", "had128", "copy", "Copy")):
+                    if not any(key in name for key in ("gemv", "gemm", "moe_", "moes_", "moeg", "reconstruct", "had128", "copy", "Copy", "Cijk")):
                         continue
                     key = (name.replace("(anonymous namespace)::", "").split("(")[0][:80], r.get("Grid_Size", ""))
                     d = acc.setdefault(key, {}).setdefault(r["Counter_Name"], {})
@@ -703,7 +738,7 @@ def summarize_trace(path):
     with open(path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "moeg", "rms_norm", "silu_mul")):
+            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "moeg", "rms_norm", "silu_mul", "Cijk")):
                 continue
             grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
             d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
@@ -715,8 +750,63 @@ def summarize_trace(path):
     return 0
 
 
+RATE_OPS = ["v_bfe_u32", "v_mad_u64_u32", "v_bitop3_b32", "v_mad_u32_u16", "v_perm_b32", "v_alignbit_b32",
+            "v_dot2_f32_f16", "v_pk_fma_f16", "v_add_u32", "v_mul_lo_u32"]
+
+
+def rates():
+    """Issue rates of single VALU instruction kinds (8 independent chains per lane, 4 waves per
+    SIMD on every CU) and of random 16-bit LDS gathers from a 128 KiB table (one 1024-thread
+    workgroup per CU), from ampstein_amd/lib/libexl3_probe.so.  Rates are wave64 instructions per
+    SIMD per ns; `rel` divides by v_bfe_u32's rate (clock-independent)."""
+    import ctypes
+    import torch
+    from ampstein_amd import build as B
+    assert torch.cuda.is_available(), "bench.py --rates needs a GPU"
+    torch.cuda.set_device(0)
+    L = ctypes.CDLL(B.PROBE_LIB)
+    L.exl3_probe_valu.restype = ctypes.c_float
+    L.exl3_probe_valu.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    L.exl3_probe_lds_gather.restype = ctypes.c_float
+    L.exl3_probe_lds_gather.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_lane = L.exl3_probe_chains()
+    blocks, iters = 4 * cus, 4000                       # 4 workgroups of 4 waves per CU: 4 waves per SIMD
+    out = torch.zeros(16 * blocks, dtype=torch.int32, device="cuda")
+    simds = 4 * cus
+    res = {"cus": cus, "waves_per_simd": 4, "valu": {}}
+    for op, name in enumerate(RATE_OPS):
+        best = None
+        for _ in range(3):
+            ms = L.exl3_probe_valu(op, out.data_ptr(), blocks, iters)
+            assert ms > 0, f"probe {name} failed"
+            best = ms if best is None else min(best, ms)
+        insts = blocks * 4 * iters * per_lane              # wave instructions
+        res["valu"][name] = {"ms": round(best, 3), "per_simd_per_ns": round(insts / simds / (best * 1e6), 4)}
+    base = res["valu"]["v_bfe_u32"]["per_simd_per_ns"]
+    for name in RATE_OPS:
+        res["valu"][name]["rel"] = round(res["valu"][name]["per_simd_per_ns"] / base, 3)
+    g_iters = 1000
+    lds = {}
+    for mode, name in ((0, "gather"), (1, "valu_only")):
+        best = None
+        for _ in range(3):
+            ms = L.exl3_probe_lds_gather(out.data_ptr(), cus, g_iters, mode)
+            assert ms > 0, "lds probe failed"
+            best = ms if best is None else min(best, ms)
+        gathers = cus * 16 * g_iters * per_lane            # wave-level ds_read_u16 instructions
+        lds[name] = {"ms": round(best, 3), "wave_gathers_per_cu_per_ns": round(gathers / cus / (best * 1e6), 4),
+                     "weights_per_s": round(gathers * 64 / (best * 1e-3) / 1e12, 3)}
+    lds["note"] = "weights_per_s in T/s: 64 lanes x wave gathers; one 16-bit table entry per weight"
+    res["lds_gather_128k"] = lds
+    print(json.dumps(res))
+    return 0
+
+
 def main():
     args = parse()
+    if args.rates:
+        return rates()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace)
     if args.summarize_pmc:

@@ -59,7 +59,8 @@ int exl3_amd_version(void);
                                              * value (32 / 64 / 96 / 128; LDS-tiled: 64 / 128 / 256)  */
 #define EXL3_AMD_POLICY_MOE_OUTPUT      4   /* exl3_amd_moe output kernel                              */
 #define EXL3_AMD_MOE_OUTPUT_ATOMIC      1   /*   per-row atomics instead of the per-token lists         */
-#define EXL3_AMD_POLICY_RECON_GEMM      5   /* dense GEMM of exl3_amd_recon_mm                         */
+#define EXL3_AMD_POLICY_RECON_MM        5   /* kernel of exl3_amd_recon_mm                             */
+#define EXL3_AMD_RECON_MM_8WAVES        1   /*   8 waves of 128 x 64 instead of 4 waves of 128 x 128    */
 #define EXL3_AMD_POLICY_COUNT           6
 int exl3_amd_set_policy(int key, int value);
 int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */
@@ -74,6 +75,15 @@ int exl3_amd_init(int device);
  * XCD-local split-k hand-off is off and a finish kernel sums the partials).  No counterpart in
  * the reference; for tests and benchmarks. */
 int exl3_amd_device_info(int device, int* num_cus, int* num_xcd);
+
+/* Test hooks (no counterpart in the reference).  The per-device workspace holds split-k
+ * partials and, during exl3_amd_moe, the token-sorted MoE's plan (row map, row tiles, tile lists,
+ * chunk sums, per-token position lists).  read_workspace copies `bytes` from byte `offset` of it
+ * to host memory; fill_workspace sets every byte of it (e.g. 0xff: int -1, fp32 NaN) so that a
+ * test can show that a call reads nothing it did not write.  Both synchronise the device; neither
+ * may be called while work that uses the workspace is being captured. */
+int exl3_amd_debug_read_workspace(int device, int64_t offset, int64_t bytes, void* host_dst);
+int exl3_amd_debug_fill_workspace(int device, int byte_value);
 
 /* W_hat (k, n) fp16 = decoded trellis columns [n_offset, n_offset + n) of a packed tensor
  * whose full width is n_packed, in the Hadamard basis.  k % 16 == 0, n % 128 == 0,
@@ -294,6 +304,22 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
                        const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
                        int m, int k, int n, float K, int mcg, int mul1,
                        uint16_t* h, const uint16_t* w, uint16_t* r, float eps, void* stream);
+
+/* exl3_amd_reconstruct_had written transposed: WT (n, k) row-major, WT[c][r] = W[r][c], the same
+ * fp16 values bit for bit.  The layout exl3_amd_recon_mm reads.  No counterpart in the reference
+ * (reconstruct_had_slice, quant/reconstruct.cu:431-490, writes (k, n) for cuBLAS); the recon
+ * route's many-rows branch (src/torch/amp_torch.cpp:11203-11209) uses it. */
+int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                               const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                               float K, int mcg, int mul1, void* stream);
+
+/* Dense fp16 GEMM of the recon route: C (m, n) = A (m, k) . WT^T with the weight stored transposed,
+ * WT (n, k) row-major; fp32 accumulation; C fp32 (c_fp32) or fp16.  svh non-null: each 128-column
+ * chunk of the fp32 row is rotated (H128 / sqrt(128)) and multiplied by svh before the store (the
+ * rotated branch's output rotation).  k % 32 == 0, n % 128 == 0, any m.  Hand-written MFMA kernel
+ * (exl3_dense.hip).  Replaces the cuBLAS GEMM of the recon route (src/torch/amp_torch.cpp:11083-11230). */
+int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                      int m, int k, int n, void* stream);
 
 /* exl3_amd_reconstruct_t with the output rotation folded in: WT (n, k) = (W_hat H128 diag(svh)
  * / sqrt(128))^T for columns [n_offset, n_offset + n), svh the full (n_packed) vector.  fp32

@@ -144,3 +144,25 @@ def host_runs(sel, rw, mn, mx, rows=8):
             prev, cnt = loc[s], 0
         cnt += 1
     return len(starts), starts + [len(order)], order
+
+
+def routing(T, E, topk, seed, sentinel=0):
+    """Top-k routing of T tokens over E experts (distinct experts per token); `sentinel`
+    assignments get the id E (the reference's "less than top-k" bin)."""
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((T, E))
+    sel = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    rw = np.take_along_axis(p, sel, axis=1).astype(np.float16)
+    flat = sel.reshape(-1).astype(np.int64)
+    if sentinel:
+        flat[rng.choice(flat.size, sentinel, replace=False)] = E
+    order = np.argsort(flat, kind="stable")
+    token_sorted = (order // topk).astype(np.int64)
+    weight_sorted = rw.reshape(-1)[order]
+    count = np.bincount(flat, minlength=E + 1).astype(np.int64)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    start = np.concatenate([[0], np.cumsum(count)[:-1]]).astype(np.int64)
+    return flat, order, inv, token_sorted, weight_sorted, count, start

@@ -116,7 +116,7 @@ def test_gemm_optional_rotations(torch_cuda, orc, suh, svh):
 
 
 def test_gemm_forced_kernel_and_rows(torch_cuda, orc):
-    """force_shape_idx 2 runs the MFMA kernel for m <= 8; 1 forces the GEMV (m <= 8 only)."""
+    """force_shape_idx 2 runs the MFMA kernel for m <= 8; 1 forces the GEMV for any row count."""
     torch = torch_cuda
     from ampstein_amd import ops, _lib
     L = synth.layer(256, 128, 4, 0, seed=88)
@@ -127,9 +127,11 @@ def test_gemm_forced_kernel_and_rows(torch_cuda, orc):
     assert ops.exl3_gemm(A, t, C, s, torch.empty_like(A), v, 2) == 91
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4, cb=0)
     assert rel_err(C.cpu().numpy(), ref) < TOL
-    A9 = torch.zeros((9, 256), dtype=torch.half, device="cuda")
-    with pytest.raises(_lib.Exl3Error, match="at most 8"):
-        ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, torch.empty_like(A9), v, 1)
+    x9 = synth.activations(9, 256, seed=89)
+    A9 = torch.from_numpy(x9).cuda()
+    C9 = torch.empty((9, 128), dtype=torch.float, device="cuda")
+    assert ops.exl3_gemm(A9, t, C9, s, torch.empty_like(A9), v, 1) == 90
+    assert rel_err(C9.cpu().numpy(), orc.linear_f64(x9, L.trellis, L.suh, L.svh, 4, cb=0)) < TOL
     with pytest.raises(_lib.Exl3Error, match="A_had"):
         ops.exl3_gemm(A9, t, torch.empty((9, 128), dtype=torch.half, device="cuda"), s, None, v)
 
@@ -170,7 +172,7 @@ def test_gemm_recon(torch_cuda, orc, branch, K, cb):
 
 
 @pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2), (2.5, 2), (8, 0)])
-def test_reconstruct_t_had(orc, K, cb, monkeypatch):
+def test_reconstruct_t_had(orc, K, cb):
     """W' = W_hat H128 diag(svh) / sqrt(128), transposed: within one fp16 ulp of the fp64 product
     of the oracle's bit-exact W_hat (fp32 butterflies, one rounding), and the recon GEMM's rotated
     branch with the fold against fp64 within 2e-3."""
@@ -189,7 +191,10 @@ def test_reconstruct_t_had(orc, K, cb, monkeypatch):
     ulp = np.abs(ref).clip(min=2.0 ** -14) * 2.0 ** -10
     assert np.all(np.abs(got - ref) <= ulp + 1e-12)
     x = synth.activations(300, k, seed=1)
-    monkeypatch.setattr(ops, "RECON_FOLD_SVH", True)         # 300 rows >= k / 4: the folded branch
-    y = ops.exl3_gemm_recon(torch.from_numpy(x).cuda(), t, s, v, K, cb == 2, cb == 1, fused_rows=1 << 30)
+    xd = torch.from_numpy(x).cuda()
+    xh = torch.empty_like(xd)
+    ops.had_r_128(xd, xh, s, None, 1.0)
+    y = torch.empty((300, n), dtype=torch.half, device="cuda")
+    ops.recon_mm(xh, wt, y)                                  # the folded weight: no output rotation left
     yr = orc.linear(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb, y_fp32=True).astype(np.float64)
     assert np.abs(y.float().cpu().numpy() - yr).max() / np.abs(yr).max() < 2e-3

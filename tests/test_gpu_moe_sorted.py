@@ -12,31 +12,9 @@ import pytest
 import torch
 
 from ampstein_amd import _lib
-from tests.moe_ref import ExpertSet, act_fn, f16, had
+from tests.moe_ref import ExpertSet, act_fn, f16, had, routing
 
 pytestmark = pytest.mark.gpu
-
-
-def routing(T, E, topk, seed, sentinel=0):
-    """Top-k routing of T tokens over E experts (distinct experts per token); `sentinel`
-    assignments get the id E (the reference's "less than top-k" bin)."""
-    rng = np.random.default_rng(seed)
-    logits = rng.standard_normal((T, E))
-    sel = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
-    p = np.exp(logits - logits.max(axis=1, keepdims=True))
-    p /= p.sum(axis=1, keepdims=True)
-    rw = np.take_along_axis(p, sel, axis=1).astype(np.float16)
-    flat = sel.reshape(-1).astype(np.int64)
-    if sentinel:
-        flat[rng.choice(flat.size, sentinel, replace=False)] = E
-    order = np.argsort(flat, kind="stable")
-    token_sorted = (order // topk).astype(np.int64)
-    weight_sorted = rw.reshape(-1)[order]
-    count = np.bincount(flat, minlength=E + 1).astype(np.int64)
-    inv = np.empty_like(order)
-    inv[order] = np.arange(order.size)
-    start = np.concatenate([[0], np.cumsum(count)[:-1]]).astype(np.int64)
-    return flat, order, inv, token_sorted, weight_sorted, count, start
 
 
 def model_row(es, x_row, e, act, limit):
@@ -86,7 +64,7 @@ def model(es, x, flat, token_sorted, weight_sorted, count, start, max_tok, lo, h
     return out, slot_rows
 
 
-def run_moe(es, x, rt, max_tok, concurrency, lo, hi, act, limit, Ks, scratch_mode=False, m_tile=16):
+def run_moe(es, x, rt, max_tok, concurrency, lo, hi, act, limit, Ks, scratch_mode=False, m_tile=16, poison=False):
     flat, order, inv, token_sorted, weight_sorted, count, start = rt
     from ampstein_amd import ops
     T, H = x.shape
@@ -115,6 +93,8 @@ def run_moe(es, x, rt, max_tok, concurrency, lo, hi, act, limit, Ks, scratch_mod
                 acc += int(count[e])
         scratch = torch.full((max(acc, 1), H), float("nan"), dtype=torch.float, device=dev)
         fused_base = torch.from_numpy(fb).to(dev)
+    if poison:       # every workspace int -1, every fp32 NaN: any read of state this call did not write shows
+        _lib.check(_lib.lib().exl3_amd_debug_fill_workspace(torch.cuda.current_device(), 0xFF))
     ops.exl3_moe(xs, out, torch.from_numpy(count).to(dev), torch.from_numpy(token_sorted).to(dev),
                  torch.from_numpy(weight_sorted).to(dev), ts[0], ts[1], ti[0], ti[1], act, Kg, Ku, Kd,
                  tb["g_trellis"], tb["g_suh"], tb["g_svh"], tb["u_trellis"], tb["u_suh"], tb["u_svh"],
@@ -139,7 +119,7 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_exl3_moe(orc, case):
+def test_exl3_moe(orc, case, poison=False):
     name, E, H, I, T, topk, cb, Ks, act, limit, max_tok, conc, lo, hi, sentinel = case
     print(f"exl3_moe case {name}", flush=True)
     es = ExpertSet(torch, orc, E, H, I, H, Ks, cb, seed=CASES.index(case) + 31)
@@ -147,15 +127,69 @@ def test_exl3_moe(orc, case):
     x = rng.standard_normal((T, H)).astype(np.float16)
     rt = routing(T, E, topk, seed=len(name), sentinel=sentinel)
     flat, order, inv, token_sorted, weight_sorted, count, start = rt
-    out, _, _, elig = run_moe(es, x, rt, max_tok, conc, lo, hi, act, limit, Ks)
+    out, _, _, elig = run_moe(es, x, rt, max_tok, conc, lo, hi, act, limit, Ks, poison=poison)
     ref, _ = model(es, x, flat, token_sorted, weight_sorted, count, start, max_tok, lo, hi, act, limit)
     y = out.cpu().numpy().astype(np.float64)
+    assert np.isfinite(y).all(), "non-finite output"
     assert len(elig) > 0
     touched = np.abs(ref).sum(axis=1) > 0
     assert np.all(y[~touched] == 0.0), "rows without an in-range expert must stay untouched"
     err = np.abs(y - ref).max() / np.abs(ref).max()
     print(f"  experts in range {len(elig)}/{E}, rel err {err:.2e}", flush=True)
     assert err < 2e-3
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_exl3_moe_poisoned_workspace(orc, case):
+    """The same cases with the library workspace filled with 0xff bytes before the call (plan
+    ints -1, chunk sums NaN): the call reads only state it wrote, so the results are unchanged."""
+    test_exl3_moe(orc, case, poison=True)
+
+
+READBACK_CASES = [CASES[0], CASES[5], CASES[1]]
+
+
+@pytest.mark.parametrize("case", READBACK_CASES, ids=[c[0] for c in READBACK_CASES])
+def test_exl3_moe_plan_readback(orc, case):
+    """The plan the GPU built for the call's last pass (row map, row tiles, per (matrix, rate)
+    tile lists and counts, per-token position lists, position -> row map) read back from the
+    workspace and compared with the host model (tests/moe_plan_model.py): identical, except that
+    the order within a tile list is the order of LDS atomics and is compared as a set."""
+    from tests import moe_plan_model as pm
+    name, E, H, I, T, topk, cb, Ks, act, limit, max_tok, conc, lo, hi, sentinel = case
+    es = ExpertSet(torch, orc, E, H, I, H, Ks, cb, seed=CASES.index(case) + 31)
+    x = np.random.default_rng(5).standard_normal((T, H)).astype(np.float16)
+    rt = routing(T, E, topk, seed=len(name), sentinel=sentinel)
+    flat, order, inv, token_sorted, weight_sorted, count, start = rt
+    run_moe(es, x, rt, max_tok, conc, lo, hi, act, limit, Ks, poison=True)
+    num_assign = len(token_sorted)
+    pool = min(conc * max_tok, num_assign)
+    tr = pm.tile_rows_for(num_assign, E)
+    lay = pm.Layout(E, T, num_assign, H, I, pool, tr, True)
+    codes = [pm.rate_code(k) for k in Ks]
+    w0 = ((num_assign - 1) // pool) * pool                     # the last pass
+    info, tiles, lists, invd, total = pm.plan(count, E, num_assign, max_tok, lo, hi, pool, tr, w0, [codes] * 3)
+    dev = torch.cuda.current_device()
+
+    def ints(off, n):
+        buf = np.empty(max(n, 1), np.int32)
+        _lib.check(_lib.lib().exl3_amd_debug_read_workspace(dev, 4 * off, 4 * n, buf.ctypes.data))
+        return buf[:n]
+
+    assert np.array_equal(ints(lay.rowinfo, 3 * pool).reshape(pool, 3), info.astype(np.int32))
+    assert np.array_equal(ints(lay.rt, 3 * len(tiles)).reshape(-1, 3), np.array(tiles, np.int32).reshape(-1, 3))
+    counts = ints(lay.counts, 3 * pm.MOES_RATES).reshape(3, pm.MOES_RATES)
+    for m in range(3):
+        for s_ in range(pm.MOES_RATES):
+            assert counts[m, s_] == len(lists[m][s_]), (m, s_)
+            got = ints(lay.lists + (m * pm.MOES_RATES + s_) * lay.rt_cap, int(counts[m, s_]))
+            assert sorted(got.tolist()) == sorted(lists[m][s_]), (m, s_)
+    tstart, tpos = pm.tokens(token_sorted, T)
+    assert np.array_equal(ints(lay.tok_start, T + 1), tstart)
+    assert np.array_equal(ints(lay.tok_pos, len(tpos)), tpos)
+    inv_row = ints(lay.inv_row, num_assign)
+    for pos_, r in invd.items():
+        assert inv_row[pos_] == r, pos_
 
 
 @pytest.mark.parametrize("case", CASES[:3], ids=[c[0] for c in CASES[:3]])

@@ -1,0 +1,106 @@
+"""The recon route's hand-written dense GEMM (exl3_amd_recon_mm, exl3_dense.hip) and the
+transposed original-basis reconstruct (exl3_amd_reconstruct_had_t) through the C ABI.
+
+recon_mm is a floating-point kernel: it is checked against a plain PyTorch fp32 matmul of the same
+fp16 operands (and the output rotation against the fp64 Hadamard), bar max |y - ref| / max |ref|
+< 2e-3 (fp16 output) or 1e-5 (fp32 output, only the summation order differs).
+reconstruct_had_t must equal reconstruct_had transposed, bit for bit.
+"""
+import numpy as np
+import pytest
+from scipy.linalg import hadamard
+
+from ampstein_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from ampstein_amd import ops
+    ops.init(0)
+    return torch
+
+
+def rel(y, ref):
+    y = np.asarray(y, np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 128, 128), (37, 256, 384), (256, 1024, 1024), (300, 512, 640),
+                                   (513, 2048, 256), (1024, 96, 2048)])
+@pytest.mark.parametrize("out", ["fp16", "fp32"])
+@pytest.mark.parametrize("rot", [False, True])
+@pytest.mark.parametrize("variant", [0, 1], ids=["4waves", "8waves"])
+def test_recon_mm_matches_torch_fp32(torch_cuda, kernel_policy, m, k, n, out, rot, variant):
+    torch = torch_cuda
+    from ampstein_amd import ops, _lib
+    kernel_policy(_lib.POLICY_RECON_MM, variant)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m * 7 + k + n)
+    a = torch.randn((m, k), generator=g, device="cuda").half()
+    wt = (torch.randn((n, k), generator=g, device="cuda") * 0.05).half()
+    svh = (torch.randint(0, 2, (n,), generator=g, device="cuda") * 2 - 1).half() if rot else None
+    c = torch.full((m, n), float("nan"), dtype=torch.half if out == "fp16" else torch.float, device="cuda")
+    ops.recon_mm(a, wt, c, svh)
+    ref = (a.float() @ wt.float().t()).double().cpu().numpy()
+    if rot:
+        H = hadamard(128) / np.sqrt(128.0)
+        ref = (ref.reshape(m, n // 128, 128) @ H).reshape(m, n) * svh.double().cpu().numpy()
+    y = c.float().cpu().numpy()
+    assert np.isfinite(y).all()
+    assert rel(y, ref) < (2e-3 if out == "fp16" else 1e-5), (m, k, n, out, rot)
+
+
+def test_recon_mm_rejects(torch_cuda):
+    torch = torch_cuda
+    from ampstein_amd import _lib
+    lib = _lib.lib()
+    a = torch.zeros((4, 64), dtype=torch.half, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.exl3_amd_recon_mm(a.data_ptr(), a.data_ptr(), a.data_ptr(), 0, None, 4, 48, 128, st) == _lib.EINVAL
+    assert lib.exl3_amd_recon_mm(a.data_ptr(), a.data_ptr(), a.data_ptr(), 0, None, 4, 64, 100, st) == _lib.EINVAL
+    assert lib.exl3_amd_recon_mm(None, a.data_ptr(), a.data_ptr(), 0, None, 4, 64, 128, st) == _lib.EINVAL
+    assert lib.exl3_amd_recon_mm(None, None, None, 0, None, 0, 64, 128, st) == 0      # empty: nothing to do
+
+
+@pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2, 2), (2.5, 2), (8, 0)])
+def test_reconstruct_had_t_bit_exact(torch_cuda, orc, K, cb):
+    torch = torch_cuda
+    from ampstein_amd import ops
+    k, n = 256, 384
+    L = synth.layer(k, n, K, cb, seed=5100 + int(10 * K) + cb)
+    t, s, v = L.torch()
+    w = torch.empty((k, n), dtype=torch.half, device="cuda")
+    wt = torch.empty((n, k), dtype=torch.half, device="cuda")
+    ops.reconstruct_had_slice(w, t, s, v, K, cb == 1, cb == 2, 0)
+    ops.reconstruct_had_t(wt, t, s, v, K, cb == 1, cb == 2, 0)
+    W = w.cpu().numpy().view(np.uint16)
+    assert np.array_equal(wt.cpu().numpy().view(np.uint16), W.T)
+    ref = orc.reconstruct_had(L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
+    assert np.array_equal(W, ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("branch", ["rotated", "fused_w"])
+def test_recon_hip_matches_library(torch_cuda, orc, branch):
+    """exl3_gemm_recon on this build's GEMM and on the vendor library (the comparison path):
+    both within 2e-3 of the fp64 linear on the same reconstructed weights, 2048 rows."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    L = synth.layer(1024, 768, 4, 0, seed=5200)
+    x = synth.activations(2048, 1024, seed=5201)
+    t, s, v = L.torch()
+    xd = torch.from_numpy(x).cuda()
+    fr = 2048 if branch == "fused_w" else 1 << 30
+    yh = ops.exl3_gemm_recon(xd, t, s, v, 4.0, fused_rows=fr).float().cpu().numpy()
+    yl = ops.exl3_gemm_recon(xd, t, s, v, 4.0, fused_rows=fr, gemm="library").float().cpu().numpy()
+    if branch == "fused_w":
+        W = orc.reconstruct_had(L.trellis, L.suh, L.svh, 4).astype(np.float64)
+        ref = x.astype(np.float64) @ W
+    else:
+        ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4)
+    assert rel(yh, ref) < 2e-3
+    assert rel(yl, ref) < 2e-3
