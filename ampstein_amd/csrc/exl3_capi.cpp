@@ -376,6 +376,32 @@ Workspace ws_of(const DeviceState* d)
     return Workspace { d->partials, WS_PARTIAL_BYTES, d->counters, WS_COUNTERS, d->sink, d->num_cus, d->num_xcd };
 }
 
+// Balanced M = 1 stream (exl3_gemv.hip gemv1b_kernel): every wave streams the same R slices of
+// the residue-ordered pair list and every SIMD holds the same number of waves (4, else 3 or 2),
+// R >= 4 and 4 R <= k/16 (a workgroup's range meets two pairs at most).  Plain single-row
+// launches only (no routing weights, indices, per-matrix widths, fused input or norm), integer
+// 3INST / MCG, XCD hand-off on.
+void plan_balanced(GemvArgs& g, const Workspace& w, int bits)
+{
+    if (g.A_up || g.norm_h || g.weights || g.indices || g.size_n || g.had_src || g.c_list || g.row0 || bits > 8)
+        return;
+    const long KS = g.k / 16, P = (long) g.bszm * (g.n / 128);
+    if (P % g.xcd) return;
+    for (int wps = 4; wps >= 2; --wps)
+    {
+        const long waves = (long) wps * 4 * w.num_cus;
+        if ((P * KS) % waves) continue;
+        const long R = P * KS / waves;
+        if (R < 4 || 4 * R > KS || waves % (4L * g.xcd)) continue;
+        const long S = (KS + 4 * R - 1) / (4 * R) + 1;     // most workgroups one pair can meet
+        if ((size_t) P * S * 128 * 4 > w.partial_bytes) continue;
+        g.stream_m1 = 2;
+        g.slices_per_block = (int) R;
+        g.slots = (int) S;
+        return;
+    }
+}
+
 // Plan the work split, pick the XCD hand-off when the device and shape allow it, launch.
 int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s, const char* what)
 {
@@ -409,6 +435,8 @@ int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s
     g.xcd = 0;
     if (w.num_xcd > 0 && chunks % w.num_xcd == 0 && pairs * 32 <= w.counter_ints / 2)
         g.xcd = w.num_xcd;
+    if (g.xcd && g.m == 1 && g.stream_m1 == 1 && cb != 2 && policy(EXL3_AMD_POLICY_GEMV_SPLIT) == EXL3_AMD_GEMV_SPLIT_BALANCED)
+        plan_balanced(g, w, bits);
     int rc = dispatch_gemv(bits, cb, g, s);
     return rc ? hip_fail(rc, what) : 0;
 }

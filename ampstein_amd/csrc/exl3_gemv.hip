@@ -44,8 +44,11 @@
 #ifndef EXL3_GEMV_PRIO
 #define EXL3_GEMV_PRIO 3
 #endif
+// 2 slices: measured on MI355X against 4 (and 1, 8) over the 32-layer Llama-3-8B sweep in a graph,
+// interleaved runs: 2130-2205 GB/s against 2030-2070 (more loads in flight lengthened the stream
+// of every launch)
 #ifndef EXL3_GEMV_PF
-#define EXL3_GEMV_PF (EXL3_INST_K <= 4 ? 4 : 2)
+#define EXL3_GEMV_PF 2
 #endif
 
 using namespace exl3;
@@ -59,7 +62,7 @@ namespace {
     do {                                                                                        \
         uint64_t t_;                                                                            \
         asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_) : "s"(dep));        \
-        if ((threadIdx.x & 63) == 0)                                                            \
+        if ((g).trace && (threadIdx.x & 63) == 0)          /* no trace buffer set: no stamp */  \
             (g).trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + (slot_i)] = t_; \
     } while (0)
 #else
@@ -511,14 +514,15 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
     if (prev != splits - 1) return;
     if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // all slots' loads in flight together (16 per round: one L2 round trip for most shapes)
     float s0 = 0.0f, s1 = 0.0f;
-    for (int p0 = 0; p0 < splits; p0 += 8)
+    for (int p0 = 0; p0 < splits; p0 += 16)
     {
-        f32x2 vv[8];
+        f32x2 vv[16];
         #pragma unroll
-        for (int u = 0; u < 8; ++u) vv[u] = load_l2_f32x2(pbase + (size_t) min(p0 + u, splits - 1) * 128 + 2 * lane);
+        for (int u = 0; u < 16; ++u) vv[u] = load_l2_f32x2(pbase + (size_t) min(p0 + u, splits - 1) * 128 + 2 * lane);
         #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 16; ++u)
             if (p0 + u < splits) { s0 += vv[u].x; s1 += vv[u].y; }
     }
     store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
@@ -802,7 +806,7 @@ void gemv1_kernel(const GemvArgs g)
         uint32_t hw, xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n\ts_getreg_b32 %1, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(hw), "=s"(xcc));
         GEMV_STAMP(g, 0, hw);
-        if ((threadIdx.x & 63) == 0)
+        if (g.trace && (threadIdx.x & 63) == 0)
             g.trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + 5] = ((uint64_t) xcc << 32) | hw;
     }
 #endif
@@ -997,6 +1001,218 @@ void gemv1_kernel(const GemvArgs g)
 }
 
 // ---------------------------------------------------------------------------------------------
+// Balanced M = 1 stream (gemv1b_kernel).  gemv1_kernel gives every workgroup the same work, so a
+// launch whose workgroup count is not a multiple of the resident capacity (the stacked gate / up
+// bundle: 896 workgroups on 256 CUs, 3 or 4 waves per SIMD) leaves a quarter to a half of the
+// SIMDs idle for the last third of the launch (per-wave timestamps on MI355X: loop ends from 8
+// to 22 us).  Here every wave of the grid streams exactly R slices, and the grid is sized to put
+// the same number of waves on every SIMD.
+//
+// Work order.  Column chunks of all matrices form pairs p = j * chunks + chunk; the pairs of XCD
+// residue x (p % xcd == x) are concatenated, KS slices each.  Workgroup b (residue x = b % xcd,
+// local index lb = b / xcd) takes slices [4 R lb, 4 R lb + 4 R) of that list, wave w the R slices
+// from 4 R lb + w R.  4 R <= KS, so a workgroup's range covers the tail of one pair (A) and the
+// head of the next (B) at most.  The four waves' sums meet in LDS per pair; the workgroup stores
+// one partial of 128 fp32 per pair into slot lb - first(pair) and counts itself in the pair's
+// counter; the last arrival (same XCD: the hand-off of finish_m1_wave) sums the pair's slots in
+// slot order, rotates, scales by svh and stores.  Decode, prefetch ring and the 4x4x4
+// matrix-core dot are gemv1_kernel's.
+template <int K, int CB>
+__global__ __launch_bounds__(GEMV_THREADS)
+__attribute__((amdgpu_waves_per_eu(4, 4)))             // 4 waves per SIMD: at most 128 registers
+void gemv1b_kernel(const GemvArgs g)
+{
+    __shared__ __align__(16) uint32_t xdup[GEMV_WAVES][2][128];
+    __shared__ __align__(16) float red[2][GEMV_WAVES][128];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);
+    const int KS = g.k / 16, R = g.slices_per_block, chunks = g.n / 128;
+    const int X = g.xcd, xq = blockIdx.x % X, lb = blockIdx.x / X;
+    const int per_x = g.bszm * chunks / X;                // pairs of this residue
+    const int T0 = lb * GEMV_WAVES * R;                   // the workgroup's first slice
+    if (T0 >= per_x * KS) return;
+    const int qA = T0 / KS, Bd = (qA + 1) * KS;           // pair A and the first slice of pair B
+    const bool straddle = T0 + GEMV_WAVES * R > Bd;
+    const int t0 = T0 + wave * R;
+    const int n0 = min(max(Bd - t0, 0), R);               // this wave's slices in pair A
+    const int sA0 = t0 - qA * KS, sB0 = t0 - Bd;          // slice i: A at sA0 + i, B at sB0 + i
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
+#ifdef EXL3_GEMV_TRACE
+    {
+        uint32_t hw, xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n\ts_getreg_b32 %1, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(hw), "=s"(xcc));
+        GEMV_STAMP(g, 0, hw);
+        if (g.trace && (threadIdx.x & 63) == 0)
+            g.trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + 5] = ((uint64_t) xcc << 32) | hw;
+    }
+#endif
+
+    // the two pairs' matrices (every field selected by a uniform condition: indexed arrays of
+    // views would live in scratch)
+    MatView va, vb;
+    const int pa = xq + X * qA, pb = straddle ? pa + X : pa;
+    const int ja = pa / chunks, jb = pb / chunks;
+    const int cha = pa - ja * chunks, chb = pb - jb * chunks;
+    resolve(g, ja, va);
+    resolve(g, jb, vb);
+    const int tiles_n = va.stride / 16;
+    const size_t rstride = (size_t) tiles_n * tile_words(K);
+    const uint32_t lofs = lane_word_off<K>(lane);
+    const uint32_t* baseA = (const uint32_t*) va.trellis + (size_t) cha * 8 * tile_words(K);
+    const uint32_t* baseB = (const uint32_t*) vb.trellis + (size_t) chb * 8 * tile_words(K);
+    const int prev_off = (lane & 7) == 0 ? 8 * K - 1 : -1;
+    const bool has_suh = va.suh != nullptr;
+    auto addr = [&](int i) {
+        return (i < n0 ? baseA + (size_t) (sA0 + i) * rstride : baseB + (size_t) (sB0 + i) * rstride) + lofs;
+    };
+    // input pair of slice i's 128-row chunk (pair A or B's input and suh)
+    auto xload = [&](int i, uint32_t& xv, uint32_t& sv) {
+        const bool sb = i >= n0;
+        const int sl = sb ? sB0 + i : sA0 + i;
+        const uint16_t* A = sb ? vb.A : va.A;
+        const uint16_t* su = has_suh ? (sb ? vb.suh : va.suh) : A;
+        xv = *(to_global((const uint32_t*) A + lane) + (size_t) (sl >> 3) * 64);
+        sv = *(to_global((const uint32_t*) su + lane) + (size_t) (sl >> 3) * 64);
+    };
+    // first slice of the input chunk after slice i's (a pair change starts a new chunk)
+    auto next_group = [&](int i) {
+        const int sl = i < n0 ? sA0 + i : sB0 + i;
+        const int e = i + 8 - (sl & 7);
+        return i < n0 ? min(e, n0) : e;
+    };
+
+    uint32_t xv, sv, xvn = 0u, svn = 0u;
+    xload(0, xv, sv);
+    int gnext = next_group(0);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int KB = kbits(K);
+    constexpr int PF = EXL3_GEMV_PF;
+    uint32_t ring[PF][KB + 1];
+    #pragma unroll
+    for (int d = 0; d < PF; ++d) load_slot_k<K>(addr(min(d, R - 1)), prev_off, lane, ring[d]);
+    if (gnext < R) xload(gnext, xvn, svn);
+
+    f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
+    int xb = 0;
+    const int c0 = (lane >> 3) * 16 + (lane & 7);          // this lane's columns c0, c0 + 8
+    // this wave's sums of one pair into red[sg][wave] (columns), or zeros
+    auto deposit = [&](int sg, bool zero) {
+        const int e = lane & 3;
+        auto pick = [&](const f32x4& a) { return e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w; };
+        red[sg][wave][c0] = zero ? 0.0f : pick(accv[0]) + pick(accv[1]);
+        red[sg][wave][c0 + 8] = zero ? 0.0f : pick(accv[2]) + pick(accv[3]);
+    };
+
+    for (int i0 = 0; i0 < R; i0 += PF)
+    {
+        #pragma unroll
+        for (int d = 0; d < PF; ++d)
+        {
+            const int i = i0 + d;
+            if (i >= R) break;
+            if (i == n0 && n0 > 0)                        // pair A done: its sums to LDS, restart
+            {
+                deposit(0, false);
+                #pragma unroll
+                for (int a = 0; a < 4; ++a) accv[a] = (f32x4) { 0, 0, 0, 0 };
+            }
+            if (i == 0 || i == gnext)
+            {
+                if (i != 0) { xv = xvn; sv = svn; gnext = next_group(i); if (gnext < R) xload(gnext, xvn, svn); }
+                const uint32_t xr = rotate_pair(xv, sv, has_suh, lane);
+                if (i == 0) GEMV_STAMP(g, 1, __builtin_amdgcn_readfirstlane(xr));
+                if (i == 0) __builtin_amdgcn_s_setprio(0);
+                xb ^= 1;
+                const f16x2 pq = as_h2(xr);
+                const f16x2 d0 = { pq.x, pq.x }, d1 = { pq.y, pq.y };
+                *(u32x2*) (&xdup[wave][xb][2 * lane]) = (u32x2) { as_u32(d0), as_u32(d1) };
+                __builtin_amdgcn_wave_barrier();
+            }
+            const int xrow = ((i < n0 ? sA0 + i : sB0 + i) & 7) * 16;
+            uint32_t wv[KB + 1];
+            #pragma unroll
+            for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
+            // past the last slice: the last slice again (just read, an L2 hit), so that the load
+            // is unconditional and the wait counts stay static
+            load_slot_k<K>(addr(min(i + PF, R - 1)), prev_off, lane, ring[d]);
+            const uint32_t* xs = &xdup[wave][xb][xrow];
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            #pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+            {
+                uint32_t raw[32];
+                if (gq == 0) raw8<K, CB, 0>(wv, raw, a3, b3);
+                else if (gq == 1) raw8<K, CB, 8>(wv, raw, a3, b3);
+                else if (gq == 2) raw8<K, CB, 16>(wv, raw, a3, b3);
+                else raw8<K, CB, 24>(wv, raw, a3, b3);
+                #pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    const u32x2 xbv = *(const u32x2*) (xs + 2 * gq + 8 * h);
+                    const h4 bx = __builtin_bit_cast(h4, xbv);
+                    const int w = 8 * gq + 2 * h;
+                    const h4 wa = __builtin_bit_cast(h4, (u32x2) { raw[w], raw[w + 1] });
+                    const h4 wb = __builtin_bit_cast(h4, (u32x2) { raw[w + 4], raw[w + 5] });
+                    accv[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wa, bx, accv[h], 0, 0, 0);
+                    accv[2 + h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wb, bx, accv[2 + h], 0, 0, 0);
+                }
+            }
+        }
+    }
+    GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(accv[0].x)));
+    __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
+    if (n0 == R) deposit(0, false);                       // all in pair A
+    else deposit(1, false);                               // the rest is in pair B
+    if (n0 == 0) deposit(0, true);                        // no slices of pair A
+    if (straddle && n0 == R) deposit(1, true);            // no slices of pair B
+    __syncthreads();
+
+    // wave 0 finishes pair A, wave 1 pair B (when the workgroup straddles); the others end
+    const bool sg = wave == 1;
+    if (wave > 1 || (sg && !straddle)) return;
+    const float v0 = red[sg][0][2 * lane] + red[sg][1][2 * lane] + red[sg][2][2 * lane] + red[sg][3][2 * lane];
+    const float v1 = red[sg][0][2 * lane + 1] + red[sg][1][2 * lane + 1] + red[sg][2][2 * lane + 1] + red[sg][3][2 * lane + 1];
+    const int q = qA + (sg ? 1 : 0);
+    const int WR = GEMV_WAVES * R;
+    const int first = (q * KS) / WR, n = ((q + 1) * KS - 1) / WR - first + 1;
+    void* Cp = sg ? vb.C : va.C;
+    const uint16_t* svh = sg ? vb.svh : va.svh;
+    const float scale = sg ? vb.scale : va.scale;
+    const int pp = sg ? pb : pa;
+    const int col = (sg ? chb : cha) * 128 + 2 * lane;
+    const uint32_t svp = svh ? *to_global((const uint32_t*) (svh + col)) : 0u;
+    if (n == 1)
+    {
+        store_output(v0, v1, Cp, g.c_fp32, svh != nullptr, svp, (size_t) col, lane, scale);
+        return;
+    }
+    float* pbase = g.partials + (size_t) pp * g.slots * 128;
+    *to_global_w((f32x2*) (pbase + (size_t) (lb - first) * 128 + 2 * lane)) = (f32x2) { v0, v1 };
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    int* ctr = g.counters + (size_t) pp * 32;
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != n - 1) return;
+    if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int p0 = 0; p0 < n; p0 += 16)
+    {
+        f32x2 pv[16];
+        #pragma unroll
+        for (int u = 0; u < 16; ++u) pv[u] = load_l2_f32x2(pbase + (size_t) min(p0 + u, n - 1) * 128 + 2 * lane);
+        #pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (p0 + u < n) { a0 += pv[u].x; a1 += pv[u].y; }
+    }
+    store_output(a0, a1, Cp, g.c_fp32, svh != nullptr, svp, (size_t) col, lane, scale);
+    GEMV_STAMP(g, 3, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Row-batched GEMV on the matrix cores (m = 1..16 rows per launch; the decode path uses it for
 // m >= 2).  v_mfma_f32_16x16x32_f16 with
 //   A (16 x 32): 16 output columns x 16 k-rows of the weight, each weight as its two fp16
@@ -1053,7 +1269,7 @@ void gemvm_kernel(const GemvArgs g)
         uint32_t hw, xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n\ts_getreg_b32 %1, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(hw), "=s"(xcc));
         GEMV_STAMP(g, 0, hw);
-        if ((threadIdx.x & 63) == 0)
+        if (g.trace && (threadIdx.x & 63) == 0)
             g.trace[(((size_t) blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8 + 5] = ((uint64_t) xcc << 32) | hw;
     }
 #endif
@@ -1259,6 +1475,16 @@ int launch_gemvm_t(const GemvArgs& g, hipStream_t s)
 template <int K, int CB>
 int launch_gemv_m(const GemvArgs& g, hipStream_t s)
 {
+    if (g.m == 1 && g.stream_m1 == 2)
+    {
+        if constexpr (CB == 2) return -1;                // (the planner never picks it for MUL1)
+        else
+        {
+            const int waves = g.bszm * (g.n / 128) * (g.k / 16) / g.slices_per_block;
+            hipLaunchKernelGGL((gemv1b_kernel<K, CB>), dim3(waves / GEMV_WAVES), dim3(GEMV_THREADS), 0, s, g);
+            return (int) hipGetLastError();
+        }
+    }
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
     if (g.A_up) return -1;             // the fused SwiGLU input exists in the M = 1 stream kernel only
     if (g.mfma_rows)

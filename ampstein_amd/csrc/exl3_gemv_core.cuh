@@ -7,6 +7,9 @@
 
 namespace exl3 {
 
+// Weight-stream loads: nontemporal (the packed weights are read once per launch)
+#define EXL3_WLOAD(ptr) __builtin_nontemporal_load(ptr)
+
 // Load this lane's K words of a slice into w[1..K] and the word before them (the last word of
 // the previous lane of the same tile, cyclically: the window start of the lane's first
 // position) into w[0], all from global memory: no cross-lane traffic in the loop.
@@ -21,7 +24,7 @@ __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint3
         #pragma unroll
         for (int i = 0; i < K / 4; ++i)
         {
-            u32x4 v = __builtin_nontemporal_load(to_global((const u32x4*) p) + i);
+            u32x4 v = EXL3_WLOAD(to_global((const u32x4*) p) + i);
             w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
         }
     }
@@ -30,14 +33,14 @@ __device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint3
         #pragma unroll
         for (int i = 0; i < K / 2; ++i)
         {
-            u32x2 v = __builtin_nontemporal_load(to_global((const u32x2*) p) + i);
+            u32x2 v = EXL3_WLOAD(to_global((const u32x2*) p) + i);
             w[2 * i] = v.x; w[2 * i + 1] = v.y;
         }
     }
     else
     {
         #pragma unroll
-        for (int i = 0; i < K; ++i) w[i] = __builtin_nontemporal_load(to_global(p) + i);
+        for (int i = 0; i < K; ++i) w[i] = EXL3_WLOAD(to_global(p) + i);
     }
 }
 
@@ -45,7 +48,7 @@ template <int K>
 __device__ __forceinline__ void load_slot(const uint32_t* __restrict__ p, int prev_off, uint32_t* w)
 {
     load_words<K>(p, w + 1);
-    w[0] = __builtin_nontemporal_load(to_global(p) + prev_off);
+    w[0] = EXL3_WLOAD(to_global(p) + prev_off);
 }
 
 // Slot load for any rate code.  Integer K: load_slot, p = the lane's first word (chunk base +

@@ -61,7 +61,9 @@ int exl3_amd_version(void);
 #define EXL3_AMD_MOE_OUTPUT_ATOMIC      1   /*   per-row atomics instead of the per-token lists         */
 #define EXL3_AMD_POLICY_RECON_MM        5   /* kernel of exl3_amd_recon_mm                             */
 #define EXL3_AMD_RECON_MM_8WAVES        1   /*   8 waves of 128 x 64 instead of 4 waves of 128 x 128    */
-#define EXL3_AMD_POLICY_COUNT           6
+#define EXL3_AMD_POLICY_GEMV_SPLIT      6   /* work split of the single-row GEMV                       */
+#define EXL3_AMD_GEMV_SPLIT_BALANCED    1   /*   equal work per wave and waves per SIMD (gemv1b_kernel)  */
+#define EXL3_AMD_POLICY_COUNT           7
 int exl3_amd_set_policy(int key, int value);
 int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */
 
