@@ -124,6 +124,7 @@ POLICY_MOE_TILE_ROWS = 3
 POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1
 POLICY_RECON_MM, RECON_MM_8WAVES = 5, 1
 POLICY_GEMV_SPLIT, GEMV_SPLIT_BALANCED = 6, 1
+POLICY_GEMV_SLICES = 7
 
 
 class policy:

@@ -326,11 +326,16 @@ int gemv_plan(int m, int k, int n, int bszm, int num_cus, GemvArgs& g, size_t pa
     if (stream)
     {
         int pref = k >= 8192 ? 64 : 16;
-        // more workgroups than one round of 4 per CU (stacked gate/up: 1792): double the split
-        // while the count exceeds that round (measured: gate/up 26.7 -> 25.8 us at 896)
-        while (ok_sb(2 * pref) && (long) bszm * chunks * (KS / pref) > 4L * num_cus) pref *= 2;
+        // more than 8 workgroups per CU: double the split while the count exceeds that (measured
+        // with the 2-slice prefetch ring, 32-layer graph sweep, us per launch at 16 / 32 / 64 / 128
+        // slices per workgroup: stacked gate / up 23.3 / 21.6 / 22.3 / 23.4 -> 32, 1792 workgroups)
+        while (ok_sb(2 * pref) && (long) bszm * chunks * (KS / pref) > 8L * num_cus) pref *= 2;
         for (int d = pref; d >= 4; d /= 2)
             if (ok_sb(d) && ((size_t) (KS / d) * bszm * m * n * 4 <= partial_bytes || KS / d == 1)) { best = d; break; }
+        // policy EXL3_AMD_POLICY_GEMV_SLICES: a forced split (k-slices per workgroup) when valid
+        const int forced = policy(EXL3_AMD_POLICY_GEMV_SLICES);
+        if (forced > 0 && ok_sb(forced) && ((size_t) (KS / forced) * bszm * m * n * 4 <= partial_bytes || KS / forced == 1))
+            best = forced;
     }
     if (best < 0) return -1;
     if ((size_t) (KS / best) * bszm * m * n * 4 > partial_bytes && KS / best > 1) return -1;

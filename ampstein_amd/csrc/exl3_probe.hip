@@ -110,6 +110,41 @@ __global__ __launch_bounds__(1024) void lds_gather_probe(uint32_t* out, int iter
     if ((threadIdx.x & 63) == 0) out[blockIdx.x * 16 + (threadIdx.x >> 6)] = acc;
 }
 
+// Read-only streaming probe: `bytes` (a multiple of 1 KiB * wgs * 4) read with 16-byte loads,
+// 4 waves per workgroup, one 1 KiB block per wave per step, 2 blocks in flight per wave (the
+// GEMV's ring depth); one lane per wave stores an xor checksum.
+//   pattern 0: the blocks of a wave are contiguous (wave w reads bytes [w B, (w + 1) B));
+//   pattern 1: the GEMV's order: the matrix is `rows` rows of `row_bytes`, wave w reads the 1 KiB
+//              column block w % (row_bytes / 1 KiB) of rows (w / cols) * R .. + R (stride row_bytes).
+typedef uint32_t pu32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void stream_probe(const pu32x4* __restrict__ buf, size_t blocks_per_wave, int pattern,
+                                                    size_t row_blocks, uint32_t* out)
+{
+    const int lane = threadIdx.x & 63;
+    const size_t w = (size_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    size_t b0, stride;
+    if (pattern == 0) { b0 = w * blocks_per_wave; stride = 1; }
+    else
+    {
+        const size_t col = w % row_blocks, grp = w / row_blocks;
+        b0 = grp * blocks_per_wave * row_blocks + col;
+        stride = row_blocks;
+    }
+    pu32x4 acc = { 0u, 0u, 0u, 0u };
+    pu32x4 r0 = __builtin_nontemporal_load(buf + b0 * 64 + lane);
+    pu32x4 r1 = __builtin_nontemporal_load(buf + (b0 + (blocks_per_wave > 1 ? stride : 0)) * 64 + lane);
+    for (size_t i = 2; i < blocks_per_wave + 2; i += 2)
+    {
+        const size_t i0 = i < blocks_per_wave ? i : blocks_per_wave - 1, i1 = i + 1 < blocks_per_wave ? i + 1 : blocks_per_wave - 1;
+        acc.x ^= r0.x; acc.y ^= r0.y; acc.z ^= r0.z; acc.w ^= r0.w;
+        r0 = __builtin_nontemporal_load(buf + (b0 + i0 * stride) * 64 + lane);
+        acc.x ^= r1.x; acc.y ^= r1.y; acc.z ^= r1.z; acc.w ^= r1.w;
+        r1 = __builtin_nontemporal_load(buf + (b0 + i1 * stride) * 64 + lane);
+    }
+    const uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (lane == 0) out[w] = v;
+}
+
 template <int OP>
 hipError_t launch_valu(uint32_t* out, int blocks, int iters, hipStream_t s)
 {
@@ -170,6 +205,25 @@ float exl3_probe_lds_gather(uint32_t* out, int blocks, int iters, int mode)
     (void) hipEventDestroy(e0);
     (void) hipEventDestroy(e1);
     return rc == hipSuccess ? ms : -1.0f;
+}
+
+// One streaming launch on `stream` (no timing: the caller times a sequence, e.g. in a graph).
+// bytes must be a multiple of 1 KiB * 4 * wgs; pattern 1 also needs row_bytes % 1 KiB == 0 and
+// (bytes / row_bytes) % (waves / (row_bytes / 1 KiB)) == 0.  Returns 0 or a HIP error.
+int exl3_probe_stream(const void* buf, size_t bytes, int wgs, int pattern, size_t row_bytes, uint32_t* out, void* stream)
+{
+    const size_t waves = (size_t) wgs * 4, blocks = bytes / 1024;
+    if (!buf || !out || wgs <= 0 || blocks % waves) return (int) hipErrorInvalidValue;
+    size_t row_blocks = 1;
+    if (pattern == 1)
+    {
+        row_blocks = row_bytes / 1024;
+        const size_t rows = bytes / row_bytes;
+        if (row_bytes % 1024 || bytes % row_bytes || waves % row_blocks || rows % (waves / row_blocks)) return (int) hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(stream_probe, dim3(wgs), dim3(256), 0, (hipStream_t) stream, (const pu32x4*) buf, blocks / waves,
+                       pattern, row_blocks, out);
+    return (int) hipGetLastError();
 }
 
 }  // extern "C"

@@ -799,6 +799,43 @@ def rates():
                      "weights_per_s": round(gathers * 64 / (best * 1e-3) / 1e12, 3)}
     lds["note"] = "weights_per_s in T/s: 64 lanes x wave gathers; one 16-bit table entry per weight"
     res["lds_gather_128k"] = lds
+    # read-only streaming at the decode GEMV's launch sizes, 24 launches over distinct buffers in
+    # one graph (HIP events around the replays): contiguous per wave vs the GEMV's column order
+    L.exl3_probe_stream.restype = ctypes.c_int
+    L.exl3_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    streams = {}
+    for name, nbytes, row_bytes, wgs in (("q_4096x4096", 8 << 20, 32 << 10, 512),
+                                         ("down_14336x4096", 28 << 20, 32 << 10, 448),
+                                         ("gate_up_2x4096x14336", 56 << 20, 112 << 10, 896)):
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i) for i in range(24)]
+        sink = torch.zeros(wgs * 4, dtype=torch.int32, device="cuda")
+        row = {}
+        for pattern in (0, 1):
+            st = torch.cuda.Stream()
+            def seq():
+                for b in bufs:
+                    rc = L.exl3_probe_stream(b.data_ptr(), nbytes, wgs, pattern, row_bytes, sink.data_ptr(), st.cuda_stream)
+                    assert rc == 0, rc
+            with torch.cuda.stream(st):
+                seq()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=st):
+                seq()
+            gr.replay(); torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                gr.replay()
+            e1.record(); torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (5 * len(bufs))
+            row["contiguous" if pattern == 0 else "gemv_order"] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+        row["workgroups"] = wgs
+        streams[name] = row
+        del bufs
+        torch.cuda.empty_cache()
+    res["stream_read"] = streams
     print(json.dumps(res))
     return 0
 

@@ -63,7 +63,10 @@ int exl3_amd_version(void);
 #define EXL3_AMD_RECON_MM_8WAVES        1   /*   8 waves of 128 x 64 instead of 4 waves of 128 x 128    */
 #define EXL3_AMD_POLICY_GEMV_SPLIT      6   /* work split of the single-row GEMV                       */
 #define EXL3_AMD_GEMV_SPLIT_BALANCED    1   /*   equal work per wave and waves per SIMD (gemv1b_kernel)  */
-#define EXL3_AMD_POLICY_COUNT           7
+#define EXL3_AMD_POLICY_GEMV_SLICES     7   /* single-row stream GEMV: k-slices per workgroup (0 = by the
+                                             * planner; a valid forced value: 4, 8, 16 or a multiple of 32
+                                             * dividing k / 16)                                        */
+#define EXL3_AMD_POLICY_COUNT           8
 int exl3_amd_set_policy(int key, int value);
 int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */
 
@@ -144,8 +147,8 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
  * that GPU's array: calls that overlap on one GPU (concurrent streams) race.  Call
  * exl3_amd_init(device) first to take the XCD-local hand-off; without it the partials are
  * summed by a second kernel.
- * No counterpart in the reference (the reference's exl3_gemm takes its lock buffer from a
- * per-device context that allocates on first use, quant/exl3_devctx.cu:81-93). */
+ * No counterpart in the reference: an entry point of this build for the callers that cannot
+ * allocate. */
 int exl3_amd_gemm_noalloc(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp32,
                           const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
                           int m, int k, int n, float K, int mcg, int mul1, int force_shape_idx,
