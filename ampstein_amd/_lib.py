@@ -27,6 +27,9 @@ SIGNATURES = {
     "exl3_amd_debug_read_workspace": (_i32, [_i32, ctypes.c_int64, ctypes.c_int64, _vp]),
     "exl3_amd_debug_fill_workspace": (_i32, [_i32, _i32]),
     "exl3_amd_device_info": (_i32, [_i32, _vp, _vp]),
+    "exl3_amd_xcd_status": (_i32, [_i32, _vp, _vp, _vp]),
+    "exl3_amd_xcd_rearm": (_i32, [_i32]),
+    "exl3_amd_debug_handoff_map": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_t": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_reconstruct_t_had": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
@@ -125,6 +128,7 @@ POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1
 POLICY_RECON_MM, RECON_MM_8WAVES = 5, 1
 POLICY_GEMV_SPLIT, GEMV_SPLIT_BALANCED = 6, 1
 POLICY_GEMV_SLICES = 7
+POLICY_XCD_FAKE = 8
 
 
 class policy:
@@ -148,3 +152,18 @@ def check(rc: int) -> int:
     if rc < 0:
         raise Exl3Error(rc, lib().exl3_amd_last_error().decode())
     return rc
+
+
+def xcd_status(device: int = 0):
+    """(XCD count the init probe verified, count in use, alarms serviced) of the per-launch XCD
+    hand-off check; synchronises the device."""
+    vals = [ctypes.c_int(0) for _ in range(3)]
+    check(lib().exl3_amd_xcd_status(device, *[ctypes.byref(v) for v in vals]))
+    return tuple(v.value for v in vals)
+
+
+def handoff_map(kind: int, xcd: int, p0: int, p1: int, p2: int, b: int):
+    """The kernels' workgroup -> hand-off coordinates, computed on the host (exl3_amd_debug_handoff_map)."""
+    out = (ctypes.c_int * 4)()
+    check(lib().exl3_amd_debug_handoff_map(kind, xcd, p0, p1, p2, b, out))
+    return tuple(out)

@@ -71,6 +71,10 @@ struct DeviceState
     bool ready = false;
     int num_cus = 0;
     int num_xcd = 0;            // > 0 when workgroup b is verified to run on XCD b % num_xcd
+    int probe_xcd = 0;          // the init probe's verdict (num_xcd until the hand-off check trips)
+    int xcd_alarms = 0;         // alarms serviced (the hand-off check saw one counter on two XCDs)
+    uint32_t* alarm_host = nullptr;     // pinned, device-mapped alarm word (host view)
+    uint32_t* alarm_dev = nullptr;      // the same word's device address
     float* partials = nullptr;
     int* counters = nullptr;
     uint32_t* sink = nullptr;           // 8 KiB, zeroed, never written after init
@@ -168,6 +172,17 @@ int init_device(int device, DeviceState** out)
             if (hipMemset(sk, 0, 8192) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
                 return fail(EXL3_AMD_EHIP, "sink initialisation failed");
             d.sink = (uint32_t*) sk;
+            // hand-off check: the alarm word (pinned host memory that kernels store to with system
+            // scope, read by the host at every call)
+            void* al = nullptr;
+            void* al_dev = nullptr;
+            if (hipHostMalloc(&al, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+                return fail(EXL3_AMD_ENOMEM, "alarm-word allocation failed");
+            memset(al, 0, 64);
+            if (hipHostGetDevicePointer(&al_dev, al, 0) != hipSuccess || !al_dev)
+                return fail(EXL3_AMD_EHIP, "alarm-word device address failed");
+            d.alarm_host = (uint32_t*) al;
+            d.alarm_dev = (uint32_t*) al_dev;
             d.filt_idx = (int64_t*) f;
             d.filt_w = (uint16_t*) (d.filt_idx + MGEMM_MAX_FILTER);
             // workgroup -> XCD dispatch order (round-robin on MI355X), verified on this device
@@ -202,8 +217,9 @@ int init_device(int device, DeviceState** out)
                                 host[7], host[8]);
                     free(host);
                 }
-                d.num_xcd = ok && nx >= 1 ? nx : 0;
+                d.num_xcd = ok && nx >= 1 && nx <= 31 ? nx : 0;
                 if (const char* e = getenv("EXL3_AMD_XCD")) if (atoi(e) == 0) d.num_xcd = 0;
+                d.probe_xcd = d.num_xcd;
             }
             d.num_cus = cus;
             d.partials = (float*) p;
@@ -222,6 +238,40 @@ int init_device(int device, DeviceState** out)
 // The first call on a device allocates and clears the workspace, which a stream capture cannot
 // record: such a call is refused (no allocation, no synchronisation) and the capture stays
 // intact.  exl3_amd_init(device) before the capture avoids it.
+// The XCD hand-off check's alarm (set by a kernel that saw one counter's arrivals come from two
+// XCDs): turn the hand-off off for the device and zero every counter on `s`, so
+// that no later call reads what the mixed launch left.  Called by every entry point that launches
+// work; a plain host read of pinned memory when nothing happened.
+void xcd_service(int device, hipStream_t s)
+{
+    DeviceState& d = g_dev[device];
+    if (!d.ready || !d.alarm_host || d.num_xcd == 0) return;
+    if (__atomic_load_n(d.alarm_host, __ATOMIC_ACQUIRE) == 0) return;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (d.num_xcd == 0) return;
+    d.num_xcd = 0;
+    ++d.xcd_alarms;
+    fprintf(stderr, "exl3_amd: device %d: workgroups of one split-k hand-off counter ran on different XCDs; the "
+            "XCD-local hand-off is now off for this device (outputs of the launch that raised this are not reliable)\n",
+            device);
+    (void) exl3k_fill_u32((uint32_t*) d.counters, 0u, WS_COUNTER_INTS, s);
+    const NoAllocState& st = g_noalloc[device];
+    if (st.ready)
+    {
+        (void) exl3k_fill_u32((uint32_t*) (st.ptr + NOALLOC_PARTIAL_BYTES), 0u, NOALLOC_COUNTER_INTS, s);
+    }
+}
+
+// The guard the kernels of one launch carry.
+XcdGuard xcd_guard(uint32_t* alarm)
+{
+    const int fake = policy(EXL3_AMD_POLICY_XCD_FAKE);
+    return XcdGuard { alarm, fake > 0 ? fake - 1 : -1 };
+}
+
+// Most arrivals one 64-bit hand-off counter records (16-bit count and id-sum fields).
+constexpr int XCD_MAX_ARRIVALS = 3000;
+
 int current_device(DeviceState** out, void* stream)
 {
     (void) hipGetLastError();
@@ -237,7 +287,9 @@ int current_device(DeviceState** out, void* stream)
                         "on first use; call exl3_amd_init(%d) before capturing", dev, dev);
         }
     }
-    return init_device(dev, out);
+    if (int rc = init_device(dev, out)) return rc;
+    xcd_service(dev, (hipStream_t) stream);
+    return 0;
 }
 
 // Row-batched matrix-core GEMV (exl3_gemv.hip gemvm_kernel) for 2..16 rows (policy
@@ -374,11 +426,13 @@ struct Workspace
     const uint32_t* sink;
     int num_cus;
     int num_xcd;
+    uint32_t* alarm;            // device address of the alarm word
 };
 
 Workspace ws_of(const DeviceState* d)
 {
-    return Workspace { d->partials, WS_PARTIAL_BYTES, d->counters, WS_COUNTERS, d->sink, d->num_cus, d->num_xcd };
+    return Workspace { d->partials, WS_PARTIAL_BYTES, d->counters, WS_COUNTERS, d->sink, d->num_cus, d->num_xcd,
+                       d->alarm_dev };
 }
 
 // Balanced M = 1 stream (exl3_gemv.hip gemv1b_kernel): every wave streams the same R slices of
@@ -438,8 +492,10 @@ int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s
 #endif
     const size_t pairs = (size_t) g.bszm * chunks;
     g.xcd = 0;
-    if (w.num_xcd > 0 && chunks % w.num_xcd == 0 && pairs * 32 <= w.counter_ints / 2)
+    if (w.num_xcd > 0 && w.alarm && chunks % w.num_xcd == 0 && pairs * 32 <= w.counter_ints / 2 &&
+        g.slots <= XCD_MAX_ARRIVALS && g.bszm <= XCD_MAX_ARRIVALS)
         g.xcd = w.num_xcd;
+    g.xg = xcd_guard(w.alarm);
     if (g.xcd && g.m == 1 && g.stream_m1 == 1 && cb != 2 && policy(EXL3_AMD_POLICY_GEMV_SPLIT) == EXL3_AMD_GEMV_SPLIT_BALANCED)
         plan_balanced(g, w, bits);
     int rc = dispatch_gemv(bits, cb, g, s);
@@ -494,7 +550,7 @@ void exl3_amd_debug_set_trace(void* p) { g_trace = (uint64_t*) p; }
 
 const char* exl3_amd_last_error(void) { return g_last_error.c_str(); }
 
-int exl3_amd_version(void) { return 10100; }
+int exl3_amd_version(void) { return 10200; }
 
 int exl3_amd_set_policy(int key, int value)
 {
@@ -553,6 +609,71 @@ int exl3_amd_device_info(int device, int* num_cus, int* num_xcd)
     if (num_cus) *num_cus = d->num_cus;
     if (num_xcd) *num_xcd = d->num_xcd;
     return 0;
+}
+
+int exl3_amd_xcd_status(int device, int* probe_xcd, int* active_xcd, int* alarms)
+{
+    g_last_error.clear();
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    if (hipDeviceSynchronize() != hipSuccess) return fail(EXL3_AMD_EHIP, "xcd_status: device synchronisation failed");
+    xcd_service(device, nullptr);
+    if (hipDeviceSynchronize() != hipSuccess) return fail(EXL3_AMD_EHIP, "xcd_status: device synchronisation failed");
+    if (probe_xcd) *probe_xcd = d->probe_xcd;
+    if (active_xcd) *active_xcd = d->num_xcd;
+    if (alarms) *alarms = d->xcd_alarms;
+    return 0;
+}
+
+int exl3_amd_xcd_rearm(int device)
+{
+    g_last_error.clear();
+    DeviceState* d;
+    if (int rc = init_device(device, &d)) return rc;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemset(d->counters, 0, WS_COUNTER_INTS * sizeof(int)) != hipSuccess)
+        return fail(EXL3_AMD_EHIP, "xcd_rearm: reset failed");
+    const NoAllocState& st = g_noalloc[device];
+    if (st.ready && hipMemset(st.ptr + NOALLOC_PARTIAL_BYTES, 0, NOALLOC_COUNTER_INTS * sizeof(int)) != hipSuccess)
+        return fail(EXL3_AMD_EHIP, "xcd_rearm: reset failed");
+    if (hipDeviceSynchronize() != hipSuccess) return fail(EXL3_AMD_EHIP, "xcd_rearm: reset failed");
+    __atomic_store_n(d->alarm_host, 0u, __ATOMIC_RELEASE);
+    d->num_xcd = d->probe_xcd;
+    return 0;
+}
+
+int exl3_amd_debug_handoff_map(int kind, int xcd, int p0, int p1, int p2, int b, int* out)
+{
+    g_last_error.clear();
+    if (!out || b < 0) return fail(EXL3_AMD_EINVAL, "debug_handoff_map: bad argument");
+    switch (kind)
+    {
+    case 0:
+        if (p0 < 1) return fail(EXL3_AMD_EINVAL, "debug_handoff_map: splits must be positive");
+        gemv_block_coords(xcd, p0, b, out[0], out[1]);
+        return 0;
+    case 1:
+        if (p0 < 1 || (xcd > 0 && p0 % xcd)) return fail(EXL3_AMD_EINVAL, "debug_handoff_map: bad chunk count");
+        moe_chunk_coords(xcd, p0, b, out[0], out[1]);
+        return 0;
+    case 2:
+    {
+        // plan_balanced's invariants: whole workgroups of 4 R slices per residue list, 4 R <= k / 16
+        if (xcd < 1 || p0 < 1 || p0 % xcd || p1 < 1 || p2 < 1 || 4 * p2 > p1 || ((long) p0 / xcd * p1) % (4L * p2))
+            return fail(EXL3_AMD_EINVAL, "debug_handoff_map: bad balanced plan");
+        Gemv1bBlock o { 0, 0, 0, false };
+        const bool v = gemv1b_block(xcd, p0, p1, p2, b, o);
+        out[0] = v; out[1] = o.pa; out[2] = o.pb; out[3] = o.straddle;
+        return 0;
+    }
+    case 3:
+        if (p1 < 1 || p2 < 1) return fail(EXL3_AMD_EINVAL, "debug_handoff_map: bad balanced plan");
+        gemv1b_pair_span(p1, p2, b, out[0], out[1]);
+        return 0;
+    default:
+        return fail(EXL3_AMD_EINVAL, "debug_handoff_map: unknown kind %d", kind);
+    }
 }
 
 int exl3_amd_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n_packed, int n,
@@ -798,7 +919,9 @@ int exl3_amd_gemm_noalloc(const uint16_t* A, const uint16_t* trellis, void* C, i
     w.num_cus = st.num_cus;
     // the XCD-local hand-off only where exl3_amd_init (or an earlier call of another entry point)
     // has already verified the dispatch order; otherwise the finish kernel sums the partials
-    w.num_xcd = (dev < MAX_DEVICES && g_dev[dev].ready) ? g_dev[dev].num_xcd : 0;
+    xcd_service(dev, (hipStream_t) stream);
+    w.num_xcd = g_dev[dev].ready ? g_dev[dev].num_xcd : 0;
+    w.alarm = g_dev[dev].ready ? g_dev[dev].alarm_dev : nullptr;
     return gemm_impl(&w, A, trellis, C, c_fp32, suh, A_had, svh, m, k, n, K, mcg, mul1, force_shape_idx, stream,
                      "exl3_gemm_noalloc");
 }
@@ -1008,7 +1131,9 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     if (ca + cb_ > WS_COUNTERS) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_moe_coop: batch exceeds the counter workspace");
     a.ctr_a = d->counters;
     a.ctr_b = d->counters + ca;
-    a.xcd = (d->num_xcd > 0 && (I / 128) % d->num_xcd == 0 && (Ho / 128) % d->num_xcd == 0) ? d->num_xcd : 0;
+    a.xcd = (d->num_xcd > 0 && (I / 128) % d->num_xcd == 0 && (Ho / 128) % d->num_xcd == 0 &&
+             (long) nproj * a.splits_a <= XCD_MAX_ARRIVALS && (long) topk * a.splits_b <= XCD_MAX_ARRIVALS) ? d->num_xcd : 0;
+    a.xg = xcd_guard(d->alarm_dev);
 
     const int cb = mcg ? 1 : (mul1 ? 2 : 0);
     hipStream_t s = (hipStream_t) stream;

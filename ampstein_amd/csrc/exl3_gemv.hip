@@ -32,6 +32,7 @@
 #include "exl3_common.cuh"
 #include "exl3_gemv_core.cuh"
 #include "exl3_kernels.h"
+#include "exl3_xcd.cuh"
 
 #ifndef EXL3_INST_K
 #define EXL3_INST_K 4
@@ -259,7 +260,7 @@ __device__ __forceinline__ uint32_t load_l2_u32(const void* p)
 // partials are summed by the separate gemv_finish kernel.  Agent-scope atomics would not need
 // the assumption but write back through the whole-device coherence point: 2.5-11 us per
 // launch measured on MI355X.
-__device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag)
+__device__ __forceinline__ bool arrive_last(const XcdGuard& q, int* ctr, int total, int* flag)
 {
     // the workgroup-scope release waits for LDS only: wait for this thread's global stores to be
     // acknowledged by the L2 before the counter can move
@@ -268,10 +269,7 @@ __device__ __forceinline__ bool arrive_last(int* ctr, int total, int* flag)
     __syncthreads();
     if (threadIdx.x == 0)
     {
-        const int prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const bool last = prev == total - 1;
-        if (last) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        *flag = last;
+        *flag = xcd_arrive(q, ctr, total);
     }
     __syncthreads();
     const bool last = *flag;
@@ -344,7 +342,7 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
             *to_global_w((f32x4*) (pbase + (size_t) slot * m * 128 + 4 * e)) = *(const f32x4*) (res + (e >> 5) * rs + 4 * (e & 31));
         if (!g.xcd) return;
         GEMV_STAMP(g, 4, 0);
-        if (!arrive_last(g.counters + ((size_t) j * chunks + chunk) * 32, splits, flag)) return;
+        if (!arrive_last(g.xg, g.counters + ((size_t) j * chunks + chunk) * 32, splits, flag)) return;
         GEMV_STAMP(g, 6, *flag);
         // sum the slots: threads split into G groups over the m * 64 column pairs; group gi takes
         // slots gi, gi + G, ...; the groups then combine in order through LDS
@@ -396,7 +394,7 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
     }
     if (g.weights && g.xcd)
     {
-        if (!arrive_last(g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
+        if (!arrive_last(g.xg, g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
         weighted_reduce(g, chunk, true);
     }
 }
@@ -508,11 +506,9 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     int* ctr = g.counters + ((size_t) j * (g.n / 128) + chunk) * 32;
-    int prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != splits - 1) return;
-    if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int last = 0;
+    if (lane == 0) last = xcd_arrive(g.xg, ctr, splits);
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // all slots' loads in flight together (16 per round: one L2 round trip for most shapes)
     float s0 = 0.0f, s1 = 0.0f;
@@ -533,24 +529,14 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
 __device__ void inactive_arrive(const GemvArgs& g, int chunk, int slot, int* flag)
 {
     if (!(g.weights && g.xcd) || slot != 0) return;
-    if (!arrive_last(g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
+    if (!arrive_last(g.xg, g.counters + g.counters_half + (size_t) chunk * 32, g.bszm, flag)) return;
     weighted_reduce(g, chunk, true);
 }
 
 // Workgroup -> (chunk, split slot).  XCD mode: the splits of a chunk share one XCD.
 __device__ __forceinline__ void block_coords(const GemvArgs& g, int splits, int& chunk, int& slot)
 {
-    if (g.xcd > 0)
-    {
-        const int xb = blockIdx.x % g.xcd, lb = blockIdx.x / g.xcd;
-        chunk = xb + g.xcd * (lb / splits);
-        slot = lb % splits;
-    }
-    else
-    {
-        chunk = blockIdx.x / splits;
-        slot = blockIdx.x - chunk * splits;
-    }
+    gemv_block_coords(g.xcd, splits, (int) blockIdx.x, chunk, slot);
 }
 
 template <int K, int CB, int MT>
@@ -1028,12 +1014,12 @@ void gemv1b_kernel(const GemvArgs g)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t a3 = sconst(89226354u), b3 = vconst(64248484u);
     const int KS = g.k / 16, R = g.slices_per_block, chunks = g.n / 128;
-    const int X = g.xcd, xq = blockIdx.x % X, lb = blockIdx.x / X;
-    const int per_x = g.bszm * chunks / X;                // pairs of this residue
+    const int X = g.xcd, lb = blockIdx.x / X;
+    Gemv1bBlock blk;
+    if (!gemv1b_block(X, g.bszm * chunks, KS, R, (int) blockIdx.x, blk)) return;
     const int T0 = lb * GEMV_WAVES * R;                   // the workgroup's first slice
-    if (T0 >= per_x * KS) return;
-    const int qA = T0 / KS, Bd = (qA + 1) * KS;           // pair A and the first slice of pair B
-    const bool straddle = T0 + GEMV_WAVES * R > Bd;
+    const int qA = blk.qA, Bd = (qA + 1) * KS;            // pair A and the first slice of pair B
+    const bool straddle = blk.straddle;
     const int t0 = T0 + wave * R;
     const int n0 = min(max(Bd - t0, 0), R);               // this wave's slices in pair A
     const int sA0 = t0 - qA * KS, sB0 = t0 - Bd;          // slice i: A at sA0 + i, B at sB0 + i
@@ -1051,7 +1037,7 @@ void gemv1b_kernel(const GemvArgs g)
     // the two pairs' matrices (every field selected by a uniform condition: indexed arrays of
     // views would live in scratch)
     MatView va, vb;
-    const int pa = xq + X * qA, pb = straddle ? pa + X : pa;
+    const int pa = blk.pa, pb = blk.pb;
     const int ja = pa / chunks, jb = pb / chunks;
     const int cha = pa - ja * chunks, chb = pb - jb * chunks;
     resolve(g, ja, va);
@@ -1174,8 +1160,8 @@ void gemv1b_kernel(const GemvArgs g)
     const float v0 = red[sg][0][2 * lane] + red[sg][1][2 * lane] + red[sg][2][2 * lane] + red[sg][3][2 * lane];
     const float v1 = red[sg][0][2 * lane + 1] + red[sg][1][2 * lane + 1] + red[sg][2][2 * lane + 1] + red[sg][3][2 * lane + 1];
     const int q = qA + (sg ? 1 : 0);
-    const int WR = GEMV_WAVES * R;
-    const int first = (q * KS) / WR, n = ((q + 1) * KS - 1) / WR - first + 1;
+    int first, n;
+    gemv1b_pair_span(KS, R, q, first, n);
     void* Cp = sg ? vb.C : va.C;
     const uint16_t* svh = sg ? vb.svh : va.svh;
     const float scale = sg ? vb.scale : va.scale;
@@ -1192,11 +1178,9 @@ void gemv1b_kernel(const GemvArgs g)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     int* ctr = g.counters + (size_t) pp * 32;
-    int prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != n - 1) return;
-    if (lane == 0) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int last = 0;
+    if (lane == 0) last = xcd_arrive(g.xg, ctr, n);
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     float a0 = 0.0f, a1 = 0.0f;
     for (int p0 = 0; p0 < n; p0 += 16)

@@ -6,6 +6,81 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Per-launch check of the XCD-local hand-off.  The hand-off publishes split-k partials with a
+// workgroup-scope release, which does not write the XCD's L2 back: the last arrival at a counter
+// sees the other arrivals' partials only when they ran on its XCD.  The library enables it after
+// the init probe has seen round-robin dispatch (workgroup b on XCD (b0 + b) % xcd); this guard
+// checks the assumption at every counter, every launch: the counter is a 64-bit word that also
+// sums the arrivals' XCC ids and their squares, and the last arrival stores 1 to the host-visible
+// alarm word when the ids differ (exl3_xcd.cuh).  The host reads the alarm at every call and,
+// once it is set, turns the hand-off off for the device (the finish kernel and agent-scope paths
+// sum the partials instead).
+struct XcdGuard
+{
+    uint32_t* alarm;            // pinned host word (device-mapped), 0 until a mixed arrival is seen
+    int fake_block;             // test hook: linear workgroup that reports XCC id + 1 (-1: none)
+};
+
+// Workgroup -> hand-off coordinates of the GEMV kernels (grid.x = splits x chunks).  XCD mode: the
+// splits of chunk c are workgroups b with b % xcd == c % xcd.  Shared with the host-side mapping
+// check (exl3_amd_debug_handoff_map).
+__host__ __device__ inline void gemv_block_coords(int xcd, int splits, int b, int& chunk, int& slot)
+{
+    if (xcd > 0)
+    {
+        const int xb = b % xcd, lb = b / xcd;
+        chunk = xb + xcd * (lb / splits);
+        slot = lb % splits;
+    }
+    else
+    {
+        chunk = b / splits;
+        slot = b - chunk * splits;
+    }
+}
+
+// MoE stages: workgroup b -> (column chunk, rest = split / projection / run).  XCD mode: chunk
+// c's workgroups are b with b % xcd == c % xcd (chunks % xcd == 0).
+__host__ __device__ inline void moe_chunk_coords(int xcd, int chunks, int b, int& chunk, int& rest)
+{
+    if (xcd > 0)
+    {
+        const int x = b % xcd, lb = b / xcd, cq = chunks / xcd;
+        chunk = x + xcd * (lb % cq);
+        rest = lb / cq;
+    }
+    else
+    {
+        chunk = b % chunks;
+        rest = b / chunks;
+    }
+}
+
+// Balanced M = 1 stream (gemv1b_kernel): the pairs p = j * chunks + chunk of residue x = b % xcd
+// are concatenated, KS slices each; workgroup b (local index lb = b / xcd) streams slices
+// [4 R lb, 4 R lb + 4 R) of that list, covering the tail of pair pa and the head of pair pb at most.
+// Returns false for a workgroup past the list's end.  first / count: the local indices that
+// contribute to the pair with list position q.
+struct Gemv1bBlock { int pa, pb, qA; bool straddle; };
+__host__ __device__ inline bool gemv1b_block(int xcd, int pairs, int KS, int R, int b, Gemv1bBlock& o)
+{
+    const int xq = b % xcd, lb = b / xcd;
+    const int per_x = pairs / xcd;
+    const int T0 = lb * 4 * R;
+    if (T0 >= per_x * KS) return false;
+    o.qA = T0 / KS;
+    o.straddle = T0 + 4 * R > (o.qA + 1) * KS;
+    o.pa = xq + xcd * o.qA;
+    o.pb = o.straddle ? o.pa + xcd : o.pa;
+    return true;
+}
+__host__ __device__ inline void gemv1b_pair_span(int KS, int R, int q, int& first, int& count)
+{
+    const int WR = 4 * R;
+    first = (q * KS) / WR;
+    count = ((q + 1) * KS - 1) / WR - first + 1;
+}
+
 // One GEMV launch over bszm "slots" (grid.y).  Single-matrix exl3_gemm: bszm = 1 and the
 // direct pointers.  Multi-matrix exl3_mgemm: device pointer tables, resolved per slot in the
 // kernel (quant/exl3_gemm_kernel.cuh:88-343 semantics).
@@ -50,8 +125,10 @@ struct GemvArgs
     int xcd;                    // > 0: XCD-local hand-off through L2 counters (workgroups b and b + xcd on one XCD)
     const uint32_t* sink;       // workspace: 8 KiB never written, target of the stream's past-the-end prefetches
     float* partials;            // workspace: bszm * slots * m * n fp32
-    int* counters;              // workspace: zeroed; [0, half) per (slot, chunk), [half, ..) per chunk
+    int* counters;              // workspace: zeroed; [0, half) per (slot, chunk), [half, ..) per chunk;
+                                // XCD mode: 64-bit at each 128-byte line
     int counters_half;
+    XcdGuard xg;                // hand-off check (used when xcd > 0)
     uint64_t* trace;            // instrumented builds only (EXL3_GEMV_TRACE): per-wave timestamps
 };
 
@@ -221,6 +298,7 @@ struct MoeArgs
     int* ctr_b;                 // [bsz][Ho/128] x 32
     int splits_a, splits_b;
     int xcd;                    // > 0: chunk c runs on XCD c % xcd (workgroup-scope hand-off)
+    XcdGuard xg;                // hand-off check (used when xcd > 0)
     int run_lo, run_hi;         // this launch takes the runs of run_lo + 1 .. run_hi slots
 };
 
@@ -238,6 +316,7 @@ int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* 
                           int K, int cb, hipStream_t s);
 
 int exl3k_xcd_probe(int* out, int blocks_x, int blocks_y, hipStream_t s);
+int exl3k_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
 int exl3k_mgemm_filter(const int64_t* indices, const uint16_t* weights, int bszm, int min_index,
                        int max_index, int num_tokens, int64_t* idx_out, uint16_t* w_out, hipStream_t s);
 

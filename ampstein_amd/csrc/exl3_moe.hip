@@ -25,6 +25,7 @@
 #include "exl3_common.cuh"
 #include "exl3_gemv_core.cuh"
 #include "exl3_kernels.h"
+#include "exl3_xcd.cuh"
 
 #ifndef EXL3_MOE_CB
 #define EXL3_MOE_CB 0
@@ -504,7 +505,7 @@ __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, in
 // total_r), re-arming it when its arrival is the last; last[r] tells the epilogue which rows this
 // workgroup completes.  One counter round trip for the run instead of one per row.
 template <typename CtrOf>
-__device__ __forceinline__ void arrive_rows(int nrows, CtrOf ctr_of, int* last, bool xcd)
+__device__ __forceinline__ void arrive_rows(int nrows, CtrOf ctr_of, int* last, bool xcd, const XcdGuard& q)
 {
     if (xcd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (xcd) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -514,14 +515,12 @@ __device__ __forceinline__ void arrive_rows(int nrows, CtrOf ctr_of, int* last, 
     {
         int total;
         int* ctr = ctr_of((int) threadIdx.x, total);
-        int prev;
-        if (xcd) prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        else prev = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool done = prev == total - 1;
-        if (done)
+        bool done;
+        if (xcd) done = xcd_arrive(q, ctr, total);      // 64-bit counter with the XCC record
+        else
         {
-            if (xcd) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            else __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            done = __hip_atomic_fetch_add(to_global_w(ctr), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+            if (done) __hip_atomic_store(to_global_w(ctr), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         last[threadIdx.x] = done;
     }
@@ -543,17 +542,7 @@ __device__ __forceinline__ f32x2 load_l2_f32x2(const float* p)
 // workgroup -> (chunk, rest): chunk c on XCD c % xcd when enabled
 __device__ __forceinline__ void chunk_coords(int xcd, int chunks, int& chunk, int& rest)
 {
-    if (xcd > 0)
-    {
-        const int x = blockIdx.x % xcd, b = blockIdx.x / xcd, cq = chunks / xcd;
-        chunk = x + xcd * (b % cq);
-        rest = b / cq;
-    }
-    else
-    {
-        chunk = blockIdx.x % chunks;
-        rest = blockIdx.x / chunks;
-    }
+    moe_chunk_coords(xcd, chunks, (int) blockIdx.x, chunk, rest);
 }
 
 __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, int& nrows)
@@ -614,7 +603,7 @@ void moe_a_kernel(const MoeArgs a)
     // completed (slot, chunk) rows: one wave each
     __shared__ int last[ROWS];
     arrive_rows(nrows, [&](int r, int& total) { total = nproj * S; return a.ctr_a + ((size_t) rows[r] * chunks + chunk) * 32; },
-                last, a.xcd > 0);
+                last, a.xcd > 0, a.xg);
     for (int r = wave; r < nrows; r += NW)
     {
         if (!last[r]) continue;
@@ -711,7 +700,7 @@ void moe_b_kernel(const MoeArgs a)
                     const int row = rows[r] / a.topk;
                     total = token_active_slots(a, row) * S;
                     return a.ctr_b + ((size_t) row * chunks + chunk) * 32; },
-                last, a.xcd > 0);
+                last, a.xcd > 0, a.xg);
     for (int r = wave; r < nrows; r += NW)
     {
         if (!last[r]) continue;

@@ -66,7 +66,10 @@ int exl3_amd_version(void);
 #define EXL3_AMD_POLICY_GEMV_SLICES     7   /* single-row stream GEMV: k-slices per workgroup (0 = by the
                                              * planner; a valid forced value: 4, 8, 16 or a multiple of 32
                                              * dividing k / 16)                                        */
-#define EXL3_AMD_POLICY_COUNT           8
+#define EXL3_AMD_POLICY_XCD_FAKE        8   /* test hook of the XCD hand-off check: value v > 0 makes
+                                             * linear workgroup v - 1 of every hand-off launch report
+                                             * XCC id + 1, as if dispatch had put it on another XCD   */
+#define EXL3_AMD_POLICY_COUNT           9
 int exl3_amd_set_policy(int key, int value);
 int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */
 
@@ -80,6 +83,27 @@ int exl3_amd_init(int device);
  * XCD-local split-k hand-off is off and a finish kernel sums the partials).  No counterpart in
  * the reference; for tests and benchmarks. */
 int exl3_amd_device_info(int device, int* num_cus, int* num_xcd);
+
+/* Per-launch check of the XCD-local split-k hand-off (no counterpart in the reference).  Every
+ * hand-off counter also sums its arrivals' XCC ids and their squares; the last arrival sets the
+ * device's alarm (pinned host memory) when the ids differ, i.e. when dispatch put workgroups of
+ * one counter on two XCDs.  Every call reads the alarm first: once it is set, the library turns
+ * the hand-off off for the device (num_xcd 0, the finish kernel and agent-scope hand-offs take
+ * over), zeroes the counters, and reports on stderr.  Outputs of the launch that raised the alarm
+ * are not reliable.
+ * xcd_status synchronises the device, services the alarm and reports the probe's XCD count, the
+ * count in use and the alarms seen so far.  xcd_rearm (tests) clears the alarm and restores the
+ * probe's count.  For tests and monitoring. */
+int exl3_amd_xcd_status(int device, int* probe_xcd, int* active_xcd, int* alarms);
+int exl3_amd_xcd_rearm(int device);
+
+/* Host-side view of the hand-off's workgroup mapping (the kernels' own functions; no device
+ * needed): kind 0, GEMV split grid (p0 splits): out = { chunk, slot }; kind 1, MoE stage grid
+ * (p0 chunks): out = { chunk, rest }; kind 2, balanced single-row stream (p0 pairs, p1 k / 16,
+ * p2 slices per wave): out = { valid, pair A, pair B, straddles }; kind 3, its pair span (p1, p2,
+ * b = pair position q): out = { first local index, count }.  No counterpart in the reference;
+ * for the CPU test of the mapping. */
+int exl3_amd_debug_handoff_map(int kind, int xcd, int p0, int p1, int p2, int b, int* out);
 
 /* Test hooks (no counterpart in the reference).  The per-device workspace holds split-k
  * partials and, during exl3_amd_moe, the token-sorted MoE's plan (row map, row tiles, tile lists,
