@@ -37,11 +37,6 @@
 #ifndef EXL3_INST_K
 #define EXL3_INST_K 4
 #endif
-// Prefetch ring depth (k-slices in flight per wave); HBM needs many bytes in flight
-// dot products of the M = 1 stream on MFMA (1) or v_dot2 (0)
-#ifndef EXL3_GEMV_MFMA
-#define EXL3_GEMV_MFMA 1
-#endif
 #ifndef EXL3_GEMV_PRIO
 #define EXL3_GEMV_PRIO 3
 #endif
@@ -836,15 +831,19 @@ void gemv1_kernel(const GemvArgs g)
     // (unconditional load: without svh it reads the input, k >= 128, and is unused)
     const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
 
-    float acc0 = 0.0f, acc1 = 0.0f, sx = 0.0f;
-#if EXL3_GEMV_MFMA
-    // Dot products on the matrix pipe: v_mfma_f32_4x4x4_16b_f16 with A = two decoded words of
-    // this lane (lo, hi of windows w, w + 1) and B = (x_r, x_r, x_r+1, x_r+1), the same for every
-    // lane: lane l's own dot accumulates in element l % 4 of the 4 x 4 block result.  The x pairs
-    // come from LDS (broadcast reads, no VALU); 2 accumulators per column break the chains.
+    float sx = 0.0f;
+    // Dot products on the matrix pipe, v_mfma_f32_16x16x32_f16: lane l's A operand is 4 k rows
+    // of one of its columns as decoded (lo, hi) fp16 pairs; B is block-diagonal over the four
+    // 16-lane groups (lane 16 q + n holds the rows' (x, x) pairs iff n == q, zeros otherwise), so
+    // the 32-long dot of row r, column n is lane 16 n + r's own 8 products: D[r][n] accumulates
+    // lane 16 n + r's dot.  The x pairs come from LDS (the off-diagonal lanes read a zero region
+    // at the same offsets).  The matrix pipe runs beside the other waves' decode VALU; the
+    // 4x4x4 form this replaces issued like VALU (measured gate/up 23.1 -> 22.2 us).
     __shared__ __align__(16) uint32_t xdup[GEMV_WAVES][2][128];
+    __shared__ __align__(16) uint32_t xzero[GEMV_WAVES][128];
+    *(u32x2*) &xzero[wave][2 * lane] = (u32x2) { 0u, 0u };
+    const bool diag = (lane & 15) == (lane >> 4);
     f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
-#endif
     for (int c = 0; c < nchunks; ++c)
     {
         const uint32_t xr = rotate_pair(ACT ? silu_mul_pair(xv, uv) : xv, sv, has_suh, lane);
@@ -856,15 +855,17 @@ void gemv1_kernel(const GemvArgs g)
             const bool mine = WS == 8 || (lane >= lane0 && lane < lane0 + 8 * per);
             sx += wave_sum(mine ? (float) p.x + (float) p.y : 0.0f, lane);
         }
-#if EXL3_GEMV_MFMA
         uint32_t* xd = xdup[wave][c & 1];
         {
+            // rows 2 lane, 2 lane + 1 of the chunk at slice position 4 g + 2 h + e for slice row
+            // t = 2 g + e + 8 h: each B operand is 4 contiguous words
             const f16x2 p = as_h2(xr);
             const f16x2 d0 = { p.x, p.x }, d1 = { p.y, p.y };
-            *(u32x2*) (xd + 2 * lane) = (u32x2) { as_u32(d0), as_u32(d1) };
+            const int t = (2 * lane) & 15;
+            *(u32x2*) (xd + ((2 * lane) & ~15) + 4 * ((t & 7) >> 1) + 2 * (t >> 3)) = (u32x2) { as_u32(d0), as_u32(d1) };
         }
+        const uint32_t* bbase = diag ? xd + (lane0 / 8) * 16 : xzero[wave];
         __builtin_amdgcn_wave_barrier();
-#endif
         // prefetch the next chunk's x (clamped: stays inside this wave's range)
         const int cn = min(c + 1, nchunks - 1);
         xv = *(to_global(xg) + (size_t) (a / 8 + cn) * 64);
@@ -878,21 +879,12 @@ void gemv1_kernel(const GemvArgs g)
             uint32_t wv[KB + 1];
             #pragma unroll
             for (int w = 0; w <= KB; ++w) wv[w] = ring[d][w];
-#if !EXL3_GEMV_MFMA
-            uint32_t raw[32];
-            raw32<K, CB>(wv, raw, a3, b3);
-#endif
             // refill with slice i + PF; past the last slice it reads the 8 KiB sink, which every
             // wave's tail reads and nothing writes (L2-resident: no HBM traffic, and the hand-off's
             // wait for the partial stores does not wait on HBM).  Unconditional, so the wait
             // counts stay static.
             load_slot_k<K>(i + PF <= last ? base + (size_t) (i + PF) * rstride : sinkp, prev_off, lane, ring[d]);
-#if EXL3_GEMV_MFMA
-            // x pairs of this slice's rows 2g, 2g+1 (h = 0) and 2g+8, 2g+9 (h = 1)
-            const uint32_t* xs = xd + (lane0 / 8 + s8) * 16;
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            // decode per group of 8 windows, right before its 4 MFMAs: 8 live words instead of 32
-            // (the registers that keep the kernel at 4 waves per SIMD)
+            // decode per group of 8 windows, right before its 2 MFMAs: 8 live words instead of 32
             #pragma unroll
             for (int gq = 0; gq < 4; ++gq)
             {
@@ -901,54 +893,38 @@ void gemv1_kernel(const GemvArgs g)
                 else if (gq == 1) raw8<K, CB, 8>(wv, raw, a3, b3);
                 else if (gq == 2) raw8<K, CB, 16>(wv, raw, a3, b3);
                 else raw8<K, CB, 24>(wv, raw, a3, b3);
+                const f16x8 bx = __builtin_bit_cast(f16x8, *(const u32x4*) (bbase + s8 * 16 + 4 * gq));
                 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int cc = 0; cc < 2; ++cc)
                 {
-                    const u32x2 xb = *(const u32x2*) (xs + 2 * gq + 8 * h);
-                    const h4 bx = __builtin_bit_cast(h4, xb);
-                    // windows w = 8 gq + 2 h (+1): column a; + 4: column b
-                    const int w = 8 * gq + 2 * h;
-                    const h4 wa = __builtin_bit_cast(h4, (u32x2) { raw[w], raw[w + 1] });
-                    const h4 wb = __builtin_bit_cast(h4, (u32x2) { raw[w + 4], raw[w + 5] });
-                    accv[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wa, bx, accv[h], 0, 0, 0);
-                    accv[2 + h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wb, bx, accv[2 + h], 0, 0, 0);
+                    // windows 8 gq + 4 cc + (0..3): column cc, rows 2 gq, 2 gq + 1, 2 gq + 8, 2 gq + 9
+                    const int w = 8 * gq + 4 * cc;
+                    const u32x4 aw = { raw[w], raw[w + 1], raw[w + 2], raw[w + 3] };
+                    accv[2 * (gq & 1) + cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, aw), bx, accv[2 * (gq & 1) + cc], 0, 0, 0);
                 }
             }
-#else
-            // this slice's 16 inputs: lanes lane0 + 8 s8 .. + 7 hold pairs (x[2q], x[2q+1])
-            uint32_t x16[16];
-            #pragma unroll
-            for (int q = 0; q < 8; ++q)
-            {
-                const uint32_t p = __builtin_amdgcn_readlane(xr, lane0 + 8 * s8 + q);
-                x16[2 * q] = (p & 0xffffu) | (p << 16);
-                x16[2 * q + 1] = (p >> 16) | (p & 0xffff0000u);
-            }
-            #pragma unroll
-            for (int w = 0; w < 32; ++w)
-            {
-                const int gq = w >> 3, jj = w & 7;
-                const int row = 2 * gq + (jj & 1) + 8 * ((jj >> 1) & 1);
-                float& acc = (jj >> 2) ? acc1 : acc0;
-                acc = __builtin_amdgcn_fdot2(as_h2(x16[row]), as_h2(raw[w]), acc, false);
-            }
-#endif
         }
     }
-#if EXL3_GEMV_MFMA
-    {
-        const int e = lane & 3;
-        auto pick = [&](const f32x4& v) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; };
-        acc0 = pick(accv[0]) + pick(accv[1]);
-        acc1 = pick(accv[2]) + pick(accv[3]);
-    }
-#endif
-
-    GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(acc0 + acc1)));
+    GEMV_STAMP(g, 2, __builtin_amdgcn_readfirstlane(__float_as_uint(accv[0].x)));
     __builtin_amdgcn_s_setprio(EXL3_GEMV_PRIO);
-    const int c0 = (lane >> 3) * 16 + (lane & 7);
-    red[wave][c0] = acc0;
-    red[wave][c0 + 8] = acc1;
+    {
+        // lane L holds D[4 (L / 16) + i][L % 16]; for n = L % 16 < 4 that is the dot of lane
+        // o = 16 n + 4 (L / 16) + i, whose columns are (o / 8) 16 + o % 8 (+ 8 for cc = 1)
+        const int n = lane & 15;
+        if (n < 4)
+        {
+            const f32x4 s0 = accv[0] + accv[2], s1 = accv[1] + accv[3];
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const int o = 16 * n + 4 * (lane >> 4) + i;
+                const int co = (o >> 3) * 16 + (o & 7);
+                red[wave][co] = s0[i];
+                red[wave][co + 8] = s1[i];
+            }
+        }
+    }
     if (lane == 0) sumx_w[wave] = sx;
     __syncthreads();
     if (!g.weights)
@@ -1079,15 +1055,29 @@ void gemv1b_kernel(const GemvArgs g)
     for (int d = 0; d < PF; ++d) load_slot_k<K>(addr(min(d, R - 1)), prev_off, lane, ring[d]);
     if (gnext < R) xload(gnext, xvn, svn);
 
+    // 16x16x32 dot with block-diagonal B, as in gemv1_kernel
+    __shared__ __align__(16) uint32_t xzero[GEMV_WAVES][128];
+    *(u32x2*) &xzero[wave][2 * lane] = (u32x2) { 0u, 0u };
+    const bool diag = (lane & 15) == (lane >> 4);
     f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
     int xb = 0;
-    const int c0 = (lane >> 3) * 16 + (lane & 7);          // this lane's columns c0, c0 + 8
-    // this wave's sums of one pair into red[sg][wave] (columns), or zeros
+    const uint32_t* bbase = xzero[wave];
+    // this wave's sums of one pair into red[sg][wave] (columns), or zeros: lane L holds the dots
+    // of lanes o = 16 n + 4 (L / 16) + i (n = L % 16 < 4), columns (o / 8) 16 + o % 8 (+ 8)
     auto deposit = [&](int sg, bool zero) {
-        const int e = lane & 3;
-        auto pick = [&](const f32x4& a) { return e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w; };
-        red[sg][wave][c0] = zero ? 0.0f : pick(accv[0]) + pick(accv[1]);
-        red[sg][wave][c0 + 8] = zero ? 0.0f : pick(accv[2]) + pick(accv[3]);
+        const int n = lane & 15;
+        if (n < 4)
+        {
+            const f32x4 s0 = accv[0] + accv[2], s1 = accv[1] + accv[3];
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const int o = 16 * n + 4 * (lane >> 4) + i;
+                const int co = (o >> 3) * 16 + (o & 7);
+                red[sg][wave][co] = zero ? 0.0f : s0[i];
+                red[sg][wave][co + 8] = zero ? 0.0f : s1[i];
+            }
+        }
     };
 
     for (int i0 = 0; i0 < R; i0 += PF)
@@ -1112,7 +1102,10 @@ void gemv1b_kernel(const GemvArgs g)
                 xb ^= 1;
                 const f16x2 pq = as_h2(xr);
                 const f16x2 d0 = { pq.x, pq.x }, d1 = { pq.y, pq.y };
-                *(u32x2*) (&xdup[wave][xb][2 * lane]) = (u32x2) { as_u32(d0), as_u32(d1) };
+                const int t = (2 * lane) & 15;
+                *(u32x2*) (&xdup[wave][xb][((2 * lane) & ~15) + 4 * ((t & 7) >> 1) + 2 * (t >> 3)]) =
+                    (u32x2) { as_u32(d0), as_u32(d1) };
+                bbase = diag ? xdup[wave][xb] : xzero[wave];
                 __builtin_amdgcn_wave_barrier();
             }
             const int xrow = ((i < n0 ? sA0 + i : sB0 + i) & 7) * 16;
@@ -1122,8 +1115,6 @@ void gemv1b_kernel(const GemvArgs g)
             // past the last slice: the last slice again (just read, an L2 hit), so that the load
             // is unconditional and the wait counts stay static
             load_slot_k<K>(addr(min(i + PF, R - 1)), prev_off, lane, ring[d]);
-            const uint32_t* xs = &xdup[wave][xb][xrow];
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
             #pragma unroll
             for (int gq = 0; gq < 4; ++gq)
             {
@@ -1132,16 +1123,14 @@ void gemv1b_kernel(const GemvArgs g)
                 else if (gq == 1) raw8<K, CB, 8>(wv, raw, a3, b3);
                 else if (gq == 2) raw8<K, CB, 16>(wv, raw, a3, b3);
                 else raw8<K, CB, 24>(wv, raw, a3, b3);
+                const f16x8 bx = __builtin_bit_cast(f16x8, *(const u32x4*) (bbase + xrow + 4 * gq));
                 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int cc = 0; cc < 2; ++cc)
                 {
-                    const u32x2 xbv = *(const u32x2*) (xs + 2 * gq + 8 * h);
-                    const h4 bx = __builtin_bit_cast(h4, xbv);
-                    const int w = 8 * gq + 2 * h;
-                    const h4 wa = __builtin_bit_cast(h4, (u32x2) { raw[w], raw[w + 1] });
-                    const h4 wb = __builtin_bit_cast(h4, (u32x2) { raw[w + 4], raw[w + 5] });
-                    accv[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wa, bx, accv[h], 0, 0, 0);
-                    accv[2 + h] = __builtin_amdgcn_mfma_f32_4x4x4f16(wb, bx, accv[2 + h], 0, 0, 0);
+                    const int w = 8 * gq + 4 * cc;
+                    const u32x4 aw = { raw[w], raw[w + 1], raw[w + 2], raw[w + 3] };
+                    accv[2 * (gq & 1) + cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, aw), bx, accv[2 * (gq & 1) + cc], 0, 0, 0);
                 }
             }
         }
