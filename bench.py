@@ -909,7 +909,7 @@ def main():
                    "packed_bytes_per_step": bundled.bytes, "launch": "hip-graph replay"},
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm",
-                     "kernel": "gemv1_kernel<4,0,8> as the stacked gate/up exl3_mgemm (2 x 4096x14336, grid 448x2, 16 k-slices per wave)",
+                     "kernel": "gemv1_kernel<4,0,8> as the stacked gate/up exl3_mgemm (2 x 4096x14336, grid 896x2 workgroups, 8 k-slices per wave)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes_per_launch"] if traffic and "bytes_per_launch" in traffic else None,
