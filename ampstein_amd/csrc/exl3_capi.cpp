@@ -174,15 +174,19 @@ int init_device(int device, DeviceState** out)
             d.sink = (uint32_t*) sk;
             // hand-off check: the alarm word (pinned host memory that kernels store to with system
             // scope, read by the host at every call)
+            // (without it the hand-off stays off: every launch must be checkable)
             void* al = nullptr;
             void* al_dev = nullptr;
-            if (hipHostMalloc(&al, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
-                return fail(EXL3_AMD_ENOMEM, "alarm-word allocation failed");
-            memset(al, 0, 64);
-            if (hipHostGetDevicePointer(&al_dev, al, 0) != hipSuccess || !al_dev)
-                return fail(EXL3_AMD_EHIP, "alarm-word device address failed");
-            d.alarm_host = (uint32_t*) al;
-            d.alarm_dev = (uint32_t*) al_dev;
+            if (hipHostMalloc(&al, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess && al)
+            {
+                memset(al, 0, 64);
+                if (hipHostGetDevicePointer(&al_dev, al, 0) == hipSuccess && al_dev)
+                {
+                    d.alarm_host = (uint32_t*) al;
+                    d.alarm_dev = (uint32_t*) al_dev;
+                }
+            }
+            (void) hipGetLastError();
             d.filt_idx = (int64_t*) f;
             d.filt_w = (uint16_t*) (d.filt_idx + MGEMM_MAX_FILTER);
             // workgroup -> XCD dispatch order (round-robin on MI355X), verified on this device
@@ -217,7 +221,7 @@ int init_device(int device, DeviceState** out)
                                 host[7], host[8]);
                     free(host);
                 }
-                d.num_xcd = ok && nx >= 1 && nx <= 31 ? nx : 0;
+                d.num_xcd = ok && nx >= 1 && nx <= 31 && d.alarm_dev ? nx : 0;
                 if (const char* e = getenv("EXL3_AMD_XCD")) if (atoi(e) == 0) d.num_xcd = 0;
                 d.probe_xcd = d.num_xcd;
             }

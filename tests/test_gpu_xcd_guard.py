@@ -3,7 +3,7 @@
 1. The tests that ran before this module in the same process (every hand-off path of the GEMV
    and the MoE) raised no alarm, and the hand-off is still on.
 2. The flag path, per hand-off kernel (single-row per-chunk split, balanced single-row split,
-   LDS multi-row kernel): with the test policy EXL3_AMD_POLICY_XCD_FAKE, workgroup X (X = the
+   LDS multi-row kernel, and the coop MoE's gate/up and down stages): with the test policy EXL3_AMD_POLICY_XCD_FAKE, workgroup X (X = the
    device's XCD count) reports XCC + 1, as if dispatch had put it on another XCD than workgroup 0
    of its counter.  The launch's output stays right (real dispatch is unchanged), the alarm is
    seen, the library turns the hand-off off, the next calls (finish-kernel path) are right too,
@@ -77,6 +77,36 @@ def test_flag_path(torch_cuda, orc, kernel_policy, path):
         run("hand-off off")
         run("hand-off off, again")
         assert _lib.xcd_status(0) == (probe, 0, alarms0 + 1)
+    finally:
+        _lib.check(_lib.lib().exl3_amd_xcd_rearm(0))
+    assert _lib.xcd_status(0)[:2] == (probe, probe)
+
+
+def test_flag_path_moe_coop(torch_cuda, orc, kernel_policy):
+    """The same on exl3_amd_moe_coop (gate/up and down hand-offs of moe_a / moe_b, I = Ho = 1024:
+    8 column chunks, XCD mode): workgroup X shares chunk 0's row counters with workgroup 0."""
+    torch = torch_cuda
+    from tests import moe_ref
+    from tests.test_gpu_moe import rel_err, routing, run
+    probe, active, alarms0 = _lib.xcd_status(0)
+    if probe == 0:
+        pytest.skip("the XCD-local hand-off is off on this device")
+    rng = np.random.default_rng(9800)
+    es = moe_ref.ExpertSet(torch, orc, 16, 256, 1024, 1024, rng.choice([2, 3, 4], 16), 2, seed=9801)
+    sel, rw = routing(rng, 8, 16, 8)
+    x = rng.standard_normal((8, 256)).astype(np.float16)
+    ref = moe_ref.reference(es, x, sel, rw, -1, -1, 0, True, 0.0, 1024)
+    try:
+        y, _ = run(torch, es, x, sel, rw)
+        assert rel_err(y, ref) < 2e-3
+        assert _lib.xcd_status(0) == (probe, probe, alarms0)
+        kernel_policy(_lib.POLICY_XCD_FAKE, probe + 1)
+        print(f"[xcd guard] moe_coop: workgroup {probe} reports another XCC", flush=True)
+        y, _ = run(torch, es, x, sel, rw)
+        assert rel_err(y, ref) < 2e-3
+        assert _lib.xcd_status(0) == (probe, 0, alarms0 + 1)
+        y, _ = run(torch, es, x, sel, rw)                  # agent-scope hand-off
+        assert rel_err(y, ref) < 2e-3
     finally:
         _lib.check(_lib.lib().exl3_amd_xcd_rearm(0))
     assert _lib.xcd_status(0)[:2] == (probe, probe)
