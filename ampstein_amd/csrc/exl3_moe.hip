@@ -30,12 +30,7 @@
 #ifndef EXL3_MOE_CB
 #define EXL3_MOE_CB 0
 #endif
-#ifndef EXL3_GEMV_PF
-#define EXL3_GEMV_PF 2
-#endif
-#ifndef EXL3_MOE_PF1
-#define EXL3_MOE_PF1 4          // k-slices in flight per wave, single-row body, K <= 4
-#endif
+constexpr int EXL3_MOE_PF1 = 4;  // k-slices in flight per wave, single-row body, K <= 4
 
 using namespace exl3;
 
@@ -474,9 +469,6 @@ template <int CB, int MT, bool HS>
 __device__ __forceinline__ void moe_gemv_k(int bits, const uint16_t* trellis, int tiles_n, int chunk, int ks0, int nks,
                            const XSrc& xsrc, uint32_t* xs, int xs_stride, int nrows, float* red, float* res)
 {
-#ifdef EXL3_MOE_ONLY_K
-    moe_gemv<EXL3_MOE_ONLY_K, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res); return;
-#endif
     if constexpr (HS)
     {
         if (bits == 17) moe_gemv<17, CB, MT>(trellis, tiles_n, chunk, ks0, nks, xsrc, xs, xs_stride, nrows, red, res);
