@@ -242,6 +242,19 @@ int init_device(int device, DeviceState** out)
 // The first call on a device allocates and clears the workspace, which a stream capture cannot
 // record: such a call is refused (no allocation, no synchronisation) and the capture stays
 // intact.  exl3_amd_init(device) before the capture avoids it.
+// Makes `device` current for the scope (calls that take a device argument and
+// synchronise, copy or launch on it).
+struct DeviceScope
+{
+    int prev = -1;
+    explicit DeviceScope(int device)
+    {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != device) (void) hipSetDevice(device);
+    }
+    ~DeviceScope() { if (prev >= 0) (void) hipSetDevice(prev); }
+};
+
 // The XCD hand-off check's alarm (set by a kernel that saw one counter's arrivals come from two
 // XCDs): turn the hand-off off for the device and zero every counter on `s`, so
 // that no later call reads what the mixed launch left.  Called by every entry point that launches
@@ -589,6 +602,7 @@ int exl3_amd_debug_read_workspace(int device, int64_t offset, int64_t bytes, voi
     if (int rc = init_device(device, &d)) return rc;
     if (offset < 0 || bytes < 0 || (uint64_t) (offset + bytes) > WS_PARTIAL_BYTES || (bytes && !host_dst))
         return fail(EXL3_AMD_EINVAL, "debug_read_workspace: range outside the %zu-byte workspace", WS_PARTIAL_BYTES);
+    DeviceScope scope(device);
     if (hipDeviceSynchronize() != hipSuccess ||
         hipMemcpy(host_dst, (char*) d->partials + offset, (size_t) bytes, hipMemcpyDeviceToHost) != hipSuccess)
         return fail(EXL3_AMD_EHIP, "debug_read_workspace: copy failed");
@@ -600,6 +614,7 @@ int exl3_amd_debug_fill_workspace(int device, int byte_value)
     g_last_error.clear();
     DeviceState* d;
     if (int rc = init_device(device, &d)) return rc;
+    DeviceScope scope(device);
     if (hipDeviceSynchronize() != hipSuccess || hipMemset(d->partials, byte_value & 0xff, WS_PARTIAL_BYTES) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return fail(EXL3_AMD_EHIP, "debug_fill_workspace: memset failed");
@@ -620,6 +635,7 @@ int exl3_amd_xcd_status(int device, int* probe_xcd, int* active_xcd, int* alarms
     g_last_error.clear();
     DeviceState* d;
     if (int rc = init_device(device, &d)) return rc;
+    DeviceScope scope(device);
     if (hipDeviceSynchronize() != hipSuccess) return fail(EXL3_AMD_EHIP, "xcd_status: device synchronisation failed");
     xcd_service(device, nullptr);
     if (hipDeviceSynchronize() != hipSuccess) return fail(EXL3_AMD_EHIP, "xcd_status: device synchronisation failed");
@@ -634,6 +650,7 @@ int exl3_amd_xcd_rearm(int device)
     g_last_error.clear();
     DeviceState* d;
     if (int rc = init_device(device, &d)) return rc;
+    DeviceScope scope(device);
     std::lock_guard<std::mutex> lock(g_mutex);
     if (hipDeviceSynchronize() != hipSuccess ||
         hipMemset(d->counters, 0, WS_COUNTER_INTS * sizeof(int)) != hipSuccess)
