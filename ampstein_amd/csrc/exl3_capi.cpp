@@ -796,6 +796,19 @@ int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint
     return rc ? hip_fail(rc, "reconstruct_had_t") : 0;
 }
 
+// CU count of the current device (cached per device; 0 if unknown)
+int current_cus()
+{
+    static std::atomic<int> cache[MAX_DEVICES];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+
 int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
                       int m, int k, int n, void* stream)
 {
@@ -808,7 +821,7 @@ int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32
     if (!A || !WT || !C) return fail(EXL3_AMD_EINVAL, "recon_mm: null pointer");
     (void) hipGetLastError();
     int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n,
-                              policy(EXL3_AMD_POLICY_RECON_MM), (hipStream_t) stream);
+                              policy(EXL3_AMD_POLICY_RECON_MM), current_cus(), (hipStream_t) stream);
     return rc ? hip_fail(rc, "recon_mm") : 0;
 }
 

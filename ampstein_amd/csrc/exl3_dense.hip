@@ -199,147 +199,177 @@ void dense_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
 // slice of stage s computes.
 constexpr int DENSE4_T = 256;
 
-template <int D>
-__global__ __launch_bounds__(DENSE4_T, 1)
-void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
-                        const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+// Tile body of the four-wave form: WN = columns per wave (128: the 256 x 256 tile; 64: a 256 x 128
+// half tile, used for the last partial round of tiles), output tile (mb, nb) of 256 x 2 WN.
+template <int D, int WN, bool BUF>
+__device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT,
+                                            void* __restrict__ C, const uint16_t* __restrict__ svh, int M, int k, int n,
+                                            int c_fp32, int mb, int nb)
 {
     constexpr int NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
-    __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
+    constexpr int BN = 2 * WN;
+    constexpr int NTN = WN / 32;                         // 32-column MFMA blocks per wave
+    constexpr int NT = 4 * NTN;                          // MFMAs per 16-k slice
+    constexpr int NR = 4 + NTN;                          // operand reads per slice
+    constexpr int NDMA = 4 + NTN;                        // DMAs per stage per wave (A: 4, WT: NTN)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int NST = k / 32;
-    const int nbn = (n + DENSE_BN - 1) / DENSE_BN;
-    const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
-    int nb, mb;
-    if (nbn % 8 == 0)
-    {
-        const int x = blockIdx.x % 8, r = blockIdx.x / 8;
-        nb = x + 8 * (r / nmb);
-        mb = r % nmb;
-    }
-    else
-    {
-        nb = blockIdx.x / nmb;
-        mb = blockIdx.x % nmb;
-    }
 
-    // wave w's DMAs j = 0..3 fill the 1 KiB blocks q = w + 4 j (rows 16 q .. 16 q + 15) of each operand
+    // wave w's DMAs fill the 1 KiB blocks q = w + 4 j (rows 16 q .. 16 q + 15) of each operand:
+    // j < 4 for A (256 rows), j < NTN for WT (BN rows)
     const u32x4* a_src[4];
-    const u32x4* b_src[4];
+    const u32x4* b_src[NTN];
     #pragma unroll
     for (int j = 0; j < 4; ++j)
     {
         const int q = wave + 4 * j, row = 16 * q + (lane >> 2), ch = (lane & 3) ^ ((row >> 2) & 3);
         a_src[j] = (const u32x4*) (A + (size_t) min(mb * DENSE_BM + row, M - 1) * k + 8 * ch);
-        b_src[j] = (const u32x4*) (WT + (size_t) min(nb * DENSE_BN + row, n - 1) * k + 8 * ch);
+        if (j < NTN) b_src[j] = (const u32x4*) (WT + (size_t) min(nb * BN + row, n - 1) * k + 8 * ch);
     }
-    auto issue = [&](int st) {
-        const int c = min(st, NST - 1);
-        const int buf = (st % NB) * DENSE_TILE_U32;
+    // BUF: the DMAs go through buffer resources over A and WT (operands below 4 GiB, checked on
+    // the host): a 32-bit lane offset fixed per DMA slot and the stage's byte offset in an SGPR,
+    // so that no VALU address arithmetic sits between the MFMAs (measured 1-2 % faster than
+    // global_load_lds with 64-bit lane addresses)
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*) A, (short) 0, (int) (uint32_t) ((size_t) M * k * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*) WT, (short) 0, (int) (uint32_t) ((size_t) n * k * 2), 0x00020000);
+    uint32_t a_off[4], b_off[NTN];
+    if constexpr (BUF)
+    {
         #pragma unroll
         for (int j = 0; j < 4; ++j)
         {
-            __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
-                                             (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*) (b_src[j] + 4 * c),
-                                             (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
+            a_off[j] = (uint32_t) ((const char*) a_src[j] - (const char*) A);
+            if (j < NTN) b_off[j] = (uint32_t) ((const char*) b_src[j] - (const char*) WT);
         }
-    };
-
-    const int wm = wave & 1, wn = wave >> 1;
-    const int l32 = lane & 31, lh = lane >> 5;
-    #pragma unroll
-    for (int g = 0; g < D; ++g) issue(g);
-    DENSE_VM_LGKM0(8 * (D - 1));
-    __builtin_amdgcn_s_barrier();
-
-    acc16 acc[4][4];
-    #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (acc16) { };
-
-    // The loop body is written out in issue order, fenced by sched_barrier: the 16 MFMAs of a slice
-    // alternate with the 8 operand reads of the next slice and (first half) the 8 LDS DMAs of stage
-    // s + D, so that no burst of memory instructions holds up the matrix pipe (a wave whose VMEM
-    // issue stalls cannot issue MFMAs meanwhile).  Reads are issued in the order the MFMAs consume
-    // them (a[0], b[0..3], a[1..3]), so each MFMA waits only for its own operands.
-    h8v a0[4], b0[4], a1[4], b1[4];
-    auto read_one = [&](int st, int sl, int q, h8v* av, h8v* bv) {
-        const uint32_t* As = lds + DENSE_A0 + (st % NB) * DENSE_TILE_U32;
-        const uint32_t* Bs = lds + DENSE_B0 + (st % NB) * DENSE_TILE_U32;
-        constexpr int ord[8] = { 0, 4, 5, 6, 7, 1, 2, 3 };       // a0, b0..b3, a1..a3
-        const int o = ord[q];
-        if (o < 4) av[o] = __builtin_bit_cast(h8v, *(const u32x4*) (As + x_off(128 * wm + 32 * o + l32, 2 * sl + lh)));
-        else bv[o - 4] = __builtin_bit_cast(h8v, *(const u32x4*) (Bs + x_off(128 * wn + 32 * (o - 4) + l32, 2 * sl + lh)));
-    };
+    }
+    // DMA q of a stage: A and WT blocks alternate while both last, then the rest of A
     auto issue_one = [&](int st, int q) {
-        const int c = min(st, NST - 1);
-        const int buf = (st % NB) * DENSE_TILE_U32, j = q >> 1;
-        if (q & 1)
+        const int c = min(st, NST - 1);                  // past the end: rewrites a buffer nobody reads
+        const int buf = (st % NB) * DENSE_TILE_U32;
+        const bool isb = q < 2 * NTN && (q & 1);
+        const int j = q < 2 * NTN ? q >> 1 : q - NTN;
+        if constexpr (BUF)
+        {
+            if (isb)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 4 * j)), 16,
+                                                         b_off[j], c * 64, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 4 * j)), 16,
+                                                         a_off[j], c * 64, 0, 0);
+            return;
+        }
+        if (isb)
             __builtin_amdgcn_global_load_lds((const void*) (b_src[j] + 4 * c),
                                              (lds_ptr_t) (lds + DENSE_B0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
         else
             __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
                                              (lds_ptr_t) (lds + DENSE_A0 + buf + 256 * (wave + 4 * j)), 16, 0, 0);
     };
+
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lh = lane >> 5;
     #pragma unroll
-    for (int q = 0; q < 8; ++q) read_one(0, 0, q, a0, b0);
+    for (int g = 0; g < D; ++g)
+        #pragma unroll
+        for (int q = 0; q < NDMA; ++q) issue_one(g, q);
+    DENSE_VM_LGKM0(NDMA * (D - 1));
+    __builtin_amdgcn_s_barrier();
+
+    acc16 acc[4][NTN];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+        #pragma unroll
+        for (int j = 0; j < NTN; ++j) acc[i][j] = (acc16) { };
+
+    // The loop body is written out in issue order, fenced by sched_barrier: the NR operand reads of
+    // the next slice are spread over the NT MFMAs of a slice (read r after MFMA r NT / NR), and
+    // half of stage s + D's NDMA LDS DMAs sit in each slice, one every NT / (NDMA / 2) MFMAs, so
+    // that no burst of memory instructions holds up the matrix pipe (a wave whose VMEM issue
+    // stalls cannot issue MFMAs meanwhile; without the DMAs the loop runs ~1.5x faster, and DMAs
+    // of a quarter the size are no cheaper: the cost is per instruction).  Reads are issued in the
+    // order the MFMAs consume them (a[0], b[0..NTN-1], a[1..3]), so each MFMA waits only for its
+    // own operands.
+    h8v a0[4], b0[NTN], a1[4], b1[NTN];
+    auto read_one = [&](int st, int sl, int q, h8v* av, h8v* bv) {
+        const uint32_t* As = lds + DENSE_A0 + (st % NB) * DENSE_TILE_U32;
+        const uint32_t* Bs = lds + DENSE_B0 + (st % NB) * DENSE_TILE_U32;
+        if (q == 0) av[0] = __builtin_bit_cast(h8v, *(const u32x4*) (As + x_off(128 * wm + l32, 2 * sl + lh)));
+        else if (q <= NTN) bv[q - 1] = __builtin_bit_cast(h8v, *(const u32x4*) (Bs + x_off(WN * wn + 32 * (q - 1) + l32, 2 * sl + lh)));
+        else av[q - NTN] = __builtin_bit_cast(h8v, *(const u32x4*) (As + x_off(128 * wm + 32 * (q - NTN) + l32, 2 * sl + lh)));
+    };
+    #pragma unroll
+    for (int q = 0; q < NR; ++q) read_one(0, 0, q, a0, b0);
     for (int s = 0; s < NST; ++s)
     {
+        // first slice: after MFMA t, events [t E / NT, (t + 1) E / NT) of the interleaved list
+        // read 0, DMA 0, read 1, DMA 1, ... (E = NR + NDMA)
         #pragma unroll
-        for (int t = 0; t < 16; ++t)
+        for (int t = 0; t < NT; ++t)
         {
-            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[t >> 2], b0[t & 3], acc[t >> 2][t & 3], 0, 0, 0);
-            if (t & 1) issue_one(s + D, t >> 1);
-            else read_one(s, 1, t >> 1, a1, b1);
+            acc[t / NTN][t % NTN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[t / NTN], b0[t % NTN], acc[t / NTN][t % NTN], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (r * NT / NR == t) read_one(s, 1, r, a1, b1);
+            #pragma unroll
+            for (int i = 0; i < NDMA / 2; ++i)
+                if ((i + 1) * NT / (NDMA / 2) - 1 == t) issue_one(s + D, i);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // stage s + 1 landed for this wave, its own reads of stage s are complete: barrier, after
-        // which every wave's reads of stage s are complete too (its buffer is refilled next stage)
-        DENSE_VM_LGKM0(8 * (D - 1));
+        // stage s + 1 landed for this wave (stages s + 2 .. s + D - 1 and the first half of
+        // s + D may be in flight), its own reads of stage s are complete: barrier, after which
+        // every wave's reads of stage s are complete too (its buffer is refilled from the next
+        // stage's first DMA on)
+        DENSE_VM_LGKM0(NDMA * (D - 2) + NDMA / 2);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         // slice 0 of stage s + 1 read under the MFMAs of slice 1 (past the end: an unread buffer)
         #pragma unroll
-        for (int t = 0; t < 16; ++t)
+        for (int t = 0; t < NT; ++t)
         {
-            acc[t >> 2][t & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[t >> 2], b1[t & 3], acc[t >> 2][t & 3], 0, 0, 0);
-            if (!(t & 1)) read_one(s + 1, 0, t >> 1, a0, b0);
+            acc[t / NTN][t % NTN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[t / NTN], b1[t % NTN], acc[t / NTN][t % NTN], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (r * NT / NR == t) read_one(s + 1, 0, r, a0, b0);
+            #pragma unroll
+            for (int i = 0; i < NDMA / 2; ++i)
+                if ((i + 1) * NT / (NDMA / 2) - 1 == t) issue_one(s + D, NDMA / 2 + i);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     DENSE_VM_LGKM0(0);
     __builtin_amdgcn_s_barrier();
 
-    // epilogue: 4 rounds; round r holds rows 128 wm + 32 r + (0..31) of each wave in E[64][256]
+    // epilogue: 4 rounds; round r holds rows 128 wm + 32 r + (0..31) of each wave in E[64][BN]
+    constexpr int NCH = BN / 128;                        // 128-column chunks per row
     float* E = (float*) lds;
     const bool has_svh = svh != nullptr;
     #pragma unroll
     for (int r = 0; r < 4; ++r)
     {
         #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NTN; ++j)
         {
             #pragma unroll
             for (int jj = 0; jj < 4; ++jj)
             {
                 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    E[(32 * wm + 8 * jj + 4 * lh + i) * DENSE_BN + 128 * wn + 32 * j + l32] = acc[r][j][4 * jj + i];
+                    E[(32 * wm + 8 * jj + 4 * lh + i) * BN + WN * wn + 32 * j + l32] = acc[r][j][4 * jj + i];
             }
         }
         __syncthreads();
         #pragma unroll 2
-        for (int q = 0; q < 32; ++q)
+        for (int q = 0; q < 16 * NCH; ++q)
         {
-            const int rc = wave * 32 + q;
-            const int er = rc >> 1, ch = rc & 1;
+            const int rc = wave * 16 * NCH + q;
+            const int er = rc / NCH, ch = rc % NCH;
             const int row = mb * DENSE_BM + 128 * (er >> 5) + 32 * r + (er & 31);
-            const int col = nb * DENSE_BN + 128 * ch + 2 * lane;
-            if (nb * DENSE_BN + 128 * ch >= n) continue;
-            const f32x2 v = *(const f32x2*) (E + er * DENSE_BN + 128 * ch + 2 * lane);
+            const int col = nb * BN + 128 * ch + 2 * lane;
+            if (nb * BN + 128 * ch >= n) continue;       // half block: chunk past n (uniform per wave)
+            const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
             if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
         }
@@ -347,15 +377,81 @@ void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restri
     }
 }
 
+// Four-wave form (default): one wave per SIMD, each wave a 128 x 128 quarter of the 256 x 256 tile
+// (4 x 4 accumulators of v_mfma_f32_32x32x16_f16, held in AGPRs).  Per 16-k slice a wave reads 8
+// operand blocks for 16 MFMAs (the eight-wave form: 6 for 8), so the LDS serves a third less per
+// flop.  With one wave per SIMD the wave hides its own LDS latency: the operand reads of slice
+// s + 1 are issued between the MFMAs of slice s (two register sets), and the stage barrier sits
+// between the two slices of a stage, so the first slice of stage s + 1 is read while the second
+// slice of stage s computes.
+//
+// Grid: full tiles first (column blocks 0 .. nfull - 1 of 256), then, when the tiles would leave
+// a last round less than half full, the remaining column blocks as 256 x 128 half tiles (2 per
+// block).  The dispatcher hands the half tiles to the CUs as they finish their last full tile, so
+// the partial round takes about half a tile's time instead of a whole one (8192 -> 28672 at 2048
+// rows: 896 tiles = 3.5 rounds on 256 CUs).
+template <int D, bool BUF>
+__global__ __launch_bounds__(DENSE4_T, 1)
+void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
+                        const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int nfull)
+{
+    __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
+    const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
+    // tile -> (nb, mb): with a multiple of 8 column blocks, the 8 consecutive workgroups that
+    // share an XCD take one column block's row blocks in turn
+    auto map = [&](int b, int nbn, int& nb, int& mb) {
+        if (nbn % 8 == 0)
+        {
+            const int x = b % 8, r = b / 8;
+            nb = x + 8 * (r / nmb);
+            mb = r % nmb;
+        }
+        else
+        {
+            nb = b / nmb;
+            mb = b % nmb;
+        }
+    };
+    const int b = blockIdx.x;
+    int nb, mb;
+    if (b < nfull * nmb)
+    {
+        map(b, nfull, nb, mb);
+        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb);
+    }
+    else
+    {
+        const int nbn = (n + DENSE_BN - 1) / DENSE_BN;
+        map(b - nfull * nmb, 2 * (nbn - nfull), nb, mb);
+        dense4_tile<D, 64, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb + 2 * nfull);
+    }
+}
+
 }  // namespace
 
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                     int m, int k, int n, int variant, hipStream_t s)
+                     int m, int k, int n, int variant, int cus, hipStream_t s)
 {
-    const int blocks = ((n + DENSE_BN - 1) / DENSE_BN) * ((m + DENSE_BM - 1) / DENSE_BM);
+    const int nbn = (n + DENSE_BN - 1) / DENSE_BN, nmb = (m + DENSE_BM - 1) / DENSE_BM;
+    const int blocks = nbn * nmb;
     if (variant == 1)
+    {
         hipLaunchKernelGGL((dense_gemm_kernel<3>), dim3(blocks), dim3(DENSE_T), 0, s, A, WT, C, svh, m, k, n, c_fp32);
+        return (int) hipGetLastError();
+    }
+    // half tiles for a last round at most half full: whole column blocks (n a multiple of 256),
+    // at least one full round before it
+    const int rem = cus > 0 ? blocks % cus : 0;
+    int nfull = nbn;
+    if (variant != 2 && n % DENSE_BN == 0 && blocks > cus && rem > 0 && 2 * rem <= cus && rem % nmb == 0)
+        nfull = nbn - rem / nmb;
+    const int grid = nfull * nmb + 2 * (nbn - nfull) * nmb;
+    // buffer-resource DMAs for operands below 4 GiB (32-bit offsets and record counts)
+    // (variant 3 forces the 64-bit-address form, for tests)
+    const bool buf = variant != 3 && (size_t) m * k * 2 < (1ull << 32) && (size_t) n * k * 2 < (1ull << 32);
+    if (buf)
+        hipLaunchKernelGGL((dense_gemm4_kernel<3, true>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull);
     else
-        hipLaunchKernelGGL((dense_gemm4_kernel<3>), dim3(blocks), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32);
+        hipLaunchKernelGGL((dense_gemm4_kernel<3, false>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull);
     return (int) hipGetLastError();
 }

@@ -61,6 +61,9 @@ int exl3_amd_version(void);
 #define EXL3_AMD_MOE_OUTPUT_ATOMIC      1   /*   per-row atomics instead of the per-token lists         */
 #define EXL3_AMD_POLICY_RECON_MM        5   /* kernel of exl3_amd_recon_mm                             */
 #define EXL3_AMD_RECON_MM_8WAVES        1   /*   8 waves of 128 x 64 instead of 4 waves of 128 x 128    */
+#define EXL3_AMD_RECON_MM_WHOLE_TILES   2   /*   four-wave form without half tiles in a last round      */
+#define EXL3_AMD_RECON_MM_GLOBAL_DMA    3   /*   four-wave form, DMAs on 64-bit lane addresses (the form
+                                                 used for operands of 4 GiB and more)                   */
 #define EXL3_AMD_POLICY_GEMV_SPLIT      6   /* work split of the single-row GEMV                       */
 #define EXL3_AMD_GEMV_SPLIT_BALANCED    1   /*   equal work per wave and waves per SIMD (gemv1b_kernel)  */
 #define EXL3_AMD_POLICY_GEMV_SLICES     7   /* single-row stream GEMV: k-slices per workgroup (0 = by the

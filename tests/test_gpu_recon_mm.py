@@ -34,7 +34,7 @@ def rel(y, ref):
                                    (513, 2048, 256), (1024, 96, 2048)])
 @pytest.mark.parametrize("out", ["fp16", "fp32"])
 @pytest.mark.parametrize("rot", [False, True])
-@pytest.mark.parametrize("variant", [0, 1], ids=["4waves", "8waves"])
+@pytest.mark.parametrize("variant", [0, 1, 3], ids=["4waves", "8waves", "4waves-global-dma"])
 def test_recon_mm_matches_torch_fp32(torch_cuda, kernel_policy, m, k, n, out, rot, variant):
     torch = torch_cuda
     from ampstein_amd import ops, _lib
@@ -53,6 +53,50 @@ def test_recon_mm_matches_torch_fp32(torch_cuda, kernel_policy, m, k, n, out, ro
     y = c.float().cpu().numpy()
     assert np.isfinite(y).all()
     assert rel(y, ref) < (2e-3 if out == "fp16" else 1e-5), (m, k, n, out, rot)
+
+
+def half_tile_cases(cus):
+    """(m, k, n) whose 256 x 256 tiles leave a last round at most half full, so that the four-wave
+    form runs the remaining column blocks as 256 x 128 half tiles: one row block with cus + 44
+    column blocks, two row blocks (partial rows) with cus / 2 + 2, and the 8192 -> 28672 prefill
+    shape (configs[3], 896 tiles)."""
+    return [(256, 64, 256 * (cus + 44)), (300, 96, 256 * (cus // 2 + 2)), (2048, 8192, 28672)]
+
+
+@pytest.mark.parametrize("case", [0, 1, 2])
+@pytest.mark.parametrize("rot", [False, True])
+def test_recon_mm_half_tiles(torch_cuda, kernel_policy, case, rot):
+    """The grid with half tiles in its last round against the same GEMM with whole tiles only
+    (policy EXL3_AMD_RECON_MM_WHOLE_TILES) and against torch's fp32 matmul, bar 2e-3 (fp16 out)."""
+    torch = torch_cuda
+    from ampstein_amd import ops, _lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    m, k, n = half_tile_cases(cus)[case]
+    nmb, nbn = (m + 255) // 256, n // 256
+    rem = nbn * nmb % cus
+    assert nbn * nmb > cus and 0 < 2 * rem <= cus and rem % nmb == 0     # the half-tile grid applies
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + k + n + case)
+    a = torch.randn((m, k), generator=g, device="cuda").half()
+    wt = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+    svh = (torch.randint(0, 2, (n,), generator=g, device="cuda") * 2 - 1).half() if rot else None
+    outs = []
+    for variant in (0, _lib.RECON_MM_WHOLE_TILES, _lib.RECON_MM_GLOBAL_DMA):
+        kernel_policy(_lib.POLICY_RECON_MM, variant)
+        c = torch.full((m, n), float("nan"), dtype=torch.half, device="cuda")
+        ops.recon_mm(a, wt, c, svh)
+        torch.cuda.synchronize()
+        outs.append(c)
+    # the same tile arithmetic every way (one k order per output): bit-identical
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ref = a.float() @ wt.float().t()
+    if rot:
+        H = torch.from_numpy(hadamard(128) / np.sqrt(128.0)).float().cuda()
+        ref = (ref.view(m, n // 128, 128) @ H).view(m, n) * svh.float()
+    y = outs[0].float()
+    assert torch.isfinite(y).all()
+    err = float((y - ref).abs().max() / ref.abs().max())
+    assert err < 2e-3, (m, k, n, rot, err)
 
 
 def test_recon_mm_rejects(torch_cuda):
