@@ -715,12 +715,12 @@ int exl3_amd_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n_pack
     return rc ? hip_fail(rc, "reconstruct") : 0;
 }
 
-int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_packed, int n,
-                           int n_offset, float K, int mcg, int mul1, void* stream)
+static int reconstruct_t_impl(uint16_t* WT, const uint16_t* trellis, int k, int n_packed, int n,
+                              int n_offset, float K, int mcg, int mul1, int slabs, void* stream)
 {
-    g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "reconstruct_t", true)) return rc;
+    if (slabs && k % 32) return fail(EXL3_AMD_EINVAL, "reconstruct_t: k must be a multiple of 32 for the slab layout");
     if (k < 0 || n < 0 || n_packed < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t: negative size");
     if (k % 16 || n_packed % 16) return fail(EXL3_AMD_EINVAL, "reconstruct_t: k and the packed width must be multiples of 16");
     if ((size_t) k * n == 0) return 0;
@@ -730,8 +730,16 @@ int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_p
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
     DeviceState* d;
     if (int rc = current_device(&d, stream)) return rc;
-    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, nullptr, (hipStream_t) stream);
+    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, nullptr, slabs,
+                                  (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_t") : 0;
+}
+
+int exl3_amd_reconstruct_t(uint16_t* WT, const uint16_t* trellis, int k, int n_packed, int n,
+                           int n_offset, float K, int mcg, int mul1, void* stream)
+{
+    g_last_error.clear();
+    return reconstruct_t_impl(WT, trellis, k, n_packed, n, n_offset, K, mcg, mul1, 0, stream);
 }
 
 int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint16_t* svh, int k, int n_packed,
@@ -749,7 +757,7 @@ int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
     DeviceState* d;
     if (int rc = current_device(&d, stream)) return rc;
-    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, svh + n_offset,
+    int rc = exl3k_reconstruct_tr(WT, trellis, k, n, n_packed / 16, n_offset / 16, bits, cb, svh + n_offset, 0,
                                   (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_t_had") : 0;
 }
@@ -775,11 +783,10 @@ int exl3_amd_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_
     return rc ? hip_fail(rc, "reconstruct_had") : 0;
 }
 
-int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
-                               const uint16_t* svh, int k, int n_packed, int n, int n_offset,
-                               float K, int mcg, int mul1, void* stream)
+static int reconstruct_had_t_impl(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                                  const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                                  float K, int mcg, int mul1, int slabs, void* stream)
 {
-    g_last_error.clear();
     int bits, half, cb;
     if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "reconstruct_had_t", true)) return rc;
     if (k < 0 || n < 0 || n_packed < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_had_t: negative size");
@@ -791,13 +798,31 @@ int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint
     if (n_offset % 128) return fail(EXL3_AMD_EINVAL, "n_offset must be divisible by 128");
     if (n_offset < 0) return fail(EXL3_AMD_EINVAL, "n_offset must be non-negative");
     if (n_offset + n > n_packed) return fail(EXL3_AMD_EINVAL, "reconstruct slice exceeds packed tensor bounds");
-    int rc = exl3k_reconstruct_had_tr(WT, trellis, suh, svh, k, n, n_packed / 16, n_offset / 16, bits, cb,
+    int rc = exl3k_reconstruct_had_tr(WT, trellis, suh, svh, k, n, n_packed / 16, n_offset / 16, bits, cb, slabs,
                                       (hipStream_t) stream);
     return rc ? hip_fail(rc, "reconstruct_had_t") : 0;
 }
 
+int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                               const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                               float K, int mcg, int mul1, void* stream)
+{
+    g_last_error.clear();
+    return reconstruct_had_t_impl(WT, trellis, suh, svh, k, n_packed, n, n_offset, K, mcg, mul1, 0, stream);
+}
+
+int exl3_amd_reconstruct_t_slabs(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                                 const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                                 float K, int mcg, int mul1, int original_basis, void* stream)
+{
+    g_last_error.clear();
+    if (original_basis)
+        return reconstruct_had_t_impl(WT, trellis, suh, svh, k, n_packed, n, n_offset, K, mcg, mul1, 1, stream);
+    return reconstruct_t_impl(WT, trellis, k, n_packed, n, n_offset, K, mcg, mul1, 1, stream);
+}
+
 // CU count of the current device (cached per device; 0 if unknown)
-int current_cus()
+static int current_cus()
 {
     static std::atomic<int> cache[MAX_DEVICES];
     int dev = 0;
@@ -809,10 +834,9 @@ int current_cus()
     return c;
 }
 
-int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                      int m, int k, int n, void* stream)
+static int recon_mm_impl(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                         int m, int k, int n, int a_slabs, int w_slabs, void* stream)
 {
-    g_last_error.clear();
     if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "recon_mm: negative size");
     if (k % 32) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be a multiple of 32");
     if (n % 128) return fail(EXL3_AMD_EINVAL, "recon_mm: n must be a multiple of 128");
@@ -820,9 +844,23 @@ int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32
     if (k == 0) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be positive");
     if (!A || !WT || !C) return fail(EXL3_AMD_EINVAL, "recon_mm: null pointer");
     (void) hipGetLastError();
-    int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n,
+    int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n, a_slabs ? 1 : 0, w_slabs ? 1 : 0,
                               policy(EXL3_AMD_POLICY_RECON_MM), current_cus(), (hipStream_t) stream);
     return rc ? hip_fail(rc, "recon_mm") : 0;
+}
+
+int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                      int m, int k, int n, void* stream)
+{
+    g_last_error.clear();
+    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, 0, 0, stream);
+}
+
+int exl3_amd_recon_mm_slabs(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                            int m, int k, int n, int a_slabs, int w_slabs, void* stream)
+{
+    g_last_error.clear();
+    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, a_slabs, w_slabs, stream);
 }
 
 int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
@@ -834,8 +872,24 @@ int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,
     if (pre && post) return fail(EXL3_AMD_EINVAL, "had_r_128: give pre or post scale, not both");
     if ((size_t) rows * cols == 0) return 0;
     if (!x || !y) return fail(EXL3_AMD_EINVAL, "had_r_128: null pointer");
-    int rc = exl3k_had128(x, y, rows, cols, fp32 ? 1 : 0, pre, post, scale, (hipStream_t) stream);
+    int rc = exl3k_had128(x, y, rows, cols, fp32 ? 1 : 0, pre, post, scale, 0, (hipStream_t) stream);
     return rc ? hip_fail(rc, "had_r_128") : 0;
+}
+
+int exl3_amd_to_slabs(const uint16_t* x, uint16_t* y, int rows, int cols, int rotate, const uint16_t* pre,
+                      float scale, void* stream)
+{
+    g_last_error.clear();
+    if (rows < 0 || cols < 0) return fail(EXL3_AMD_EINVAL, "to_slabs: negative size");
+    if (cols % (rotate ? 128 : 32)) return fail(EXL3_AMD_EINVAL, "to_slabs: columns must be divisible by %d", rotate ? 128 : 32);
+    if ((size_t) rows * cols == 0) return 0;
+    if (!x || !y) return fail(EXL3_AMD_EINVAL, "to_slabs: null pointer");
+    if (x == y) return fail(EXL3_AMD_EINVAL, "to_slabs: the output cannot overwrite the input");
+    if (!rotate && pre) return fail(EXL3_AMD_EINVAL, "to_slabs: a pre scale needs the rotation");
+    (void) hipGetLastError();
+    int rc = rotate ? exl3k_had128(x, y, rows, cols, 0, pre, nullptr, scale, 1, (hipStream_t) stream)
+                    : exl3k_slab_copy(x, y, rows, cols, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "to_slabs") : 0;
 }
 
 }  // extern "C"
@@ -882,7 +936,7 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     if (suh && !A_had) return fail(EXL3_AMD_EINVAL, "%s: must supply A_had with suh", name);
     if (suh)
     {
-        int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, s);
+        int rc = exl3k_had128(A, A_had, m, k, 0, suh, nullptr, 1.0f, 0, s);
         if (rc) return hip_fail(rc, name);
     }
     const uint16_t* A_rot = suh ? A_had : A;

@@ -45,10 +45,13 @@ __device__ __forceinline__ void fwht8_stage(float* e, int lane)
     }
 }
 
+// slab_rows > 0 (fp16 only): y is written in k slabs, [cols / 32][slab_rows][32] (the dense recon
+// GEMM's operand layout), not row-major.
 template <bool FP32>
 __global__ __launch_bounds__(256)
 void had128_kernel(const void* __restrict__ in, void* __restrict__ out, long jobs, int cols,
-                   const uint16_t* __restrict__ pre, const uint16_t* __restrict__ post, float r_scale)
+                   const uint16_t* __restrict__ pre, const uint16_t* __restrict__ post, float r_scale,
+                   int slab_rows)
 {
     const int lane = threadIdx.x & 63;
     const int g = lane & 15;
@@ -139,16 +142,41 @@ void had128_kernel(const void* __restrict__ in, void* __restrict__ out, long job
                 #pragma unroll
                 for (int q = 0; q < 4; ++q) ow[q] = as_u32(as_h2(ow[q]) * as_h2(sw[q]));  // fp16 multiply
             }
+            const size_t oidx = slab_rows ? (size_t) (col >> 5) * slab_rows * 32 + (size_t) row * 32 + (col & 31) : idx;
             __builtin_nontemporal_store((u32x4) { ow[0], ow[1], ow[2], ow[3] },
-                                        to_global_w((u32x4*) ((uint16_t*) out + idx)));
+                                        to_global_w((u32x4*) ((uint16_t*) out + oidx)));
         }
+    }
+}
+
+// y (rows x cols fp16, k slabs [cols / 32][rows][32]) = x (row-major): thread t moves the 16 bytes
+// of columns 8 (t % 4) .. + 7 of one 32-column slab of a row
+__global__ __launch_bounds__(256)
+void slab_copy_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int rows, int cols)
+{
+    const long total = (long) rows * (cols / 8);
+    for (long t = (long) blockIdx.x * 256 + threadIdx.x; t < total; t += (long) gridDim.x * 256)
+    {
+        const long row = t / (cols / 8);
+        const int col = (int) (t - row * (cols / 8)) * 8;
+        const u32x4 v = __builtin_nontemporal_load(to_global((const u32x4*) (x + (size_t) row * cols + col)));
+        __builtin_nontemporal_store(v, to_global_w((u32x4*) (y + (size_t) (col >> 5) * rows * 32 + (size_t) row * 32 + (col & 31))));
     }
 }
 
 }  // namespace
 
+int exl3k_slab_copy(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t s)
+{
+    const long total = (long) rows * (cols / 8);
+    if (total == 0) return 0;
+    const long want = (total + 255) / 256;
+    hipLaunchKernelGGL(slab_copy_kernel, dim3((unsigned) (want < 4096 ? want : 4096)), dim3(256), 0, s, x, y, rows, cols);
+    return (int) hipGetLastError();
+}
+
 int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
-                 const uint16_t* pre, const uint16_t* post, float scale, hipStream_t s)
+                 const uint16_t* pre, const uint16_t* post, float scale, int slabs, hipStream_t s)
 {
     const float r_scale = scale * 0.088388347648f;
     const long jobs = (long) rows * (cols / 128);
@@ -156,7 +184,8 @@ int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
     // 16 chunks per workgroup per step; at most 8 workgroups per CU (grid-stride beyond)
     const long want = (jobs + 15) / 16;
     dim3 grid((unsigned) (want < 2048 ? want : 2048));
-    if (fp32) hipLaunchKernelGGL(had128_kernel<true>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale);
-    else      hipLaunchKernelGGL(had128_kernel<false>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale);
+    if (fp32) hipLaunchKernelGGL(had128_kernel<true>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale, 0);
+    else      hipLaunchKernelGGL(had128_kernel<false>, grid, dim3(256), 0, s, in, out, jobs, cols, pre, post, r_scale,
+                                 slabs ? rows : 0);
     return (int) hipGetLastError();
 }

@@ -310,7 +310,7 @@ constexpr int EXL3_MOE_SBMAX = 64;     // k-slices per workgroup of the MoE GEMV
 int exl3k_reconstruct(uint16_t* W, const uint16_t* trellis, int k, int n, int tiles_n,
                       int nt_off, int K, int cb, hipStream_t s);
 int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                         int nt_off, int K, int cb, const uint16_t* svh, hipStream_t s);
+                         int nt_off, int K, int cb, const uint16_t* svh, int slabs, hipStream_t s);
 int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* suh,
                           const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
                           int K, int cb, hipStream_t s);
@@ -323,13 +323,14 @@ int exl3k_mgemm_filter(const int64_t* indices, const uint16_t* weights, int bszm
 // reconstruct_had written transposed: WT (n, k)
 int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
                              const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
-                             int K, int cb, hipStream_t s);
+                             int K, int cb, int slabs, hipStream_t s);
 // Dense fp16 GEMM C (m, n) = A (m, k) . WT (n, k)^T, fp32 accumulation; svh non-null: output
 // rotation per 128-column chunk, x svh (exl3_dense.hip)
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                     int m, int k, int n, int variant, int cus, hipStream_t s);
+                     int m, int k, int n, int a_slabs, int w_slabs, int variant, int cus, hipStream_t s);
 int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
-                 const uint16_t* pre, const uint16_t* post, float scale, hipStream_t s);
+                 const uint16_t* pre, const uint16_t* post, float scale, int slabs, hipStream_t s);
+int exl3k_slab_copy(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t s);
 
 int exl3k_gemv_k1(const GemvArgs& g, int cb, hipStream_t s);
 int exl3k_gemv_k2(const GemvArgs& g, int cb, hipStream_t s);

@@ -120,7 +120,7 @@ void reconstruct_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ t
 template <int K, int CB>
 __global__ __launch_bounds__(256)
 void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict__ trellis,
-                          int k, int tiles_n, int nt_off, const uint16_t* __restrict__ svh)
+                          int k, int tiles_n, int nt_off, const uint16_t* __restrict__ svh, int slabs)
 {
     __shared__ __align__(16) uint32_t sh[128][32 + 4];    // [column][64 k as 32 pairs] (+pad)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -168,7 +168,11 @@ void reconstruct_t_kernel(uint16_t* __restrict__ WT, const uint16_t* __restrict_
         {
             const int row = (threadIdx.x >> 3) + 32 * i;
             const u32x4 v = *(const u32x4*) &sh[row][4 * piece];
-            *to_global_w((u32x4*) (WT + (size_t) (chunk * 128 + row) * k + blockIdx.y * 64 + 8 * piece)) = v;
+            const int kk = blockIdx.y * 64 + 8 * piece;
+            // k slabs ([k / 32][n][32], n = gridDim.x * 128) or row-major (n, k)
+            const size_t o = slabs ? (size_t) (kk >> 5) * gridDim.x * 128 * 32 + (size_t) (chunk * 128 + row) * 32 + (kk & 31)
+                                   : (size_t) (chunk * 128 + row) * k + kk;
+            *to_global_w((u32x4*) (WT + o)) = v;
         }
     }
 }
@@ -229,7 +233,7 @@ template <int K, int CB, bool TR>
 __global__ __launch_bounds__(256)
 void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict__ trellis,
                             const uint16_t* __restrict__ suh, const uint16_t* __restrict__ svh,
-                            int n, int tiles_n, int nt_off, int k)
+                            int n, int tiles_n, int nt_off, int k, int slabs)
 {
     __shared__ __align__(16) uint32_t blk[128 * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -322,7 +326,10 @@ void reconstruct_had_kernel(uint16_t* __restrict__ W, const uint16_t* __restrict
             const int R = 2 * lane;
             const uint32_t lo = b16[rh_dw(R, c >> 1) * 2 + (c & 1)];
             const uint32_t hi = b16[rh_dw(R + 1, c >> 1) * 2 + (c & 1)];
-            *(uint32_t*) (W + (size_t) (nb * 128 + c) * k + kb * 128 + R) = lo | (hi << 16);
+            const int kk = kb * 128 + R;
+            const size_t o = slabs ? (size_t) (kk >> 5) * n * 32 + (size_t) (nb * 128 + c) * 32 + (kk & 31)
+                                   : (size_t) (nb * 128 + c) * k + kk;
+            *(uint32_t*) (W + o) = lo | (hi << 16);
         }
     }
 }
@@ -338,10 +345,10 @@ int launch_reconstruct_t(uint16_t* W, const uint16_t* trellis, int k, int n, int
 
 template <int K, int CB>
 int launch_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                          int nt_off, const uint16_t* svh, hipStream_t s)
+                          int nt_off, const uint16_t* svh, int slabs, hipStream_t s)
 {
     dim3 grid(n / 128, (k / 16 + 3) / 4);
-    hipLaunchKernelGGL((reconstruct_t_kernel<K, CB>), grid, dim3(256), 0, s, WT, trellis, k, tiles_n, nt_off, svh);
+    hipLaunchKernelGGL((reconstruct_t_kernel<K, CB>), grid, dim3(256), 0, s, WT, trellis, k, tiles_n, nt_off, svh, slabs);
     return (int) hipGetLastError();
 }
 
@@ -352,18 +359,18 @@ int launch_reconstruct_had_t(uint16_t* W, const uint16_t* trellis, const uint16_
 {
     dim3 grid(n / 128, k / 128);
     hipLaunchKernelGGL((reconstruct_had_kernel<K, CB, false>), grid, dim3(256), 0, s, W, trellis, suh, svh, n, tiles_n,
-                       nt_off, k);
+                       nt_off, k, 0);
     return (int) hipGetLastError();
 }
 
 template <int K, int CB>
 int launch_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
                               const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
-                              hipStream_t s)
+                              int slabs, hipStream_t s)
 {
     dim3 grid(n / 128, k / 128);
     hipLaunchKernelGGL((reconstruct_had_kernel<K, CB, true>), grid, dim3(256), 0, s, WT, trellis, suh, svh, n, tiles_n,
-                       nt_off, k);
+                       nt_off, k, slabs);
     return (int) hipGetLastError();
 }
 
@@ -416,14 +423,14 @@ int exl3k_reconstruct_had(uint16_t* W, const uint16_t* trellis, const uint16_t* 
 }
 
 int exl3k_reconstruct_tr(uint16_t* WT, const uint16_t* trellis, int k, int n, int tiles_n,
-                         int nt_off, int K, int cb, const uint16_t* svh, hipStream_t s)
+                         int nt_off, int K, int cb, const uint16_t* svh, int slabs, hipStream_t s)
 {
-    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, svh, s)
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_tr, WT, trellis, k, n, tiles_n, nt_off, svh, slabs, s)
 }
 
 int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
                              const uint16_t* svh, int k, int n, int tiles_n, int nt_off,
-                             int K, int cb, hipStream_t s)
+                             int K, int cb, int slabs, hipStream_t s)
 {
-    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_had_tr, WT, trellis, suh, svh, k, n, tiles_n, nt_off, s)
+    EXL3_DISPATCH_K_CB(K, cb, launch_reconstruct_had_tr, WT, trellis, suh, svh, k, n, tiles_n, nt_off, slabs, s)
 }

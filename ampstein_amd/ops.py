@@ -33,6 +33,10 @@ Tensor = torch.Tensor
 # the activation rotations are HBM-bound and short): AMP_RECON_FUSED_ROWS=0 never takes the fused
 # branch (the opt-in MI355X routing).
 RECON_FUSED_ROWS = int(os.environ.get("AMP_RECON_FUSED_ROWS", "2048")) or (1 << 30)
+# The fused branch's x (the caller's, row-major) is copied into k slabs before the GEMM from this
+# many weight columns on: the copy costs ~ rows x k, the faster GEMM saves ~ rows x k x n (at
+# 2048 rows, measured: +4 % with the copy at 8192 -> 28672, -4 % at 28672 -> 8192).
+RECON_FUSED_X_SLABS_MIN_N = 16384
 
 def _ptr(t: Optional[Tensor]):
     return None if t is None else t.data_ptr()
@@ -187,23 +191,89 @@ def reconstruct_had_t(unpacked_t: Tensor, packed: Tensor, suh: Tensor, svh: Tens
             _stream(unpacked_t)))
 
 
+def _rows_k(t: Tensor) -> tuple:
+    """(rows, k) of a recon operand: 2-D row-major (rows, k), or 3-D (k / 32, rows, 32) in the k-slab
+    layout (slab c holds the 32 k from 32 c of every row)."""
+    if t.dim() == 3:
+        _need(t.size(2) == 32, "slab operand: last dimension must be 32")
+        return t.size(1), t.size(0) * 32
+    _need(t.dim() == 2, "recon operand must be 2-D (row-major) or 3-D (k slabs)")
+    return t.size(0), t.size(1)
+
+
+def slabs_of(t: Tensor) -> Tensor:
+    """The k-slab form (k / 32, rows, 32) of a row-major (rows, k) tensor (a torch copy, for tests)."""
+    return t.view(t.size(0), t.size(1) // 32, 32).transpose(0, 1).contiguous()
+
+
 def recon_mm(a: Tensor, wt: Tensor, out: Tensor, svh: Optional[Tensor] = None) -> None:
     """out (m, n) = a (m, k) @ wt (n, k)^T on the hand-written MFMA kernel (exl3_amd_recon_mm),
     fp32 accumulation, out fp16 or fp32; with svh each 128-column chunk of the fp32 result is
-    rotated (H128 / sqrt(128)) and scaled by svh before the store."""
+    rotated (H128 / sqrt(128)) and scaled by svh before the store.  a and wt may each be given in
+    the k-slab layout, (k / 32, rows, 32) (exl3_amd_recon_mm_slabs)."""
     _dtype(a, torch.half, "a")
     _dtype(wt, torch.half, "wt")
     _need(out.dtype in (torch.half, torch.float), "out is incorrect datatype, must be half or float")
-    _need(a.dim() == 2 and wt.dim() == 2 and out.dim() == 2 and a.size(1) == wt.size(1)
-          and out.shape == (a.size(0), wt.size(0)), "recon_mm: incompatible shapes")
+    (m, k), (n, kw) = _rows_k(a), _rows_k(wt)
+    _need(out.dim() == 2 and k == kw and out.shape == (m, n), "recon_mm: incompatible shapes")
     _need(a.is_contiguous() and wt.is_contiguous() and out.is_contiguous(), "recon_mm: tensors must be contiguous")
     if svh is not None:
         _dtype(svh, torch.half, "svh")
-        _need(svh.numel() >= wt.size(0), "svh too short")
+        _need(svh.numel() >= n, "svh too short")
     _cuda(a, wt, out, svh)
     with torch.cuda.device(a.device):
-        check(_lib.lib().exl3_amd_recon_mm(a.data_ptr(), wt.data_ptr(), out.data_ptr(), int(out.dtype == torch.float),
-                                           _ptr(svh), a.size(0), a.size(1), wt.size(0), _stream(a)))
+        if a.dim() == 2 and wt.dim() == 2:
+            check(_lib.lib().exl3_amd_recon_mm(a.data_ptr(), wt.data_ptr(), out.data_ptr(), int(out.dtype == torch.float),
+                                               _ptr(svh), m, k, n, _stream(a)))
+        else:
+            check(_lib.lib().exl3_amd_recon_mm_slabs(a.data_ptr(), wt.data_ptr(), out.data_ptr(),
+                                                     int(out.dtype == torch.float), _ptr(svh), m, k, n,
+                                                     int(a.dim() == 3), int(wt.dim() == 3), _stream(a)))
+
+
+def reconstruct_t_slabs(unpacked_s: Tensor, packed: Tensor, K: float, mcg: bool = False, mul1: bool = False,
+                        suh: Optional[Tensor] = None, svh: Optional[Tensor] = None, n_offset: int = 0) -> None:
+    """reconstruct_t (suh, svh None) or reconstruct_had_t (both given) written in the k-slab
+    layout: unpacked_s (k / 32, n, 32) (exl3_amd_reconstruct_t_slabs)."""
+    bits, half = bits_from_K(K)
+    _need(not half or mul1, "reconstruct: half-integer bitrates require the mul1 codebook")
+    _need(packed.dim() == 3 and unpacked_s.dim() == 3 and unpacked_s.size(2) == 32, "reconstruct_t_slabs: bad tensor ranks")
+    n, k = unpacked_s.size(1), unpacked_s.size(0) * 32
+    _need(k == packed.size(0) * 16 and n_offset >= 0 and n_offset + n <= packed.size(1) * 16,
+          "unpacked and packed shapes are incompatible")
+    _need(packed.size(2) == 16 * bits + (8 if half else 0), "packed tile size does not match K")
+    _need((suh is None) == (svh is None), "reconstruct_t_slabs: give both suh and svh or neither")
+    _dtype(unpacked_s, torch.half, "unpacked")
+    _trellis_dtype(packed, "packed")
+    if suh is not None:
+        _dtype(suh, torch.half, "suh")
+        _dtype(svh, torch.half, "svh")
+        _need(suh.numel() >= k and svh.numel() >= n, "reconstruct_t_slabs: suh / svh size")
+    if unpacked_s.numel() == 0:
+        return
+    _cuda(unpacked_s, packed, suh, svh)
+    with torch.cuda.device(unpacked_s.device):
+        check(_lib.lib().exl3_amd_reconstruct_t_slabs(
+            unpacked_s.data_ptr(), packed.data_ptr(), _ptr(suh), _ptr(svh), k, packed.size(1) * 16, n,
+            int(n_offset), float(K), int(bool(mcg)), int(bool(mul1)), int(suh is not None), _stream(unpacked_s)))
+
+
+def to_slabs(x: Tensor, y: Tensor, rotate: bool = False, pre_scale: Optional[Tensor] = None,
+             scale: float = 1.0) -> None:
+    """y (k / 32, rows, 32) = x (rows, k) in the k-slab layout, copied or rotated like had_r_128
+    (H128(x o pre_scale) * scale / sqrt(128)) on the way (exl3_amd_to_slabs)."""
+    _dtype(x, torch.half, "x")
+    _dtype(y, torch.half, "y")
+    _need(x.dim() == 2 and y.dim() == 3 and y.shape == (x.size(1) // 32, x.size(0), 32) and x.size(1) % 32 == 0,
+          "to_slabs: incompatible shapes")
+    _need(x.is_contiguous() and y.is_contiguous(), "to_slabs: tensors must be contiguous")
+    if pre_scale is not None:
+        _dtype(pre_scale, torch.half, "pre_scale")
+        _need(pre_scale.numel() >= x.size(1), "pre_scale too short")
+    _cuda(x, y, pre_scale)
+    with torch.cuda.device(x.device):
+        check(_lib.lib().exl3_amd_to_slabs(x.data_ptr(), y.data_ptr(), x.size(0), x.size(1), int(bool(rotate)),
+                                           _ptr(pre_scale), float(scale), _stream(x)))
 
 
 def had_r_128(input: Tensor, output: Tensor, pre_scale: Optional[Tensor] = None,
@@ -639,13 +709,16 @@ def _library_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
 
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
                     mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None,
-                    gemm: str = "hip") -> Tensor:
+                    gemm: str = "hip", slabs: bool = True) -> Tensor:
     """The reference's many-rows policy (amp_torch.cpp:11149-11230): reconstruct the weight to
     fp16 once, then one dense GEMM.  rows >= 2048: original-basis W and y = x @ W; otherwise
-    y = had(had(x o suh) @ W_hat) o svh.  The weight is reconstructed transposed, (n, k), and the
-    dense GEMM is this build's MFMA kernel (recon_mm), which in the rotated branch also applies
-    the output rotation and svh in its epilogue.  gemm="library" runs the same reconstructions
-    with the vendor GEMM (torch.mm) instead, for comparison."""
+    y = had(had(x o suh) @ W_hat) o svh.  The weight is reconstructed transposed, and the dense
+    GEMM is this build's MFMA kernel (recon_mm), which in the rotated branch also applies the
+    output rotation and svh in its epilogue.  With slabs (the default) the reconstructed weight
+    and the GEMM's activation operand are written in the k-slab layout, which the GEMM streams
+    faster (x itself is copied into slabs for wide weights, RECON_FUSED_X_SLABS_MIN_N); slabs=False keeps both
+    row-major (same results bit for bit).  gemm="library" runs the same reconstructions with the
+    vendor GEMM (torch.mm) instead, for comparison."""
     _need(trellis.dim() == 3, "exl3_gemm_recon: trellis must be 3-D")
     _need(gemm in ("hip", "library"), "exl3_gemm_recon: gemm must be 'hip' or 'library'")
     k, n = trellis.size(0) * 16, trellis.size(1) * 16
@@ -653,8 +726,26 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
           f"exl3_gemm_recon: incompatible shapes (x {tuple(x.shape)}, weight {k} x {n})")
     rows = x.size(0)
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    slabs = slabs and gemm == "hip" and k % 32 == 0
+    fused = rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows)
+    if slabs:
+        wt = torch.empty((k // 32, n, 32), dtype=x.dtype, device=x.device)
+        if fused:
+            reconstruct_t_slabs(wt, trellis, K, mcg, mul1, suh, svh)
+            xa = x.contiguous()
+            if n >= RECON_FUSED_X_SLABS_MIN_N:
+                xs = torch.empty((k // 32, rows, 32), dtype=x.dtype, device=x.device)
+                to_slabs(xa, xs)
+                xa = xs
+            recon_mm(xa, wt, y)
+        else:
+            xh = torch.empty((k // 32, rows, 32), dtype=x.dtype, device=x.device)
+            to_slabs(x.contiguous(), xh, True, suh, 1.0)
+            reconstruct_t_slabs(wt, trellis, K, mcg, mul1)
+            recon_mm(xh, wt, y, svh)
+        return y
     wt = torch.empty((n, k), dtype=x.dtype, device=x.device)
-    if rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows):
+    if fused:
         reconstruct_had_t(wt, trellis, suh, svh, K, mcg, mul1, 0)
         if gemm == "hip":
             recon_mm(x.contiguous(), wt, y)

@@ -295,14 +295,16 @@ def prefill_bench(torch):
     """M = 2048 fp16 x N(0,1) against 8192->28672 and 28672->8192 at 4 bpw (3INST).  Paths, all on
     this build's kernels: fused = the MFMA GEMM decoding the trellis in its loop (exl3_gemm, m > 8);
     recon = the reference's routing for rows >= 2048 (amp_torch.cpp:11149-11230): reconstruct_had_t
-    then the dense MFMA GEMM (recon_mm); recon_rotated = its rows < 2048 branch (had128 on x,
-    reconstruct_t, recon_mm with the output rotation in its epilogue); dense_gemm = recon_mm alone on
-    a reconstructed W_hat^T.  Beside them, labelled comparisons on the vendor library (torch.mm on
-    hipBLASLt / rocBLAS, tuned): the same dense GEMM and the rotated recon route around it."""
+    then the dense MFMA GEMM (recon_mm); recon_rotated = its rows < 2048 branch (x rotated, W_hat
+    reconstructed, recon_mm with the output rotation in its epilogue); both recon routes lay the
+    GEMM's operands out in k slabs.  dense_gemm = recon_mm alone on a reconstructed W_hat^T and x,
+    row-major; dense_gemm_slabs = the same operands in k slabs.  Beside them, labelled comparisons
+    on the vendor library (torch.mm on hipBLASLt / rocBLAS, tuned): the same dense GEMM and the
+    rotated recon route around it."""
     from ampstein_amd import ops
     M = 2048
     res = {}
-    mine = ("fused", "recon", "recon_rotated", "dense_gemm")
+    mine = ("fused", "recon", "recon_rotated", "dense_gemm", "dense_gemm_slabs")
     lib = ("library_dense_gemm", "library_recon_rotated")
     for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
         t, s, v = host_trellis(torch, k, n, 4, 4000 + si)
@@ -311,12 +313,14 @@ def prefill_bench(torch):
         C = torch.empty((M, n), dtype=torch.half, device="cuda")
         wt = torch.empty((n, k), dtype=torch.half, device="cuda")
         ops.reconstruct_t(wt, t, 4.0)
+        xs, wts = ops.slabs_of(x), ops.slabs_of(wt)
         flops = 2.0 * M * k * n
         row = {}
         for name, fn in (("fused", lambda: ops.exl3_gemm(x, t, C, s, ah, v)),
                          ("recon", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=2048)),
                          ("recon_rotated", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30)),
                          ("dense_gemm", lambda: ops.recon_mm(x, wt, C)),
+                         ("dense_gemm_slabs", lambda: ops.recon_mm(xs, wts, C)),
                          ("library_dense_gemm", lambda: ops._library_mm(x, wt.t(), C)),
                          ("library_recon_rotated", lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30,
                                                                              gemm="library"))):
@@ -324,7 +328,7 @@ def prefill_bench(torch):
             row[name] = {"us": round(us, 1), "TFLOPS": round(flops / us / 1e6, 1),
                          "frac_mfma_peak": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
         res[f"{k}x{n}"] = row
-        del t, s, v, x, ah, C, wt
+        del t, s, v, x, ah, C, wt, xs, wts
         torch.cuda.empty_cache()
     tot = lambda name: sum(2.0 * M * int(sh.split("x")[0]) * int(sh.split("x")[1]) for sh in res) / \
         sum(res[sh][name]["us"] for sh in res) / 1e6
@@ -336,6 +340,7 @@ def prefill_bench(torch):
             "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(best[route] / MFMA_F16_PEAK_TFLOPS, 4),
             "paths_TFLOPS": {nm: round(best[nm], 1) for nm in mine},
             "dense_gemm_frac_mfma_peak": round(best["dense_gemm"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "dense_gemm_slabs_frac_mfma_peak": round(best["dense_gemm_slabs"] / MFMA_F16_PEAK_TFLOPS, 4),
             "comparison_library_TFLOPS": {nm: round(best[nm], 1) for nm in lib},
             "per_shape": res}
 

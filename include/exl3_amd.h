@@ -361,6 +361,31 @@ int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32
 int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint16_t* svh, int k, int n_packed,
                                int n, int n_offset, float K, int mcg, int mul1, void* stream);
 
+/* The k-slab layout of a (rows, k) fp16 operand: element (r, c) at (c / 32) * rows * 32 + r * 32
+ * + c % 32, i.e. k / 32 slabs, each the 64 bytes of every row for 32 consecutive k.  One k stage
+ * of the dense GEMM is then one contiguous slab, and each of its LDS DMAs reads a contiguous
+ * kilobyte (8 whole cache lines) instead of 64 bytes of 16 rows; measured ~6 % faster per operand
+ * so laid out at 2048 x 8192 x 28672.  The three entry points below use it; none has a
+ * counterpart in the reference (the recon route, src/torch/amp_torch.cpp:11149-11230, hands
+ * row-major tensors to cuBLAS). */
+
+/* exl3_amd_recon_mm with A (a_slabs) and / or WT (w_slabs) in the k-slab layout; results bit for
+ * bit those of exl3_amd_recon_mm on the row-major operands. */
+int exl3_amd_recon_mm_slabs(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
+                            int m, int k, int n, int a_slabs, int w_slabs, void* stream);
+
+/* exl3_amd_reconstruct_t (original_basis = 0; suh, svh unused) or exl3_amd_reconstruct_had_t
+ * (original_basis = 1) writing WT (n rows of k) in the k-slab layout; k % 32 == 0. */
+int exl3_amd_reconstruct_t_slabs(uint16_t* WT, const uint16_t* trellis, const uint16_t* suh,
+                                 const uint16_t* svh, int k, int n_packed, int n, int n_offset,
+                                 float K, int mcg, int mul1, int original_basis, void* stream);
+
+/* y (rows, cols) in the k-slab layout from x row-major (fp16): a copy (rotate = 0, cols % 32 == 0)
+ * or exl3_amd_had_r_128's rotation H128(x o pre) * scale / sqrt(128) (rotate = 1, cols % 128 ==
+ * 0).  y must not overlap x. */
+int exl3_amd_to_slabs(const uint16_t* x, uint16_t* y, int rows, int cols, int rotate, const uint16_t* pre,
+                      float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,3 +148,126 @@ def test_recon_hip_matches_library(torch_cuda, orc, branch):
         ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4)
     assert rel(yh, ref) < 2e-3
     assert rel(yl, ref) < 2e-3
+
+
+# ------------------------------------------------------------------ k-slab operand layout
+@pytest.mark.parametrize("m,k,n", [(37, 96, 384), (300, 512, 640), (513, 256, 1024), (2048, 1024, 768)])
+@pytest.mark.parametrize("variant", [0, 1, 3], ids=["4waves", "8waves", "4waves-global-dma"])
+def test_recon_mm_slabs_bit_identical(torch_cuda, kernel_policy, m, k, n, variant):
+    """recon_mm on A and / or WT in the k-slab layout equals recon_mm on the row-major operands
+    bit for bit (same tiles, same k order), fp16 and fp32 output, with and without svh."""
+    torch = torch_cuda
+    from ampstein_amd import ops, _lib
+    kernel_policy(_lib.POLICY_RECON_MM, variant)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + 3 * k + n)
+    a = torch.randn((m, k), generator=g, device="cuda").half()
+    wt = (torch.randn((n, k), generator=g, device="cuda") * 0.05).half()
+    svh = (torch.randint(0, 2, (n,), generator=g, device="cuda") * 2 - 1).half()
+    a_s, wt_s = ops.slabs_of(a), ops.slabs_of(wt)
+    for dt in (torch.half, torch.float):
+        for sv in (None, svh):
+            ref = torch.full((m, n), float("nan"), dtype=dt, device="cuda")
+            ops.recon_mm(a, wt, ref, sv)
+            for aa, ww in ((a_s, wt), (a, wt_s), (a_s, wt_s)):
+                c = torch.full((m, n), float("nan"), dtype=dt, device="cuda")
+                ops.recon_mm(aa, ww, c, sv)
+                torch.cuda.synchronize()
+                assert torch.equal(c, ref), (m, k, n, dt, sv is None, aa.dim(), ww.dim())
+
+
+def test_recon_mm_slabs_half_tiles(torch_cuda):
+    """The half-tile grid (8192 -> 28672 at 2048 rows) on slab operands: bit-identical to the
+    row-major call."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    m, k, n = 2048, 8192, 28672
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    a = torch.randn((m, k), generator=g, device="cuda").half()
+    wt = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+    ref = torch.empty((m, n), dtype=torch.half, device="cuda")
+    ops.recon_mm(a, wt, ref)
+    c = torch.full((m, n), float("nan"), dtype=torch.half, device="cuda")
+    ops.recon_mm(ops.slabs_of(a), ops.slabs_of(wt), c)
+    torch.cuda.synchronize()
+    assert torch.equal(c, ref)
+
+
+@pytest.mark.parametrize("K,cb", [(4, 0), (3, 1), (2.5, 2), (8, 0)])
+@pytest.mark.parametrize("original", [False, True])
+def test_reconstruct_t_slabs_bit_exact(torch_cuda, K, cb, original):
+    """reconstruct_t_slabs equals the row-major reconstruct_t / reconstruct_had_t laid out in k
+    slabs, bit for bit, on a column slice (n_offset 128) of a wider packed tensor."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    k, n_packed, n, off = 384, 512, 256, 128
+    L = synth.layer(k, n_packed, K, cb, seed=5300 + int(10 * K) + cb + 7 * original)
+    t, s, v = L.torch()
+    ref = torch.empty((n, k), dtype=torch.half, device="cuda")
+    if original:
+        ops.reconstruct_had_t(ref, t, s, v, K, cb == 1, cb == 2, off)
+    else:
+        ops.reconstruct_t(ref, t, K, cb == 1, cb == 2, off)
+    ws = torch.full((k // 32, n, 32), float("nan"), dtype=torch.half, device="cuda")
+    ops.reconstruct_t_slabs(ws, t, K, cb == 1, cb == 2, s if original else None, v if original else None, off)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.view(torch.int16), ops.slabs_of(ref).view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 384), (2048, 1024)])
+def test_to_slabs(torch_cuda, rows, cols):
+    """to_slabs: the copy is exact; the rotation equals had_r_128 (pre scale) laid out in slabs."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows + cols)
+    x = torch.randn((rows, cols), generator=g, device="cuda").half()
+    pre = (torch.randint(0, 2, (cols,), generator=g, device="cuda") * 2 - 1).half()
+    y = torch.full((cols // 32, rows, 32), float("nan"), dtype=torch.half, device="cuda")
+    ops.to_slabs(x, y)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ops.slabs_of(x))
+    h = torch.empty_like(x)
+    ops.had_r_128(x, h, pre, None, 1.0)
+    ops.to_slabs(x, y, True, pre, 1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), ops.slabs_of(h).view(torch.int16))
+
+
+@pytest.mark.parametrize("branch", ["rotated", "fused_w"])
+def test_recon_slabs_route_bit_identical(torch_cuda, orc, branch):
+    """exl3_gemm_recon with slab operands (the default) equals the row-major route bit for bit,
+    and the fp64 linear within 2e-3."""
+    torch = torch_cuda
+    from ampstein_amd import ops
+    L = synth.layer(1024, 768, 4, 0, seed=5400)
+    x = synth.activations(300, 1024, seed=5401)
+    t, s, v = L.torch()
+    xd = torch.from_numpy(x).cuda()
+    fr = 1 if branch == "fused_w" else 1 << 30
+    ys = ops.exl3_gemm_recon(xd, t, s, v, 4.0, fused_rows=fr)
+    yr = ops.exl3_gemm_recon(xd, t, s, v, 4.0, fused_rows=fr, slabs=False)
+    torch.cuda.synchronize()
+    assert torch.equal(ys, yr)
+    if branch == "fused_w":
+        W = orc.reconstruct_had(L.trellis, L.suh, L.svh, 4).astype(np.float64)
+        ref = x.astype(np.float64) @ W
+    else:
+        ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, 4)
+    assert rel(ys.float().cpu().numpy(), ref) < 2e-3
+
+
+def test_slab_entry_points_reject(torch_cuda):
+    torch = torch_cuda
+    from ampstein_amd import _lib
+    lib = _lib.lib()
+    a = torch.zeros((4, 256), dtype=torch.half, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    p = a.data_ptr()
+    assert lib.exl3_amd_recon_mm_slabs(p, p, p, 0, None, 4, 48, 128, 1, 1, st) == _lib.EINVAL     # k % 32
+    assert lib.exl3_amd_to_slabs(p, p, 4, 256, 0, None, 1.0, st) == _lib.EINVAL                    # in place
+    assert lib.exl3_amd_to_slabs(p, p + 4096, 4, 96, 1, None, 1.0, st) == _lib.EINVAL              # rotation: cols % 128
+    assert lib.exl3_amd_to_slabs(p, p + 4096, 4, 48, 0, None, 1.0, st) == _lib.EINVAL              # copy: cols % 32
+    assert lib.exl3_amd_to_slabs(p, p + 4096, 4, 256, 0, p, 1.0, st) == _lib.EINVAL                # pre without rotation
+    assert lib.exl3_amd_reconstruct_t_slabs(p, p, None, None, 48, 128, 128, 0, 4.0, 0, 0, 0, st) == _lib.EINVAL   # k % 32
