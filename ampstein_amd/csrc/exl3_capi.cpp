@@ -835,7 +835,7 @@ static int current_cus()
 }
 
 static int recon_mm_impl(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                         int m, int k, int n, int a_slabs, int w_slabs, void* stream)
+                         int m, int k, int n, int a_slabs, int w_slabs, int ldc, void* stream)
 {
     if (m < 0 || k < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "recon_mm: negative size");
     if (k % 32) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be a multiple of 32");
@@ -844,7 +844,8 @@ static int recon_mm_impl(const uint16_t* A, const uint16_t* WT, void* C, int c_f
     if (k == 0) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be positive");
     if (!A || !WT || !C) return fail(EXL3_AMD_EINVAL, "recon_mm: null pointer");
     (void) hipGetLastError();
-    int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n, a_slabs ? 1 : 0, w_slabs ? 1 : 0,
+    if (ldc < n || ldc % 8) return fail(EXL3_AMD_EINVAL, "recon_mm: output row stride must be >= n and a multiple of 8");
+    int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n, a_slabs ? 1 : 0, w_slabs ? 1 : 0, ldc,
                               policy(EXL3_AMD_POLICY_RECON_MM), current_cus(), (hipStream_t) stream);
     return rc ? hip_fail(rc, "recon_mm") : 0;
 }
@@ -853,14 +854,14 @@ int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32
                       int m, int k, int n, void* stream)
 {
     g_last_error.clear();
-    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, 0, 0, stream);
+    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, 0, 0, n, stream);
 }
 
 int exl3_amd_recon_mm_slabs(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                            int m, int k, int n, int a_slabs, int w_slabs, void* stream)
+                            int m, int k, int n, int a_slabs, int w_slabs, int ldc, void* stream)
 {
     g_last_error.clear();
-    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, a_slabs, w_slabs, stream);
+    return recon_mm_impl(A, WT, C, c_fp32, svh, m, k, n, a_slabs, w_slabs, ldc, stream);
 }
 
 int exl3_amd_had_r_128(const void* x, void* y, int rows, int cols, int fp32,

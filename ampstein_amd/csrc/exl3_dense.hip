@@ -71,7 +71,8 @@ struct DenseOperand
 template <int D>
 __global__ __launch_bounds__(DENSE_T, 1)
 void dense_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
-                       const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int a_slabs, int w_slabs)
+                       const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int a_slabs, int w_slabs,
+                       int ldc)
 {
     constexpr int MT = 4, NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
     __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
@@ -198,7 +199,7 @@ void dense_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
             if (nb * DENSE_BN + 128 * ch >= n) continue;          // half block: chunk past n (uniform per wave)
             const f32x2 v = *(const f32x2*) (E + er * DENSE_BN + 128 * ch + 2 * lane);
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
-            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * ldc + col, lane);
         }
         __syncthreads();
     }
@@ -219,7 +220,7 @@ constexpr int DENSE4_T = 256;
 template <int D, int WN, bool BUF>
 __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT,
                                             void* __restrict__ C, const uint16_t* __restrict__ svh, int M, int k, int n,
-                                            int c_fp32, int mb, int nb, int a_slabs, int w_slabs)
+                                            int c_fp32, int mb, int nb, int a_slabs, int w_slabs, int ldc)
 {
     constexpr int NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
     constexpr int BN = 2 * WN;
@@ -387,7 +388,7 @@ __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __res
             if (nb * BN + 128 * ch >= n) continue;       // half block: chunk past n (uniform per wave)
             const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
-            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
+            if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * ldc + col, lane);
         }
         __syncthreads();
     }
@@ -410,7 +411,7 @@ template <int D, bool BUF>
 __global__ __launch_bounds__(DENSE4_T, 1)
 void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
                         const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int nfull,
-                        int a_slabs, int w_slabs)
+                        int a_slabs, int w_slabs, int ldc)
 {
     __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
     const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
@@ -434,27 +435,27 @@ void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restri
     if (b < nfull * nmb)
     {
         map(b, nfull, nb, mb);
-        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb, a_slabs, w_slabs);
+        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb, a_slabs, w_slabs, ldc);
     }
     else
     {
         const int nbn = (n + DENSE_BN - 1) / DENSE_BN;
         map(b - nfull * nmb, 2 * (nbn - nfull), nb, mb);
-        dense4_tile<D, 64, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb + 2 * nfull, a_slabs, w_slabs);
+        dense4_tile<D, 64, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb + 2 * nfull, a_slabs, w_slabs, ldc);
     }
 }
 
 }  // namespace
 
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                     int m, int k, int n, int a_slabs, int w_slabs, int variant, int cus, hipStream_t s)
+                     int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus, hipStream_t s)
 {
     const int nbn = (n + DENSE_BN - 1) / DENSE_BN, nmb = (m + DENSE_BM - 1) / DENSE_BM;
     const int blocks = nbn * nmb;
     if (variant == 1)
     {
         hipLaunchKernelGGL((dense_gemm_kernel<3>), dim3(blocks), dim3(DENSE_T), 0, s, A, WT, C, svh, m, k, n, c_fp32,
-                           a_slabs, w_slabs);
+                           a_slabs, w_slabs, ldc);
         return (int) hipGetLastError();
     }
     // half tiles for a last round at most half full: whole column blocks (n a multiple of 256),
@@ -469,9 +470,9 @@ int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32,
     const bool buf = variant != 3 && (size_t) m * k * 2 < (1ull << 32) && (size_t) n * k * 2 < (1ull << 32);
     if (buf)
         hipLaunchKernelGGL((dense_gemm4_kernel<3, true>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull,
-                           a_slabs, w_slabs);
+                           a_slabs, w_slabs, ldc);
     else
         hipLaunchKernelGGL((dense_gemm4_kernel<3, false>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull,
-                           a_slabs, w_slabs);
+                           a_slabs, w_slabs, ldc);
     return (int) hipGetLastError();
 }

@@ -216,19 +216,23 @@ def recon_mm(a: Tensor, wt: Tensor, out: Tensor, svh: Optional[Tensor] = None) -
     _need(out.dtype in (torch.half, torch.float), "out is incorrect datatype, must be half or float")
     (m, k), (n, kw) = _rows_k(a), _rows_k(wt)
     _need(out.dim() == 2 and k == kw and out.shape == (m, n), "recon_mm: incompatible shapes")
-    _need(a.is_contiguous() and wt.is_contiguous() and out.is_contiguous(), "recon_mm: tensors must be contiguous")
+    _need(a.is_contiguous() and wt.is_contiguous(), "recon_mm: tensors must be contiguous")
+    # out may be a column block of a wider row-major tensor (rows ldc elements apart)
+    _need(out.stride(1) == 1 and (m <= 1 or out.stride(0) >= n), "recon_mm: out rows must be contiguous")
+    ldc = out.stride(0) if m > 1 else n
     if svh is not None:
         _dtype(svh, torch.half, "svh")
         _need(svh.numel() >= n, "svh too short")
-    _cuda(a, wt, out, svh)
+    _cuda(a, wt, svh)
+    _need(out.is_cuda, "tensors must be on a GPU device")
     with torch.cuda.device(a.device):
-        if a.dim() == 2 and wt.dim() == 2:
+        if a.dim() == 2 and wt.dim() == 2 and ldc == n:
             check(_lib.lib().exl3_amd_recon_mm(a.data_ptr(), wt.data_ptr(), out.data_ptr(), int(out.dtype == torch.float),
                                                _ptr(svh), m, k, n, _stream(a)))
         else:
             check(_lib.lib().exl3_amd_recon_mm_slabs(a.data_ptr(), wt.data_ptr(), out.data_ptr(),
                                                      int(out.dtype == torch.float), _ptr(svh), m, k, n,
-                                                     int(a.dim() == 3), int(wt.dim() == 3), _stream(a)))
+                                                     int(a.dim() == 3), int(wt.dim() == 3), ldc, _stream(a)))
 
 
 def reconstruct_t_slabs(unpacked_s: Tensor, packed: Tensor, K: float, mcg: bool = False, mul1: bool = False,
@@ -707,6 +711,29 @@ def _library_mm(a: Tensor, b: Tensor, out: Tensor) -> None:
             tun.enable(False)
 
 
+def _recon_slabs(x: Tensor, y: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float, mcg: bool,
+                 mul1: bool, fused: bool, k: int, n: int, rows: int) -> None:
+    """exl3_gemm_recon's slab route: the x operand in k slabs (rotated, a copy, or x itself), the
+    weight reconstructed in k slabs, one recon_mm_slabs.  (Measured and not kept: the x pass on a
+    side stream beside the reconstruction, 1 % slower; the weight in 2-8 column chunks whose GEMMs
+    start on side streams as their chunks are written, 1-2 % faster at 2 chunks and up to 2x
+    slower at 4-8, where the chunks' GEMMs do not run side by side.)"""
+    if fused and n < RECON_FUSED_X_SLABS_MIN_N:
+        xa = x
+    else:
+        xa = torch.empty((k // 32, rows, 32), dtype=x.dtype, device=x.device)
+        if fused:
+            to_slabs(x, xa)
+        else:
+            to_slabs(x, xa, True, suh, 1.0)
+    wt = torch.empty((k // 32, n, 32), dtype=x.dtype, device=x.device)
+    if fused:
+        reconstruct_t_slabs(wt, trellis, K, mcg, mul1, suh, svh)
+    else:
+        reconstruct_t_slabs(wt, trellis, K, mcg, mul1)
+    recon_mm(xa, wt, y, None if fused else svh)
+
+
 def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: float,
                     mul1: bool = False, mcg: bool = False, fused_rows: Optional[int] = None,
                     gemm: str = "hip", slabs: bool = True) -> Tensor:
@@ -729,20 +756,7 @@ def exl3_gemm_recon(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, K: flo
     slabs = slabs and gemm == "hip" and k % 32 == 0
     fused = rows >= (RECON_FUSED_ROWS if fused_rows is None else fused_rows)
     if slabs:
-        wt = torch.empty((k // 32, n, 32), dtype=x.dtype, device=x.device)
-        if fused:
-            reconstruct_t_slabs(wt, trellis, K, mcg, mul1, suh, svh)
-            xa = x.contiguous()
-            if n >= RECON_FUSED_X_SLABS_MIN_N:
-                xs = torch.empty((k // 32, rows, 32), dtype=x.dtype, device=x.device)
-                to_slabs(xa, xs)
-                xa = xs
-            recon_mm(xa, wt, y)
-        else:
-            xh = torch.empty((k // 32, rows, 32), dtype=x.dtype, device=x.device)
-            to_slabs(x.contiguous(), xh, True, suh, 1.0)
-            reconstruct_t_slabs(wt, trellis, K, mcg, mul1)
-            recon_mm(xh, wt, y, svh)
+        _recon_slabs(x.contiguous(), y, trellis, suh, svh, K, mcg, mul1, fused, k, n, rows)
         return y
     wt = torch.empty((n, k), dtype=x.dtype, device=x.device)
     if fused:

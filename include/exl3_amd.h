@@ -369,10 +369,11 @@ int exl3_amd_reconstruct_t_had(uint16_t* WT, const uint16_t* trellis, const uint
  * counterpart in the reference (the recon route, src/torch/amp_torch.cpp:11149-11230, hands
  * row-major tensors to cuBLAS). */
 
-/* exl3_amd_recon_mm with A (a_slabs) and / or WT (w_slabs) in the k-slab layout; results bit for
- * bit those of exl3_amd_recon_mm on the row-major operands. */
+/* exl3_amd_recon_mm with A (a_slabs) and / or WT (w_slabs) in the k-slab layout, and C rows ldc
+ * elements apart (ldc >= n, a multiple of 8: C may be a column block of a wider output); results
+ * bit for bit those of exl3_amd_recon_mm on the row-major operands. */
 int exl3_amd_recon_mm_slabs(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                            int m, int k, int n, int a_slabs, int w_slabs, void* stream);
+                            int m, int k, int n, int a_slabs, int w_slabs, int ldc, void* stream);
 
 /* exl3_amd_reconstruct_t (original_basis = 0; suh, svh unused) or exl3_amd_reconstruct_had_t
  * (original_basis = 1) writing WT (n rows of k) in the k-slab layout; k % 32 == 0. */

@@ -236,12 +236,13 @@ def test_to_slabs(torch_cuda, rows, cols):
 
 
 @pytest.mark.parametrize("branch", ["rotated", "fused_w"])
-def test_recon_slabs_route_bit_identical(torch_cuda, orc, branch):
-    """exl3_gemm_recon with slab operands (the default) equals the row-major route bit for bit,
-    and the fp64 linear within 2e-3."""
+@pytest.mark.parametrize("n", [768, 16384])
+def test_recon_slabs_route_bit_identical(torch_cuda, orc, branch, n):
+    """exl3_gemm_recon with slab operands (the default; n = 16384: the fused branch copies x into
+    slabs) equals the row-major route bit for bit, and the fp64 linear within 2e-3."""
     torch = torch_cuda
     from ampstein_amd import ops
-    L = synth.layer(1024, 768, 4, 0, seed=5400)
+    L = synth.layer(1024, n, 4, 0, seed=5400 + n)
     x = synth.activations(300, 1024, seed=5401)
     t, s, v = L.torch()
     xd = torch.from_numpy(x).cuda()
@@ -265,7 +266,9 @@ def test_slab_entry_points_reject(torch_cuda):
     a = torch.zeros((4, 256), dtype=torch.half, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     p = a.data_ptr()
-    assert lib.exl3_amd_recon_mm_slabs(p, p, p, 0, None, 4, 48, 128, 1, 1, st) == _lib.EINVAL     # k % 32
+    assert lib.exl3_amd_recon_mm_slabs(p, p, p, 0, None, 4, 48, 128, 1, 1, 128, st) == _lib.EINVAL     # k % 32
+    assert lib.exl3_amd_recon_mm_slabs(p, p, p, 0, None, 4, 64, 128, 1, 1, 120, st) == _lib.EINVAL     # ldc < n
+    assert lib.exl3_amd_recon_mm_slabs(p, p, p, 0, None, 4, 64, 128, 1, 1, 132, st) == _lib.EINVAL     # ldc % 8
     assert lib.exl3_amd_to_slabs(p, p, 4, 256, 0, None, 1.0, st) == _lib.EINVAL                    # in place
     assert lib.exl3_amd_to_slabs(p, p + 4096, 4, 96, 1, None, 1.0, st) == _lib.EINVAL              # rotation: cols % 128
     assert lib.exl3_amd_to_slabs(p, p + 4096, 4, 48, 0, None, 1.0, st) == _lib.EINVAL              # copy: cols % 32
