@@ -562,8 +562,10 @@ def pmc_child(workload="decode"):
                  gate/up stacked mgemm, down gemm: four GEMV grids);
       gateup  -- the stacked gate/up mgemm alone, 2 x 4 launches (the traffic passes);
       prefill -- the MFMA GEMM at 2048 rows on 8192 -> 28672 and 28672 -> 8192;
-      dense   -- the recon route's dense GEMM (recon_mm, both kernel forms) and the vendor
-                 library's torch.mm on the same operands, 2048 rows, both shapes;
+      dense   -- the recon route's dense GEMM at 2048 rows, both shapes: on k-slab operands
+                 (dense_gemm4_kernel<3, true>, the route's form), on row-major operands
+                 (dense_gemm4_kernel<3, false>: the 64-bit-address DMA form, and the 8-wave
+                 dense_gemm_kernel), and the vendor library's torch.mm on the row-major operands;
       moe     -- exl3_moe_coop, 256 experts, 16 tokens, twice;
       moes    -- the token-sorted exl3_moe on the same experts, T = 512 and 2048;
       qwenm   -- the row-batched matrix-core GEMV (gemvm_kernel) on the configs[2] shapes 5120 -> 17408
@@ -608,10 +610,14 @@ def pmc_child(workload="decode"):
             x = host_normal(torch, (2048, k), 4020)
             wt = host_normal(torch, (n, k), 4021)
             C = torch.empty((2048, n), dtype=torch.half, device="cuda")
-            for var in (0, _lib.RECON_MM_8WAVES):
+            xs, wts = ops.slabs_of(x), ops.slabs_of(wt)
+            for _ in range(2):
+                ops.recon_mm(xs, wts, C)              # the route's form: k slabs, buffer DMAs
+            for var in (_lib.RECON_MM_GLOBAL_DMA, _lib.RECON_MM_8WAVES):
                 with _lib.policy(_lib.POLICY_RECON_MM, var):
                     for _ in range(2):
-                        ops.recon_mm(x, wt, C)
+                        ops.recon_mm(x, wt, C)        # row-major operands
+            del xs, wts
             for _ in range(2):
                 torch.mm(x, wt.t(), out=C)            # the vendor library's default solution
             del x, wt, C
