@@ -62,8 +62,20 @@ void had128_kernel(const void* __restrict__ in, void* __restrict__ out, long job
         const long job = base + (lane >> 4);
         const bool valid = job < jobs;
         const long jc = valid ? job : jobs - 1;
-        const long row = jc / chunks;
-        const int c = (int) (jc - row * chunks);
+        // jobs row-major over (row, chunk); for slab output chunk-major, so that the 4 consecutive
+        // rows of a wave write 4 x 64 contiguous bytes per slab
+        long row;
+        int c;
+        if (slab_rows)
+        {
+            c = (int) (jc / slab_rows);
+            row = jc - (long) c * slab_rows;
+        }
+        else
+        {
+            row = jc / chunks;
+            c = (int) (jc - row * chunks);
+        }
         const int col = c * 128 + 8 * g;
         const size_t idx = (size_t) row * cols + col;
         float e[8];
@@ -149,16 +161,23 @@ void had128_kernel(const void* __restrict__ in, void* __restrict__ out, long job
     }
 }
 
-// y (rows x cols fp16, k slabs [cols / 32][rows][32]) = x (row-major): thread t moves the 16 bytes
-// of columns 8 (t % 4) .. + 7 of one 32-column slab of a row
+// y (rows x cols fp16, k slabs [cols / 32][rows][32]) = x (row-major), with had128_kernel's slab
+// mapping: 16 threads per 128-column chunk of a row (16 contiguous bytes each: the group reads
+// 256 contiguous bytes), chunk-major over rows, so that the 4 consecutive rows of a wave write
+// 4 x 64 contiguous bytes per slab.  Tail chunks of cols % 128 columns: threads past the row end
+// do nothing.
 __global__ __launch_bounds__(256)
 void slab_copy_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int rows, int cols)
 {
-    const long total = (long) rows * (cols / 8);
+    const int chunks = (cols + 127) / 128;
+    const long total = (long) rows * chunks * 16;
     for (long t = (long) blockIdx.x * 256 + threadIdx.x; t < total; t += (long) gridDim.x * 256)
     {
-        const long row = t / (cols / 8);
-        const int col = (int) (t - row * (cols / 8)) * 8;
+        const long job = t >> 4;
+        const int c = (int) (job / rows);
+        const long row = job - (long) c * rows;
+        const int col = c * 128 + 8 * (int) (t & 15);
+        if (col >= cols) continue;
         const u32x4 v = __builtin_nontemporal_load(to_global((const u32x4*) (x + (size_t) row * cols + col)));
         __builtin_nontemporal_store(v, to_global_w((u32x4*) (y + (size_t) (col >> 5) * rows * 32 + (size_t) row * 32 + (col & 31))));
     }
@@ -168,7 +187,7 @@ void slab_copy_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, 
 
 int exl3k_slab_copy(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t s)
 {
-    const long total = (long) rows * (cols / 8);
+    const long total = (long) rows * ((cols + 127) / 128) * 16;
     if (total == 0) return 0;
     const long want = (total + 255) / 256;
     hipLaunchKernelGGL(slab_copy_kernel, dim3((unsigned) (want < 4096 ? want : 4096)), dim3(256), 0, s, x, y, rows, cols);
