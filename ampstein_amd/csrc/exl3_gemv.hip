@@ -796,6 +796,7 @@ void gemv1_kernel(const GemvArgs g)
     const int W = SB / GEMV_WAVES;
     const int a = slot * SB + wave * W;                 // first k-slice of this wave
     const int nchunks = WS < 8 ? 1 : W / 8;
+    __builtin_assume(nchunks >= 1);                     // the planner's W is 1, 2, 4 or a multiple of 8
     constexpr int per = WS;                             // slices per input chunk
     const int lane0 = WS < 8 ? (a & 7) * 8 : 0;         // x lanes of the first slice
     const int tiles_n = v.stride / 16;
