@@ -720,8 +720,8 @@ static int reconstruct_t_impl(uint16_t* WT, const uint16_t* trellis, int k, int 
 {
     int bits, half, cb;
     if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "reconstruct_t", true)) return rc;
-    if (slabs && k % 32) return fail(EXL3_AMD_EINVAL, "reconstruct_t: k must be a multiple of 32 for the slab layout");
     if (k < 0 || n < 0 || n_packed < 0) return fail(EXL3_AMD_EINVAL, "reconstruct_t: negative size");
+    if (slabs && k % 32) return fail(EXL3_AMD_EINVAL, "reconstruct_t: k must be a multiple of 32 for the slab layout");
     if (k % 16 || n_packed % 16) return fail(EXL3_AMD_EINVAL, "reconstruct_t: k and the packed width must be multiples of 16");
     if ((size_t) k * n == 0) return 0;
     if (!WT || !trellis) return fail(EXL3_AMD_EINVAL, "reconstruct_t: null pointer");
