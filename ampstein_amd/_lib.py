@@ -128,7 +128,7 @@ POLICY_GEMM_STAGING, GEMM_STAGING_REGS = 1, 1
 POLICY_MOE_GEMM, MOE_GEMM_LDS = 2, 1
 POLICY_MOE_TILE_ROWS = 3
 POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1
-POLICY_RECON_MM, RECON_MM_8WAVES, RECON_MM_WHOLE_TILES, RECON_MM_GLOBAL_DMA = 5, 1, 2, 3
+POLICY_RECON_MM, RECON_MM_8WAVES, RECON_MM_WHOLE_TILES, RECON_MM_GLOBAL_DMA, RECON_MM_NO_SPLIT = 5, 1, 2, 3, 5
 POLICY_GEMV_SPLIT, GEMV_SPLIT_BALANCED = 6, 1
 POLICY_GEMV_SLICES = 7
 POLICY_XCD_FAKE = 8

@@ -821,19 +821,6 @@ int exl3_amd_reconstruct_t_slabs(uint16_t* WT, const uint16_t* trellis, const ui
     return reconstruct_t_impl(WT, trellis, k, n_packed, n, n_offset, K, mcg, mul1, 1, stream);
 }
 
-// CU count of the current device (cached per device; 0 if unknown)
-static int current_cus()
-{
-    static std::atomic<int> cache[MAX_DEVICES];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
-    int c = cache[dev].load(std::memory_order_relaxed);
-    if (c > 0) return c;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev].store(c, std::memory_order_relaxed);
-    return c;
-}
-
 static int recon_mm_impl(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
                          int m, int k, int n, int a_slabs, int w_slabs, int ldc, void* stream)
 {
@@ -843,10 +830,13 @@ static int recon_mm_impl(const uint16_t* A, const uint16_t* WT, void* C, int c_f
     if ((size_t) m * n == 0) return 0;
     if (k == 0) return fail(EXL3_AMD_EINVAL, "recon_mm: k must be positive");
     if (!A || !WT || !C) return fail(EXL3_AMD_EINVAL, "recon_mm: null pointer");
-    (void) hipGetLastError();
     if (ldc < n || ldc % 8) return fail(EXL3_AMD_EINVAL, "recon_mm: output row stride must be >= n and a multiple of 8");
+    // the library workspace holds the split-k partial tiles
+    DeviceState* d;
+    if (int rc = current_device(&d, stream)) return rc;
     int rc = exl3k_dense_gemm(A, WT, C, c_fp32 ? 1 : 0, svh, m, k, n, a_slabs ? 1 : 0, w_slabs ? 1 : 0, ldc,
-                              policy(EXL3_AMD_POLICY_RECON_MM), current_cus(), (hipStream_t) stream);
+                              policy(EXL3_AMD_POLICY_RECON_MM), d->num_cus, d->partials, WS_PARTIAL_BYTES,
+                              (hipStream_t) stream);
     return rc ? hip_fail(rc, "recon_mm") : 0;
 }
 

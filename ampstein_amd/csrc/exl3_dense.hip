@@ -217,10 +217,15 @@ constexpr int DENSE4_T = 256;
 
 // Tile body of the four-wave form: WN = columns per wave (128: the 256 x 256 tile; 64: a 256 x 128
 // half tile, used for the last partial round of tiles), output tile (mb, nb) of 256 x 2 WN.
+//
+// k range: stages st0 .. st0 + nst - 1 (of 32 k).  part non-null (split k): the tile's fp32 sums
+// go to part (256 x 256, row-major) for the fixup kernel instead of the epilogue's rotation and
+// store.
 template <int D, int WN, bool BUF>
 __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT,
                                             void* __restrict__ C, const uint16_t* __restrict__ svh, int M, int k, int n,
-                                            int c_fp32, int mb, int nb, int a_slabs, int w_slabs, int ldc)
+                                            int c_fp32, int mb, int nb, int a_slabs, int w_slabs, int ldc,
+                                            int st0, int nst, float* __restrict__ part)
 {
     constexpr int NB = DenseLds<D>::NB, DENSE_B0 = DenseLds<D>::B0;
     constexpr int BN = 2 * WN;
@@ -230,7 +235,7 @@ __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __res
     constexpr int NDMA = 4 + NTN;                        // DMAs per stage per wave (A: 4, WT: NTN)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int NST = k / 32;
+    const int NST = nst;
 
     // wave w's DMAs fill the 1 KiB blocks q = w + 4 j (rows 16 q .. 16 q + 15) of each operand:
     // j < 4 for A (256 rows), j < NTN for WT (BN rows)
@@ -262,7 +267,7 @@ __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __res
     }
     // DMA q of a stage: A and WT blocks alternate while both last, then the rest of A
     auto issue_one = [&](int st, int q) {
-        const int c = min(st, NST - 1);                  // past the end: rewrites a buffer nobody reads
+        const int c = st0 + min(st, NST - 1);            // past the end: rewrites a buffer nobody reads
         const int buf = (st % NB) * DENSE_TILE_U32;
         const bool isb = q < 2 * NTN && (q & 1);
         const int j = q < 2 * NTN ? q >> 1 : q - NTN;
@@ -387,6 +392,11 @@ __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __res
             const int col = nb * BN + 128 * ch + 2 * lane;
             if (nb * BN + 128 * ch >= n) continue;       // half block: chunk past n (uniform per wave)
             const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
+            if (part)
+            {
+                *(f32x2*) (part + (size_t) (row - mb * DENSE_BM) * DENSE_BN + 128 * ch + 2 * lane) = v;
+                continue;
+            }
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
             if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * ldc + col, lane);
         }
@@ -411,7 +421,7 @@ template <int D, bool BUF>
 __global__ __launch_bounds__(DENSE4_T, 1)
 void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ WT, void* __restrict__ C,
                         const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int nfull,
-                        int a_slabs, int w_slabs, int ldc)
+                        int a_slabs, int w_slabs, int ldc, int splits, float* __restrict__ part)
 {
     __shared__ __align__(16) uint32_t lds[DenseLds<D>::U32];
     const int nmb = (M + DENSE_BM - 1) / DENSE_BM;
@@ -431,24 +441,64 @@ void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restri
         }
     };
     const int b = blockIdx.x;
+    const int NST = k / 32;
     int nb, mb;
-    if (b < nfull * nmb)
+    if (splits > 1)
+    {
+        // split k: workgroups S t .. S t + S - 1 take the S k ranges of tile t
+        const int t = b / splits, h = b % splits;
+        nb = t / nmb;
+        mb = t % nmb;
+        const int s0 = h * NST / splits, s1 = (h + 1) * NST / splits;
+        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb, a_slabs, w_slabs, ldc, s0, s1 - s0,
+                                 part + (size_t) b * DENSE_BM * DENSE_BN);
+    }
+    else if (b < nfull * nmb)
     {
         map(b, nfull, nb, mb);
-        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb, a_slabs, w_slabs, ldc);
+        dense4_tile<D, 128, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb, a_slabs, w_slabs, ldc, 0, NST, nullptr);
     }
     else
     {
         const int nbn = (n + DENSE_BN - 1) / DENSE_BN;
         map(b - nfull * nmb, 2 * (nbn - nfull), nb, mb);
-        dense4_tile<D, 64, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb + 2 * nfull, a_slabs, w_slabs, ldc);
+        dense4_tile<D, 64, BUF>(lds, A, WT, C, svh, M, k, n, c_fp32, mb, nb + 2 * nfull, a_slabs, w_slabs, ldc, 0, NST,
+                                nullptr);
     }
+}
+
+// Split-k fixup: tile t's S fp32 partial sums added in k order, then the epilogue's rotation and
+// store.  One wave per (row, 128-column chunk) of a tile.
+__global__ __launch_bounds__(256)
+void dense_split_fixup(const float* __restrict__ part, void* __restrict__ C, const uint16_t* __restrict__ svh, int M,
+                       int n, int ldc, int c_fp32, int nmb, int tiles, int splits)
+{
+    const int lane = threadIdx.x & 63;
+    const long job = (long) blockIdx.x * 4 + (threadIdx.x >> 6);  // (tile, row, chunk)
+    if (job >= (long) tiles * DENSE_BM * 2) return;
+    const int t = (int) (job / (DENSE_BM * 2)), rc = (int) (job % (DENSE_BM * 2));
+    const int r = rc >> 1, ch = rc & 1;
+    const int nb = t / nmb, mb = t % nmb;
+    const int row = mb * DENSE_BM + r, c0 = nb * DENSE_BN + 128 * ch;
+    if (row >= M || c0 >= n) return;
+    const float* p = part + (size_t) t * splits * DENSE_BM * DENSE_BN + (size_t) r * DENSE_BN + 128 * ch + 2 * lane;
+    float v0 = 0.0f, v1 = 0.0f;
+    for (int h = 0; h < splits; ++h)
+    {
+        const f32x2 a = __builtin_nontemporal_load((const f32x2*) (p + (size_t) h * DENSE_BM * DENSE_BN));
+        v0 += a.x;
+        v1 += a.y;
+    }
+    const bool has_svh = svh != nullptr;
+    const uint32_t svp = has_svh ? *(const uint32_t*) (svh + c0 + 2 * lane) : 0u;
+    gemm_store(v0, v1, C, c_fp32, has_svh, svp, (size_t) row * ldc + c0 + 2 * lane, lane);
 }
 
 }  // namespace
 
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                     int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus, hipStream_t s)
+                     int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus,
+                     float* part, size_t part_bytes, hipStream_t s)
 {
     const int nbn = (n + DENSE_BN - 1) / DENSE_BN, nmb = (m + DENSE_BM - 1) / DENSE_BM;
     const int blocks = nbn * nmb;
@@ -458,21 +508,38 @@ int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32,
                            a_slabs, w_slabs, ldc);
         return (int) hipGetLastError();
     }
+    // split k when the tiles fill at most half the CUs: S = as many k ranges as keep every CU
+    // busy, at least 4 stages of 32 k each, and the S fp32 partial tiles within `part`
+    int splits = 1;
+    if (variant != 5 && part && cus > 0 && 2 * blocks <= cus)
+    {
+        const long tile_bytes = (long) DENSE_BM * DENSE_BN * sizeof(float);
+        splits = min(cus / blocks, (k / 32) / 4);
+        splits = (int) min((long) splits, (long) (part_bytes / (tile_bytes * blocks)));
+        if (splits < 2) splits = 1;
+    }
     // half tiles for a last round at most half full: whole column blocks (n a multiple of 256),
     // at least one full round before it
     const int rem = cus > 0 ? blocks % cus : 0;
     int nfull = nbn;
-    if (variant != 2 && n % DENSE_BN == 0 && blocks > cus && rem > 0 && 2 * rem <= cus && rem % nmb == 0)
+    if (splits == 1 && variant != 2 && n % DENSE_BN == 0 && blocks > cus && rem > 0 && 2 * rem <= cus && rem % nmb == 0)
         nfull = nbn - rem / nmb;
-    const int grid = nfull * nmb + 2 * (nbn - nfull) * nmb;
+    const int grid = splits > 1 ? blocks * splits : nfull * nmb + 2 * (nbn - nfull) * nmb;
+    float* sp = splits > 1 ? part : nullptr;
     // buffer-resource DMAs for operands below 4 GiB (32-bit offsets and record counts)
     // (variant 3 forces the 64-bit-address form, for tests)
     const bool buf = variant != 3 && (size_t) m * k * 2 < (1ull << 32) && (size_t) n * k * 2 < (1ull << 32);
     if (buf)
         hipLaunchKernelGGL((dense_gemm4_kernel<3, true>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull,
-                           a_slabs, w_slabs, ldc);
+                           a_slabs, w_slabs, ldc, splits, sp);
     else
         hipLaunchKernelGGL((dense_gemm4_kernel<3, false>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull,
-                           a_slabs, w_slabs, ldc);
+                           a_slabs, w_slabs, ldc, splits, sp);
+    if (splits > 1)
+    {
+        const long jobs = (long) blocks * DENSE_BM * 2;
+        hipLaunchKernelGGL(dense_split_fixup, dim3((unsigned) ((jobs + 3) / 4)), dim3(256), 0, s, part, C, svh, m, n, ldc,
+                           c_fp32, nmb, blocks, splits);
+    }
     return (int) hipGetLastError();
 }

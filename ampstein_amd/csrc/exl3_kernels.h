@@ -327,7 +327,8 @@ int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16
 // Dense fp16 GEMM C (m, n) = A (m, k) . WT (n, k)^T, fp32 accumulation; svh non-null: output
 // rotation per 128-column chunk, x svh (exl3_dense.hip)
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
-                     int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus, hipStream_t s);
+                     int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus,
+                     float* part, size_t part_bytes, hipStream_t s);
 int exl3k_had128(const void* in, void* out, int rows, int cols, int fp32,
                  const uint16_t* pre, const uint16_t* post, float scale, int slabs, hipStream_t s);
 int exl3k_slab_copy(const uint16_t* x, uint16_t* y, int rows, int cols, hipStream_t s);

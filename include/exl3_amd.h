@@ -64,6 +64,8 @@ int exl3_amd_version(void);
 #define EXL3_AMD_RECON_MM_WHOLE_TILES   2   /*   four-wave form without half tiles in a last round      */
 #define EXL3_AMD_RECON_MM_GLOBAL_DMA    3   /*   four-wave form, DMAs on 64-bit lane addresses (the form
                                                  used for operands of 4 GiB and more)                   */
+#define EXL3_AMD_RECON_MM_NO_SPLIT      5   /*   four-wave form without the split k of launches whose
+                                                 tiles fill at most half the CUs                        */
 #define EXL3_AMD_POLICY_GEMV_SPLIT      6   /* work split of the single-row GEMV                       */
 #define EXL3_AMD_GEMV_SPLIT_BALANCED    1   /*   equal work per wave and waves per SIMD (gemv1b_kernel)  */
 #define EXL3_AMD_POLICY_GEMV_SLICES     7   /* single-row stream GEMV: k-slices per workgroup (0 = by the
@@ -349,7 +351,9 @@ int exl3_amd_reconstruct_had_t(uint16_t* WT, const uint16_t* trellis, const uint
  * WT (n, k) row-major; fp32 accumulation; C fp32 (c_fp32) or fp16.  svh non-null: each 128-column
  * chunk of the fp32 row is rotated (H128 / sqrt(128)) and multiplied by svh before the store (the
  * rotated branch's output rotation).  k % 32 == 0, n % 128 == 0, any m.  Hand-written MFMA kernel
- * (exl3_dense.hip).  Replaces the cuBLAS GEMM of the recon route (src/torch/amp_torch.cpp:11083-11230). */
+ * (exl3_dense.hip); launches whose 256 x 256 tiles fill at most half the CUs split k, with the
+ * partial tiles in the library workspace (the first call on a device allocates it, like the
+ * GEMV's).  Replaces the cuBLAS GEMM of the recon route (src/torch/amp_torch.cpp:11083-11230). */
 int exl3_amd_recon_mm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
                       int m, int k, int n, void* stream);
 

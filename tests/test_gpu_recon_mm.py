@@ -99,6 +99,48 @@ def test_recon_mm_half_tiles(torch_cuda, kernel_policy, case, rot):
     assert err < 2e-3, (m, k, n, rot, err)
 
 
+@pytest.mark.parametrize("m,k,n", [(16, 4096, 4096), (64, 14336, 4096), (300, 2048, 1152), (2048, 14336, 4096)])
+@pytest.mark.parametrize("out", ["fp16", "fp32"])
+@pytest.mark.parametrize("rot", [False, True])
+def test_recon_mm_split_k(torch_cuda, kernel_policy, m, k, n, out, rot):
+    """Launches whose 256 x 256 tiles fill at most half the CUs split k (partial tiles in the
+    library workspace, summed in k order by the fixup kernel, which also rotates and stores):
+    against the same GEMM without the split (policy EXL3_AMD_RECON_MM_NO_SPLIT) and against
+    torch's fp32 matmul, bar 2e-3 (fp16 out) or 1e-5 (fp32 out); n = 1152 ends on a half column
+    block.  Slab operands give the split's result bit for bit."""
+    torch = torch_cuda
+    from ampstein_amd import ops, _lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = ((m + 255) // 256) * ((n + 255) // 256)
+    assert 2 * tiles <= cus                                                  # the split applies
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + k + n + 5)
+    a = torch.randn((m, k), generator=g, device="cuda").half()
+    wt = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+    svh = (torch.randint(0, 2, (n,), generator=g, device="cuda") * 2 - 1).half() if rot else None
+    dt = torch.half if out == "fp16" else torch.float
+    ref = a.float() @ wt.float().t()
+    if rot:
+        H = torch.from_numpy(hadamard(128) / np.sqrt(128.0)).float().cuda()
+        ref = (ref.view(m, n // 128, 128) @ H).view(m, n) * svh.float()
+    ys = {}
+    for variant in (0, _lib.RECON_MM_NO_SPLIT):
+        kernel_policy(_lib.POLICY_RECON_MM, variant)
+        c = torch.full((m, n), float("nan"), dtype=dt, device="cuda")
+        ops.recon_mm(a, wt, c, svh)
+        torch.cuda.synchronize()
+        y = c.float()
+        assert torch.isfinite(y).all()
+        err = float((y - ref).abs().max() / ref.abs().max())
+        assert err < (2e-3 if out == "fp16" else 1e-5), (m, k, n, out, rot, variant, err)
+        ys[variant] = c
+    kernel_policy(_lib.POLICY_RECON_MM, 0)
+    c = torch.full((m, n), float("nan"), dtype=dt, device="cuda")
+    ops.recon_mm(ops.slabs_of(a), ops.slabs_of(wt), c, svh)
+    torch.cuda.synchronize()
+    assert torch.equal(c, ys[0])
+
+
 def test_recon_mm_rejects(torch_cuda):
     torch = torch_cuda
     from ampstein_amd import _lib
