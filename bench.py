@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--summarize-pmc", metavar="PMC_DIR", nargs="+",
                     help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
                          "directories (one per counter pass) and exit")
+    ap.add_argument("--recon-rows", action="store_true",
+                    help="print the prefill route table: fused GEMM against the recon route with and without its split k, 16..2048 rows")
     ap.add_argument("--rates", action="store_true",
                     help="print the gfx950 issue-rate microbenchmarks (ampstein_amd/csrc/exl3_probe.hip) and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -765,6 +767,33 @@ RATE_OPS = ["v_bfe_u32", "v_mad_u64_u32", "v_bitop3_b32", "v_mad_u32_u16", "v_pe
             "v_dot2_f32_f16", "v_pk_fma_f16", "v_add_u32", "v_mul_lo_u32"]
 
 
+def recon_rows():
+    """Prefill routes by row count (4 bpw 3INST, x N(0,1)): per shape and rows, us per call of the
+    fused MFMA GEMM (exl3_gemm), the recon route's rotated branch (exl3_gemm_recon: x rotation,
+    reconstruct, dense GEMM with split k when its tiles fill at most half the CUs) and the same
+    route without the split (policy EXL3_AMD_RECON_MM_NO_SPLIT).  One JSON line per shape."""
+    import torch
+    from ampstein_amd import ops, _lib
+    torch.cuda.set_device(0)
+    ops.init(0)
+    for si, (k, n) in enumerate(((4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672), (28672, 8192))):
+        t, s, v = host_trellis(torch, k, n, 4, 7000 + si)
+        row = {"shape": f"{k}x{n}", "us": "fused / recon (split k) / recon (no split)"}
+        for m in (16, 64, 128, 256, 512, 1024, 2048):
+            x = host_normal(torch, (m, k), 7100 + m)
+            C = torch.empty((m, n), dtype=torch.half, device="cuda")
+            ah = torch.empty_like(x)
+            f = timed(torch, lambda: ops.exl3_gemm(x, t, C, s, ah, v))
+            r = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30))
+            with _lib.policy(_lib.POLICY_RECON_MM, _lib.RECON_MM_NO_SPLIT):
+                r0 = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30))
+            row[str(m)] = [round(f, 1), round(r, 1), round(r0, 1)]
+        print(json.dumps(row), flush=True)
+        del t, s, v
+        torch.cuda.empty_cache()
+    return 0
+
+
 def rates():
     """Issue rates of single VALU instruction kinds (8 independent chains per lane, 4 waves per
     SIMD on every CU) and of random 16-bit LDS gathers from a 128 KiB table (one 1024-thread
@@ -855,6 +884,8 @@ def main():
     args = parse()
     if args.rates:
         return rates()
+    if args.recon_rows:
+        return recon_rows()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace)
     if args.summarize_pmc:
