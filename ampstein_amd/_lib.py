@@ -124,7 +124,7 @@ def lib():
 # Kernel-path policy keys and values (include/exl3_amd.h EXL3_AMD_POLICY_*): 0 = the library's
 # own choice; the other values select alternative paths with the same results.
 POLICY_GEMV_ROWS, GEMV_ROWS_LDS, GEMV_ROWS_MFMA_ALL = 0, 1, 2
-POLICY_GEMM_STAGING, GEMM_STAGING_REGS = 1, 1
+POLICY_GEMM_STAGING, GEMM_STAGING_REGS, GEMM_STAGING_NO_SPLIT = 1, 1, 2
 POLICY_MOE_GEMM, MOE_GEMM_LDS = 2, 1
 POLICY_MOE_TILE_ROWS = 3
 POLICY_MOE_OUTPUT, MOE_OUTPUT_ATOMIC = 4, 1

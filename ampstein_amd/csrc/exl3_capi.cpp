@@ -932,18 +932,31 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     }
     const uint16_t* A_rot = suh ? A_had : A;
     // Medium batches: the row-batched matrix-core GEMV in 16-row groups when it beats the tiled
-    // GEMM, whose 256 x 256 tiles leave most CUs idle at small m.  Measured on MI355X (K = 2..4,
-    // k x n from 4096 x 1024 to 17408 x 5120, m = 16..192): a 16-row group takes ~8 us + 0.37 ns
-    // per 1000 weights; a GEMM round (up to one tile per CU) ~28 ns per k.
+    // GEMM.  Measured on MI355X (K = 2..4, k x n from 4096 x 1024 to 17408 x 5120, m = 16..192):
+    // a 16-row group takes ~8 us + 0.37 ns per 1000 weights; a GEMM round (up to one tile per CU)
+    // ~28 ns per k; with the split k, ~27 us + 28 ns per k of a split (input rotation, the
+    // partial tiles and the fixup included).  The groups win at 16 rows, break even at 24-32.
     // force_shape_idx 1 takes the GEMV for any row count (16-row groups, each split in two
     // launches of at most 8 rows when the matrix-core GEMV is off or its plan does not fit).
+    // The tiled GEMM splits k when its tiles fill at most half the CUs (LDS-DMA form): S ranges per
+    // tile, as many as fill the CUs, at least 4 stages of 32 k each, the S fp32 partial tiles
+    // within the workspace; the fixup kernel sums them in k order and runs the epilogue.
+    const long blocks = (long) ((n + 255) / 256) * ((m + 255) / 256);
+    const int staging = policy(EXL3_AMD_POLICY_GEMM_STAGING);
+    int splits = 1;
+    if (staging == 0 && 2 * blocks <= ws->num_cus)
+    {
+        const long tile_bytes = 256L * 256 * sizeof(float);
+        long sp = std::min((long) ws->num_cus / blocks, (long) (k / 32) / 4);
+        sp = std::min(sp, (long) (ws->partial_bytes / (tile_bytes * blocks)));
+        splits = sp >= 2 ? (int) sp : 1;
+    }
     bool groups = force_shape_idx == 1;
     if (force_shape_idx == 0 && gemv_mfma_mode() != 0)
     {
-        const long blocks = (long) ((n + 255) / 256) * ((m + 255) / 256);
         const long rounds = (blocks + ws->num_cus - 1) / ws->num_cus;
         const double t_groups = ((m + 15) / 16) * (8.0 + 3.7e-7 * (double) n * k);
-        const double t_gemm = 0.028 * k * rounds;
+        const double t_gemm = splits > 1 ? 27.0 + 0.028 * k / splits : 0.028 * k * rounds;
         groups = t_groups < t_gemm;
     }
     if (groups)
@@ -961,7 +974,9 @@ int gemm_impl(const Workspace* ws, const uint16_t* A, const uint16_t* trellis, v
     gg.A_rot = A_rot;
     gg.trellis = trellis; gg.C = C; gg.svh = svh;
     gg.m = m; gg.k = k; gg.n = n; gg.c_fp32 = c_fp32 ? 1 : 0;
-    gg.reg_staging = policy(EXL3_AMD_POLICY_GEMM_STAGING) == EXL3_AMD_GEMM_STAGING_REGS;
+    gg.reg_staging = staging == EXL3_AMD_GEMM_STAGING_REGS;
+    gg.splits = splits;
+    gg.part = ws->partials;
     int rc = dispatch_gemm(bits, cb, gg, s);
     return rc ? hip_fail(rc, name) : EXL3_AMD_TAG_GEMM;
 }

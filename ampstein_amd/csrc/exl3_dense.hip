@@ -394,7 +394,8 @@ __device__ __forceinline__ void dense4_tile(uint32_t* lds, const uint16_t* __res
             const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
             if (part)
             {
-                *(f32x2*) (part + (size_t) (row - mb * DENSE_BM) * DENSE_BN + 128 * ch + 2 * lane) = v;
+                // rows past M are neither stored nor read by the fixup
+                if (row < M) *(f32x2*) (part + (size_t) (row - mb * DENSE_BM) * DENSE_BN + 128 * ch + 2 * lane) = v;
                 continue;
             }
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
@@ -467,7 +468,9 @@ void dense_gemm4_kernel(const uint16_t* __restrict__ A, const uint16_t* __restri
     }
 }
 
-// Split-k fixup: tile t's S fp32 partial sums added in k order, then the epilogue's rotation and
+// Split-k fixup (this GEMM and the fused trellis GEMM, exl3_gemm.hip, whose tiles are also 256 x
+// 256 with tile t = (column block t / nmb, row block t % nmb)): tile t's S fp32 partial sums,
+// part[(t S + h) 256 x 256], added in k order (h = 0 .. S - 1), then the epilogue's rotation and
 // store.  One wave per (row, 128-column chunk) of a tile.
 __global__ __launch_bounds__(256)
 void dense_split_fixup(const float* __restrict__ part, void* __restrict__ C, const uint16_t* __restrict__ svh, int M,
@@ -535,11 +538,15 @@ int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32,
     else
         hipLaunchKernelGGL((dense_gemm4_kernel<3, false>), dim3(grid), dim3(DENSE4_T), 0, s, A, WT, C, svh, m, k, n, c_fp32, nfull,
                            a_slabs, w_slabs, ldc, splits, sp);
-    if (splits > 1)
-    {
-        const long jobs = (long) blocks * DENSE_BM * 2;
-        hipLaunchKernelGGL(dense_split_fixup, dim3((unsigned) ((jobs + 3) / 4)), dim3(256), 0, s, part, C, svh, m, n, ldc,
-                           c_fp32, nmb, blocks, splits);
-    }
+    if (splits > 1) return exl3k_split_fixup(part, C, svh, m, n, ldc, c_fp32, nmb, blocks, splits, s);
+    return (int) hipGetLastError();
+}
+
+int exl3k_split_fixup(const float* part, void* C, const uint16_t* svh, int m, int n, int ldc, int c_fp32, int nmb,
+                      int tiles, int splits, hipStream_t s)
+{
+    const long jobs = (long) tiles * DENSE_BM * 2;
+    hipLaunchKernelGGL(dense_split_fixup, dim3((unsigned) ((jobs + 3) / 4)), dim3(256), 0, s, part, C, svh, m, n, ldc,
+                       c_fp32, nmb, tiles, splits);
     return (int) hipGetLastError();
 }

@@ -431,7 +431,8 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 template <int K, int CB>
 __global__ __launch_bounds__(GT, 1)
 void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restrict__ trellis, void* __restrict__ C,
-                     const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32)
+                     const uint16_t* __restrict__ svh, int M, int k, int n, int c_fp32, int splits,
+                     float* __restrict__ part)
 {
     using LD = DmaLds<K>;
     constexpr int RB = 256, MT = 4, TWD = tile_words(K), D = DMA_D, NB = DMA_NB;
@@ -439,11 +440,22 @@ void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restric
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = threadIdx.x;
-    const int NST = k / 32;
     const int nbn = (n + BN - 1) / BN;
     const int nmb = (M + RB - 1) / RB;
     int nb, mb;
-    if (nbn % 8 == 0)
+    // k stages st0 .. st0 + NST - 1 of this workgroup (all of k, or range h of the split)
+    int st0 = 0, NST = k / 32;
+    float* tpart = nullptr;
+    if (splits > 1)
+    {
+        const int tt = blockIdx.x / splits, h = blockIdx.x % splits;
+        nb = tt / nmb;
+        mb = tt % nmb;
+        st0 = h * (k / 32) / splits;
+        NST = (h + 1) * (k / 32) / splits - st0;
+        tpart = part + (size_t) blockIdx.x * RB * BN;
+    }
+    else if (nbn % 8 == 0)
     {
         const int x = blockIdx.x % 8, r = blockIdx.x / 8;
         nb = x + 8 * (r / nmb);
@@ -478,14 +490,14 @@ void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restric
     const size_t t_stage = (size_t) 2 * (n / 16) * TWD;
 
     auto issue_a = [&](int sa) {
-        const int c = min(sa, NST - 1);
+        const int c = st0 + min(sa, NST - 1);
         #pragma unroll
         for (int j = 0; j < 2; ++j)
             __builtin_amdgcn_global_load_lds((const void*) (a_src[j] + 4 * c),
                                              (lds_ptr_t) (lds + LD::A0 + (sa % NB) * LD::A_U32 + 256 * (wave + 8 * j)), 16, 0, 0);
     };
     auto issue_t = [&](int st) {
-        const int c = min(st, NST - 1);
+        const int c = st0 + min(st, NST - 1);
         if (tload)
             __builtin_amdgcn_global_load_lds((const void*) (t_src + c * t_stage),
                                              (lds_ptr_t) (lds + LD::T0 + (st % NB) * LD::T_U32 + 256 * wave), 16, 0, 0);
@@ -614,6 +626,12 @@ void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restric
             const f32x2 v = *(const f32x2*) (E + er * BN + 128 * ch + 2 * lane);
             const int col = nb * BN + 128 * ch + 2 * lane;
             if (nb * BN + 128 * ch >= n) continue;
+            if (tpart)
+            {
+                // rows past M are neither stored nor read by the fixup
+                if (row < M) *(f32x2*) (tpart + (size_t) (row - mb * RB) * BN + 128 * ch + 2 * lane) = v;
+                continue;
+            }
             const uint32_t svp = has_svh ? *(const uint32_t*) (svh + col) : 0u;
             if (row < M) gemm_store(v.x, v.y, C, c_fp32, has_svh, svp, (size_t) row * n + col, lane);
         }
@@ -624,12 +642,20 @@ void gemm_dma_kernel(const uint16_t* __restrict__ Ain, const uint16_t* __restric
 template <int K, int CB>
 int launch_gemm(const GemmArgs& g, hipStream_t s)
 {
-    const int blocks = ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
+    const int nmb = (g.m + BM - 1) / BM;
+    const int blocks = ((g.n + BN - 1) / BN) * nmb;
     GemmGroupArgs none;
     memset(&none, 0, sizeof(none));
+    if (!g.reg_staging && g.splits > 1)
+    {
+        hipLaunchKernelGGL((gemm_dma_kernel<K, CB>), dim3(blocks * g.splits), dim3(GT), 0, s,
+                           g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, g.splits, g.part);
+        if (int rc = (int) hipGetLastError()) return rc;
+        return exl3k_split_fixup(g.part, g.C, g.svh, g.m, g.n, g.n, g.c_fp32, nmb, blocks, g.splits, s);
+    }
     if (!g.reg_staging)
         hipLaunchKernelGGL((gemm_dma_kernel<K, CB>), dim3(blocks), dim3(GT), 0, s,
-                           g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32);
+                           g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, 1, (float*) nullptr);
     else
         hipLaunchKernelGGL((gemm_kernel<K, CB, false, BM>), dim3(blocks), dim3(GT), 0, s,
                            g.A_rot, g.trellis, g.C, g.svh, g.m, g.k, g.n, g.c_fp32, none);

@@ -142,6 +142,8 @@ struct GemmArgs
     int m, k, n;
     int c_fp32;
     int reg_staging;            // 1: register-staged operands (gemm_kernel) instead of LDS DMA
+    int splits;                 // > 1 (LDS-DMA form): k split in that many ranges per 256 x 256 tile,
+    float* part;                //   fp32 partial tiles here (splits x tiles x 256 KiB), then the fixup
 };
 
 int exl3k_gemm_k1(const GemmArgs& g, int cb, hipStream_t s);
@@ -326,6 +328,8 @@ int exl3k_reconstruct_had_tr(uint16_t* WT, const uint16_t* trellis, const uint16
                              int K, int cb, int slabs, hipStream_t s);
 // Dense fp16 GEMM C (m, n) = A (m, k) . WT (n, k)^T, fp32 accumulation; svh non-null: output
 // rotation per 128-column chunk, x svh (exl3_dense.hip)
+int exl3k_split_fixup(const float* part, void* C, const uint16_t* svh, int m, int n, int ldc, int c_fp32, int nmb,
+                      int tiles, int splits, hipStream_t s);
 int exl3k_dense_gemm(const uint16_t* A, const uint16_t* WT, void* C, int c_fp32, const uint16_t* svh,
                      int m, int k, int n, int a_slabs, int w_slabs, int ldc, int variant, int cus,
                      float* part, size_t part_bytes, hipStream_t s);

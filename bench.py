@@ -58,7 +58,7 @@ def parse():
                     help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
                          "directories (one per counter pass) and exit")
     ap.add_argument("--recon-rows", action="store_true",
-                    help="print the prefill route table: fused GEMM against the recon route with and without its split k, 16..2048 rows")
+                    help="print the route table by row count: GEMV groups, MFMA GEMM, recon route with and without its split k")
     ap.add_argument("--rates", action="store_true",
                     help="print the gfx950 issue-rate microbenchmarks (ampstein_amd/csrc/exl3_probe.hip) and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -768,26 +768,31 @@ RATE_OPS = ["v_bfe_u32", "v_mad_u64_u32", "v_bitop3_b32", "v_mad_u32_u16", "v_pe
 
 
 def recon_rows():
-    """Prefill routes by row count (4 bpw 3INST, x N(0,1)): per shape and rows, us per call of the
-    fused MFMA GEMM (exl3_gemm), the recon route's rotated branch (exl3_gemm_recon: x rotation,
-    reconstruct, dense GEMM with split k when its tiles fill at most half the CUs) and the same
-    route without the split (policy EXL3_AMD_RECON_MM_NO_SPLIT).  One JSON line per shape."""
+    """Prefill and medium-batch routes by row count (4 bpw 3INST unless noted, x N(0,1)): per shape
+    and rows, us per call of exl3_gemm as 16-row GEMV groups (force_shape_idx 1, up to 192 rows),
+    exl3_gemm on the MFMA GEMM (force 2: k split when its tiles fill at most half the CUs), the
+    recon route's rotated branch (exl3_gemm_recon: x rotation, reconstruct, dense GEMM with its own
+    split k) and the same route without the split (policy EXL3_AMD_RECON_MM_NO_SPLIT).  One JSON
+    line per shape; null where a route is not timed."""
     import torch
     from ampstein_amd import ops, _lib
     torch.cuda.set_device(0)
     ops.init(0)
-    for si, (k, n) in enumerate(((4096, 4096), (4096, 14336), (14336, 4096), (8192, 28672), (28672, 8192))):
-        t, s, v = host_trellis(torch, k, n, 4, 7000 + si)
-        row = {"shape": f"{k}x{n}", "us": "fused / recon (split k) / recon (no split)"}
-        for m in (16, 64, 128, 256, 512, 1024, 2048):
+    shapes = ((4096, 4096, 4), (4096, 14336, 4), (14336, 4096, 4), (5120, 5120, 2), (17408, 5120, 4),
+              (8192, 28672, 4), (28672, 8192, 4))
+    for si, (k, n, K) in enumerate(shapes):
+        t, s, v = host_trellis(torch, k, n, K, 7000 + si)
+        row = {"shape": f"{k}x{n}", "K": K, "us": "gemv groups / mfma gemm / recon (split k) / recon (no split)"}
+        for m in (16, 32, 64, 128, 192, 512, 2048):
             x = host_normal(torch, (m, k), 7100 + m)
             C = torch.empty((m, n), dtype=torch.half, device="cuda")
             ah = torch.empty_like(x)
-            f = timed(torch, lambda: ops.exl3_gemm(x, t, C, s, ah, v))
-            r = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30))
+            g = timed(torch, lambda: ops.exl3_gemm(x, t, C, s, ah, v, 1)) if m <= 192 else None
+            f = timed(torch, lambda: ops.exl3_gemm(x, t, C, s, ah, v, 2))
+            r = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, float(K), fused_rows=1 << 30))
             with _lib.policy(_lib.POLICY_RECON_MM, _lib.RECON_MM_NO_SPLIT):
-                r0 = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=1 << 30))
-            row[str(m)] = [round(f, 1), round(r, 1), round(r0, 1)]
+                r0 = timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, float(K), fused_rows=1 << 30))
+            row[str(m)] = [None if g is None else round(g, 1), round(f, 1), round(r, 1), round(r0, 1)]
         print(json.dumps(row), flush=True)
         del t, s, v
         torch.cuda.empty_cache()

@@ -53,6 +53,8 @@ int exl3_amd_version(void);
 #define EXL3_AMD_GEMV_ROWS_MFMA_ALL     2   /*   the matrix-core GEMV for single rows as well           */
 #define EXL3_AMD_POLICY_GEMM_STAGING    1   /* operand staging of the fused MFMA GEMM (m > 8)          */
 #define EXL3_AMD_GEMM_STAGING_REGS      1   /*   register-staged instead of LDS DMA                     */
+#define EXL3_AMD_GEMM_STAGING_NO_SPLIT  2   /*   LDS DMA without the split k of launches whose tiles
+                                                 fill at most half the CUs                              */
 #define EXL3_AMD_POLICY_MOE_GEMM        2   /* grouped GEMM of exl3_amd_moe                            */
 #define EXL3_AMD_MOE_GEMM_LDS           1   /*   the LDS-tiled kernel instead of the register decode    */
 #define EXL3_AMD_POLICY_MOE_TILE_ROWS   3   /* exl3_amd_moe row-tile height: 0 = by mean rows, else the

@@ -58,13 +58,15 @@ def test_gemm_parity_all_bitrates(torch_cuda, orc, K, cb):
 @pytest.mark.parametrize("K,cb,m,k,n", [(4, 0, 300, 512, 2048), (2, 1, 513, 1024, 384), (8, 2, 256, 256, 1024),
                                          (2.5, 2, 40, 384, 256), (3, 0, 9, 128, 128)])
 def test_gemm_dma_and_register_staging(torch_cuda, orc, kernel_policy, K, cb, m, k, n):
-    """The LDS-DMA kernel (default) and the register-staged kernel (policy EXL3_AMD_GEMM_STAGING_REGS) do the
-    same arithmetic in the same order: bit-identical outputs, both within the bar."""
+    """The LDS-DMA kernel (without the split k: policy EXL3_AMD_GEMM_STAGING_NO_SPLIT) and the
+    register-staged kernel (EXL3_AMD_GEMM_STAGING_REGS) do the same arithmetic in the same order:
+    bit-identical outputs.  The default (LDS DMA, k split where the tiles fill at most half the
+    CUs: partial tiles summed in k order by the fixup kernel) and both forms within the bar."""
     torch = torch_cuda
     L = synth.layer(k, n, K, cb, seed=900 + int(10 * K) + cb)
     x = synth.activations(m, k, seed=901 + int(10 * K))
     ys = []
-    for staging in (0, _lib.GEMM_STAGING_REGS):
+    for staging in (_lib.GEMM_STAGING_NO_SPLIT, _lib.GEMM_STAGING_REGS, 0):
         kernel_policy(_lib.POLICY_GEMM_STAGING, staging)
         tag, y, _ = run_gemm(torch, L, x, False)
         assert tag == 91
@@ -72,6 +74,25 @@ def test_gemm_dma_and_register_staging(torch_cuda, orc, kernel_policy, K, cb, m,
     assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
     assert rel_err(ys[0], ref) < TOL
+    assert rel_err(ys[2], ref) < TOL
+
+
+@pytest.mark.parametrize("K,cb,m,k,n", [(4, 0, 64, 14336, 4096), (3, 1, 200, 4096, 4096), (2.5, 2, 33, 2048, 1152),
+                                         (8, 0, 256, 4096, 8192), (4, 2, 17, 512, 256)])
+@pytest.mark.parametrize("y_fp32", [False, True])
+def test_gemm_split_k(torch_cuda, orc, kernel_policy, K, cb, m, k, n, y_fp32):
+    """The fused GEMM with its k split in S ranges per tile (force_shape_idx 2 keeps the tiled GEMM;
+    tiles filling at most half the CUs split; n = 1152 ends on a half column block, 512 x 256 has
+    too few stages to split): within the bar of the fp64 linear, as the unsplit kernel."""
+    torch = torch_cuda
+    L = synth.layer(k, n, K, cb, seed=950 + m + int(10 * K) + cb)
+    x = synth.activations(m, k, seed=951 + m)
+    ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
+    for staging in (0, _lib.GEMM_STAGING_NO_SPLIT):
+        kernel_policy(_lib.POLICY_GEMM_STAGING, staging)
+        tag, y, _ = run_gemm(torch, L, x, y_fp32, force=2)
+        assert tag == 91
+        assert rel_err(y, ref) < TOL, (staging, m, k, n)
 
 
 @pytest.mark.parametrize("m,k,n", [(9, 128, 128), (256, 512, 1024), (300, 256, 384), (513, 1024, 1024)])
@@ -87,16 +108,19 @@ def test_gemm_shapes(torch_cuda, orc, m, k, n, y_fp32):
     assert np.array_equal(A_had.view(np.uint16), orc.had128(x, pre=L.suh).view(np.uint16))
 
 
-@pytest.mark.parametrize("m,k,n,K,cb", [(9, 5120, 17408, 2, 0), (16, 17408, 5120, 4, 1), (33, 4096, 14336, 3, 2),
-                                          (64, 5120, 5120, 2.5, 2), (100, 4096, 1024, 4, 0)])
-def test_gemm_medium_batch_routing(torch_cuda, orc, m, k, n, K, cb):
-    """m > 8 with few 256-row tiles per CU: 16-row groups of the matrix-core GEMV (tag 90), the
-    rotated input still written into A_had; the same call forced onto the MFMA GEMM agrees."""
+@pytest.mark.parametrize("m,k,n,K,cb,route", [(9, 5120, 17408, 2, 0, 90), (16, 17408, 5120, 4, 1, 90),
+                                                (33, 4096, 14336, 3, 2, 91), (64, 5120, 5120, 2.5, 2, 91),
+                                                (100, 4096, 1024, 4, 0, 91)])
+def test_gemm_medium_batch_routing(torch_cuda, orc, m, k, n, K, cb, route):
+    """m > 8 with few 256-row tiles per CU: one or two 16-row groups of the matrix-core GEMV (tag
+    90) against the MFMA GEMM with its k split (tag 91, from ~32 rows), by the library's time
+    model; the rotated input written into A_had either way; the call forced onto the MFMA GEMM
+    agrees."""
     torch = torch_cuda
     L = synth.layer(k, n, K, cb, seed=650 + m + n)
     x = synth.activations(m, k, seed=651 + m)
     tag, y, A_had = run_gemm(torch, L, x, False, force=0)
-    assert tag == 90
+    assert tag == route
     assert np.array_equal(A_had.view(np.uint16), orc.had128(x, pre=L.suh).view(np.uint16))
     ref = orc.linear_f64(x, L.trellis, L.suh, L.svh, int(K), half=K != int(K), cb=cb)
     assert rel_err(y, ref) < TOL

@@ -4,8 +4,10 @@ device array) against exl3_amd_gemm through the C ABI, and both against the CPU 
 Two calls in a row on the same GPU, the second with a smaller input, so the second runs on the
 scratch the first left behind (counters re-armed, partials overwritten).  Shapes cover the M = 1
 stream kernel with a split k (the XCD hand-off after exl3_amd_init), the row-batched kernel
-(m = 5), a half rate, and the MFMA GEMM (m > 8, which uses no scratch).  A shape whose split
-partials exceed the 16 MiB scratch is refused with EXL3_AMD_EUNSUPPORTED.
+(m = 5), a half rate, the MFMA GEMM with its k split (m = 96: partial tiles in the scratch, fewer
+splits than exl3_amd_gemm's 64 MiB workspace allows, so the two agree to the bar, not bit for bit)
+and 16-row GEMV groups (m = 40).  A shape whose split partials exceed the 16 MiB scratch is
+refused with EXL3_AMD_EUNSUPPORTED.
 Bar: max relative error 2e-3 (tests/tol.py) against exl3_amd_gemm and against the fp64 linear.
 """
 import numpy as np
@@ -48,6 +50,7 @@ CASES = [
     ((5120, 5120, 4, 0, 5), (2048, 1024, 3, 0, 2)),
     ((2048, 2048, 2.5, 2, 1), (512, 512, 2.5, 2, 1)),
     ((1024, 1024, 4, 0, 40), (512, 768, 4, 0, 20)),
+    ((4096, 4096, 4, 0, 96), (1024, 1024, 4, 0, 40)),
 ]
 
 
