@@ -169,7 +169,8 @@ int exl3_amd_gemm(const uint16_t* A, const uint16_t* trellis, void* C, int c_fp3
                   void* stream);
 
 /* exl3_amd_gemm without any allocation: the same operation, arguments, kernels and error codes,
- * but the GEMV's split-k partials, completion counters and prefetch sink live in a file-scope
+ * but the GEMV's split-k partials (and the MFMA GEMM's partial tiles when it splits k, with no
+ * more splits than 16 MiB holds), completion counters and prefetch sink live in a file-scope
  * device array of the library (16 MiB of partials, 256 KiB of counters, 8 KiB sink) instead of
  * the workspace exl3_amd_gemm allocates on first use.  It calls no hipMalloc / hipFree and no
  * allocating library routine, so it serves callers that cannot allocate (code under stream
