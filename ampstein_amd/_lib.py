@@ -77,6 +77,22 @@ SIGNATURES = {
                                       _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
     "exl3_amd_gemm_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i32, _i32, _i32, _f32, _i32, _i32, _vp, _vp, _vp, _f32, _vp]),
+    "exl3_amd_gemm_res": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _i32, _i32, _i32, _f32, _i32, _i32, _vp, _vp, _vp]),
+    "exl3_amd_res_sq": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
+    "exl3_amd_norm_sq": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
+    "exl3_amd_mgemm_norm_in": (_i32, [_vp, _i32, _i32, _i32,             # h, bszm_in, m, k
+                                      _vp, _i32,                         # B table, num_B
+                                      _vp, _i32, _i32, _i32,             # C, bszm_out, n, c_fp32
+                                      _vp, _i32,                         # suh table, num_suh
+                                      _vp, ctypes.c_int64,               # A_had, numel
+                                      _vp, _i32,                         # svh table, num_svh
+                                      _vp, _vp, _i32,                    # size_n_list, c_ptrs, num_c_ptrs
+                                      _vp, _i32,                         # n_stride_list, num
+                                      _vp, _i32, _i32,                   # had_src_list, num, num_had_src
+                                      _f32, _i32, _i32,                  # K, mcg, mul1
+                                      _vp, _vp, _f32, _vp,               # sq, w, eps, r
+                                      _vp]),
     "exl3_amd_moe": (_i32, [_vp, _i32, _i32, _vp,                       # hidden, bsz, hidden_dim, output
                             _vp, _i32, _vp, _vp, _i32,                  # expert_count (+len), token/weight_sorted, n
                             _vp, _vp, _i32, _i32,                       # temp_state_g/u, concurrency, max_tokens

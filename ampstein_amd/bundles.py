@@ -58,8 +58,9 @@ class Multi:
         self.A_had = torch.zeros((len(linears), out.size(1), linears[0].in_features), dtype=torch.half, device=dev)
         self.K, self.mcg, self.mul1 = linears[0].K, linears[0].mcg, linears[0].mul1
 
-    def run(self, x: torch.Tensor) -> torch.Tensor:
-        return ops.mgemm(x, self.B, self.out, self.suh, self.A_had, self.svh, self.K, self.mcg, self.mul1)
+    def run(self, x: torch.Tensor, norm_in=None) -> torch.Tensor:
+        return ops.mgemm(x, self.B, self.out, self.suh, self.A_had, self.svh, self.K, self.mcg, self.mul1,
+                         norm_in=norm_in)
 
 
 class Sliced:
@@ -97,6 +98,7 @@ class Sliced:
         self.K, self.mcg, self.mul1 = linears[0].K, linears[0].mcg, linears[0].mul1
         self.outs = outs
 
-    def run(self, x: torch.Tensor):
-        ops.mgemm(x, self.B, self.carrier, self.suh, self.A_had, self.svh, self.K, self.mcg, self.mul1, self.opts)
+    def run(self, x: torch.Tensor, norm_in=None):
+        ops.mgemm(x, self.B, self.carrier, self.suh, self.A_had, self.svh, self.K, self.mcg, self.mul1, self.opts,
+                  norm_in=norm_in)
         return self.outs

@@ -459,7 +459,7 @@ Workspace ws_of(const DeviceState* d)
 // 3INST / MCG, XCD hand-off on.
 void plan_balanced(GemvArgs& g, const Workspace& w, int bits)
 {
-    if (g.A_up || g.norm_h || g.weights || g.indices || g.size_n || g.had_src || g.c_list || g.row0 || bits > 8)
+    if (g.A_up || g.norm_h || g.res_h || g.in_w || g.weights || g.indices || g.size_n || g.had_src || g.c_list || g.row0 || bits > 8)
         return;
     const long KS = g.k / 16, P = (long) g.bszm * (g.n / 128);
     if (P % g.xcd) return;
@@ -515,6 +515,15 @@ int launch_gemv(const Workspace& w, int bits, int cb, GemvArgs& g, hipStream_t s
     g.xg = xcd_guard(w.alarm);
     if (g.xcd && g.m == 1 && g.stream_m1 == 1 && cb != 2 && policy(EXL3_AMD_POLICY_GEMV_SPLIT) == EXL3_AMD_GEMV_SPLIT_BALANCED)
         plan_balanced(g, w, bits);
+    if (g.in_w && !(g.m == 1 && g.stream_m1 == 1 && g.k <= 64 * SQ_SCALE_MAX_PER_LANE * 128))
+    {
+        // the other kernels read a formed input: the split norm's consumer half as its own launch
+        const int rows = g.slab_m ? g.slab_m : g.m;
+        if (int rc = exl3k_norm_sq(g.A, g.in_sq, g.in_w, g.in_r, rows, g.k, g.in_eps, s)) return hip_fail(rc, what);
+        g.A = g.in_r;
+        g.in_w = nullptr;
+        g.in_sq = nullptr;
+    }
     int rc = dispatch_gemv(bits, cb, g, s);
     return rc ? hip_fail(rc, what) : 0;
 }
@@ -1020,7 +1029,7 @@ int exl3_amd_gemm_noalloc(const uint16_t* A, const uint16_t* trellis, void* C, i
                      "exl3_gemm_noalloc");
 }
 
-int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
+static int mgemm_impl(const uint16_t* A, int bszm_in, int m, int k,
                    const uint64_t* B, int num_B,
                    void* C, int bszm_out, int n, int c_fp32,
                    const uint64_t* suh, int num_suh,
@@ -1033,6 +1042,7 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
                    const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
                    const int* n_stride_list, int num_n_stride,
                    const int* had_src_list, int num_had_src_list, int num_had_src,
+                   const float* in_sq, const uint16_t* in_w, float in_eps, uint16_t* in_r,
                    void* stream)
 {
     (void) A_had; (void) force_num_sms;
@@ -1107,6 +1117,20 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         g.indices = d->filt_idx;
         if (weights) g.weights = d->filt_w;
     }
+    if (in_w)
+    {
+        // consumer half of a split residual norm: one row forms its input in the M = 1 stream
+        // kernel (launch_gemv falls back for other plans); more rows normalise into in_r first
+        if (m == 1)
+        {
+            g.in_sq = in_sq; g.in_w = in_w; g.in_eps = in_eps; g.in_r = in_r;
+        }
+        else
+        {
+            if (int rc = exl3k_norm_sq(A, in_sq, in_w, in_r, m, k, in_eps, s)) return hip_fail(rc, "exl3_mgemm_norm_in");
+            g.A = in_r;
+        }
+    }
     // more than 8 rows: the GEMV in 16-row groups (slab strides stay those of all m rows); a
     // group runs on the row-batched matrix-core kernel, or as two launches of at most 8 rows on
     // the LDS kernel (launch_gemv)
@@ -1120,6 +1144,52 @@ int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
         if (int rc = launch_gemv(ws_of(d), bits, cb, gr, s, "exl3_mgemm")) return rc;
     }
     return EXL3_AMD_TAG_GEMV;
+}
+
+int exl3_amd_mgemm(const uint16_t* A, int bszm_in, int m, int k,
+                   const uint64_t* B, int num_B,
+                   void* C, int bszm_out, int n, int c_fp32,
+                   const uint64_t* suh, int num_suh,
+                   uint16_t* A_had, int64_t a_had_numel,
+                   const uint64_t* svh, int num_svh,
+                   const int64_t* indices, int num_indices,
+                   const uint16_t* weights,
+                   float K, int force_shape_idx, int mcg, int mul1,
+                   int min_index, int max_index, int force_num_sms, int num_tokens,
+                   const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
+                   const int* n_stride_list, int num_n_stride,
+                   const int* had_src_list, int num_had_src_list, int num_had_src,
+                   void* stream)
+{
+    return mgemm_impl(A, bszm_in, m, k, B, num_B, C, bszm_out, n, c_fp32, suh, num_suh, A_had, a_had_numel, svh, num_svh,
+                      indices, num_indices, weights, K, force_shape_idx, mcg, mul1, min_index, max_index, force_num_sms,
+                      num_tokens, size_n_list, c_ptrs, num_c_ptrs, n_stride_list, num_n_stride, had_src_list,
+                      num_had_src_list, num_had_src, nullptr, nullptr, 0.0f, nullptr, stream);
+}
+
+int exl3_amd_mgemm_norm_in(const uint16_t* h, int bszm_in, int m, int k,
+                           const uint64_t* B, int num_B,
+                           void* C, int bszm_out, int n, int c_fp32,
+                           const uint64_t* suh, int num_suh,
+                           uint16_t* A_had, int64_t a_had_numel,
+                           const uint64_t* svh, int num_svh,
+                           const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
+                           const int* n_stride_list, int num_n_stride,
+                           const int* had_src_list, int num_had_src_list, int num_had_src,
+                           float K, int mcg, int mul1,
+                           const float* sq, const uint16_t* w, float eps, uint16_t* r,
+                           void* stream)
+{
+    g_last_error.clear();
+    if (!sq || !w || !r) return fail(EXL3_AMD_EINVAL, "exl3_mgemm_norm_in: null pointer");
+    if (((uintptr_t) h | (uintptr_t) sq | (uintptr_t) w | (uintptr_t) r) & 3)
+        return fail(EXL3_AMD_EINVAL, "exl3_mgemm_norm_in: h, sq, w and r must be 4-byte aligned");
+    if (bszm_in != 1) return fail(EXL3_AMD_EINVAL, "exl3_mgemm_norm_in: the input must be one slab (broadcast)");
+    if (k > 64 * SQ_SCALE_MAX_PER_LANE * 128 || m > 65535)
+        return fail(EXL3_AMD_EINVAL, "exl3_mgemm_norm_in: k above %d or more than 65535 rows", 64 * SQ_SCALE_MAX_PER_LANE * 128);
+    return mgemm_impl(h, bszm_in, m, k, B, num_B, C, bszm_out, n, c_fp32, suh, num_suh, A_had, a_had_numel, svh, num_svh,
+                      nullptr, 0, nullptr, K, -1, mcg, mul1, -1, -1, 0, 1, size_n_list, c_ptrs, num_c_ptrs,
+                      n_stride_list, num_n_stride, had_src_list, num_had_src_list, num_had_src, sq, w, eps, r, stream);
 }
 
 int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
@@ -1579,6 +1649,74 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
     if (tag < 0) return tag;
     if (int rc = exl3_amd_rms_norm_res(h, C, w, h, r, m, n, eps, stream)) return rc;
     return tag;
+}
+
+int exl3_amd_gemm_res(const uint16_t* A, const uint16_t* up, uint16_t* act, const uint16_t* trellis, uint16_t* C,
+                      const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                      int m, int k, int n, float K, int mcg, int mul1,
+                      uint16_t* h, float* sq, void* stream)
+{
+    g_last_error.clear();
+    int bits, half, cb;
+    if (int rc = parse_K(K, mcg, mul1, &bits, &half, &cb, "exl3_gemm")) return rc;
+    if (m < 1 || k < 1 || n < 1) return fail(EXL3_AMD_EINVAL, "exl3_gemm_res: sizes must be positive");
+    if (k % 16) return fail(EXL3_AMD_EINVAL, "exl3_gemm: k must be a multiple of 16");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "exl3_gemm: n must be a multiple of 128");
+    if (k % 128) return fail(EXL3_AMD_EUNSUPPORTED, "exl3_gemm: k %% 128 != 0 is not implemented in this build");
+    if (!A || !trellis || !C || !h || !sq || (up && !act)) return fail(EXL3_AMD_EINVAL, "exl3_gemm_res: null pointer");
+    if (((uintptr_t) C | (uintptr_t) h | (uintptr_t) sq) & 3)
+        return fail(EXL3_AMD_EINVAL, "exl3_gemm_res: C, h and sq must be 4-byte aligned");
+    DeviceState* d;
+    if (int rc = current_device(&d, stream)) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    if (m == 1)
+    {
+        // the residual add and the chunk sums in the epilogue of whichever GEMV kernel the plan
+        // picks (the fused SwiGLU input needs the stream kernel)
+        GemvArgs g = gemv_args_single(A, trellis, C, 0, suh, svh, m, k, n);
+        GemvArgs probe = g;
+        if (!gemv_plan(m, k, n, 1, d->num_cus, probe, WS_PARTIAL_BYTES) && (!up || probe.stream_m1 == 1))
+        {
+            g.A_up = up;
+            g.res_h = h; g.res_sq = sq;
+            int rc = launch_gemv(ws_of(d), bits, cb, g, s, "exl3_gemm_res");
+            return rc ? rc : EXL3_AMD_TAG_GEMV;
+        }
+    }
+    int tag = up ? exl3_amd_gemm_silu_mul(A, up, act, trellis, C, 0, suh, A_had, svh, m, k, n, K, mcg, mul1, stream)
+                 : exl3_amd_gemm(A, trellis, C, 0, suh, A_had, svh, m, k, n, K, mcg, mul1, 0, stream);
+    if (tag < 0) return tag;
+    if (int rc = exl3k_res_sq(h, C, sq, m, n, s)) return hip_fail(rc, "exl3_gemm_res");
+    return tag;
+}
+
+int exl3_amd_res_sq(uint16_t* h, const uint16_t* c, float* sq, int rows, int n, void* stream)
+{
+    g_last_error.clear();
+    if (rows < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "res_sq: negative size");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "res_sq: n (%d) must be a multiple of 128", n);
+    if (rows == 0 || n == 0) return 0;
+    if (!h || !sq) return fail(EXL3_AMD_EINVAL, "res_sq: null pointer");
+    if (((uintptr_t) h | (uintptr_t) c | (uintptr_t) sq) & 3) return fail(EXL3_AMD_EINVAL, "res_sq: pointers must be 4-byte aligned");
+    if (rows > 65535) return fail(EXL3_AMD_EINVAL, "res_sq: at most 65535 rows");
+    int rc = exl3k_res_sq(h, c, sq, rows, n, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "res_sq") : 0;
+}
+
+int exl3_amd_norm_sq(const uint16_t* h, const float* sq, const uint16_t* w, uint16_t* r, int rows, int n, float eps,
+                     void* stream)
+{
+    g_last_error.clear();
+    if (rows < 0 || n < 0) return fail(EXL3_AMD_EINVAL, "norm_sq: negative size");
+    if (n % 128) return fail(EXL3_AMD_EINVAL, "norm_sq: n (%d) must be a multiple of 128", n);
+    if (n > 64 * SQ_SCALE_MAX_PER_LANE * 128) return fail(EXL3_AMD_EINVAL, "norm_sq: n (%d) above %d", n, 64 * SQ_SCALE_MAX_PER_LANE * 128);
+    if (rows == 0 || n == 0) return 0;
+    if (!h || !sq || !w || !r) return fail(EXL3_AMD_EINVAL, "norm_sq: null pointer");
+    if (((uintptr_t) h | (uintptr_t) sq | (uintptr_t) w | (uintptr_t) r) & 3)
+        return fail(EXL3_AMD_EINVAL, "norm_sq: pointers must be 4-byte aligned");
+    if (rows > 65535) return fail(EXL3_AMD_EINVAL, "norm_sq: at most 65535 rows");
+    int rc = exl3k_norm_sq(h, sq, w, r, rows, n, eps, (hipStream_t) stream);
+    return rc ? hip_fail(rc, "norm_sq") : 0;
 }
 
 }  // extern "C"

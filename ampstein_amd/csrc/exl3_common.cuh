@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "exl3_kernels.h"
+
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -372,6 +374,64 @@ __device__ __forceinline__ void gemm_store(float v0, float v1, void* C, int c_fp
         f16x2 h = { (f16) v0, (f16) v1 };
         *(uint32_t*) ((uint16_t*) C + idx) = as_u32(h);
     }
+}
+
+// The decode step's residual norm split over 128-column chunks (rms_norm_res,
+// amp_kernels.cu:279-365, computed by its neighbours): the producer of a row adds its residual
+// chunk by chunk and keeps each chunk's sum of squares; the consumer of the row forms the scale
+// from those sums and normalises its input on load.  Lane l of a wave owns columns 2 l, 2 l + 1 of
+// a chunk.  Each function is the only statement of its step, so every kernel that uses it
+// produces the same bits.
+
+// Sum over the wave in every lane: xor butterfly 1, 2, .., 32 on DPP / permlane (no LDS; every
+// lane active).  One fixed order, so every caller forms the same bits.
+__device__ __forceinline__ float xor_sum64(float v, int lane)
+{
+    v += xor_partner<1>(v, lane);
+    v += xor_partner<2>(v, lane);
+    v += xor_partner<4>(v, lane);
+    v += xor_partner<8>(v, lane);
+    v += xor_partner<16>(v, lane);
+    v += xor_partner<32>(v, lane);
+    return v;
+}
+
+// y = fp16(h + c) for the lane's pair, h's pair hv already loaded from h + idx (y is stored
+// back there); returns the chunk's fp32 sum of y^2 in every lane (explicit fma per pair, then
+// xor_sum64).
+__device__ __forceinline__ float res_pair_sq(uint32_t hv, uint32_t cpair, uint16_t* h, size_t idx, int lane)
+{
+    const f16x2 a = as_h2(hv), b = as_h2(cpair);
+    const f16x2 y = { (f16) ((float) a.x + (float) b.x), (f16) ((float) a.y + (float) b.y) };
+    *to_global_w((uint32_t*) (h + idx)) = as_u32(y);
+    return xor_sum64(__builtin_fmaf((float) y.x, (float) y.x, (float) y.y * (float) y.y), lane);
+}
+
+// The row's scale 1 / sqrt(mean(y^2) + eps) from its nchunks chunk sums (nchunks <= 64 *
+// SQ_SCALE_MAX_PER_LANE, exl3_kernels.h), in two steps so that a kernel can issue the loads early
+// and reduce later: lane l loads chunks l, l + 64, ...; sq_scale adds them in that order, then
+// xor_sum64.  Uniform across the wave.
+__device__ __forceinline__ void sq_load(const float* sq, int nchunks, int lane, float (&v)[SQ_SCALE_MAX_PER_LANE])
+{
+    #pragma unroll
+    for (int i = 0; i < SQ_SCALE_MAX_PER_LANE; ++i)
+        v[i] = lane + 64 * i < nchunks ? *to_global(sq + lane + 64 * i) : 0.0f;
+}
+
+__device__ __forceinline__ float sq_scale(const float (&v)[SQ_SCALE_MAX_PER_LANE], int dim, float eps, int lane)
+{
+    float t = v[0];
+    #pragma unroll
+    for (int i = 1; i < SQ_SCALE_MAX_PER_LANE; ++i) t += v[i];
+    t = xor_sum64(t, lane);
+    return 1.0f / sqrtf(t / (float) dim + eps);
+}
+
+// The normalised pair fp16(fp16(y * scale) * w).
+__device__ __forceinline__ uint32_t norm_pair(uint32_t yv, uint32_t wv, float scale)
+{
+    const f16x2 y = as_h2(yv);
+    return as_u32((f16x2) { (f16) ((float) y.x * scale), (f16) ((float) y.y * scale) } * as_h2(wv));
 }
 
 }  // namespace exl3

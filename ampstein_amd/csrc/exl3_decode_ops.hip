@@ -89,6 +89,37 @@ void rms_norm_res_kernel(const uint16_t* x, const uint16_t* __restrict__ r, cons
     }
 }
 
+// Split residual norm, producer half on its own: one wave per (128-column chunk, row), the same
+// res_pair_sq as the GEMV epilogue's.  c null adds (-0, -0): h exactly unchanged.
+__global__ __launch_bounds__(64)
+void res_sq_kernel(uint16_t* h, const uint16_t* __restrict__ c, float* __restrict__ sq, int n)
+{
+    const int lane = threadIdx.x, chunk = blockIdx.x, row = blockIdx.y;
+    const size_t idx = (size_t) row * n + chunk * 128 + 2 * lane;
+    const uint32_t cp = c ? *to_global((const uint32_t*) (c + idx)) : 0x80008000u;
+    const float t = res_pair_sq(*to_global((const uint32_t*) (h + idx)), cp, h, idx, lane);
+    if (lane == 0) sq[(size_t) row * (n / 128) + chunk] = t;
+}
+
+// Consumer half on its own: r = norm_pair(h, w, scale); every wave forms the row's scale with
+// sq_scale, as the M = 1 stream kernel's waves do.  Grid (n / 512, rows), 4 waves of one chunk.
+__global__ __launch_bounds__(256)
+void norm_sq_kernel(const uint16_t* __restrict__ h, const float* __restrict__ sq, const uint16_t* __restrict__ w,
+                    uint16_t* __restrict__ r, int n, float eps)
+{
+    const int lane = threadIdx.x & 63, row = blockIdx.y;
+    const int chunk = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nch = n / 128;
+    float sv[SQ_SCALE_MAX_PER_LANE];
+    sq_load(sq + (size_t) row * nch, nch, lane, sv);
+    const float scale = sq_scale(sv, n, eps, lane);
+    if (chunk >= nch) return;
+    const int col = chunk * 128 + 2 * lane;
+    const uint32_t yv = *to_global((const uint32_t*) (h + (size_t) row * n + col));
+    const uint32_t wv = *to_global((const uint32_t*) (w + col));
+    *to_global_w((uint32_t*) (r + (size_t) row * n + col)) = norm_pair(yv, wv, scale);
+}
+
 __global__ __launch_bounds__(256)
 void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ out, long n)
 {
@@ -115,5 +146,19 @@ int exl3k_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long n, 
     long grid = (n + 255) / 256;
     if (grid > 2048) grid = 2048;
     hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned) grid), dim3(256), 0, s, g, u, out, n);
+    return (int) hipGetLastError();
+}
+
+int exl3k_res_sq(uint16_t* h, const uint16_t* c, float* sq, long rows, int n, hipStream_t s)
+{
+    hipLaunchKernelGGL(res_sq_kernel, dim3((unsigned) (n / 128), (unsigned) rows), dim3(64), 0, s, h, c, sq, n);
+    return (int) hipGetLastError();
+}
+
+int exl3k_norm_sq(const uint16_t* h, const float* sq, const uint16_t* w, uint16_t* r, long rows, int n, float eps,
+                  hipStream_t s)
+{
+    hipLaunchKernelGGL(norm_sq_kernel, dim3((unsigned) ((n / 128 + 3) / 4), (unsigned) rows), dim3(256), 0, s,
+                       h, sq, w, r, n, eps);
     return (int) hipGetLastError();
 }

@@ -190,7 +190,7 @@ __device__ __forceinline__ void rotate_chunks(const uint16_t* __restrict__ A, co
 // Half output: had_fh_r_128_inner (hadamard_inner.cuh:216-281); float output: had_ff.
 // `scale` is 1/sqrt(128), times the routing weight in weighted mode.
 // svp: this lane's svh pair (svh[col], svh[col + 1]), loaded ahead by the caller.
-__device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_fp32, bool has_svh, uint32_t svp,
+__device__ __forceinline__ uint32_t store_output(float v0, float v1, void* C, int c_fp32, bool has_svh, uint32_t svp,
                                              size_t idx, int lane, float scale)
 {
     if (has_svh)
@@ -204,7 +204,7 @@ __device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_
             f16x2 h = { (f16) v0, (f16) v1 };
             h = h * s;
             *to_global_w((uint32_t*) ((uint16_t*) C + idx)) = as_u32(h);
-            return;
+            return as_u32(h);
         }
         v0 *= (float) s.x;
         v1 *= (float) s.y;
@@ -213,12 +213,27 @@ __device__ __forceinline__ void store_output(float v0, float v1, void* C, int c_
     {
         f32x2 o = { v0, v1 };
         *to_global_w((f32x2*) ((float*) C + idx)) = o;
+        return 0u;
     }
     else
     {
         f16x2 h = { (f16) v0, (f16) v1 };
         *to_global_w((uint32_t*) ((uint16_t*) C + idx)) = as_u32(h);
+        return as_u32(h);
     }
+}
+
+// Producer of a split residual norm (res_h non-null): fold the lane's stored fp16 output pair of
+// row `row` into the residual stream and store the chunk's sum of squares.  Wave-level.
+// hpre: the lane's h pair when the caller loaded it ahead (has_pre), else loaded here.
+__device__ __forceinline__ void res_store(const GemvArgs& g, int row, int chunk, int lane, uint32_t cpair,
+                                          bool has_pre = false, uint32_t hpre = 0u)
+{
+    if (!g.res_h) return;
+    const size_t idx = (size_t) row * g.n + chunk * 128 + 2 * lane;
+    const uint32_t hv = has_pre ? hpre : *to_global((const uint32_t*) (g.res_h + idx));
+    const float t = res_pair_sq(hv, cpair, g.res_h, idx, lane);
+    if (lane == 0) *to_global_w(g.res_sq + (size_t) row * (g.n / 128) + chunk) = t;
 }
 
 __device__ __forceinline__ float wave_sum(float v, int lane)
@@ -375,7 +390,8 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
                 s1 += tmp[(q * pairs + r * 64 + lane) * 2 + 1];
             }
             const int col = chunk * 128 + 2 * lane;
-            store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale);
+            res_store(g, r, chunk, lane,
+                      store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale));
         }
     }
     else
@@ -383,8 +399,9 @@ __device__ void block_epilogue(const GemvArgs& g, const MatView& v, int j, int c
         for (int r = wave; r < m; r += GEMV_WAVES)
         {
             const int col = chunk * 128 + 2 * lane;
-            store_output(res[r * rs + 2 * lane], res[r * rs + 2 * lane + 1], v.C, g.c_fp32, v.svh != nullptr,
-                         svp, (size_t) r * v.stride + col, lane, v.scale);
+            res_store(g, r, chunk, lane,
+                      store_output(res[r * rs + 2 * lane], res[r * rs + 2 * lane + 1], v.C, g.c_fp32, v.svh != nullptr,
+                                   svp, (size_t) r * v.stride + col, lane, v.scale));
         }
     }
     if (g.weights && g.xcd)
@@ -485,13 +502,14 @@ __device__ __forceinline__ void norm_arrive(const GemvArgs& g, const uint16_t* C
 // arrival, sum the slots in order, rotate and store.  Wave-level only: the workgroup's other
 // waves have ended.
 __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int chunk, int slot, int splits,
-                               float v0, float v1, uint32_t svp)
+                               float v0, float v1, uint32_t svp, uint32_t hpre)
 {
     const int lane = threadIdx.x & 63;
     const int col = chunk * 128 + 2 * lane;
     if (splits == 1)
     {
-        store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+        res_store(g, 0, chunk, lane, store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale),
+                  true, hpre);
         if (g.norm_h) norm_arrive(g, (const uint16_t*) v.C);
         return;
     }
@@ -516,7 +534,8 @@ __device__ void finish_m1_wave(const GemvArgs& g, const MatView& v, int j, int c
         for (int u = 0; u < 16; ++u)
             if (p0 + u < splits) { s0 += vv[u].x; s1 += vv[u].y; }
     }
-    store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale);
+    res_store(g, 0, chunk, lane, store_output(s0, s1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) col, lane, v.scale),
+              true, hpre);
     if (g.norm_h) norm_arrive(g, (const uint16_t*) v.C);
 }
 
@@ -717,7 +736,8 @@ void gemv_finish(const GemvArgs g, int splits)
         }
         const int col = chunk * 128 + c;
         const uint32_t svp = v.svh ? *to_global((const uint32_t*) (v.svh + col)) : 0u;
-        store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale);
+        res_store(g, r, chunk, lane,
+                  store_output(v0, v1, v.C, g.c_fp32, v.svh != nullptr, svp, (size_t) r * v.stride + col, lane, v.scale));
     }
 }
 
@@ -749,7 +769,7 @@ __device__ __forceinline__ uint32_t rotate_pair(uint32_t xv, uint32_t sv, bool h
     return as_u32(o);
 }
 
-// Fused SwiGLU input (ACT): the pair of silu(gate) * up, rounded to fp16 as silu_mul does.
+// Fused SwiGLU input (IN = GEMV_IN_SILU): the pair of silu(gate) * up, rounded to fp16 as silu_mul does.
 __device__ __forceinline__ uint32_t silu_mul_pair(uint32_t gv, uint32_t uv)
 {
     const f16x2 gh = as_h2(gv), uh = as_h2(uv);
@@ -757,8 +777,17 @@ __device__ __forceinline__ uint32_t silu_mul_pair(uint32_t gv, uint32_t uv)
     return as_u32(o);
 }
 
-template <int K, int CB, int WS, bool ACT>
+// Input forms (IN): 0 the input itself; 1 the fused SwiGLU pair (A = gate, A_up = up); 2 the
+// consumer half of a split residual norm (A = the residual stream h, norm weights in_w, chunk
+// sums of squares in_sq): every wave forms the scale itself, from the same sums in the same order.
+enum { GEMV_IN_PLAIN = 0, GEMV_IN_SILU = 1, GEMV_IN_NORM = 2 };
+
+template <int K, int CB, int WS, int IN>
 __global__ __launch_bounds__(GEMV_THREADS)
+// the split-norm input form asks for 4 waves per SIMD (at most 128 registers: left alone it takes
+// 109 VGPRs + 24 AGPRs and runs 3 waves per SIMD, 21 -> 24 us on the stacked gate / up launch);
+// the other forms keep their own allocation
+__attribute__((amdgpu_waves_per_eu(IN == 2 ? 4 : 1)))
 void gemv1_kernel(const GemvArgs g)
 {
     __shared__ __align__(16) float red[GEMV_WAVES][128];
@@ -809,7 +838,8 @@ void gemv1_kernel(const GemvArgs g)
     const bool has_suh = v.suh != nullptr;
     const uint32_t* xg = (const uint32_t*) v.A + lane;                       // x pairs
     const uint32_t* sg = (const uint32_t*) (has_suh ? v.suh : v.A) + lane;   // suh pairs
-    const uint32_t* ug = (const uint32_t*) (ACT ? g.A_up : v.A) + lane;      // up pairs (fused SwiGLU)
+    // up pairs (fused SwiGLU) or norm weight pairs (split norm)
+    const uint32_t* ug = (const uint32_t*) (IN == GEMV_IN_SILU ? g.A_up : IN == GEMV_IN_NORM ? g.in_w : v.A) + lane;
 
     constexpr int PF = EXL3_GEMV_PF;
     static_assert(8 % PF == 0, "prefetch depth must divide 8");
@@ -821,7 +851,10 @@ void gemv1_kernel(const GemvArgs g)
     uint32_t xv = *(to_global(xg) + (size_t) (a / 8) * 64);
     uint32_t sv = *(to_global(sg) + (size_t) (a / 8) * 64);
     uint32_t uv = 0u;
-    if constexpr (ACT) uv = *(to_global(ug) + (size_t) (a / 8) * 64);
+    if constexpr (IN != GEMV_IN_PLAIN) uv = *(to_global(ug) + (size_t) (a / 8) * 64);
+    // split norm: the chunk sums with the inputs; the scale is formed once the weights are in flight
+    float sqv[SQ_SCALE_MAX_PER_LANE];
+    if constexpr (IN == GEMV_IN_NORM) sq_load(g.in_sq, g.k / 128, lane, sqv);
     // keep them ahead of the weight loads: loads return in issue order, so an input load the
     // scheduler moved behind the ring would wait for the ring's slices
     __builtin_amdgcn_sched_barrier(0);
@@ -831,6 +864,10 @@ void gemv1_kernel(const GemvArgs g)
     // svh pair for the epilogue, behind the first weights
     // (unconditional load: without svh it reads the input, k >= 128, and is unused)
     const uint32_t svp = *to_global((const uint32_t*) ((v.svh ? v.svh + chunk * 128 : v.A) + 2 * lane));
+    // the residual pair for a split norm's producer epilogue (unconditional as svp)
+    const uint32_t hpre = *to_global((const uint32_t*) ((g.res_h ? g.res_h + chunk * 128 : v.A) + 2 * lane));
+    float nscale = 0.0f;
+    if constexpr (IN == GEMV_IN_NORM) nscale = sq_scale(sqv, g.k, g.in_eps, lane);
 
     float sx = 0.0f;
     // Dot products on the matrix pipe, v_mfma_f32_16x16x32_f16: lane l's A operand is 4 k rows
@@ -847,7 +884,8 @@ void gemv1_kernel(const GemvArgs g)
     f32x4 accv[4] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
     for (int c = 0; c < nchunks; ++c)
     {
-        const uint32_t xr = rotate_pair(ACT ? silu_mul_pair(xv, uv) : xv, sv, has_suh, lane);
+        const uint32_t xi = IN == GEMV_IN_SILU ? silu_mul_pair(xv, uv) : IN == GEMV_IN_NORM ? norm_pair(xv, uv, nscale) : xv;
+        const uint32_t xr = rotate_pair(xi, sv, has_suh, lane);
         if (c == 0) GEMV_STAMP(g, 1, __builtin_amdgcn_readfirstlane(xr));
         if (c == 0) __builtin_amdgcn_s_setprio(0);
         if (CB == 2)
@@ -871,7 +909,7 @@ void gemv1_kernel(const GemvArgs g)
         const int cn = min(c + 1, nchunks - 1);
         xv = *(to_global(xg) + (size_t) (a / 8 + cn) * 64);
         sv = *(to_global(sg) + (size_t) (a / 8 + cn) * 64);
-        if constexpr (ACT) uv = *(to_global(ug) + (size_t) (a / 8 + cn) * 64);
+        if constexpr (IN != GEMV_IN_PLAIN) uv = *(to_global(ug) + (size_t) (a / 8 + cn) * 64);
         #pragma unroll
         for (int s8 = 0; s8 < per; ++s8)
         {
@@ -942,7 +980,7 @@ void gemv1_kernel(const GemvArgs g)
             v0 = v0 * kinv + bias;
             v1 = v1 * kinv + bias;
         }
-        finish_m1_wave(g, v, j, chunk, slot, splits, v0, v1, svp);
+        finish_m1_wave(g, v, j, chunk, slot, splits, v0, v1, svp, hpre);
         GEMV_STAMP(g, 3, 0);
         return;
     }
@@ -1417,23 +1455,23 @@ int launch_gemv_t(const GemvArgs& g, hipStream_t s)
     });
 }
 
+template <int K, int CB, int IN>
+void launch_gemv1_in(const GemvArgs& g, hipStream_t s, dim3 grid)
+{
+    const int W = g.slices_per_block / GEMV_WAVES;
+    if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1, IN>), grid, dim3(GEMV_THREADS), 0, s, g);
+    else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2, IN>), grid, dim3(GEMV_THREADS), 0, s, g);
+    else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4, IN>), grid, dim3(GEMV_THREADS), 0, s, g);
+    else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8, IN>), grid, dim3(GEMV_THREADS), 0, s, g);
+}
+
 template <int K, int CB>
 int launch_gemv1(const GemvArgs& g, hipStream_t s)
 {
-    const int W = g.slices_per_block / GEMV_WAVES;
     return launch_common(g, s, [&](dim3 grid) {
-        if (g.A_up)
-        {
-            if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1, true>), grid, dim3(GEMV_THREADS), 0, s, g);
-            else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2, true>), grid, dim3(GEMV_THREADS), 0, s, g);
-            else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4, true>), grid, dim3(GEMV_THREADS), 0, s, g);
-            else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8, true>), grid, dim3(GEMV_THREADS), 0, s, g);
-            return;
-        }
-        if (W == 1) hipLaunchKernelGGL((gemv1_kernel<K, CB, 1, false>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else if (W == 2) hipLaunchKernelGGL((gemv1_kernel<K, CB, 2, false>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else if (W == 4) hipLaunchKernelGGL((gemv1_kernel<K, CB, 4, false>), grid, dim3(GEMV_THREADS), 0, s, g);
-        else hipLaunchKernelGGL((gemv1_kernel<K, CB, 8, false>), grid, dim3(GEMV_THREADS), 0, s, g);
+        if (g.A_up) launch_gemv1_in<K, CB, GEMV_IN_SILU>(g, s, grid);
+        else if (g.in_w) launch_gemv1_in<K, CB, GEMV_IN_NORM>(g, s, grid);
+        else launch_gemv1_in<K, CB, GEMV_IN_PLAIN>(g, s, grid);
     });
 }
 
@@ -1460,7 +1498,7 @@ int launch_gemv_m(const GemvArgs& g, hipStream_t s)
         }
     }
     if (g.m == 1 && g.stream_m1) return launch_gemv1<K, CB>(g, s);
-    if (g.A_up) return -1;             // the fused SwiGLU input exists in the M = 1 stream kernel only
+    if (g.A_up || g.in_w) return -1;   // the fused input forms exist in the M = 1 stream kernel only
     if (g.mfma_rows)
     {
         if (g.m == 1) return launch_gemvm_t<K, CB, 1>(g, s);

@@ -95,6 +95,16 @@ struct GemvArgs
     uint16_t* norm_r;
     int* norm_ctr;              // workspace counter on its own 128-byte line, zero between calls
     float norm_eps;
+    // non-null res_h (producer of a split residual norm): after C is stored, res_h = fp16(res_h + C)
+    // and res_sq[row * (n / 128) + chunk] = that chunk's fp32 sum of squares (single matrix, fp16 C)
+    uint16_t* res_h;
+    float* res_sq;
+    // non-null in_w (consumer of a split residual norm; M = 1 stream kernel, k <= 32768): the
+    // input is fp16(fp16(A * scale) * in_w), scale = 1 / sqrt(sum(in_sq[0 .. k/128)) / k + in_eps)
+    const float* in_sq;
+    const uint16_t* in_w;
+    float in_eps;
+    uint16_t* in_r;             // (m, k) scratch for the other kernels: the normalised input is formed there first
     const uint16_t* trellis;    // (k/16, n/16, 16K) uint16 (single matrix)
     void* C;                    // (bszm, m, n) fp16 or fp32
     const uint16_t* suh;        // (k) fp16 or null (single matrix)
@@ -255,6 +265,15 @@ struct MoesGatherArgs
 
 int exl3k_rms_norm_res(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* y, uint16_t* n,
                        long rows, int dim, float eps, hipStream_t s);
+// Most chunk sums of squares one lane of the split norm's consumer loads: rows of at most
+// 64 * 4 * 128 = 32768 columns.
+constexpr int SQ_SCALE_MAX_PER_LANE = 4;
+
+// Split residual norm, standalone halves (exl3_decode_ops.hip): h = fp16(h + c) with per-chunk
+// sums of squares (c null: h unchanged), and r = fp16(fp16(h * scale) * w) from those sums.
+int exl3k_res_sq(uint16_t* h, const uint16_t* c, float* sq, long rows, int n, hipStream_t s);
+int exl3k_norm_sq(const uint16_t* h, const float* sq, const uint16_t* w, uint16_t* r, long rows, int n, float eps,
+                  hipStream_t s);
 int exl3k_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, long n, hipStream_t s);
 
 int exl3k_moes_plan(const MoesArgs& a, int pass_row0, hipStream_t s);

@@ -14,7 +14,11 @@ and finally h, out = rms_norm_res(h, d_last, norm).  `fuse_swiglu=False` runs si
 exl3_gemm as two launches, as graphdec.uc does.  `fuse_norm=True` also folds each residual
 norm into the GEMV before it (o_proj with the post-attention norm, down_proj with the next
 layer's input norm or the final norm): the wave that completes the row's last column chunk
-normalises the row, and 4 launches per layer remain.
+normalises the row, and 4 launches per layer remain.  `split_norm=True` divides each residual
+norm between its neighbours instead: o_proj and down_proj add the residual in their chunk
+epilogue and keep each chunk's sum of squares (exl3_gemm_res), and the next bundle (q/k/v,
+gate/up) normalises its input while loading it (mgemm with norm_in); 4 launches per layer, no
+serial pass, plus one launch at each end of the step (the first layer's sums, the final norm).
 """
 from __future__ import annotations
 
@@ -41,13 +45,15 @@ class LayerWeights:
 
 class DecodeStack:
     def __init__(self, layers: List[LayerWeights], final_norm: torch.Tensor, eps: float = 1e-5,
-                 fuse_swiglu: bool = True, fuse_norm: bool = False):
+                 fuse_swiglu: bool = True, fuse_norm: bool = False, split_norm: bool = False):
         dev = final_norm.device
         L0 = layers[0]
         self.hidden = L0.q.in_features
         self.inter = L0.gate.out_features
         self.layers, self.final_norm, self.eps, self.fuse = layers, final_norm, eps, fuse_swiglu
-        self.fuse_norm = fuse_norm
+        if fuse_norm and split_norm:
+            raise ValueError("DecodeStack: fuse_norm and split_norm are two forms of the same fusion; pick one")
+        self.fuse_norm, self.split_norm = fuse_norm, split_norm
         z = lambda *sh: torch.zeros(sh, dtype=torch.half, device=dev)
         H, I = self.hidden, self.inter
         self.x_in = z(1, H)
@@ -58,6 +64,7 @@ class DecodeStack:
         self.act = z(1, I)
         self.a_had_h = z(1, H)
         self.a_had_i = z(1, I)
+        self.sq = torch.zeros((1, H // 128), dtype=torch.float, device=dev)
         self.qkv, self.gu, self.qbuf, self.oout, self.guout, self.dout = [], [], [], [], [], []
         for Lw in layers:
             qb, kb, vb = z(1, 1, Lw.q.out_features), z(1, 1, Lw.k.out_features), z(1, 1, Lw.v.out_features)
@@ -78,6 +85,26 @@ class DecodeStack:
         h, r, eps = self.h, self.r, self.eps
         h.copy_(self.x_in)
         nl = len(self.layers)
+        if self.split_norm:
+            sq = self.sq
+            ops.res_sq(h, None, sq)
+            for i, Lw in enumerate(self.layers):
+                self.qkv[i].run(h.view(1, 1, -1), norm_in=(sq, Lw.input_norm, eps, r))
+                o = Lw.o
+                ops.exl3_gemm_res(self.qbuf[i].view(1, -1), o.trellis, self.oout[i], o.suh, o.svh, h, sq,
+                                  o.mcg, o.mul1, A_had=self.a_had_h)
+                self.gu[i].run(h.view(1, 1, -1), norm_in=(sq, Lw.post_norm, eps, r))
+                dn = Lw.down
+                g, u = self.guout[i][0], self.guout[i][1]
+                if self.fuse:
+                    ops.exl3_gemm_res(g, dn.trellis, self.dout[i], dn.suh, dn.svh, h, sq, dn.mcg, dn.mul1,
+                                      up=u, act=self.act, A_had=self.a_had_i)
+                else:
+                    ops.silu_mul(g, u, out=self.act)
+                    ops.exl3_gemm_res(self.act, dn.trellis, self.dout[i], dn.suh, dn.svh, h, sq, dn.mcg, dn.mul1,
+                                      A_had=self.a_had_i)
+            ops.norm_sq(h, sq, self.final_norm, eps, r=self.out)
+            return self.out
         if self.fuse_norm:
             ops.rms_norm_res(h, self.zero, self.layers[0].input_norm, eps, y=h, n=r)
         for i, Lw in enumerate(self.layers):

@@ -350,11 +350,14 @@ def exl3_mgemm(A: Tensor, B: Tensor, C: Tensor, suh: Tensor, A_had: Tensor, svh:
                max_index: int = -1, force_num_sms: int = 0, num_tokens: int = 1,
                size_n_list: Optional[Tensor] = None, c_ptrs: Optional[Tensor] = None,
                n_stride_list: Optional[Tensor] = None, had_src_list: Optional[Tensor] = None,
-               num_had_src: int = 0) -> int:
+               num_had_src: int = 0, norm_in: Optional[tuple] = None) -> int:
     """Multi-matrix EXL3 matmul over device pointer tables (exl3_gemm.cu:352-394 semantics).
     A (bszm_in, m, k) fp16; B / suh / svh int64 tensors of device addresses; C (bszm_out, m, n)
     fp16 or fp32; indices / weights (.., num_indices) int64 / fp16; optional int32 lists and
-    int64 c_ptrs for per-matrix widths and sliced mode.  Returns the kernel tag."""
+    int64 c_ptrs for per-matrix widths and sliced mode.  norm_in = (sq, w, eps, r): A is the
+    residual stream h and the input is its split-norm form rmsnorm(h) * w, from the chunk sums
+    sq (m, k / 128) fp32 (res_sq / exl3_gemm_res), with r (m, k) as scratch.  Returns the
+    kernel tag."""
     _dtype(A, torch.half, "A")
     for t, name in ((B, "B"), (suh, "suh"), (svh, "svh")):
         _dtype(t, torch.long, name)
@@ -375,6 +378,30 @@ def exl3_mgemm(A: Tensor, B: Tensor, C: Tensor, suh: Tensor, A_had: Tensor, svh:
                         (n_stride_list, "n_stride_list", torch.int32), (had_src_list, "had_src_list", torch.int32)):
         if t is not None:
             _dtype(t, dt, name)
+    if norm_in is not None:
+        sq, w, eps, r = norm_in
+        _dtype(sq, torch.float, "sq")
+        _dtype(w, torch.half, "w")
+        _dtype(r, torch.half, "r")
+        _need(indices is None and weights is None and num_tokens == 1 and min_index < 0,
+              "mgemm norm_in: no indices, routing weights or token groups")
+        _need(sq.numel() == A.size(1) * (A.size(2) // 128) and w.numel() == A.size(2)
+              and r.numel() == A.size(1) * A.size(2), "mgemm norm_in: sq / w / r shapes")
+        _cuda(sq, w, r)
+        with torch.cuda.device(A.device):
+            return check(_lib.lib().exl3_amd_mgemm_norm_in(
+                A.data_ptr(), A.size(0), A.size(1), A.size(2),
+                B.data_ptr(), B.size(0),
+                C.data_ptr(), C.size(0), C.size(2), int(C.dtype == torch.float),
+                suh.data_ptr(), suh.size(0),
+                _ptr(A_had), A_had.numel() if A_had is not None else 0,
+                svh.data_ptr(), svh.size(0),
+                _ptr(size_n_list), _ptr(c_ptrs), c_ptrs.size(0) if c_ptrs is not None else 0,
+                _ptr(n_stride_list), n_stride_list.size(0) if n_stride_list is not None else 0,
+                _ptr(had_src_list), had_src_list.size(0) if had_src_list is not None else 0, int(num_had_src),
+                float(K), int(bool(mcg)), int(bool(mul1)),
+                sq.data_ptr(), w.data_ptr(), float(eps), r.data_ptr(),
+                _stream(A)))
     with torch.cuda.device(A.device):
         return check(_lib.lib().exl3_amd_mgemm(
             A.data_ptr(), A.size(0), A.size(1), A.size(2),
@@ -393,10 +420,10 @@ def exl3_mgemm(A: Tensor, B: Tensor, C: Tensor, suh: Tensor, A_had: Tensor, svh:
 
 
 def mgemm(x: Tensor, B_ptrs: Tensor, C: Tensor, suh_ptrs: Tensor, A_had: Tensor, svh_ptrs: Tensor,
-          K: float, mcg: bool, mul1: bool, opts: Optional[dict] = None) -> Tensor:
+          K: float, mcg: bool, mul1: bool, opts: Optional[dict] = None, norm_in: Optional[tuple] = None) -> Tensor:
     """torch.mgemm of the engine (amp_torch.cpp:10194-10330): stacked bundle (x broadcast,
     C (num, m, n)) or, with opts {size_n_list, c_ptrs, n_stride_list, had_src_list,
-    num_had_src}, sliced mode.  Returns C."""
+    num_had_src}, sliced mode.  norm_in: see exl3_mgemm.  Returns C."""
     o = opts or {}
     if opts is not None:
         for key in ("size_n_list", "c_ptrs", "n_stride_list", "had_src_list"):
@@ -404,7 +431,7 @@ def mgemm(x: Tensor, B_ptrs: Tensor, C: Tensor, suh_ptrs: Tensor, A_had: Tensor,
         _need(isinstance(o.get("num_had_src"), int), "mgemm: num_had_src missing")
     exl3_mgemm(x, B_ptrs, C, suh_ptrs, A_had, svh_ptrs, None, None, K, -1, int(mcg), int(mul1),
                -1, -1, 0, 1, o.get("size_n_list"), o.get("c_ptrs"), o.get("n_stride_list"),
-               o.get("had_src_list"), int(o.get("num_had_src", 0)))
+               o.get("had_src_list"), int(o.get("num_had_src", 0)), norm_in=norm_in)
     return C
 
 
@@ -692,6 +719,72 @@ def exl3_gemm_norm(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], svh: 
             A.data_ptr(), _ptr(up), _ptr(act), B.data_ptr(), C.data_ptr(), _ptr(suh), A_had.data_ptr(), _ptr(svh),
             m, k, n, float(K), mcg_i, mul1_i, h.data_ptr(), weight.data_ptr(), r.data_ptr(), float(eps),
             _stream(A)))
+
+
+def res_sq(h: Tensor, c: Optional[Tensor], sq: Tensor) -> None:
+    """Producer half of the split residual norm on its own: h = fp16(h + c) in place (c None:
+    h unchanged) and sq (rows, n / 128) fp32 = each 128-column chunk's sum of squares."""
+    _dtype(h, torch.half, "h")
+    _dtype(sq, torch.float, "sq")
+    n = h.size(-1)
+    rows = h.numel() // max(n, 1)
+    _need(n % 128 == 0 and sq.numel() == rows * (n // 128), "res_sq: h / sq shapes")
+    if c is not None:
+        _dtype(c, torch.half, "c")
+        _need(c.numel() == h.numel(), "res_sq: h / c shapes")
+    _cuda(h, c, sq)
+    with torch.cuda.device(h.device):
+        check(_lib.lib().exl3_amd_res_sq(h.data_ptr(), _ptr(c), sq.data_ptr(), rows, n, _stream(h)))
+
+
+def norm_sq(h: Tensor, sq: Tensor, weight: Tensor, eps: float, r: Optional[Tensor] = None) -> Tensor:
+    """Consumer half of the split residual norm on its own: r = fp16(fp16(h * scale) * weight),
+    scale = 1 / sqrt(sum(sq) / n + eps) from the chunk sums.  Returns r."""
+    _dtype(h, torch.half, "h")
+    _dtype(sq, torch.float, "sq")
+    _dtype(weight, torch.half, "weight")
+    n = h.size(-1)
+    rows = h.numel() // max(n, 1)
+    _need(n % 128 == 0 and sq.numel() == rows * (n // 128) and weight.numel() == n, "norm_sq: shapes")
+    r = torch.empty_like(h) if r is None else r
+    _cuda(h, sq, weight, r)
+    with torch.cuda.device(h.device):
+        check(_lib.lib().exl3_amd_norm_sq(h.data_ptr(), sq.data_ptr(), weight.data_ptr(), r.data_ptr(), rows, n,
+                                          float(eps), _stream(h)))
+    return r
+
+
+def exl3_gemm_res(A: Tensor, B: Tensor, C: Tensor, suh: Optional[Tensor], svh: Optional[Tensor],
+                  h: Tensor, sq: Tensor, mcg: bool = False, mul1: bool = False,
+                  up: Optional[Tensor] = None, act: Optional[Tensor] = None, A_had: Optional[Tensor] = None) -> int:
+    """C = exl3_gemm(A) (of silu(A) * up when up is given), then the producer half of the split
+    residual norm: h = fp16(h + C) in place, sq = its chunk sums of squares.  One launch at one
+    row (the GEMV's chunk epilogue)."""
+    _need(B.dim() == 3, "B must be 3-dimensional")
+    _dtype(A, torch.half, "A")
+    _trellis_dtype(B, "B")
+    _dtype(C, torch.half, "C")
+    _dtype(h, torch.half, "h")
+    _dtype(sq, torch.float, "sq")
+    k, n = B.size(0) * 16, B.size(1) * 16
+    m = A.numel() // k
+    _need(A.size(-1) == k and C.size(-1) == n and h.numel() == C.numel() and sq.numel() == m * (n // 128),
+          "exl3_gemm_res: incompatible shapes")
+    if up is not None:
+        _dtype(up, torch.half, "up")
+        _need(up.shape == A.shape, "silu_mul: gate/up size mismatch")
+    tile = B.size(2)
+    half_k = tile % 16 != 0
+    _need(not half_k or (tile % 16 == 8 and mul1), "exl3_gemm: half-integer bitrates require the mul1 codebook")
+    K = tile // 16 + (0.5 if half_k else 0.0)
+    mcg_i, mul1_i = _codebook_flags(mcg, mul1)
+    act = torch.empty_like(A) if (act is None and up is not None) else act
+    A_had = torch.empty_like(A) if A_had is None else A_had
+    _cuda(A, B, C, suh, svh, h, sq, up, act, A_had)
+    with torch.cuda.device(A.device):
+        return check(_lib.lib().exl3_amd_gemm_res(
+            A.data_ptr(), _ptr(up), _ptr(act), B.data_ptr(), C.data_ptr(), _ptr(suh), A_had.data_ptr(), _ptr(svh),
+            m, k, n, float(K), mcg_i, mul1_i, h.data_ptr(), sq.data_ptr(), _stream(A)))
 
 
 def _library_mm(a: Tensor, b: Tensor, out: Tensor) -> None:

@@ -245,7 +245,9 @@ def decode_step_bench(torch, layers, steps=20):
     rms_norm_res, q/k/v sliced mgemm, o gemm, rms_norm_res, gate/up stacked mgemm, SwiGLU + down,
     final norm) captured into one graph over the same 32 layers; attention is outside the path
     (the q projection feeds o).  fused_swiglu: the down GEMV forms silu(gate) * up in its input
-    load; fused_norm_swiglu: o and down also run the residual norm in their last column chunk."""
+    load; fused_norm_swiglu: o and down also run the residual norm in their last column chunk;
+    split_norm_swiglu: each norm divided between its neighbours (o / down add the residual and
+    keep chunk sums of squares, q/k/v and gate/up normalise their input on load)."""
     from ampstein_amd.decode import DecodeStack, LayerWeights
     H = 4096
     ones = torch.ones(H, dtype=torch.half, device="cuda")
@@ -254,9 +256,11 @@ def decode_step_bench(torch, layers, steps=20):
     nbytes = sum(r[n].trellis.numel() * 2 for r in layers for n in ("q", "k", "v", "o", "gate", "up", "down"))
     x = host_normal(torch, (1, H), 2004)
     res = {}
-    for name, fuse, fnorm, launches in (("fused_norm_swiglu", True, True, 4), ("fused_swiglu", True, False, 6),
-                                        ("separate_silu_mul", False, False, 7)):
-        st = DecodeStack(lw, ones, fuse_swiglu=fuse, fuse_norm=fnorm)
+    for name, fuse, fnorm, snorm, launches in (("split_norm_swiglu", True, False, True, 4),
+                                               ("fused_norm_swiglu", True, True, False, 4),
+                                               ("fused_swiglu", True, False, False, 6),
+                                               ("separate_silu_mul", False, False, False, 7)):
+        st = DecodeStack(lw, ones, fuse_swiglu=fuse, fuse_norm=fnorm, split_norm=snorm)
         st.capture()
         for _ in range(3):
             st(x)

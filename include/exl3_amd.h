@@ -342,6 +342,53 @@ int exl3_amd_gemm_norm(const uint16_t* A, const uint16_t* up, uint16_t* act, con
                        int m, int k, int n, float K, int mcg, int mul1,
                        uint16_t* h, const uint16_t* w, uint16_t* r, float eps, void* stream);
 
+/* The decode step's residual norm (rms_norm_res, src/torch/amp_kernels.cu:279-365, bound at
+ * src/torch/amp_torch.cpp:10081, called between the linears at graphdec.uc:151-230) split
+ * between its two neighbours, so that the norm costs no launch and no serial pass of its own.
+ * A row of n columns is handled in 128-column chunks; sq holds one fp32 per chunk (rows x n/128):
+ *   producer   h = fp16(h + c), sq[chunk] = sum over the chunk of float(h)^2
+ *              (exl3_amd_gemm_res in the GEMV's epilogue; exl3_amd_res_sq on its own);
+ *   consumer   r = fp16(fp16(h * scale) * w), scale = 1 / sqrtf(sum(sq) / n + eps), the chunk
+ *              sums added in a fixed order (exl3_amd_mgemm_norm_in in the GEMV's input load;
+ *              exl3_amd_norm_sq on its own).
+ * h and r are exactly rms_norm_res's y and n except for the order in which the sum of squares
+ * is accumulated (r within one fp16 ulp); the fused and standalone forms of each half give the
+ * same bits.  No counterpart in the reference (a re-division of its rms_norm_res).  n <= 32768
+ * for the consumer.  Pointers 4-byte aligned.  Returns 0 or a negative error. */
+int exl3_amd_res_sq(uint16_t* h, const uint16_t* c, float* sq, int rows, int n, void* stream);
+int exl3_amd_norm_sq(const uint16_t* h, const float* sq, const uint16_t* w, uint16_t* r, int rows, int n, float eps,
+                     void* stream);
+
+/* exl3_gemm (or, with up, exl3_amd_gemm_silu_mul) followed by the producer half of the split
+ * residual norm: C = the linear (fp16), h = fp16(h + C), sq = its chunk sums.  With one row the
+ * GEMV's chunk epilogue does the residual add and the sums: one launch.  Otherwise two (the
+ * linear, then exl3_amd_res_sq).  Returns the exl3_gemm tag. */
+int exl3_amd_gemm_res(const uint16_t* A, const uint16_t* up, uint16_t* act, const uint16_t* trellis, uint16_t* C,
+                      const uint16_t* suh, uint16_t* A_had, const uint16_t* svh,
+                      int m, int k, int n, float K, int mcg, int mul1,
+                      uint16_t* h, float* sq, void* stream);
+
+/* exl3_amd_mgemm of the consumer half of the split residual norm: the input is rmsnorm(h) * w
+ * formed from h and its chunk sums sq (k / 128 per row), as exl3_amd_norm_sq writes it.  Stacked
+ * (one input slab broadcast to num_B matrices) or sliced mode (size_n_list .. num_had_src as in
+ * exl3_amd_mgemm); no indices, routing weights or token groups.  With one row the M = 1 stream
+ * GEMV normalises its input chunks while loading them (one launch; every wave forms the scale
+ * from the same sums in the same order); otherwise exl3_amd_norm_sq writes r (m, k) first and
+ * the GEMV reads it.  Results bit-identical to exl3_amd_norm_sq followed by exl3_amd_mgemm on r.
+ * No counterpart in the reference.  Returns the exl3_mgemm tag. */
+int exl3_amd_mgemm_norm_in(const uint16_t* h, int bszm_in, int m, int k,
+                           const uint64_t* B, int num_B,
+                           void* C, int bszm_out, int n, int c_fp32,
+                           const uint64_t* suh, int num_suh,
+                           uint16_t* A_had, int64_t a_had_numel,
+                           const uint64_t* svh, int num_svh,
+                           const int* size_n_list, const uint64_t* c_ptrs, int num_c_ptrs,
+                           const int* n_stride_list, int num_n_stride,
+                           const int* had_src_list, int num_had_src_list, int num_had_src,
+                           float K, int mcg, int mul1,
+                           const float* sq, const uint16_t* w, float eps, uint16_t* r,
+                           void* stream);
+
 /* exl3_amd_reconstruct_had written transposed: WT (n, k) row-major, WT[c][r] = W[r][c], the same
  * fp16 values bit for bit.  The layout exl3_amd_recon_mm reads.  No counterpart in the reference
  * (reconstruct_had_slice, quant/reconstruct.cu:431-490, writes (k, n) for cuBLAS); the recon

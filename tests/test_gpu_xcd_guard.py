@@ -8,6 +8,8 @@
    of its counter.  The launch's output stays right (real dispatch is unchanged), the alarm is
    seen, the library turns the hand-off off, the next calls (finish-kernel path) are right too,
    and exl3_amd_xcd_rearm restores the probe's XCD count.
+3. With the hand-off off, the split residual norm's producer (exl3_gemm_res) runs its epilogue
+   in the finish kernel: bit-identical to exl3_gemm + res_sq.
 Bar of every output: the oracle's fp64 linear, 2e-3 (tests/tol.py).
 """
 import numpy as np
@@ -107,6 +109,29 @@ def test_flag_path_moe_coop(torch_cuda, orc, kernel_policy):
         assert _lib.xcd_status(0) == (probe, 0, alarms0 + 1)
         y, _ = run(torch, es, x, sel, rw)                  # agent-scope hand-off
         assert rel_err(y, ref) < 2e-3
+    finally:
+        _lib.check(_lib.lib().exl3_amd_xcd_rearm(0))
+    assert _lib.xcd_status(0)[:2] == (probe, probe)
+
+
+def test_gemm_res_finish_kernel(torch_cuda, kernel_policy):
+    """The hand-off turned off by the hook: the split partials are summed by the finish kernel,
+    whose epilogue does the split norm's residual add and chunk sums."""
+    from tests.test_gpu_split_norm import _check_gemm_res, _gemm_res_case
+    torch = torch_cuda
+    from ampstein_amd import ops
+    probe, active, alarms0 = _lib.xcd_status(0)
+    if probe == 0:
+        pytest.skip("the XCD-local hand-off is off on this device")
+    case = _gemm_res_case(4096, 4096, False, 1, 77)
+    try:
+        kernel_policy(_lib.POLICY_XCD_FAKE, probe + 1)
+        C = torch.empty((1, 4096), dtype=torch.half, device="cuda")
+        ops.exl3_gemm(case[3], case[0], C, case[1], torch.empty_like(case[3]), case[2])   # raises the alarm
+        torch.cuda.synchronize()
+        assert _lib.xcd_status(0) == (probe, 0, alarms0 + 1)
+        print("[xcd guard] gemm_res with the finish kernel", flush=True)
+        _check_gemm_res(*case, 1, 4096)
     finally:
         _lib.check(_lib.lib().exl3_amd_xcd_rearm(0))
     assert _lib.xcd_status(0)[:2] == (probe, probe)
