@@ -647,6 +647,76 @@ void moe_a_kernel(const MoeArgs a)
     }
 }
 
+// The down epilogue's slot sum for top-k <= WKR (every partition holds at most slot k = w) and
+// at most DOWN_PF_SPLITS k-splits: the same arithmetic, in the same order, as the general loop in
+// moe_b_kernel, but each group of DOWN_PF_SLOTS slots issues all its loads (routing, split
+// partials, svh and bias pairs) before the first is consumed, so that the group costs one chain
+// of dependent round trips instead of one per slot.  Loads are clamped and unconditional.
+constexpr int DOWN_PF_SLOTS = 8, DOWN_PF_SPLITS = 2;
+
+__device__ __forceinline__ void down_sum_prefetched(const MoeArgs& a, int row, int col, int lane, int S,
+                                                    float& o0, float& o1)
+{
+    const int slots = a.bsz * a.topk;
+    for (int k0 = 0; k0 < WKR; k0 += DOWN_PF_SLOTS)
+    {
+        if (k0 >= a.topk)
+        {
+            // partitions without a slot add p = 0 (o + 0 is idempotent after the first)
+            o0 += 0.0f;
+            o1 += 0.0f;
+            continue;
+        }
+        SlotInfo sj[DOWN_PF_SLOTS];
+        f32x2 pt[DOWN_PF_SLOTS][DOWN_PF_SPLITS];
+        float sv0[DOWN_PF_SLOTS], sv1[DOWN_PF_SLOTS], bv0[DOWN_PF_SLOTS], bv1[DOWN_PF_SLOTS];
+        #pragma unroll
+        for (int u = 0; u < DOWN_PF_SLOTS; ++u)
+            sj[u] = slot_info(a, row * a.topk + min(k0 + u, a.topk - 1));
+        #pragma unroll
+        for (int u = 0; u < DOWN_PF_SLOTS; ++u)
+        {
+            const int sk = row * a.topk + min(k0 + u, a.topk - 1);
+            #pragma unroll
+            for (int qq = 0; qq < DOWN_PF_SPLITS; ++qq)
+                pt[u][qq] = load_l2_f32x2(a.part_b + ((size_t) min(qq, S - 1) * slots + sk) * a.Ho + col);
+        }
+        #pragma unroll
+        for (int u = 0; u < DOWN_PF_SLOTS; ++u)
+        {
+            const uint16_t* dsvh = tab<uint16_t>(a.d_svh, sj[u].local);
+            sv0[u] = h2f(dsvh, col); sv1[u] = h2f(dsvh, col + 1);
+            bv0[u] = 0.0f; bv1[u] = 0.0f;
+            if (a.d_bias)
+            {
+                const uint16_t* bp = tab<uint16_t>(a.d_bias, sj[u].local);
+                bv0[u] = h2f(bp, col); bv1[u] = h2f(bp, col + 1);
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < DOWN_PF_SLOTS; ++u)
+        {
+            const int k = k0 + u;                      // partition w = k
+            float p0 = 0.0f, p1 = 0.0f;
+            if (k < a.topk && sj[u].active)
+            {
+                float v0 = 0.0f, v1 = 0.0f;
+                #pragma unroll
+                for (int qq = 0; qq < DOWN_PF_SPLITS; ++qq)
+                    if (qq < S) { v0 += pt[u][qq].x; v1 += pt[u][qq].y; }
+                fwht128_wave(v0, v1, lane);
+                v0 *= EXL3_HAD_RSCALE; v1 *= EXL3_HAD_RSCALE;
+                v0 *= sv0[u]; v1 *= sv1[u];
+                if (a.d_bias) { v0 += bv0[u]; v1 += bv1[u]; }
+                p0 += sj[u].w * v0;
+                p1 += sj[u].w * v1;
+            }
+            o0 += p0;
+            o1 += p1;
+        }
+    }
+}
+
 template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_b_kernel(const MoeArgs a)
@@ -702,6 +772,9 @@ void moe_b_kernel(const MoeArgs a)
             const int col = chunk * 128 + 2 * lane;
             float o0 = 0.0f, o1 = 0.0f;
             // slots k = w, w + 16, ... summed per w, then the partitions in order (:960-979)
+            if (a.topk <= WKR && S <= DOWN_PF_SPLITS && !a.down_per_slot)
+                down_sum_prefetched(a, row, col, lane, S, o0, o1);
+            else
             for (int w = 0; w < WKR; ++w)
             {
                 float p0 = 0.0f, p1 = 0.0f;
