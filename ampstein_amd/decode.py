@@ -19,6 +19,8 @@ norm between its neighbours instead: o_proj and down_proj add the residual in th
 epilogue and keep each chunk's sum of squares (exl3_gemm_res), and the next bundle (q/k/v,
 gate/up) normalises its input while loading it (mgemm with norm_in); 4 launches per layer, no
 serial pass, plus one launch at each end of the step (the first layer's sums, the final norm).
+The split norm is the default (the fastest form measured); `split_norm=False` runs the
+reference's own sequence of rms_norm_res calls.
 """
 from __future__ import annotations
 
@@ -45,15 +47,14 @@ class LayerWeights:
 
 class DecodeStack:
     def __init__(self, layers: List[LayerWeights], final_norm: torch.Tensor, eps: float = 1e-5,
-                 fuse_swiglu: bool = True, fuse_norm: bool = False, split_norm: bool = False):
+                 fuse_swiglu: bool = True, fuse_norm: bool = False, split_norm: bool = True):
         dev = final_norm.device
         L0 = layers[0]
         self.hidden = L0.q.in_features
         self.inter = L0.gate.out_features
         self.layers, self.final_norm, self.eps, self.fuse = layers, final_norm, eps, fuse_swiglu
-        if fuse_norm and split_norm:
-            raise ValueError("DecodeStack: fuse_norm and split_norm are two forms of the same fusion; pick one")
-        self.fuse_norm, self.split_norm = fuse_norm, split_norm
+        # fuse_norm asks for the other form of the same fusion (the norm in the GEMV's last chunk)
+        self.fuse_norm, self.split_norm = fuse_norm, split_norm and not fuse_norm
         z = lambda *sh: torch.zeros(sh, dtype=torch.half, device=dev)
         H, I = self.hidden, self.inter
         self.x_in = z(1, H)

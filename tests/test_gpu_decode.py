@@ -104,7 +104,7 @@ def _stack(H, Q, KV, I, n_layers, K=4, cb=0, fuse=True):
                                    input_norm=torch.from_numpy(wi).cuda(), post_norm=torch.from_numpy(wp).cuda()))
         host.append(({k2: p[1] for k2, p in parts.items()}, wi, wp))
     wf = (rng.standard_normal(H) * 0.2 + 1).astype(np.float16)
-    return DecodeStack(layers, torch.from_numpy(wf).cuda(), fuse_swiglu=fuse), host, wf
+    return DecodeStack(layers, torch.from_numpy(wf).cuda(), fuse_swiglu=fuse, split_norm=False), host, wf
 
 
 def _model(host, wf, x, K, cb, eps=1e-5):
