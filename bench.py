@@ -183,11 +183,11 @@ def event_times(torch, sweep, reps=3):
     return [(label, nbytes, e0.elapsed_time(e1)) for rep, label, nbytes, e0, e1 in recs if rep > 0]
 
 
-def dominant_region(torch, layers, reps=3):
+def dominant_region(torch, layers, reps=3, blocks=7):
     """The dominant launch of the sweep -- the stacked gate/up exl3_mgemm (58.7 MB, half the
     step's bytes) -- as its own timed region: one launch per layer (distinct weights), captured
-    in a graph, HIP events around the replays on the replay stream.  Returns (avg us per launch,
-    bytes per launch, launches timed)."""
+    in a graph, HIP events around the replays on the replay stream.  Returns (avg us per launch
+    of the median block, bytes per launch, launches timed)."""
     from ampstein_amd import bundles
     gu_out = torch.empty((2, 1, 14336), dtype=torch.half, device="cuda")
     x = host_normal(torch, (1, 1, 4096), 2003)
@@ -203,17 +203,23 @@ def dominant_region(torch, layers, reps=3):
             b.run(x)
     graph.replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    # `blocks` timed blocks of `reps` replays each; the median block (clock and thermal state
+    # move a single short block by a few per cent)
+    per = []
     with torch.cuda.stream(stream):
-        e0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(stream)
+        for _ in range(blocks):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            per.append((e0, e1))
     torch.cuda.synchronize()
     n = reps * len(bs)
+    us = sorted(e0.elapsed_time(e1) * 1e3 / n for e0, e1 in per)
     nbytes = layers[0]["gate"].trellis.numel() * 4
-    return e0.elapsed_time(e1) * 1e3 / n, nbytes, n
+    return us[len(us) // 2], nbytes, n * blocks
 
 
 def graph_time(torch, sweep, steps, warmup):
