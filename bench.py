@@ -73,7 +73,7 @@ def host_trellis(torch, k, n, K, seed):
     identical bytes.  Uniform uint16 trellis words, +-1 fp16 suh / svh."""
     import numpy as np
     rng = np.random.default_rng(seed)
-    t = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * K), dtype=np.uint16).view(np.int16)
+    t = rng.integers(0, 65536, size=(k // 16, n // 16, int(16 * K)), dtype=np.uint16).view(np.int16)
     s = np.where(rng.integers(0, 2, k) > 0, 1.0, -1.0).astype(np.float16)
     v = np.where(rng.integers(0, 2, n) > 0, 1.0, -1.0).astype(np.float16)
     return torch.from_numpy(t).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(v).cuda()
@@ -364,18 +364,20 @@ QWEN_SHAPES = ((5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120))
 def qwen_bench(torch, min_bytes=1 << 30):
     """the four Qwen-27B-class shapes as one layer, swept over enough distinct layers
     (>= 1 GB of packed weights, beyond the 256 MB MALL) in one graph, for K in {2, 3, 5, 8} x
-    {3INST, MCG} x M in {1, 4, 8}.  The same random words serve both codebooks.  GB/s = packed
-    bytes of the sweep / graph time; per-shape us from HIP events around single launches."""
+    {3INST, MCG} x M in {1, 4, 8}, and the half rates K in {1.5, 2.5, 3.5} (MUL1, their only
+    codebook) x M in {1, 8}.  The same random words serve every codebook.  GB/s = packed bytes
+    of the sweep / graph time; per-shape us from HIP events around single launches."""
     from ampstein_amd import _lib
     from ampstein_amd.bundles import Linear
     res = {}
-    for K in (2, 3, 5, 8):
-        per_layer = sum(k * n * K // 8 for k, n in QWEN_SHAPES)
+    plans = [(K, (0, 1), (1, 4, 8)) for K in (2, 3, 5, 8)] + [(K, (2,), (1, 8)) for K in (1.5, 2.5, 3.5)]
+    for K, cbs, Ms in plans:
+        per_layer = sum(int(k * n * K) // 8 for k, n in QWEN_SHAPES)
         n_layers = max(2, -(-min_bytes // per_layer))
-        layers = [[Linear(*host_trellis(torch, k, n, K, 7000 + 100 * K + 4 * li + si), float(K))
+        layers = [[Linear(*host_trellis(torch, k, n, K, 7000 + int(100 * K) + 4 * li + si), float(K))
                    for si, (k, n) in enumerate(QWEN_SHAPES)] for li in range(n_layers)]
-        for cb in (0, 1):
-            for M in (1, 4, 8):
+        for cb in cbs:
+            for M in Ms:
                 xs = {k: host_normal(torch, (M, k), 7500 + k + M) for k in (5120, 17408)}
                 ys = {n: torch.empty((M, n), dtype=torch.half, device="cuda") for n in (5120, 1024, 17408)}
                 hads = {k: torch.empty((M, k), dtype=torch.half, device="cuda") for k in (5120, 17408)}
@@ -385,7 +387,7 @@ def qwen_bench(torch, min_bytes=1 << 30):
                     k, n = lin.in_features, lin.out_features
                     rc = L.exl3_amd_gemm(xs[k].data_ptr(), lin.trellis.data_ptr(), ys[n].data_ptr(), 0,
                                          lin.suh.data_ptr(), hads[k].data_ptr(), lin.svh.data_ptr(), M, k, n,
-                                         float(K), cb == 1, 0, 0, st)
+                                         float(K), cb == 1, cb == 2, 0, st)
                     if rc < 0:
                         raise RuntimeError(L.exl3_amd_last_error().decode())
 
@@ -395,7 +397,7 @@ def qwen_bench(torch, min_bytes=1 << 30):
                 ev = {}
                 for label, nbytes, t_ms in event_times(torch, sw, reps=2):
                     ev.setdefault(label, []).append(t_ms)
-                res[f"K{K}_{'mcg' if cb else '3inst'}_M{M}"] = {
+                res[f"K{K}_{('3inst', 'mcg', 'mul1')[cb]}_M{M}"] = {
                     "sweep_GB_s": round(per_layer * n_layers / (ms * 1e-3) / 1e9, 1),
                     "frac_hbm": round(per_layer * n_layers / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "per_shape_us": {lab: round(sum(v) / len(v) * 1e3, 2) for lab, v in ev.items()}}
