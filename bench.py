@@ -808,6 +808,22 @@ def recon_rows():
         print(json.dumps(row), flush=True)
         del t, s, v
         torch.cuda.empty_cache()
+    # the recon route's two branches at prefill sizes (configs[3] shapes): the reference's fused W
+    # (reconstruct_had, dense GEMM) and the rotated one (x rotated, reconstruct, GEMM, y rotated
+    # in the epilogue); TFLOPS of the best of 3 timings of 5 calls each
+    for si, (k, n) in enumerate(((8192, 28672), (28672, 8192))):
+        t, s, v = host_trellis(torch, k, n, 4, 7300 + si)
+        row = {"shape": f"{k}x{n}", "K": 4, "TFLOPS": "fused W / rotated"}
+        for m in (2048, 4096, 8192):
+            x = host_normal(torch, (m, k), 7400 + m)
+            best = []
+            for fr in (0, 1 << 30):
+                best.append(min(timed(torch, lambda: ops.exl3_gemm_recon(x, t, s, v, 4.0, fused_rows=fr)) for _ in range(3)))
+            row[str(m)] = [round(2.0 * m * k * n / (us * 1e-6) / 1e12, 1) for us in best]
+            del x
+            torch.cuda.empty_cache()
+        print(json.dumps(row), flush=True)
+        del t, s, v
     return 0
 
 
