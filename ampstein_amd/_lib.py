@@ -148,7 +148,7 @@ POLICY_RECON_MM, RECON_MM_8WAVES, RECON_MM_WHOLE_TILES, RECON_MM_GLOBAL_DMA, REC
 POLICY_GEMV_SPLIT, GEMV_SPLIT_BALANCED = 6, 1
 POLICY_GEMV_SLICES = 7
 POLICY_XCD_FAKE = 8
-POLICY_MOE_DOWN_SUM, MOE_DOWN_SUM_PER_SLOT = 9, 1
+POLICY_MOE_EPILOGUE, MOE_EPILOGUE_SERIAL = 9, 1
 
 
 class policy:

@@ -1298,7 +1298,7 @@ int exl3_amd_moe_coop(const uint16_t* x, int bsz, int H, int x_stride,
     a.xcd = (d->num_xcd > 0 && (I / 128) % d->num_xcd == 0 && (Ho / 128) % d->num_xcd == 0 &&
              (long) nproj * a.splits_a <= XCD_MAX_ARRIVALS && (long) topk * a.splits_b <= XCD_MAX_ARRIVALS) ? d->num_xcd : 0;
     a.xg = xcd_guard(d->alarm_dev);
-    a.down_per_slot = policy(EXL3_AMD_POLICY_MOE_DOWN_SUM) == EXL3_AMD_MOE_DOWN_SUM_PER_SLOT;
+    a.epi_serial = policy(EXL3_AMD_POLICY_MOE_EPILOGUE) == EXL3_AMD_MOE_EPILOGUE_SERIAL;
 
     const int cb = mcg ? 1 : (mul1 ? 2 : 0);
     hipStream_t s = (hipStream_t) stream;

@@ -321,7 +321,7 @@ struct MoeArgs
     int xcd;                    // > 0: chunk c runs on XCD c % xcd (workgroup-scope hand-off)
     XcdGuard xg;                // hand-off check (used when xcd > 0)
     int run_lo, run_hi;         // this launch takes the runs of run_lo + 1 .. run_hi slots
-    int down_per_slot;          // 1: the down epilogue's general per-slot loop (test policy)
+    int epi_serial;             // 1: the gate/up and down epilogues' general loops (test policy)
 };
 
 int exl3k_moe_cb0(const MoeArgs& a, hipStream_t s);

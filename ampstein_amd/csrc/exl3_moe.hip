@@ -548,6 +548,8 @@ __device__ __forceinline__ bool read_run(const MoeArgs& a, int run, int* rows, i
     return true;
 }
 
+constexpr int UP_PF_SPLITS = 4;          // k-splits whose partials the gate/up epilogue prefetches
+
 template <int CB, int MT, bool HS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CB == 2 ? (MT == 1 ? 4 : 3) : 1)))
 void moe_a_kernel(const MoeArgs a)
@@ -603,8 +605,46 @@ void moe_a_kernel(const MoeArgs a)
         const int s = rows[r];
         {
             const int col = chunk * 128 + 2 * lane;
-            auto load_sum = [&](int p, float& v0, float& v1) {
+            // every load of the epilogue issued before the first is consumed (split partials of
+            // up and gate, svh / bias / down-suh pairs): one round trip instead of a chain.  The
+            // sums run in the order of the general loop (slot order from 0.0f), so the bits are
+            // the same; more than UP_PF_SPLITS splits take the general loop.
+            const int pu_idx = a.gated ? 1 : 0;
+            f32x2 pu[UP_PF_SPLITS], pg[UP_PF_SPLITS];
+            const bool pf = S <= UP_PF_SPLITS && !a.epi_serial;
+            if (pf)
+            {
+                #pragma unroll
+                for (int qq = 0; qq < UP_PF_SPLITS; ++qq)
+                {
+                    const int qc = min(qq, S - 1);
+                    pu[qq] = load_l2_f32x2(a.part_a + (((size_t) pu_idx * S + qc) * slots + s) * a.I + col);
+                    // (ungated: the up partials again, unused)
+                    pg[qq] = load_l2_f32x2(a.part_a + (((size_t) 0 * S + qc) * slots + s) * a.I + col);
+                }
+            }
+            const uint16_t* usvh = tab<uint16_t>(a.u_svh, local);
+            const uint16_t* dsuh = tab<uint16_t>(a.d_suh, local);
+            const float us0 = h2f(usvh, col), us1 = h2f(usvh, col + 1);
+            const float ds0 = h2f(dsuh, col), ds1 = h2f(dsuh, col + 1);
+            float gs0 = 0.0f, gs1 = 0.0f;
+            if (a.gated)            // the gate tables are read only for a gated MoE
+            {
+                const uint16_t* gsvh = tab<uint16_t>(a.g_svh, local);
+                gs0 = h2f(gsvh, col); gs1 = h2f(gsvh, col + 1);
+            }
+            float ub0 = 0.0f, ub1 = 0.0f, gb0 = 0.0f, gb1 = 0.0f;
+            if (a.u_bias) { const uint16_t* b = tab<uint16_t>(a.u_bias, local); ub0 = h2f(b, col); ub1 = h2f(b, col + 1); }
+            if (a.gated && a.g_bias) { const uint16_t* b = tab<uint16_t>(a.g_bias, local); gb0 = h2f(b, col); gb1 = h2f(b, col + 1); }
+            auto load_sum = [&](int p, const f32x2* pv, float& v0, float& v1) {
                 v0 = v1 = 0.0f;
+                if (pf)
+                {
+                    #pragma unroll
+                    for (int qq = 0; qq < UP_PF_SPLITS; ++qq)
+                        if (qq < S) { v0 += pv[qq].x; v1 += pv[qq].y; }
+                    return;
+                }
                 for (int qq = 0; qq < S; ++qq)
                 {
                     const f32x2 t = load_l2_f32x2(a.part_a + (((size_t) p * S + qq) * slots + s) * a.I + col);
@@ -612,34 +652,23 @@ void moe_a_kernel(const MoeArgs a)
                 }
             };
             float u0, u1;
-            load_sum(a.gated ? 1 : 0, u0, u1);
+            load_sum(pu_idx, pu, u0, u1);
             fwht128_wave(u0, u1, lane);
             u0 *= EXL3_HAD_RSCALE; u1 *= EXL3_HAD_RSCALE;
-            const uint16_t* usvh = tab<uint16_t>(a.u_svh, local);
-            u0 *= h2f(usvh, col); u1 *= h2f(usvh, col + 1);
-            if (a.u_bias)
-            {
-                const uint16_t* b = tab<uint16_t>(a.u_bias, local);
-                u0 += h2f(b, col); u1 += h2f(b, col + 1);
-            }
+            u0 *= us0; u1 *= us1;
+            if (a.u_bias) { u0 += ub0; u1 += ub1; }
             float g0 = u0, g1 = u1;
             if (a.gated)
             {
-                load_sum(0, g0, g1);
+                load_sum(0, pg, g0, g1);
                 fwht128_wave(g0, g1, lane);
                 g0 *= EXL3_HAD_RSCALE; g1 *= EXL3_HAD_RSCALE;
-                const uint16_t* gsvh = tab<uint16_t>(a.g_svh, local);
-                g0 *= h2f(gsvh, col); g1 *= h2f(gsvh, col + 1);
-                if (a.g_bias)
-                {
-                    const uint16_t* b = tab<uint16_t>(a.g_bias, local);
-                    g0 += h2f(b, col); g1 += h2f(b, col + 1);
-                }
+                g0 *= gs0; g1 *= gs1;
+                if (a.g_bias) { g0 += gb0; g1 += gb1; }
             }
             float a0 = act_gate(a.act, a.gated, g0, u0, a.act_limit);
             float a1 = act_gate(a.act, a.gated, g1, u1, a.act_limit);
-            const uint16_t* dsuh = tab<uint16_t>(a.d_suh, local);
-            a0 *= h2f(dsuh, col); a1 *= h2f(dsuh, col + 1);
+            a0 *= ds0; a1 *= ds1;
             fwht128_wave(a0, a1, lane);
             const f16x2 o = { (f16) (a0 * EXL3_HAD_RSCALE), (f16) (a1 * EXL3_HAD_RSCALE) };
             *to_global_w((uint32_t*) (a.act_out + (size_t) s * a.I + col)) = as_u32(o);
@@ -772,7 +801,7 @@ void moe_b_kernel(const MoeArgs a)
             const int col = chunk * 128 + 2 * lane;
             float o0 = 0.0f, o1 = 0.0f;
             // slots k = w, w + 16, ... summed per w, then the partitions in order (:960-979)
-            if (a.topk <= WKR && S <= DOWN_PF_SPLITS && !a.down_per_slot)
+            if (a.topk <= WKR && S <= DOWN_PF_SPLITS && !a.epi_serial)
                 down_sum_prefetched(a, row, col, lane, S, o0, o1);
             else
             for (int w = 0; w < WKR; ++w)

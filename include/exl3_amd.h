@@ -76,9 +76,11 @@ int exl3_amd_version(void);
 #define EXL3_AMD_POLICY_XCD_FAKE        8   /* test hook of the XCD hand-off check: value v > 0 makes
                                              * linear workgroup v - 1 of every hand-off launch report
                                              * XCC id + 1, as if dispatch had put it on another XCD   */
-#define EXL3_AMD_POLICY_MOE_DOWN_SUM    9   /* exl3_amd_moe_coop down epilogue's sum over the slots    */
-#define EXL3_AMD_MOE_DOWN_SUM_PER_SLOT  1   /*   the general per-slot loop instead of the prefetched
-                                                 form (top-k <= 16, at most 2 k-splits); same bits      */
+#define EXL3_AMD_POLICY_MOE_EPILOGUE    9   /* exl3_amd_moe_coop gate/up and down epilogues            */
+#define EXL3_AMD_MOE_EPILOGUE_SERIAL    1   /*   their general loops, each load consumed as it arrives,
+                                                 instead of the forms that issue every load first
+                                                 (gate/up: at most 4 k-splits; down: top-k <= 16, at
+                                                 most 2 k-splits); same bits                            */
 #define EXL3_AMD_POLICY_COUNT           10
 int exl3_amd_set_policy(int key, int value);
 int exl3_amd_get_policy(int key);       /* the current value, or EXL3_AMD_EINVAL for an unknown key */

@@ -156,23 +156,28 @@ def test_moe_range_filter_and_empty_rows(torch_cuda, experts_mixed):
     check_runs(runs, sel, rw, 4, 12)
 
 
-@pytest.mark.parametrize("case", ["bsz1", "bsz8", "bias", "filter"])
-def test_moe_down_sum_forms_bit_identical(torch_cuda, experts_mixed, experts_small, kernel_policy, case):
-    """The down epilogue's prefetched slot sum (top-k <= 16, at most 2 k-splits) and the general
-    per-slot loop give the same bits: same operations in the same order."""
+@pytest.mark.parametrize("case", ["bsz1", "bsz8", "bias", "filter", "hi512"])
+def test_moe_epilogue_forms_bit_identical(torch_cuda, orc, experts_mixed, experts_small, kernel_policy, case):
+    """The gate/up and down epilogues' prefetched forms (every load issued first) and their
+    general loops give the same bits: same operations in the same order."""
     from ampstein_amd import _lib
     rng = np.random.default_rng(300 + len(case))
     kw = {}
     if case == "bias":
         es, (sel, rw) = experts_small, routing(rng, 4, 12, 4)
         kw = dict(mixed=False, bias=True)
+    elif case == "hi512":
+        # Hi = 512 at one token: 4 gate/up k-splits (the widest prefetched form)
+        es = moe_ref.ExpertSet(torch_cuda, orc, 8, 512, 256, 256, [3] * 8, 0, seed=31)
+        sel, rw = routing(rng, 1, 8, 8)
+        kw = dict(mixed=False)
     else:
         es, (sel, rw) = experts_mixed, routing(rng, 8 if case == "bsz8" else 1, 16, 8)
         if case == "filter":
             kw = dict(mn=4, mx=12)
     x = rng.standard_normal((sel.shape[0], 256)).astype(np.float16)
     y1, _ = run(torch_cuda, es, x, sel, rw, **kw)
-    kernel_policy(_lib.POLICY_MOE_DOWN_SUM, _lib.MOE_DOWN_SUM_PER_SLOT)
+    kernel_policy(_lib.POLICY_MOE_EPILOGUE, _lib.MOE_EPILOGUE_SERIAL)
     y2, _ = run(torch_cuda, es, x, sel, rw, **kw)
     assert np.array_equal(np.asarray(y1).view(np.uint32), np.asarray(y2).view(np.uint32))
 
