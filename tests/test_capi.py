@@ -280,3 +280,26 @@ def test_decode_neighbours_reject_bad_arguments():
     rc, msg = call_err(L.exl3_amd_gemm_norm, 16, None, None, 16, 16, None, None, None, 1, 128, 120, f(4.0), 0, 0,
                        16, 16, 16, f(1e-5), None)
     assert rc == _lib.EINVAL and "n must" in msg
+
+
+def test_header_constants_match_python():
+    """Every integer constant _lib.py mirrors (return codes, tags, policy keys and values) has the
+    value include/exl3_amd.h defines, and every policy key of the header has a Python name."""
+    import re
+    from ampstein_amd import _lib
+    defs = {}
+    for line in open(_lib.HEADER):
+        m = re.match(r"#define\s+EXL3_AMD_(\w+)\s+(-?\d+)\b", line)
+        if m:
+            defs[m.group(1)] = int(m.group(2))
+    assert defs, "no constants parsed from the header"
+    checked = 0
+    for name, val in vars(_lib).items():
+        if name.isupper() and isinstance(val, int) and not isinstance(val, bool) and name in defs:
+            assert defs[name] == val, (name, defs[name], val)
+            checked += 1
+    keys = [n for n in defs if n.startswith("POLICY_") and n != "POLICY_COUNT"]
+    assert len(keys) == defs["POLICY_COUNT"]
+    for n in keys:
+        assert hasattr(_lib, n), f"no Python name for EXL3_AMD_{n}"
+    assert checked >= len(keys)
