@@ -203,3 +203,46 @@ def test_decode_stack_split_norm(orc):
         d = np.abs(got - sep.cpu().numpy().astype(np.float64)).max() / np.abs(ref).max()
         print(f"decode stack (split norm) rel err {err:.2e}, vs separate norms {d:.2e}", flush=True)
         assert err < 5e-3
+
+
+@pytest.mark.parametrize("K,cb", [(2, 1), (3, 0), (2.5, 2), (5, 2), (8, 0)])
+def test_split_norm_codebooks(K, cb):
+    """Both halves on other bitrates and codebooks (the norm input form and the residual
+    epilogue are instances of every rate): producer bit-identical to exl3_gemm + res_sq,
+    consumer bit-identical to norm_sq + the plain bundle."""
+    k, n = 4096, 1024
+    L = synth.layer(k, n, K, cb, seed=int(10 * K) + cb)
+    L.svh = (L.svh.astype(np.float32) / 16).astype(np.float16)
+    t, s, v = L.torch("cuda")
+    mcg, mul1 = cb == 1, cb == 2
+    rng = np.random.default_rng(int(10 * K) + 7 * cb)
+    a = _h(rng.standard_normal((1, k)).astype(np.float16))
+    h0 = _h((rng.standard_normal((1, n)) * 4).astype(np.float16))
+    # producer
+    C1, h1 = torch.empty((1, n), dtype=torch.half, device="cuda"), h0.clone()
+    sq1 = torch.empty((1, n // 128), dtype=torch.float, device="cuda")
+    ops.exl3_gemm_res(a, t, C1, s, v, h1, sq1, mcg, mul1)
+    C2, h2 = torch.empty_like(C1), h0.clone()
+    sq2 = torch.empty_like(sq1)
+    ops.exl3_gemm(a, t, C2, s, torch.empty_like(a), v, 0, mcg, mul1)
+    ops.res_sq(h2, C2, sq2)
+    torch.cuda.synchronize()
+    assert torch.equal(C1, C2) and torch.equal(h1, h2)
+    assert np.array_equal(_bits(sq1), _bits(sq2))
+    # consumer: a stacked pair of this rate's matrices reading the residual row h (k wide)
+    lin = []
+    for i in range(2):
+        Li = synth.layer(k, 512, K, cb, seed=900 + int(10 * K) + i)
+        ti, si, vi = Li.torch("cuda")
+        lin.append(bundles.Linear(ti, si, vi, float(K), mcg, mul1))
+    hk = _h((rng.standard_normal((1, 1, k)) * 3).astype(np.float16))
+    w = _h((rng.standard_normal(k) * 0.3 + 1).astype(np.float16))
+    sqk = torch.empty((1, k // 128), dtype=torch.float, device="cuda")
+    ops.res_sq(hk.view(1, k), None, sqk)
+    r_ref = ops.norm_sq(hk.view(1, k), sqk, w, 1e-5)
+    o1 = torch.zeros((2, 1, 512), dtype=torch.half, device="cuda")
+    o2 = torch.zeros_like(o1)
+    bundles.Multi(lin, o1).run(hk, norm_in=(sqk, w, 1e-5, torch.empty((1, k), dtype=torch.half, device="cuda")))
+    bundles.Multi(lin, o2).run(r_ref.view(1, 1, k))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
