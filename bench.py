@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--summarize-pmc", metavar="PMC_DIR", nargs="+",
                     help="print per-kernel averages and derived figures of rocprofv3 --pmc output "
                          "directories (one per counter pass) and exit")
+    ap.add_argument("--decode-step", action="store_true",
+                    help="only the captured decode step's variants (0.3 s apart, for a kernel trace)")
     ap.add_argument("--recon-rows", action="store_true",
                     help="print the route table by row count: GEMV groups, MFMA GEMM, recon route with and without its split k")
     ap.add_argument("--rates", action="store_true",
@@ -246,7 +248,7 @@ def graph_time(torch, sweep, steps, warmup):
 
 
 # ------------------------------------------------------------------ captured decode step
-def decode_step_bench(torch, layers, steps=20):
+def decode_step_bench(torch, layers, steps=20, gap_s=0.0):
     """The linear part of the Llama-3-8B decode step with its neighbours (graphdec.uc:151-230:
     rms_norm_res, q/k/v sliced mgemm, o gemm, rms_norm_res, gate/up stacked mgemm, SwiGLU + down,
     final norm) captured into one graph over the same 32 layers; attention is outside the path
@@ -282,6 +284,8 @@ def decode_step_bench(torch, layers, steps=20):
         res[name] = {"us_per_step": round(us, 1), "us_per_layer": round(us / len(layers), 2),
                      "launches_per_layer": launches, "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
         del st
+        if gap_s:
+            time.sleep(gap_s)              # an idle gap: a kernel trace separates the variants by time
     return {"what": "32-layer decode step without attention: norms + linears + SwiGLU, one graph",
             "packed_bytes": nbytes, **res}
 
@@ -919,6 +923,13 @@ def main():
         return rates()
     if args.recon_rows:
         return recon_rows()
+    if args.decode_step:
+        import torch
+        from ampstein_amd import ops
+        torch.cuda.set_device(0)
+        ops.init(0)
+        print(json.dumps(decode_step_bench(torch, make_stack(torch, args.layers), gap_s=0.3)), flush=True)
+        return 0
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace)
     if args.summarize_pmc:
