@@ -65,6 +65,8 @@ def parse():
                     help="print the gfx950 issue-rate microbenchmarks (ampstein_amd/csrc/exl3_probe.hip) and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel/grid duration stats of a rocprofv3 kernel trace and exit")
+    ap.add_argument("--gap-ms", type=float, default=0.0,
+                    help="with --summarize-trace: one table per phase, split at idle gaps longer than this")
     return ap.parse_args()
 
 
@@ -760,22 +762,37 @@ def measure_traffic(gemv_alg_bytes_per_launch):
 
 
 # ------------------------------------------------------------------ main
-def summarize_trace(path):
+def summarize_trace(path, gap_ms=0.0):
     """Per (kernel, grid) average durations of a rocprofv3 --kernel-trace csv (this library's
-    kernels only): the figures the roofline's avg_launch_us is checked against."""
-    stats = {}
+    kernels only): the figures the roofline's avg_launch_us is checked against.  gap_ms > 0:
+    one table per phase, phases split where the GPU idles longer than gap_ms between kernels
+    (bench.py --decode-step leaves such gaps between its variants)."""
+    recs = []
     with open(path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "moeg", "rms_norm", "silu_mul", "Cijk")):
+            if not any(key in name for key in ("gemv", "reconstruct", "had128", "gemm", "moe_", "moes_", "moeg", "rms_norm",
+                                               "silu_mul", "res_sq", "norm_sq", "Cijk")):
                 continue
             grid = (r.get("Grid_Size_X") or r.get("Grid_Size"), r.get("Grid_Size_Y", "1"))
-            d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-            stats.setdefault((name, grid), []).append(d)
-    print(f"{'kernel':60s} {'grid (threads x, y)':>22s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}")
-    for (name, grid), ds in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
-        print(f"{name[:60]:60s} {str(grid):>22s} {len(ds):6d} {sum(ds) / len(ds) / 1e3:9.2f} "
-              f"{min(ds) / 1e3:9.2f} {max(ds) / 1e3:9.2f}")
+            recs.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name, grid))
+    recs.sort()
+    phases, last_end = [[]], None
+    for t0, t1, name, grid in recs:
+        if gap_ms > 0 and last_end is not None and t0 - last_end > gap_ms * 1e6:
+            phases.append([])
+        phases[-1].append((t0, t1, name, grid))
+        last_end = t1 if last_end is None else max(last_end, t1)
+    for pi, ph in enumerate(phases):
+        stats = {}
+        for t0, t1, name, grid in ph:
+            stats.setdefault((name, grid), []).append(t1 - t0)
+        if gap_ms > 0:
+            print(f"phase {pi}: {len(ph)} dispatches over {(ph[-1][1] - ph[0][0]) / 1e3:.0f} us")
+        print(f"{'kernel':60s} {'grid (threads x, y)':>22s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s}")
+        for (name, grid), ds in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
+            print(f"{name[:60]:60s} {str(grid):>22s} {len(ds):6d} {sum(ds) / len(ds) / 1e3:9.2f} "
+                  f"{min(ds) / 1e3:9.2f} {max(ds) / 1e3:9.2f}")
     return 0
 
 
@@ -931,7 +948,7 @@ def main():
         print(json.dumps(decode_step_bench(torch, make_stack(torch, args.layers), gap_s=0.3)), flush=True)
         return 0
     if args.summarize_trace:
-        return summarize_trace(args.summarize_trace)
+        return summarize_trace(args.summarize_trace, args.gap_ms)
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc)
     if args.pmc_child:
